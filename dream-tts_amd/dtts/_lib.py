@@ -1,0 +1,74 @@
+"""ctypes loader for libdtts.so and the call/raise plumbing.
+
+torch is imported before the library is opened: torch ships its own HIP runtime
+(``libamdhip64.so.7``) and the dynamic linker then resolves libdtts's dependency to that same
+loaded copy, so device pointers and streams are shared. The product path has no fallback: a
+missing or unloadable library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  -- binds the HIP runtime before libdtts loads
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG, "libdtts.so")
+
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+_F64 = ctypes.c_double
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "dtts_last_error": [],
+    "dtts_version": [],
+    "dtts_init": [],
+    "dtts_snake_ncl_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "dtts_snake_ncl_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "dtts_snake_nlc_f32": [_P, _P, _P, _P, _I64, _I64, _P],
+    "dtts_snake_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _P],
+}
+_RESTYPES = {"dtts_last_error": ctypes.c_char_p}
+
+
+class DttsError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise DttsError(f"libdtts.so is not built ({LIB_PATH}); run dream-tts_amd/build.py")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    status = getattr(lib(), name)(*args)
+    if status != 0:
+        msg = lib().dtts_last_error().decode(errors="replace")
+        raise DttsError(f"{name} failed ({status}): {msg}")
+
+
+def ptr(t) -> ctypes.c_void_p | None:
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device=None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,410 @@
+"""CPU oracle for the tts-nn fused-op hot path -- TEST INFRASTRUCTURE ONLY.
+
+ctypes bindings over ``liboracle.so`` (built from ``oracle.c`` by ``make -C oracle``). Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
+module, and only as the checker or the timed CPU baseline; the product library never does.
+
+Every function here restates the reference's CPU arithmetic (drmhse/dream-tts ``crates/tts-nn``
+on candle's CPU device); the C source names the reference file:line each one follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_I64 = ctypes.c_int64
+_P = ctypes.c_void_p
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle not built: {_LIB_PATH} (run `make -C oracle`)")
+        _lib = ctypes.CDLL(_LIB_PATH)
+    return _lib
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _f64(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _u16(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.uint16)
+
+
+# ---------------------------------------------------------------- f16
+
+def f32_to_f16(x):
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_f16_array(_ptr(x), _ptr(out), _I64(x.size))
+    return out
+
+
+def f16_to_f32(h):
+    h = _u16(h)
+    out = np.empty(h.shape, np.float32)
+    lib().or_f16_to_f32_array(_ptr(h), _ptr(out), _I64(h.size))
+    return out
+
+
+# ---------------------------------------------------------------- snake
+
+def snake_ncl_f32(x, alpha, brecip):
+    x, a, r = _f32(x), _f32(alpha), _f32(brecip)
+    lanes, c, l = x.shape
+    y = np.empty_like(x)
+    lib().or_snake_ncl_f32(_ptr(x), _ptr(a), _ptr(r), _ptr(y), _I64(lanes), _I64(c), _I64(l))
+    return y
+
+
+def snake_ncl_f16(x_bits, alpha, brecip):
+    x, a, r = _u16(x_bits), _f32(alpha), _f32(brecip)
+    lanes, c, l = x.shape
+    y = np.empty_like(x)
+    lib().or_snake_ncl_f16(_ptr(x), _ptr(a), _ptr(r), _ptr(y), _I64(lanes), _I64(c), _I64(l))
+    return y
+
+
+def snake_nlc_f32(x, alpha, brecip):
+    x, a, r = _f32(x), _f32(alpha), _f32(brecip)
+    c = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_snake_nlc_f32(_ptr(x), _ptr(a), _ptr(r), _ptr(y), _I64(x.size // c), _I64(c))
+    return y
+
+
+def snake_nlc_f16(x_bits, alpha, brecip):
+    x, a, r = _u16(x_bits), _f32(alpha), _f32(brecip)
+    c = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_snake_nlc_f16(_ptr(x), _ptr(a), _ptr(r), _ptr(y), _I64(x.size // c), _I64(c))
+    return y
+
+
+def snake_nlc_f64(x, alpha, brecip):
+    x, a, r = _f64(x), _f64(alpha), _f64(brecip)
+    c = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_snake_nlc_f64(_ptr(x), _ptr(a), _ptr(r), _ptr(y), _I64(x.size // c), _I64(c))
+    return y
+
+
+# ---------------------------------------------------------------- im2col / weights
+
+def im2col_tap_major_f32(x, k, dil, pad_left):
+    x = _f32(x)
+    cin, length = x.shape
+    cols = np.empty((k * cin, length), np.float32)
+    lib().or_im2col_tap_major_f32(_ptr(x), _ptr(cols), _I64(cin), _I64(length), _I64(k),
+                                  _I64(dil), _I64(pad_left))
+    return cols
+
+
+def tap_weight_f32(w_oik):
+    w = _f32(w_oik)
+    cout, cin, k = w.shape
+    out = np.empty((k, cin, cout), np.float32)
+    lib().or_tap_weight_f32(_ptr(w), _ptr(out), _I64(cout), _I64(cin), _I64(k))
+    return out
+
+
+def tap_major_weight_f32(w_oik):
+    w = _f32(w_oik)
+    cout, cin, k = w.shape
+    out = np.empty((cout, k * cin), np.float32)
+    lib().or_tap_major_weight_f32(_ptr(w), _ptr(out), _I64(cout), _I64(cin), _I64(k))
+    return out
+
+
+def transpose_tap_weight_f32(w_iok, stride):
+    w = _f32(w_iok)
+    cin, cout, k = w.shape
+    assert k % stride == 0
+    out = np.empty((k // stride, cin, stride * cout), np.float32)
+    lib().or_transpose_tap_weight_f32(_ptr(w), _ptr(out), _I64(cin), _I64(cout), _I64(k),
+                                      _I64(stride))
+    return out
+
+
+def transpose_bias_f32(b, stride):
+    b = _f32(b)
+    out = np.empty((stride * b.size,), np.float32)
+    lib().or_transpose_bias_f32(_ptr(b), _ptr(out), _I64(b.size), _I64(stride))
+    return out
+
+
+# ---------------------------------------------------------------- convs
+
+def conv1d_nlc_f32(x, w_tap, bias, dil, pad_left=None, snake=None, res=None):
+    """x [lanes, L, cin]; w_tap [k, cin, cout] (or [k*cin, cout]); causal when pad_left is None."""
+    x, w = _f32(x), _f32(w_tap)
+    lanes, length, cin = x.shape
+    cout = w.shape[-1]
+    k = w.size // (cin * cout)
+    if pad_left is None:
+        pad_left = (k - 1) * dil
+    a, r = (None, None) if snake is None else (_f32(snake[0]), _f32(snake[1]))
+    b, rs = _f32(bias), _f32(res)
+    y = np.empty((lanes, length, cout), np.float32)
+    lib().or_conv1d_nlc_f32(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
+                            _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),
+                            _I64(pad_left))
+    return y
+
+
+def conv1d_nlc_f64(x, w_tap, bias, dil, pad_left=None, snake=None, res=None):
+    x, w = _f64(x), _f64(w_tap)
+    lanes, length, cin = x.shape
+    cout = w.shape[-1]
+    k = w.size // (cin * cout)
+    if pad_left is None:
+        pad_left = (k - 1) * dil
+    a, r = (None, None) if snake is None else (_f64(snake[0]), _f64(snake[1]))
+    b, rs = _f64(bias), _f64(res)
+    y = np.empty((lanes, length, cout), np.float64)
+    lib().or_conv1d_nlc_f64(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
+                            _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),
+                            _I64(pad_left))
+    return y
+
+
+def conv1d_nlc_f16(x_bits, w_tap_bits, bias_bits, dil, pad_left=None, snake=None, res_bits=None,
+                   act_tanh=False):
+    x, w = _u16(x_bits), _u16(w_tap_bits)
+    lanes, length, cin = x.shape
+    cout = w.shape[-1]
+    k = w.size // (cin * cout)
+    if pad_left is None:
+        pad_left = (k - 1) * dil
+    a, r = (None, None) if snake is None else (_f32(snake[0]), _f32(snake[1]))
+    b, rs = _u16(bias_bits), _u16(res_bits)
+    y = np.empty((lanes, length, cout), np.uint16)
+    lib().or_conv1d_nlc_f16(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
+                            _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),
+                            _I64(pad_left), ctypes.c_int32(1 if act_tanh else 0))
+    return y
+
+
+def conv_transpose1d_causal_f64(x, w_iok, bias, stride):
+    x, w = _f64(x), _f64(w_iok)
+    length, cin = x.shape
+    _, cout, k = w.shape
+    b = _f64(bias)
+    y = np.empty((length * stride, cout), np.float64)
+    lib().or_conv_transpose1d_causal_f64(_ptr(x), _ptr(w), _ptr(b), _ptr(y), _I64(length),
+                                         _I64(cin), _I64(cout), _I64(k), _I64(stride))
+    return y
+
+
+def sgemm(a, b):
+    a, b = _f32(a), _f32(b)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib().or_sgemm(_ptr(a), _ptr(b), _ptr(c), _I64(m), _I64(n), _I64(k), ctypes.c_int32(0))
+    return c
+
+
+def conv1d_ncl_gemm_f32(x, w_tm, bias, k, dil, pad_left):
+    x, w = _f32(x), _f32(w_tm)
+    lanes, cin, length = x.shape
+    cout = w.shape[0]
+    b = _f32(bias)
+    y = np.empty((lanes, cout, length), np.float32)
+    lib().or_conv1d_ncl_gemm_f32(_ptr(x), _ptr(w), _ptr(b), _ptr(y), _I64(lanes), _I64(cin),
+                                 _I64(cout), _I64(length), _I64(k), _I64(dil), _I64(pad_left))
+    return y
+
+
+def conv1d_nlc_cat_gemm_f32(x, w_tap, bias, dil):
+    """One lane: x [L, cin], w_tap [k, cin, cout] -> [L, cout] (the reference's cat route)."""
+    x, w = _f32(x), _f32(w_tap)
+    length, cin = x.shape
+    cout = w.shape[-1]
+    k = w.size // (cin * cout)
+    b = _f32(bias)
+    y = np.empty((length, cout), np.float32)
+    lib().or_conv1d_nlc_cat_gemm_f32(_ptr(x), _ptr(w), _ptr(b), _ptr(y), _I64(length), _I64(cin),
+                                     _I64(cout), _I64(k), _I64(dil))
+    return y
+
+
+# ---------------------------------------------------------------- norm / rope / cache
+
+def rms_norm_f32(x, gamma, eps):
+    x, g = _f32(x), _f32(gamma)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_rms_norm_f32(_ptr(x), _ptr(g), _ptr(y), _I64(x.size // dim), _I64(dim),
+                          ctypes.c_float(eps))
+    return y
+
+
+def rms_norm_f16(x_bits, gamma_bits, eps):
+    x, g = _u16(x_bits), _u16(gamma_bits)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_rms_norm_f16(_ptr(x), _ptr(g), _ptr(y), _I64(x.size // dim), _I64(dim),
+                          ctypes.c_float(eps))
+    return y
+
+
+def rms_norm_f64(x, gamma, eps):
+    x, g = _f64(x), _f64(gamma)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_rms_norm_f64(_ptr(x), _ptr(g), _ptr(y), _I64(x.size // dim), _I64(dim),
+                          ctypes.c_double(eps))
+    return y
+
+
+def rope_table_f32(length, head_dim, base):
+    c = np.empty((length, head_dim // 2), np.float32)
+    s = np.empty((length, head_dim // 2), np.float32)
+    lib().or_rope_table_f32(_I64(length), _I64(head_dim), ctypes.c_double(base), _ptr(c), _ptr(s))
+    return c, s
+
+
+def rope_halfsplit_f32(x, cos_t, sin_t, pos):
+    x = _f32(x)
+    rows, heads, hd = x.shape
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    y = np.empty_like(x)
+    lib().or_rope_halfsplit_f32(_ptr(x), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), _ptr(p), _ptr(y),
+                                _I64(rows), _I64(heads), _I64(hd))
+    return y
+
+
+def rope_halfsplit_f16(x_bits, cos_t, sin_t, pos):
+    x = _u16(x_bits)
+    rows, heads, hd = x.shape
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    y = np.empty_like(x)
+    lib().or_rope_halfsplit_f16(_ptr(x), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), _ptr(p), _ptr(y),
+                                _I64(rows), _I64(heads), _I64(hd))
+    return y
+
+
+def qk_norm_rope_append_f32(qkv, norms, cos_t, sin_t, pos, kcache, vcache, heads, n_kv, eps):
+    """kcache/vcache (uint16 [b, n_kv, cap, D]) are updated in place; returns (q, k_f32)."""
+    qkv = _f32(qkv)
+    b = qkv.shape[0]
+    hd = norms.shape[-1]
+    cap = kcache.shape[2]
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    q = np.empty((b, heads, hd), np.float32)
+    k = np.empty((b, n_kv, hd), np.float32)
+    assert kcache.dtype == np.uint16 and kcache.flags["C_CONTIGUOUS"]
+    lib().or_qk_norm_rope_append_f32(_ptr(qkv), _ptr(_f32(norms)), _ptr(_f32(cos_t)),
+                                     _ptr(_f32(sin_t)), _ptr(p), _ptr(q), _ptr(k), _ptr(kcache),
+                                     _ptr(vcache), _I64(b), _I64(heads), _I64(n_kv), _I64(hd),
+                                     _I64(cap), ctypes.c_float(eps))
+    return q, k
+
+
+def kv_append_f32(k, v, pos, kcache, vcache):
+    k, v = _f32(k), _f32(v)
+    b, n_kv, hd = k.shape
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().or_kv_append_f32(_ptr(k), _ptr(v), _ptr(p), _ptr(kcache), _ptr(vcache), _I64(b),
+                           _I64(n_kv), _I64(hd), _I64(kcache.shape[2]))
+
+
+def kv_append_f16(k_bits, v_bits, pos, kcache, vcache):
+    k, v = _u16(k_bits), _u16(v_bits)
+    b, n_kv, hd = k.shape
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().or_kv_append_f16(_ptr(k), _ptr(v), _ptr(p), _ptr(kcache), _ptr(vcache), _I64(b),
+                           _I64(n_kv), _I64(hd), _I64(kcache.shape[2]))
+
+
+# ---------------------------------------------------------------- GEMMs
+
+def gemm_f16_f32acc(a_bits, b_kn_bits):
+    a, b = _u16(a_bits), _u16(b_kn_bits)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib().or_gemm_f16_f32acc(_ptr(a), _ptr(b), _ptr(c), _I64(m), _I64(k), _I64(n))
+    return c
+
+
+def gemm_f16_f64(a_bits, b_kn_bits):
+    a, b = _u16(a_bits), _u16(b_kn_bits)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float64)
+    lib().or_gemm_f16_f64(_ptr(a), _ptr(b), _ptr(c), _I64(m), _I64(k), _I64(n))
+    return c
+
+
+def swiglu_mul_f32(g, u):
+    g, u = _f32(g), _f32(u)
+    y = np.empty_like(g)
+    lib().or_swiglu_mul_f32(_ptr(g), _ptr(u), _ptr(y), _I64(g.size))
+    return y
+
+
+def q8_0_quantize(w):
+    w = _f32(w)
+    rows, k = w.shape
+    out = np.empty((rows, k // 32, 34), np.uint8)
+    lib().or_q8_0_quantize(_ptr(w), _ptr(out), _I64(rows), _I64(k))
+    return out
+
+
+def q8_0_dequantize(blocks, k):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    rows = blocks.shape[0]
+    w = np.empty((rows, k), np.float32)
+    lib().or_q8_0_dequantize(_ptr(blocks), _ptr(w), _I64(rows), _I64(k))
+    return w
+
+
+def q8_0_matmul_w8a8(x, blocks):
+    x = _f32(x)
+    m, k = x.shape
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = blocks.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().or_q8_0_matmul_w8a8(_ptr(x), _ptr(blocks), _ptr(y), _I64(m), _I64(k), _I64(n))
+    return y
+
+
+def q8_0_matmul_f64(x, blocks):
+    x = _f32(x)
+    m, k = x.shape
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = blocks.shape[0]
+    y = np.empty((m, n), np.float64)
+    lib().or_q8_0_matmul_f64(_ptr(x), _ptr(blocks), _ptr(y), _I64(m), _I64(k), _I64(n))
+    return y
+
+
+# ---------------------------------------------------------------- metric
+
+def abs_and_rel(a, b):
+    a, b = _f32(a), _f32(b)
+    assert a.size == b.size
+    ab, rl = ctypes.c_float(), ctypes.c_float()
+    lib().or_abs_and_rel(_ptr(a), _ptr(b), _I64(a.size), ctypes.byref(ab), ctypes.byref(rl))
+    return float(ab.value), float(rl.value)

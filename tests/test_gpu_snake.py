@@ -1,0 +1,124 @@
+"""Snake kernels (a1/a2) against the CPU oracle and double precision, through the C ABI.
+
+Tolerances: f32 outputs max-rel <= 1e-5 against the oracle (the reference's bound,
+crates/tts-nn/src/fused.rs:2452-2482) and <= 1e-6 / 2e-6 of max(|x|, r, 1) against f64
+(fused.rs:2356-2391, 2227-2337); f16 outputs within 1 f16 ulp of the oracle's f16 result.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dtts import ops, synth
+
+from _util import f16_ulp_diff, rel, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(seed, c):
+    a = np.exp(synth.normal(seed, "alpha", (c,))).astype(np.float32)
+    r = np.exp(synth.normal(seed, "brecip", (c,))).astype(np.float32)
+    return a, r
+
+
+@pytest.mark.parametrize("rows,c", [(33, 7), (601, 1536), (4801, 24), (1000, 96), (5, 1), (3, 8)])
+def test_snake_nlc_f32(dev, rows, c):
+    x = synth.normal(20, "x", (rows, c), 0, 2)
+    a, r = _params(20, c)
+    got = to_host(ops.snake_beta_nlc(to_dev(x, dev), to_dev(a, dev), to_dev(r, dev)))
+    want = oracle.snake_nlc_f32(x, a, r)
+    assert rel(got, want)[1] < 1e-5
+
+
+def test_snake_f32_generator_range_accuracy(dev):
+    # crates/tts-nn/src/fused.rs:2356-2391: x over +-12, alpha 0.03..2.33, brecip 0.5 + j;
+    # error against f64 scaled by max(|x|, r, 1) < 1e-6.
+    c, length = 8, 2048
+    xs = (-12.0 + 24.0 * (np.arange(c * length) % length) / (length - 1)).astype(np.float32)
+    x = xs.reshape(1, c, length)
+    al = np.array([0.03 + 2.3 * j / (c - 1) for j in range(c)], np.float32)
+    br = np.array([0.5 + j for j in range(c)], np.float32)
+    got = to_host(ops.snake_beta(to_dev(x, dev), to_dev(al, dev), to_dev(br, dev)))
+    want = x + br[None, :, None].astype(np.float64) * np.sin(al[None, :, None].astype(np.float64) * x) ** 2
+    scale = np.maximum(np.maximum(np.abs(x), br[None, :, None]), 1.0)
+    assert np.max(np.abs(got - want) / scale) < 1e-6
+
+
+@pytest.mark.parametrize("lanes,c,length", [(1, 7, 33), (1, 1536, 601), (1, 24, 4801),
+                                            (1, 512, 4800), (3, 5, 17)])
+def test_snake_ncl_f32(dev, lanes, c, length):
+    x = synth.normal(21, "x", (lanes, c, length), 0, 2)
+    a, r = _params(21, c)
+    got = to_host(ops.snake_beta(to_dev(x, dev), to_dev(a, dev), to_dev(r, dev)))
+    want = oracle.snake_ncl_f32(x, a, r)
+    assert rel(got, want)[1] < 1e-5
+
+
+def test_snake_f32_wide_sweep_accuracy(dev):
+    # crates/tts-nn/src/fused.rs:2227-2337: x over +-30, alpha 0.05..2.55; bound 2e-6.
+    c, length = 8, 4096
+    xs = (-30.0 + 60.0 * (np.arange(c * length) % length) / (length - 1)).astype(np.float32)
+    x = xs.reshape(length, c)
+    al = np.array([0.05 + 2.5 * j / (c - 1) for j in range(c)], np.float32)
+    br = np.array([0.5 + j for j in range(c)], np.float32)
+    got = to_host(ops.snake_beta_nlc(to_dev(x, dev), to_dev(al, dev), to_dev(br, dev)))
+    want = oracle.snake_nlc_f64(x, al, br)
+    scale = np.maximum(np.maximum(np.abs(x), br[None, :]), 1.0)
+    assert np.max(np.abs(got - want) / scale) < 2e-6
+
+
+@pytest.mark.parametrize("rows,c", [(33, 7), (601, 1536), (4801, 24), (2000, 96), (9, 8)])
+def test_snake_nlc_f16(dev, rows, c):
+    x = synth.f16_bits(synth.normal(22, "x", (rows, c), 0, 3))
+    a = synth.uniform(22, "a", (c,), 0.5, 1.5)
+    r = (1.0 / a).astype(np.float32)
+    got = to_host(ops.snake_beta_nlc(to_dev(x, dev), to_dev(a, dev), to_dev(r, dev)))
+    want = oracle.snake_nlc_f16(x, a, r)
+    assert f16_ulp_diff(got, want) <= 1
+    assert rel(synth.from_f16_bits(got), synth.from_f16_bits(want))[1] < 1e-3
+
+
+@pytest.mark.parametrize("lanes,c,length", [(1, 7, 33), (2, 96, 4800), (1, 3, 8)])
+def test_snake_ncl_f16(dev, lanes, c, length):
+    x = synth.f16_bits(synth.normal(23, "x", (lanes, c, length), 0, 3))
+    a = synth.uniform(23, "a", (c,), 0.5, 1.5)
+    r = (1.0 / a).astype(np.float32)
+    got = to_host(ops.snake_beta(to_dev(x, dev), to_dev(a, dev), to_dev(r, dev)))
+    want = oracle.snake_ncl_f16(x, a, r)
+    assert f16_ulp_diff(got, want) <= 1
+
+
+def test_snake_f16_fast_sine_accuracy(dev):
+    # The f16 path's hardware sine over the generator's range (|alpha x| up to ~75): error
+    # against f64 stays within half an f16 ulp of the result plus 2e-6 of the operand scale.
+    c, length = 8, 4096
+    xs = (-30.0 + 60.0 * (np.arange(c * length) % length) / (length - 1)).astype(np.float32)
+    x = synth.f16_bits(xs.reshape(length, c))
+    xf = synth.from_f16_bits(x)
+    al = np.array([0.05 + 2.5 * j / (c - 1) for j in range(c)], np.float32)
+    br = np.array([0.5 + j for j in range(c)], np.float32)
+    got = synth.from_f16_bits(to_host(ops.snake_beta_nlc(to_dev(x, dev), to_dev(al, dev), to_dev(br, dev))))
+    want = oracle.snake_nlc_f64(xf, al, br)
+    half_ulp = np.abs(want) * 2.0 ** -11 + 2.0 ** -25
+    scale = np.maximum(np.maximum(np.abs(xf), br[None, :]), 1.0)
+    assert np.all(np.abs(got - want) <= half_ulp + 2e-6 * scale)
+
+
+def test_snake_in_place_and_zero(dev):
+    x = synth.normal(24, "x", (100, 96), 0, 1)
+    a, r = _params(24, 96)
+    t = to_dev(x, dev)
+    ops.snake_beta_nlc(t, to_dev(a, dev), to_dev(r, dev), out=t)
+    assert rel(to_host(t), oracle.snake_nlc_f32(x, a, r))[1] < 1e-5
+    z = torch.zeros((10, 96), device=dev)
+    assert torch.count_nonzero(ops.snake_beta_nlc(z, to_dev(a, dev), to_dev(r, dev))).item() == 0
+
+
+def test_snake_rejects_bad_arguments(dev):
+    from dtts import DttsError
+
+    x = torch.zeros((4, 8), device=dev)
+    a = torch.ones(7, device=dev)
+    with pytest.raises(DttsError, match="alpha"):
+        ops.snake_beta_nlc(x, a, a)
