@@ -1,0 +1,129 @@
+"""tts-nn's channels-last conv surface (crates/tts-nn/src/nlc.rs) over libdtts.
+
+Weights go through the host layout functions once (as the reference's loaders do) and then live
+on the device in the tap-major [cout, k*cin] form the matrix-core kernel reads.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import DttsError, call, lib, ptr, stream_handle
+
+
+class ConvDesc(ctypes.Structure):
+    _fields_ = [
+        ("lanes", ctypes.c_int64), ("len", ctypes.c_int64), ("cin", ctypes.c_int64),
+        ("cout", ctypes.c_int64), ("k", ctypes.c_int64), ("dilation", ctypes.c_int64),
+        ("pad_left", ctypes.c_int64),
+        ("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("in_alpha", ctypes.c_void_p), ("in_brecip", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p), ("y_pre", ctypes.c_void_p),
+        ("out_alpha", ctypes.c_void_p), ("out_brecip", ctypes.c_void_p),
+        ("y", ctypes.c_void_p), ("act", ctypes.c_int32),
+    ]
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _need(t, name, what, dtype, shape=None):
+    if t is None:
+        return
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == dtype and t.is_contiguous()):
+        raise DttsError(f"{name}: {what} must be a contiguous {dtype} device tensor")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise DttsError(f"{name}: {what} shape {tuple(t.shape)} != {tuple(shape)}")
+
+
+def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, residual=None,
+           snake_out=None, want_pre=False, act=None, out=None):
+    """The general fused channels-last conv (dtts_conv1d_nlc_f16_ex).
+
+    x [lanes, L, cin] f16, w_tm [cout, k*cin] f16, bias [cout] f16. snake_in / snake_out are
+    (alpha, brecip) f32 pairs applied to the input as loaded / to the rounded output. Returns y,
+    or (y_pre, y) when want_pre."""
+    name = "nlc.conv1d"
+    if x.dim() != 3:
+        raise DttsError(f"{name}: x must be [lanes, L, cin]")
+    lanes, length, cin = x.shape
+    cout = w_tm.shape[0]
+    _need(x, name, "x", torch.float16)
+    _need(w_tm, name, "w_tm", torch.float16, (cout, k * cin))
+    _need(bias, name, "bias", torch.float16, (cout,))
+    _need(residual, name, "residual", torch.float16, (lanes, length, cout))
+    for pair, what, c in ((snake_in, "snake_in", cin), (snake_out, "snake_out", cout)):
+        if pair is not None:
+            for t in pair:
+                _need(t, name, what, torch.float32, (c,))
+    y = torch.empty((lanes, length, cout), dtype=torch.float16, device=x.device) if out is None else out
+    y_pre = torch.empty_like(y) if want_pre else None
+    d = ConvDesc(lanes, length, cin, cout, k, dilation,
+                 (k - 1) * dilation if pad_left is None else pad_left,
+                 _p(x), _p(w_tm), _p(bias),
+                 _p(snake_in[0]) if snake_in else None, _p(snake_in[1]) if snake_in else None,
+                 _p(residual), _p(y_pre),
+                 _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
+                 _p(y), {None: 0, "tanh": 1}[act])
+    call("dtts_conv1d_nlc_f16_ex", ctypes.byref(d), stream_handle())
+    return (y_pre, y) if want_pre else y
+
+
+def causal_conv1d(x, w_tm, bias, dilation):
+    """nlc::causal_conv1d (crates/tts-nn/src/nlc.rs:70-132), w in tap-major [cout, k*cin]."""
+    k = w_tm.shape[1] // x.shape[-1]
+    return conv1d(x, w_tm, bias, k=k, dilation=dilation)
+
+
+def snake_conv_residual(x, w_tm, bias, dilation, snake, res):
+    """nlc::snake_conv_residual (crates/tts-nn/src/nlc.rs:40-68): res + conv(SnakeBeta(x))."""
+    k = w_tm.shape[1] // x.shape[-1]
+    return conv1d(x, w_tm, bias, k=k, dilation=dilation, snake_in=snake, residual=res)
+
+
+def causal_conv_transpose1d(x, w_tm, bias_rep, stride):
+    """The polyphase transposed conv (crates/tts-nn/src/codec.rs:153-158 with
+    nlc::transpose_tap_weight): one causal conv, then [b, L, s*cout] viewed as [b, L*s, cout]."""
+    lanes, length, cin = x.shape
+    k = w_tm.shape[1] // cin
+    y = conv1d(x, w_tm, bias_rep, k=k, dilation=1)
+    return y.view(lanes, length * stride, w_tm.shape[0] // stride)
+
+
+# ---------------------------------------------------------------- host layouts
+
+def _host_layout(fn, arr, out_shape, *dims):
+    a = np.ascontiguousarray(arr)
+    es = a.dtype.itemsize
+    out = np.empty(out_shape, a.dtype)
+    status = getattr(lib(), fn)(ctypes.c_void_p(a.ctypes.data), ctypes.c_void_p(out.ctypes.data),
+                                *[ctypes.c_int64(d) for d in dims], ctypes.c_int64(es))
+    if status != 0:
+        raise DttsError(f"{fn}: {lib().dtts_last_error().decode()}")
+    return out
+
+
+def tap_major_weight(w_oik: np.ndarray) -> np.ndarray:
+    """lib.rs:630-635: torch [cout, cin, k] -> [cout, k*cin] (host, numpy in/out)."""
+    cout, cin, k = w_oik.shape
+    return _host_layout("dtts_tap_major_weight", w_oik, (cout, k * cin), cout, cin, k)
+
+
+def tap_weight_to_tap_major(w_kio: np.ndarray) -> np.ndarray:
+    k, cin, cout = w_kio.shape
+    return _host_layout("dtts_tap_weight_to_tap_major", w_kio, (cout, k * cin), k, cin, cout)
+
+
+def transpose_tap_major_weight(w_iok: np.ndarray, stride: int) -> np.ndarray:
+    """nlc.rs:158-174 in tap-major form: [cin, cout, K] -> [stride*cout, (K/stride)*cin]."""
+    cin, cout, kernel = w_iok.shape
+    return _host_layout("dtts_transpose_tap_major_weight", w_iok,
+                        (stride * cout, (kernel // stride) * cin), cin, cout, kernel, stride)
+
+
+def transpose_bias(b: np.ndarray, stride: int) -> np.ndarray:
+    """nlc.rs:177-183: [cout] -> [stride*cout]."""
+    return _host_layout("dtts_transpose_bias", b, (stride * b.shape[0],), b.shape[0], stride)

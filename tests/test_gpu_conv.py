@@ -1,0 +1,127 @@
+"""Channels-last conv (a3-a5) through the C ABI against the CPU oracle's f16-storage conv.
+
+Both sides hold activations, weights and bias in f16, snake outputs rounded to f16, f32
+accumulation and one rounding of the output; they differ only in summation order. Bar: max-abs
+<= 2e-2 at unit-scale activations (the f16 GEMM tolerance), and at most a few f16 ulps. The
+transposed conv is also held to the f64 scatter definition of ConvTranspose1d.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dtts import nlc, synth
+
+from _util import f16_ulp_diff, to_dev, to_host  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, lanes, length, cin, cout, k, wscale=None):
+    x = synth.f16_bits(synth.normal(seed, "x", (lanes, length, cin)))
+    std = wscale if wscale is not None else np.sqrt(2.0 / (cin * k))  # Kaiming normal
+    w = synth.normal(seed, "w", (cout, cin, k), 0, std)
+    wb = synth.f16_bits(w)
+    b = synth.f16_bits(synth.normal(seed, "b", (cout,), 0, 0.01))
+    return x, w, wb, b
+
+
+def _elementwise(got_bits, want_bits):
+    """Per element: one f16 ulp of the value plus the f32 summation-order error (~1e-4 here)."""
+    g = synth.from_f16_bits(got_bits).astype(np.float64)
+    w = synth.from_f16_bits(want_bits).astype(np.float64)
+    bad = np.abs(g - w) > np.abs(w) * 2.0 ** -10 + 1e-4
+    assert not bad.any(), f"{int(bad.sum())} elements off, worst {np.max(np.abs(g - w)):.3e}"
+
+
+def _close(got_bits, want_bits, tol=2e-2):
+    g = synth.from_f16_bits(got_bits)
+    w = synth.from_f16_bits(want_bits)
+    err = float(np.max(np.abs(g - w))) if g.size else 0.0
+    assert err <= tol, f"max abs {err:.3e}"
+    return err
+
+
+@pytest.mark.parametrize("lanes,cin,cout,length,k,dil", [
+    (2, 8, 12, 40, 7, 1), (1, 16, 16, 33, 7, 3), (2, 6, 9, 20, 1, 1),            # nlc.rs:294-328 (direct)
+    (1, 96, 96, 4200, 7, 9), (2, 32, 96, 4096, 7, 1), (1, 128, 192, 5000, 7, 3),  # nlc.rs:362-398
+    (2, 64, 96, 4097, 1, 1),
+    (3, 96, 96, 700, 7, 9), (2, 192, 192, 513, 7, 3), (2, 384, 384, 300, 7, 1),   # codec RU shapes
+    (2, 768, 768, 250, 1, 1), (2, 1024, 1536, 250, 7, 1),                         # RU k1, head conv
+    (2, 64, 64, 100, 7, 2), (2, 32, 32, 65, 3, 4),                                 # BN 64 / 32 tiles
+])
+def test_causal_conv_matches_oracle(dev, lanes, cin, cout, length, k, dil):
+    x, w, wb, b = _case(40, lanes, length, cin, cout, k)
+    w_tm = nlc.tap_major_weight(wb)
+    got = to_host(nlc.causal_conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), dil))
+    want = oracle.conv1d_nlc_f16(x, oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float32)
+                                 .astype(np.float16).view(np.uint16), b, dil)
+    _close(got, want)
+    _elementwise(got, want)
+
+
+@pytest.mark.parametrize("lanes,c,length,k,dil,pre", [
+    (2, 96, 3000, 1, 1, False), (2, 192, 1100, 7, 3, True), (1, 96, 2049, 7, 9, True),
+    (2, 384, 300, 7, 1, False),
+])
+def test_fused_prologue_epilogue(dev, lanes, c, length, k, dil, pre):
+    """snake on load + residual (snake_conv_residual), plus the epilogue snake and y_pre."""
+    x, w, wb, b = _case(41, lanes, length, c, c, k)
+    res = synth.f16_bits(synth.normal(41, "res", (lanes, length, c)))
+    a1 = synth.uniform(41, "a1", (c,), 0.5, 1.5)
+    r1 = (1.0 / a1).astype(np.float32)
+    a2 = synth.uniform(41, "a2", (c,), 0.5, 1.5)
+    r2 = (1.0 / a2).astype(np.float32)
+    w_tm = nlc.tap_major_weight(wb)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    y_pre, y = nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil,
+                          snake_in=(to_dev(a1, dev), to_dev(r1, dev)), residual=to_dev(res, dev),
+                          snake_out=(to_dev(a2, dev), to_dev(r2, dev)), want_pre=True)
+    want_pre = oracle.conv1d_nlc_f16(x, w_tap, b, dil, snake=(a1, r1), res_bits=res)
+    _close(to_host(y_pre), want_pre)
+    # the epilogue snake applied to the kernel's own rounded sum is exactly the oracle's snake
+    got_y = to_host(y)
+    assert f16_ulp_diff(got_y, oracle.snake_nlc_f16(to_host(y_pre), a2, r2)) <= 1
+    _close(got_y, oracle.snake_nlc_f16(want_pre, a2, r2), tol=3e-2)
+
+
+@pytest.mark.parametrize("cin,cout,length,stride", [(1536, 768, 20, 8), (768, 384, 40, 5),
+                                                    (384, 192, 64, 4), (192, 96, 128, 3),
+                                                    (32, 32, 9, 2)])
+def test_transposed_conv_matches_definition(dev, cin, cout, length, stride):
+    lanes, k = 2, 2 * stride
+    x = synth.f16_bits(synth.normal(42, "x", (lanes, length, cin)))
+    w = synth.normal(42, "w", (cin, cout, k), 0, np.sqrt(2.0 / (cout * k)))
+    wb = synth.f16_bits(w)
+    b = synth.f16_bits(synth.normal(42, "b", (cout,), 0, 0.01))
+    w_tm = nlc.transpose_tap_major_weight(wb, stride)
+    b_rep = nlc.transpose_bias(b, stride)
+    got = to_host(nlc.causal_conv_transpose1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b_rep, dev), stride))
+    assert got.shape == (lanes, length * stride, cout)
+    for li in range(lanes):
+        want = oracle.conv_transpose1d_causal_f64(synth.from_f16_bits(x[li]), synth.from_f16_bits(wb),
+                                                  synth.from_f16_bits(b), stride)
+        err = np.abs(synth.from_f16_bits(got[li]) - want)
+        assert np.max(err) <= 2e-2
+        assert np.all(err <= np.abs(want) * 2.0 ** -10 + 1e-3)
+
+
+def test_tanh_output_conv_single_channel(dev):
+    """The decoder's output conv: 96 -> 1, k=7, tanh (direct kernel)."""
+    x, w, wb, b = _case(43, 2, 1500, 96, 1, 7)
+    w_tm = nlc.tap_major_weight(wb)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    y = to_host(nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=7, act="tanh"))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, 1, act_tanh=True)
+    _close(y, want, tol=2e-3)
+
+
+def test_conv_rejects_bad_shapes(dev):
+    from dtts import DttsError
+
+    x = torch.zeros((1, 10, 32), dtype=torch.float16, device=dev)
+    w = torch.zeros((32, 7 * 32), dtype=torch.float16, device=dev)
+    with pytest.raises(DttsError, match="pad_left"):
+        nlc.conv1d(x, w, None, k=7, dilation=1, pad_left=7)
+    with pytest.raises(DttsError, match="shape"):
+        nlc.conv1d(x, w[:, :100].contiguous(), None, k=7)
