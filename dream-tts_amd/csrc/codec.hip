@@ -1,0 +1,312 @@
+// The qwen3tts codec's waveform stack (head conv, upsampling blocks, output conv) as a sequence
+// of fused channels-last convs over all lanes at once.
+//
+// Reference: Codec::forward's tail, crates/qwen3tts/src/codec.rs:426-436, with DecoderBlock
+// (codec.rs:252-258), ResidualUnit (codec.rs:215-229), TransConv (codec.rs:153-158) and SnakeBeta
+// (codec.rs:55-73). Every SnakeBeta is folded into a conv:
+//   head conv           epilogue: block 0's SnakeBeta, only the snaked tensor is stored
+//   block i TransConv   prologue: nothing (its input arrives snaked); epilogue: stores u and,
+//                       when u is wide, also SnakeBeta_{unit 0, act1}(u)
+//   unit j conv1 (k7)   prologue: act1 when u was stored unsnaked; epilogue: act2, stored snaked
+//   unit j conv2 (k1)   epilogue: + u (residual), then the next activation: unit j+1's act1
+//                       (stored both ways when wide), or the next block's / the output SnakeBeta
+//   output conv         tanh in the epilogue
+// Every tensor stored is one the unfused chain would store (f16), so the arithmetic matches the
+// composed form up to summation order.
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "conv.hpp"
+
+struct dtts_codec {
+    dtts_codec_geometry geo;
+    dtts_codec_weights w;
+    // act1 of unit 0 of each block, repeated over the TransConv's `rate` output phases (the
+    // TransConv's output channel p*C + c is channel c of phase p).
+    std::vector<float *> phase_alpha, phase_brecip;
+};
+
+namespace dtts {
+namespace {
+
+// Stages whose residual-unit input is at least this wide store it snaked as well: the unit's
+// k7 conv then reads the snaked copy instead of recomputing SnakeBeta once per output tile.
+constexpr int64_t kStoreSnakedAbove = 96;
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int64_t stage_elems(const dtts_codec_geometry &g, int64_t frames) {
+    int64_t m = frames * g.channels[0];
+    int64_t len = frames;
+    for (int64_t i = 0; i < g.n_blocks; ++i) {
+        len *= g.rates[i];
+        const int64_t e = len * g.channels[i + 1];
+        if (e > m) m = e;
+    }
+    return m;
+}
+
+int64_t hop_of(const dtts_codec_geometry &g) {
+    int64_t h = 1;
+    for (int64_t i = 0; i < g.n_blocks; ++i) h *= g.rates[i];
+    return h;
+}
+
+dtts_conv_desc desc(int64_t lanes, int64_t len, int64_t cin, int64_t cout, int64_t k, int64_t dil,
+                    const void *x, const void *w, const void *b, void *y) {
+    dtts_conv_desc d{};
+    d.lanes = lanes;
+    d.len = len;
+    d.cin = cin;
+    d.cout = cout;
+    d.k = k;
+    d.dilation = dil;
+    d.pad_left = (k - 1) * dil;
+    d.x = x;
+    d.w = w;
+    d.bias = b;
+    d.y = y;
+    return d;
+}
+
+}  // namespace
+}  // namespace dtts
+
+using dtts::set_error;
+
+extern "C" int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, dtts_codec **out) {
+    DTTS_REQUIRE(geo && w && out, "dtts_codec_create: null argument");
+    *out = nullptr;
+    const dtts_codec_geometry &g = *geo;
+    DTTS_REQUIRE(g.n_blocks >= 1 && g.n_blocks <= DTTS_CODEC_MAX_BLOCKS, "dtts_codec_create: n_blocks %lld",
+                 (long long)g.n_blocks);
+    DTTS_REQUIRE(g.latent_dim > 0 && g.head_kernel > 0 && g.ru_kernel > 0 && g.out_kernel > 0,
+                 "dtts_codec_create: bad kernel sizes");
+    for (int64_t i = 0; i <= g.n_blocks; ++i)
+        DTTS_REQUIRE(g.channels[i] > 0, "dtts_codec_create: channels[%lld] = %lld", (long long)i,
+                     (long long)g.channels[i]);
+    for (int64_t i = 0; i < g.n_blocks; ++i) DTTS_REQUIRE(g.rates[i] > 0, "dtts_codec_create: rates[%lld]", (long long)i);
+    for (int j = 0; j < 3; ++j) DTTS_REQUIRE(g.ru_dilations[j] > 0, "dtts_codec_create: ru_dilations[%d]", j);
+    DTTS_REQUIRE(w->head_w && w->out_w, "dtts_codec_create: missing head or output weights");
+    for (int64_t i = 0; i < g.n_blocks; ++i) {
+        const dtts_codec_block &b = w->blocks[i];
+        DTTS_REQUIRE(b.act_alpha && b.act_brecip && b.up_w, "dtts_codec_create: block %lld incomplete", (long long)i);
+        for (int j = 0; j < 3; ++j) {
+            const dtts_codec_unit &u = b.units[j];
+            DTTS_REQUIRE(u.act1_alpha && u.act1_brecip && u.conv1_w && u.act2_alpha && u.act2_brecip && u.conv2_w,
+                         "dtts_codec_create: block %lld unit %d incomplete", (long long)i, j);
+        }
+    }
+    DTTS_REQUIRE(w->out_alpha && w->out_brecip, "dtts_codec_create: missing output SnakeBeta");
+
+    dtts_codec *c = new (std::nothrow) dtts_codec();
+    DTTS_REQUIRE(c, "dtts_codec_create: out of host memory");
+    c->geo = g;
+    c->w = *w;
+    for (int64_t i = 0; i < g.n_blocks; ++i) {
+        const int64_t cout = g.channels[i + 1];
+        const int64_t rate = g.rates[i];
+        float *pa = nullptr, *pr = nullptr;
+        if (cout > dtts::kStoreSnakedAbove) {
+            const size_t bytes = sizeof(float) * static_cast<size_t>(rate * cout);
+            hipError_t e = hipMalloc(&pa, bytes);
+            if (e == hipSuccess) e = hipMalloc(&pr, bytes);
+            for (int64_t p = 0; p < rate && e == hipSuccess; ++p) {
+                e = hipMemcpy(pa + p * cout, w->blocks[i].units[0].act1_alpha, sizeof(float) * cout, hipMemcpyDeviceToDevice);
+                if (e == hipSuccess)
+                    e = hipMemcpy(pr + p * cout, w->blocks[i].units[0].act1_brecip, sizeof(float) * cout, hipMemcpyDeviceToDevice);
+            }
+            if (e != hipSuccess) {
+                if (pa) (void)hipFree(pa);
+                if (pr) (void)hipFree(pr);
+                dtts_codec_destroy(c);
+                set_error("dtts_codec_create: %s", hipGetErrorString(e));
+                return DTTS_ERR_HIP;
+            }
+        }
+        c->phase_alpha.push_back(pa);
+        c->phase_brecip.push_back(pr);
+    }
+    *out = c;
+    return DTTS_OK;
+}
+
+extern "C" void dtts_codec_destroy(dtts_codec *c) {
+    if (!c) return;
+    for (float *p : c->phase_alpha)
+        if (p) (void)hipFree(p);
+    for (float *p : c->phase_brecip)
+        if (p) (void)hipFree(p);
+    delete c;
+}
+
+extern "C" int64_t dtts_codec_hop(const dtts_codec *c) { return c ? dtts::hop_of(c->geo) : 0; }
+
+extern "C" size_t dtts_codec_workspace_bytes(const dtts_codec *c, int64_t lanes, int64_t frames) {
+    if (!c || lanes <= 0 || frames <= 0) return 0;
+    const size_t one = dtts::round_up(static_cast<size_t>(lanes * dtts::stage_elems(c->geo, frames)) * 2, 256);
+    return 4 * one;
+}
+
+namespace dtts {
+namespace {
+
+struct Stage {
+    dtts_conv_desc d;
+    char name[32];
+};
+
+// The decode as a list of conv launches over the workspace's four buffers.
+int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes, int64_t frames,
+               void *workspace, size_t ws_bytes, std::vector<Stage> &plan) {
+    DTTS_REQUIRE(c, "dtts_codec_decode: null codec");
+    DTTS_REQUIRE(lanes > 0 && frames > 0, "dtts_codec_decode: empty shape");
+    DTTS_REQUIRE(latent && audio && workspace, "dtts_codec_decode: null pointer");
+    const size_t need = dtts_codec_workspace_bytes(c, lanes, frames);
+    DTTS_REQUIRE(ws_bytes >= need, "dtts_codec_decode: workspace %zu bytes < %zu needed", ws_bytes, need);
+    DTTS_REQUIRE(aligned(workspace, 256), "dtts_codec_decode: workspace must be 256-byte aligned");
+
+    const dtts_codec_geometry &g = c->geo;
+    const dtts_codec_weights &w = c->w;
+    const size_t one = need / 4;
+    char *buf[4];
+    for (int i = 0; i < 4; ++i) buf[i] = static_cast<char *>(workspace) + i * one;
+    auto pick = [&](const void *a, const void *b, const void *d) -> char * {
+        for (char *p : buf)
+            if (p != a && p != b && p != d) return p;
+        return nullptr;
+    };
+    auto push = [&](const dtts_conv_desc &d, const char *fmt, long long a, long long b) {
+        Stage st;
+        st.d = d;
+        snprintf(st.name, sizeof(st.name), fmt, a, b);
+        plan.push_back(st);
+    };
+
+    // head conv, then block 0's SnakeBeta in the epilogue
+    char *x = buf[0];
+    {
+        dtts_conv_desc d = desc(lanes, frames, g.latent_dim, g.channels[0], g.head_kernel, 1, latent, w.head_w, w.head_b, x);
+        d.out_alpha = w.blocks[0].act_alpha;
+        d.out_brecip = w.blocks[0].act_brecip;
+        push(d, "head%.0lld%.0lld", 0, 0);
+    }
+    int64_t len = frames;
+    for (int64_t i = 0; i < g.n_blocks; ++i) {
+        const dtts_codec_block &blk = w.blocks[i];
+        const int64_t cin = g.channels[i], cout = g.channels[i + 1], rate = g.rates[i];
+        const bool wide = cout > kStoreSnakedAbove;
+        // TransConv: one causal conv of 2 taps over the snaked input, rate*cout phase columns
+        char *u = pick(x, nullptr, nullptr);
+        char *su = wide ? pick(x, u, nullptr) : nullptr;
+        {
+            dtts_conv_desc d = desc(lanes, len, cin, rate * cout, 2, 1, x, blk.up_w, blk.up_b, wide ? su : u);
+            if (wide) {
+                d.y_pre = u;
+                d.out_alpha = c->phase_alpha[i];
+                d.out_brecip = c->phase_brecip[i];
+            }
+            push(d, "block%lld.up%.0lld", (long long)i, 0);
+        }
+        len *= rate;
+        for (int j = 0; j < 3; ++j) {
+            const dtts_codec_unit &un = blk.units[j];
+            char *h = pick(u, su, nullptr);
+            {
+                dtts_conv_desc d = desc(lanes, len, cout, cout, g.ru_kernel, g.ru_dilations[j], wide ? su : u, un.conv1_w,
+                                        un.conv1_b, h);
+                if (!wide) {
+                    d.in_alpha = un.act1_alpha;
+                    d.in_brecip = un.act1_brecip;
+                }
+                d.out_alpha = un.act2_alpha;
+                d.out_brecip = un.act2_brecip;
+                push(d, "block%lld.unit%lld.conv1", (long long)i, j);
+            }
+            // conv2 (k=1) + residual, then the next activation
+            char *y = pick(u, h, su);
+            dtts_conv_desc d = desc(lanes, len, cout, cout, 1, 1, h, un.conv2_w, un.conv2_b, y);
+            d.residual = u;
+            if (j < 2) {
+                const dtts_codec_unit &nx = blk.units[j + 1];
+                if (wide) {
+                    // su is dead once conv1 has read it: the snaked copy of y goes there
+                    d.y_pre = y;
+                    d.y = su;
+                    d.out_alpha = nx.act1_alpha;
+                    d.out_brecip = nx.act1_brecip;
+                }
+                push(d, "block%lld.unit%lld.conv2", (long long)i, j);
+                u = y;
+            } else {
+                const bool last = i + 1 == g.n_blocks;
+                d.out_alpha = last ? w.out_alpha : w.blocks[i + 1].act_alpha;
+                d.out_brecip = last ? w.out_brecip : w.blocks[i + 1].act_brecip;
+                push(d, "block%lld.unit%lld.conv2", (long long)i, j);
+                x = y;  // snaked input of the next TransConv (or of the output conv)
+            }
+        }
+    }
+    dtts_conv_desc d = desc(lanes, len, g.channels[g.n_blocks], 1, g.out_kernel, 1, x, w.out_w, w.out_b, audio);
+    d.act = 1;
+    push(d, "out%.0lld%.0lld", 0, 0);
+    return DTTS_OK;
+}
+
+}  // namespace
+}  // namespace dtts
+
+extern "C" int dtts_codec_decode(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes,
+                                 int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    DTTS_REQUIRE(lanes >= 0 && frames >= 0, "dtts_codec_decode: negative shape");
+    if (lanes == 0 || frames == 0) return DTTS_OK;
+    std::vector<dtts::Stage> plan;
+    int rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
+    if (rc != DTTS_OK) return rc;
+    for (const dtts::Stage &st : plan)
+        if ((rc = dtts::conv1d_nlc_f16(&st.d, stream)) != DTTS_OK) return rc;
+    return DTTS_OK;
+}
+
+extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes,
+                                  int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream,
+                                  dtts_codec_stage *stages, int max_stages, int *n_stages) {
+    DTTS_REQUIRE(stages && n_stages && max_stages > 0, "dtts_codec_profile: no stage table");
+    std::vector<dtts::Stage> plan;
+    int rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
+    if (rc != DTTS_OK) return rc;
+    DTTS_REQUIRE(static_cast<int>(plan.size()) <= max_stages, "dtts_codec_profile: %zu stages > table of %d",
+                 plan.size(), max_stages);
+    std::vector<hipEvent_t> ev(plan.size() + 1);
+    for (auto &e : ev) DTTS_HIP_CHECK(hipEventCreate(&e), "dtts_codec_profile: hipEventCreate");
+    int status = DTTS_OK;
+    hipError_t he = hipEventRecord(ev[0], stream);
+    for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
+        status = dtts::conv1d_nlc_f16(&plan[i].d, stream);
+        if (status == DTTS_OK) he = hipEventRecord(ev[i + 1], stream);
+    }
+    if (he == hipSuccess && status == DTTS_OK) he = hipEventSynchronize(ev.back());
+    for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
+        const dtts_conv_desc &d = plan[i].d;
+        dtts_codec_stage &s = stages[i];
+        std::memset(&s, 0, sizeof(s));
+        snprintf(s.name, sizeof(s.name), "%s", plan[i].name);
+        snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::conv_kernel_name(&d));
+        s.lanes = d.lanes;
+        s.len = d.len;
+        s.cin = d.cin;
+        s.cout = d.cout;
+        s.k = d.k;
+        s.dilation = d.dilation;
+        s.flops = 2.0 * d.lanes * d.len * d.cin * d.cout * d.k;
+        const double outs = (d.y_pre ? 2.0 : 1.0) + (d.residual ? 1.0 : 0.0);
+        s.bytes = 2.0 * d.lanes * d.len * (d.cin + d.cout * outs) + 2.0 * d.cout * d.k * d.cin;
+        he = hipEventElapsedTime(&s.ms, ev[i], ev[i + 1]);
+    }
+    for (auto &e : ev) (void)hipEventDestroy(e);
+    if (status != DTTS_OK) return status;
+    DTTS_HIP_CHECK(he, "dtts_codec_profile");
+    *n_stages = static_cast<int>(plan.size());
+    return DTTS_OK;
+}

@@ -286,11 +286,56 @@ hipError_t launch_by_bn(const ConvParams &p, int64_t lanes, hipStream_t stream) 
 
 }  // namespace
 
-const char *conv_path_name(const dtts_conv_desc *d) {
+namespace {
+
+// Which kernel a descriptor runs on.
+struct Choice {
+    const char *path;  // "narrow", "mfma" or "direct"
+    int bn, kmax, hmax;
+    bool snake;
+};
+
+Choice choose(const dtts_conv_desc *d) {
+    Choice c{"direct", 0, 0, 0, d->in_alpha != nullptr};
+    if (conv_narrow_eligible(d)) {
+        c.path = "narrow";
+        return c;
+    }
     const int64_t halo = (d->k - 1) * d->dilation;
-    const bool tiled = d->cin % kKC == 0 && d->cout % 32 == 0 && d->k <= 7 &&
-                       ((d->k == 1) || (d->k <= 2 && halo <= 8) || halo <= 64);
-    return tiled ? "mfma" : "direct";
+    const bool aligned16 = aligned(d->x, 16) && aligned(d->w, 16) && aligned(d->y, 16) &&
+                           (!d->bias || aligned(d->bias, 16)) && (!d->residual || aligned(d->residual, 16)) &&
+                           (!d->y_pre || aligned(d->y_pre, 16));
+    if (!aligned16 || d->cin % kKC != 0 || d->cout % 32 != 0 || d->k > 7) return c;
+    if (d->k == 1) {
+        c.kmax = 1;
+        c.hmax = 0;
+    } else if (d->k <= 2 && halo <= 8) {
+        c.kmax = 2;
+        c.hmax = 8;
+    } else if (halo <= 64) {
+        c.kmax = 7;
+        c.hmax = 64;
+    } else {
+        return c;
+    }
+    c.path = "mfma";
+    c.bn = d->cout % 96 == 0 ? 96 : (d->cout % 64 == 0 ? 64 : 32);
+    return c;
+}
+
+}  // namespace
+
+const char *conv_path_name(const dtts_conv_desc *d) { return choose(d).path; }
+
+const char *conv_kernel_name(const dtts_conv_desc *d) {
+    static thread_local char buf[64];
+    const Choice c = choose(d);
+    if (std::strcmp(c.path, "mfma") == 0)
+        snprintf(buf, sizeof(buf), "conv_nlc_f16_mfma<256, %d, %d, %d, %s>", c.bn, c.kmax, c.hmax,
+                 c.snake ? "true" : "false");
+    else
+        snprintf(buf, sizeof(buf), "conv_nlc_f16_%s", c.path);
+    return buf;
 }
 
 int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
@@ -332,17 +377,16 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     p.pad_left = static_cast<int>(d->pad_left);
     p.act = d->act;
 
-    const bool aligned16 = aligned(d->x, 16) && aligned(d->w, 16) && aligned(d->y, 16) &&
-                           (!d->bias || aligned(d->bias, 16)) && (!d->residual || aligned(d->residual, 16)) &&
-                           (!d->y_pre || aligned(d->y_pre, 16));
-    const int64_t halo = (d->k - 1) * d->dilation;
+    const Choice ch = choose(d);
     hipError_t e;
-    if (aligned16 && std::strcmp(conv_path_name(d), "mfma") == 0) {
+    if (std::strcmp(ch.path, "narrow") == 0) {
+        e = conv_narrow_launch(d, stream);
+    } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
-        if (d->k == 1)
+        if (ch.kmax == 1)
             e = launch_by_bn<1, 0>(p, d->lanes, stream);
-        else if (d->k <= 2 && halo <= 8)
+        else if (ch.kmax == 2)
             e = launch_by_bn<2, 8>(p, d->lanes, stream);
         else
             e = launch_by_bn<7, 64>(p, d->lanes, stream);

@@ -9,6 +9,12 @@ namespace dtts {
 
 // "mfma" when the tiled matrix-core kernel takes the descriptor's shape, else "direct".
 const char *conv_path_name(const dtts_conv_desc *d);
+// The kernel the descriptor launches, in the form a profiler's demangled name contains.
+const char *conv_kernel_name(const dtts_conv_desc *d);
 int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream);
+
+// The single-output-channel kernel (conv_narrow.hip).
+bool conv_narrow_eligible(const dtts_conv_desc *d);
+hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream);
 
 }  // namespace dtts

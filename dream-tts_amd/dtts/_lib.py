@@ -40,8 +40,15 @@ SIGNATURES = {
     "dtts_tap_weight_to_tap_major": [_P, _P, _I64, _I64, _I64, _I64],
     "dtts_transpose_tap_major_weight": [_P, _P, _I64, _I64, _I64, _I64, _I64],
     "dtts_transpose_bias": [_P, _P, _I64, _I64, _I64],
+    "dtts_codec_create": [_P, _P, _P],
+    "dtts_codec_destroy": [_P],
+    "dtts_codec_hop": [_P],
+    "dtts_codec_workspace_bytes": [_P, _I64, _I64],
+    "dtts_codec_decode": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
+    "dtts_codec_profile": [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _I32, _P],
 }
-_RESTYPES = {"dtts_last_error": ctypes.c_char_p}
+_RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
+             "dtts_codec_hop": ctypes.c_int64, "dtts_codec_workspace_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

@@ -73,6 +73,8 @@ def from_f16_bits(h) -> np.ndarray:
     return np.asarray(h, np.uint16).view(np.float16).astype(np.float32)
 
 
-def kaiming_normal(seed: int, tag: str, shape, fan_in: int, dtype=np.float32):
-    """torch.nn.init.kaiming_normal_ (fan_in mode, gain sqrt(2)): std = sqrt(2 / fan_in)."""
-    return normal(seed, tag, shape, 0.0, float(np.sqrt(2.0 / fan_in)), dtype)
+def kaiming_normal(seed: int, tag: str, shape, fan_in: int, gain: float = float(np.sqrt(2.0)),
+                   dtype=np.float32):
+    """torch.nn.init.kaiming_normal_ (fan_in mode): std = gain / sqrt(fan_in); gain sqrt(2) is
+    nonlinearity='relu' (the default), 1 is nonlinearity='linear'."""
+    return normal(seed, tag, shape, 0.0, float(gain / np.sqrt(fan_in)), dtype)

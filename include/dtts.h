@@ -139,6 +139,94 @@ int dtts_transpose_tap_major_weight(const void *w_iok, void *w_tm, int64_t cin, 
 int dtts_transpose_bias(const void *b, void *out, int64_t cout, int64_t stride,
                         int64_t elem_size);
 
+/* ------------------------------------------------------------------ codec decoder stack */
+
+/* The qwen3tts codec's waveform stack on f16 channels-last activations, all lanes at once:
+ * Codec::forward's tail (crates/qwen3tts/src/codec.rs:426-436), i.e. head_conv, the
+ * DecoderBlocks (codec.rs:252-258: SnakeBeta, TransConv, ResidualUnits), then SnakeBeta,
+ * the output conv and tanh. The reference runs this batch-1 in f32 (codec.rs:33-43); every
+ * tensor here is f16 in HBM with f32 arithmetic inside each kernel, and each SnakeBeta runs in
+ * the epilogue of the conv that produces its input (or the prologue of its consumer).
+ *
+ * Geometry: a causal head conv latent_dim -> channels[0] (head_kernel); n_blocks blocks, block
+ * i upsampling by rates[i] (ConvTranspose1d kernel 2*rates[i]) from channels[i] to
+ * channels[i+1] and then 3 residual units (SnakeBeta, causal conv ru_kernel at
+ * ru_dilations[j], SnakeBeta, conv k=1, + input); a final SnakeBeta and a causal out conv
+ * channels[n_blocks] -> 1 (out_kernel), tanh. */
+#define DTTS_CODEC_MAX_BLOCKS 8
+
+typedef struct dtts_codec_geometry {
+    int64_t latent_dim, head_kernel, n_blocks;
+    int64_t channels[DTTS_CODEC_MAX_BLOCKS + 1];
+    int64_t rates[DTTS_CODEC_MAX_BLOCKS];
+    int64_t ru_kernel, ru_dilations[3], out_kernel;
+} dtts_codec_geometry;
+
+/* Device pointers. Conv weights are f16 in the layouts dtts_tap_major_weight /
+ * dtts_transpose_tap_major_weight produce (the transposed conv's bias repeated by
+ * dtts_transpose_bias); SnakeBeta parameters are f32 alpha = exp(alpha_log) and
+ * brecip = 1/(exp(beta_log) + 1e-9), as SnakeBeta::load folds them (codec.rs:60-68). */
+typedef struct dtts_codec_unit {
+    const float *act1_alpha, *act1_brecip;
+    const void *conv1_w, *conv1_b;
+    const float *act2_alpha, *act2_brecip;
+    const void *conv2_w, *conv2_b;
+} dtts_codec_unit;
+
+typedef struct dtts_codec_block {
+    const float *act_alpha, *act_brecip;
+    const void *up_w, *up_b;
+    dtts_codec_unit units[3];
+} dtts_codec_block;
+
+typedef struct dtts_codec_weights {
+    const void *head_w, *head_b;
+    dtts_codec_block blocks[DTTS_CODEC_MAX_BLOCKS];
+    const float *out_alpha, *out_brecip;
+    const void *out_w, *out_b;
+} dtts_codec_weights;
+
+typedef struct dtts_codec dtts_codec;
+
+/* Validates the geometry, keeps the weight pointers (the caller keeps the memory alive) and
+ * builds the small per-phase parameter tables the fused transposed convs need (device memory,
+ * freed by dtts_codec_destroy). Uses the current HIP device. */
+int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *weights,
+                      dtts_codec **out);
+void dtts_codec_destroy(dtts_codec *codec);
+
+/* Audio samples per latent frame (the product of the rates). */
+int64_t dtts_codec_hop(const dtts_codec *codec);
+
+/* Scratch bytes dtts_codec_decode needs for `lanes` x `frames` (four ping-pong activation
+ * buffers at the widest stage). */
+size_t dtts_codec_workspace_bytes(const dtts_codec *codec, int64_t lanes, int64_t frames);
+
+/* latent [lanes, frames, latent_dim] f16 -> audio [lanes, frames * hop] f16 in [-1, 1].
+ * Enqueues ~35 kernels on `stream`; workspace must hold dtts_codec_workspace_bytes bytes. */
+int dtts_codec_decode(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
+                      int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/* One launch of the decode, as dtts_codec_profile reports it. flops and bytes are algorithmic
+ * (2*MACs; each input, output and weight moved once); ms is the launch's own duration between
+ * HIP events recorded on the stream around it. */
+typedef struct dtts_codec_stage {
+    char name[32];    /* e.g. "block2.unit1.conv1" */
+    char kernel[64];  /* the HIP kernel that ran, as a profiler names it */
+    int64_t lanes, len, cin, cout, k, dilation;
+    double flops, bytes;
+    float ms;
+} dtts_codec_stage;
+
+/* dtts_codec_decode with a HIP event around every launch; synchronises the stream and fills
+ * stages[0 .. *n_stages). The per-stage timing Codec::profile does (crates/qwen3tts/src/
+ * codec.rs:465-542), at kernel granularity. */
+int dtts_codec_profile(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
+                       int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream, dtts_codec_stage *stages, int max_stages,
+                       int *n_stages);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,78 @@
+"""The codec decoder stack (dtts_codec_decode) against the oracle's f16-storage chain.
+
+The GPU stack stores exactly the tensors the oracle's composed chain stores (all f16), so the
+two differ only by f32 summation order inside each conv -- and SnakeBeta amplifies any input
+difference through the stack (the reference's reason for keeping its codec f32,
+crates/qwen3tts/src/codec.rs:33-43). Bar: the waveform within 2e-2 absolute everywhere (the f16
+tolerance at unit scale), and the GPU no further (RMS) from the oracle than f16 storage itself
+puts the oracle from exact float64 arithmetic on the same inputs (torch's conv1d /
+conv_transpose1d). Each conv is held exactly to its oracle stage in test_gpu_conv.py. The
+geometries cover both SnakeBeta placements (stored snaked copy for stages wider than 96
+channels, conv prologue at 96) and every kernel path.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec as ocodec
+from dtts import codec, synth
+
+from _codec_ref import torch_decode
+from _util import to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+SMALL = codec.Geometry(latent_dim=128, head_kernel=7, channels=(384, 192, 96), rates=(4, 3),
+                       ru_kernel=7, ru_dilations=(1, 3, 9), out_kernel=7)
+
+
+def _weights(geo, seed):
+    w = codec.random_weights(geo, seed=seed)
+    w.out_w = (w.out_w * 0.05).astype(np.float32)  # keep tanh off saturation so errors show
+    return w
+
+
+@pytest.mark.parametrize("geo,lanes,frames", [(SMALL, 3, 40), (codec.CONFIG5, 2, 3)],
+                         ids=["small", "config5-geometry"])
+def test_codec_decode_matches_oracle(dev, geo, lanes, frames):
+    w = _weights(geo, 7)
+    latent = synth.f16_bits(synth.normal(7, "latent", (lanes, frames, geo.latent_dim)))
+    model = codec.Codec(geo, w, dev)
+    got = synth.from_f16_bits(to_host(model.decode(to_dev(latent, dev))))
+    want = synth.from_f16_bits(ocodec.decode_f16(geo, ocodec.prepare(geo, w), latent))
+    assert got.shape == (lanes, frames * geo.hop)
+    assert np.isfinite(got).all()
+    exact = np.stack([torch_decode(geo, w, synth.from_f16_bits(latent[i])) for i in range(lanes)])
+    err = np.abs(got - want)
+    rms_gpu = float(np.sqrt(np.mean((got - want) ** 2)))
+    rms_f16 = float(np.sqrt(np.mean((want - exact) ** 2)))
+    msg = f"max {np.max(err):.3e} rms(gpu-oracle) {rms_gpu:.3e} rms(oracle-f64) {rms_f16:.3e}"
+    print(msg)
+    assert np.max(err) <= 2e-2, msg
+    assert rms_gpu <= 2.0 * rms_f16 + 1e-4, msg
+    assert 0.02 < np.std(want) < 0.95
+
+
+def test_codec_lanes_are_independent(dev):
+    """A lane's audio does not depend on its batch neighbours (no cross-lane taps)."""
+    geo = SMALL
+    w = _weights(geo, 8)
+    model = codec.Codec(geo, w, dev)
+    latent = synth.f16_bits(synth.normal(8, "latent", (4, 16, geo.latent_dim)))
+    full = to_host(model.decode(to_dev(latent, dev)))
+    one = to_host(model.decode(to_dev(latent[2:3].copy(), dev)))
+    assert np.array_equal(full[2:3], one)
+
+
+def test_codec_profile_covers_every_launch(dev):
+    geo = SMALL
+    model = codec.Codec(geo, _weights(geo, 9), dev)
+    latent = to_dev(synth.f16_bits(synth.normal(9, "latent", (2, 8, geo.latent_dim))), dev)
+    ref = to_host(model.decode(latent))
+    audio = torch.empty((2, 8 * geo.hop), dtype=torch.float16, device=dev)
+    stages = model.profile(latent, out=audio)
+    assert np.array_equal(to_host(audio), ref)
+    assert len(stages) == 1 + len(geo.rates) * 7 + 1
+    assert all(s["ms"] > 0 for s in stages)
+    assert stages[0]["name"] == "head" and stages[-1]["name"] == "out"
+    assert sum(s["flops"] for s in stages) == pytest.approx(2 * 8 * geo.flops_per_frame(), rel=1e-9)
