@@ -82,6 +82,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
     ap.add_argument("--stages-out", default=None, help="write the per-launch profile as JSON here")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -147,6 +149,15 @@ def main():
     if args.stages_out:
         with open(args.stages_out, "w") as f:
             json.dump(dict(ms_per_step=ms, stages=runs[-1]), f, indent=1)
+
+    if args.copy_probe:
+        src = torch.ones(1 << 29, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # an elementwise kernel (a same-dtype copy_ may go to DMA)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {src.numel() * 2} bytes read and written by a mul kernel")
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -40,6 +40,17 @@ SIGNATURES = {
     "dtts_tap_weight_to_tap_major": [_P, _P, _I64, _I64, _I64, _I64],
     "dtts_transpose_tap_major_weight": [_P, _P, _I64, _I64, _I64, _I64, _I64],
     "dtts_transpose_bias": [_P, _P, _I64, _I64, _I64],
+    "dtts_rms_norm_f32": [_P, _P, _P, _I64, _I64, _F32, _P],
+    "dtts_rms_norm_f16": [_P, _P, _P, _I64, _I64, _F32, _P],
+    "dtts_rope_table_f32": [_I64, _I64, _F64, _P, _P],
+    "dtts_rope_halfsplit_f32": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_rope_halfsplit_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_qk_norm_rope_kv_append_f32": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                        _I64, _I64, _F32, _P],
+    "dtts_qk_norm_rope_kv_append_f16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                        _I64, _I64, _F32, _P],
+    "dtts_kv_append_f32": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_kv_append_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_codec_create": [_P, _P, _P],
     "dtts_codec_destroy": [_P],
     "dtts_codec_hop": [_P],

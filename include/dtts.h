@@ -139,6 +139,64 @@ int dtts_transpose_tap_major_weight(const void *w_iok, void *w_tm, int64_t cin, 
 int dtts_transpose_bias(const void *b, void *out, int64_t cout, int64_t stride,
                         int64_t elem_size);
 
+/* ------------------------------------------------------------------ a8-a11 norm, RoPE, KV cache */
+
+/* RMSNorm over the last dim (rows x dim): y = (x / sqrt(mean(x^2) + eps)) * gamma, the sum of
+ * squares in f32. Replaces rms_norm -> candle_nn::ops::rms_norm (crates/tts-nn/src/lib.rs:
+ * 1000-1003). The f16 form keeps candle's f16 rounding points: m = sqrt(..) rounded to f16, then
+ * x/m and *gamma each rounded to f16. */
+int dtts_rms_norm_f32(const float *x, const float *gamma, float *y, int64_t rows, int64_t dim,
+                      float eps, hipStream_t stream);
+int dtts_rms_norm_f16(const dtts_f16 *x, const dtts_f16 *gamma, dtts_f16 *y, int64_t rows,
+                      int64_t dim, float eps, hipStream_t stream);
+
+/* rope_table_f32 / rope_pairs (crates/tts-nn/src/lib.rs:1178-1205), host: cos/sin [len, D/2],
+ * phase t / base^(2i/D) in f64, rounded to f32. */
+int dtts_rope_table_f32(int64_t len, int64_t head_dim, double base, float *cos_out,
+                        float *sin_out);
+
+/* Half-split RoPE (candle_nn::rotary_emb::rope as called at crates/qwen3tts/src/qwen3.rs:384-387;
+ * not the interleaved rope_i): x, y [rows, heads, D]; row r is at position pos[r] (a HOST array
+ * of `rows` int32, each in [0, table_len)); o_i = x_i c - x_{i+D/2} s, o_{i+D/2} = x_{i+D/2} c +
+ * x_i s with each product rounded (no FMA). The reference passes one start per batch; a position
+ * per lane is the batched-decode generalisation. rows <= 256. */
+int dtts_rope_halfsplit_f32(const float *x, const float *cos_t, const float *sin_t,
+                            const int32_t *pos, float *y, int64_t rows, int64_t heads,
+                            int64_t head_dim, int64_t table_len, hipStream_t stream);
+int dtts_rope_halfsplit_f16(const dtts_f16 *x, const float *cos_t, const float *sin_t,
+                            const int32_t *pos, dtts_f16 *y, int64_t rows, int64_t heads,
+                            int64_t head_dim, int64_t table_len, hipStream_t stream);
+
+/* QK-norm, RoPE and the KV-cache write of one decode position per lane, in one launch: replaces
+ * qkrope::apply / QkRope (crates/tts-nn/src/qkrope.rs:26-182, kernel qk_rope_f32 at mtl.rs:
+ * 773-838) for t = 1, with a position per lane. qkv [b, (heads + 2*n_kv) * D] (q heads, then k,
+ * then v); norms [2, D] f32 (q's weight, then k's); cos/sin [table_len, D/2]; pos a HOST int32[b]
+ * (each < min(cap, table_len), checked before anything is enqueued, as qkrope.rs:40-44 checks
+ * start + t <= capacity). Outputs: q_out [b, heads, D]; k_out [b, n_kv, D] f32 (optional, the
+ * roped k before its f16 cast: the reference's f32_kv side output); kcache, vcache
+ * [b, n_kv, cap, D] f16 written in place at [bi, h, pos[bi], :] (k roped, v as given, RNE) and
+ * nothing else. D even and <= 128, b <= 256. */
+int dtts_qk_norm_rope_kv_append_f32(const float *qkv, const float *norms, const float *cos_t,
+                                    const float *sin_t, const int32_t *pos, float *q_out,
+                                    float *k_out, dtts_f16 *kcache, dtts_f16 *vcache, int64_t b,
+                                    int64_t heads, int64_t n_kv, int64_t head_dim, int64_t cap,
+                                    int64_t table_len, float eps, hipStream_t stream);
+int dtts_qk_norm_rope_kv_append_f16(const dtts_f16 *qkv, const float *norms, const float *cos_t,
+                                    const float *sin_t, const int32_t *pos, dtts_f16 *q_out,
+                                    float *k_out, dtts_f16 *kcache, dtts_f16 *vcache, int64_t b,
+                                    int64_t heads, int64_t n_kv, int64_t head_dim, int64_t cap,
+                                    int64_t table_len, float eps, hipStream_t stream);
+
+/* The KV append alone: cache.k.slice_set(&k.to_dtype(F16), 2, start) and the same for v
+ * (crates/qwen3tts/src/qwen3.rs:389-392), one position per lane. k, v [b, n_kv, D]; caches
+ * [b, n_kv, cap, D] f16 written at pos[bi] (HOST int32[b], each < cap), RNE, bit-exact. */
+int dtts_kv_append_f32(const float *k, const float *v, const int32_t *pos, dtts_f16 *kcache,
+                       dtts_f16 *vcache, int64_t b, int64_t n_kv, int64_t head_dim, int64_t cap,
+                       hipStream_t stream);
+int dtts_kv_append_f16(const dtts_f16 *k, const dtts_f16 *v, const int32_t *pos,
+                       dtts_f16 *kcache, dtts_f16 *vcache, int64_t b, int64_t n_kv,
+                       int64_t head_dim, int64_t cap, hipStream_t stream);
+
 /* ------------------------------------------------------------------ codec decoder stack */
 
 /* The qwen3tts codec's waveform stack on f16 channels-last activations, all lanes at once:
