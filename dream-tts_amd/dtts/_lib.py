@@ -51,6 +51,13 @@ SIGNATURES = {
                                         _I64, _I64, _F32, _P],
     "dtts_kv_append_f32": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_kv_append_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_gemm_f16_skinny": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "dtts_gemm_f16_nt": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "dtts_gemm_f16_gateup_silu": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "dtts_swiglu_mul_f32": [_P, _P, _P, _I64, _P],
+    "dtts_q8_0_quantize": [_P, _P, _I64, _I64],
+    "dtts_q8_0_dequantize_f32": [_P, _P, _I64, _I64, _P],
+    "dtts_gemm_q8_0": [_P, _P, _P, _I64, _I64, _I64, _I32, _P],
     "dtts_codec_create": [_P, _P, _P],
     "dtts_codec_destroy": [_P],
     "dtts_codec_hop": [_P],

@@ -150,3 +150,92 @@ def kv_append(k, v, pos, k_cache, v_cache):
     p, pp = _pos_array(pos, b, "kv_append")
     fn = "dtts_kv_append_f32" if k.dtype == _F32 else "dtts_kv_append_f16"
     call(fn, ptr(k), ptr(v), pp, ptr(k_cache), ptr(v_cache), b, n_kv, hd, k_cache.shape[2], stream_handle())
+
+
+# ---------------------------------------------------------------- a12-a15 projections
+
+def _mat(t, name, what, dtype):
+    _check(t, name, (dtype,), what)
+    if t.dim() != 2:
+        raise DttsError(f"{name}: {what} must be 2-D, got {tuple(t.shape)}")
+
+
+def skinny_matmul(a, b):
+    """skinny::matmul (crates/tts-nn/src/skinny.rs:155-165): [m, k] f16 x [k, n] f16 -> [m, n] f32."""
+    _mat(a, "skinny_matmul", "a", _F16)
+    _mat(b, "skinny_matmul", "b", _F16)
+    m, k = a.shape
+    if b.shape[0] != k:
+        raise DttsError(f"gemm_skinny: {k} != {b.shape[0]}")
+    c = torch.empty((m, b.shape[1]), dtype=_F32, device=a.device)
+    call("dtts_gemm_f16_skinny", ptr(a), ptr(b), ptr(c), m, k, b.shape[1], stream_handle())
+    return c
+
+
+def matmul_nt(a, w):
+    """[m, k] f16 x [n, k]^T f16 -> [m, n] f32 (Proj::Half on the checkpoint's [out, in] weight)."""
+    _mat(a, "matmul_nt", "a", _F16)
+    _mat(w, "matmul_nt", "w", _F16)
+    m, k = a.shape
+    if w.shape[1] != k:
+        raise DttsError(f"matmul_nt: {k} != {w.shape[1]}")
+    c = torch.empty((m, w.shape[0]), dtype=_F32, device=a.device)
+    call("dtts_gemm_f16_nt", ptr(a), ptr(w), ptr(c), m, k, w.shape[0], stream_handle())
+    return c
+
+
+def gateup_silu(a, w_gu):
+    """silu(a . Wg^T) * (a . Wu^T), w_gu [2*ffn, k] = gate rows then up rows; f32 [m, ffn]."""
+    _mat(a, "gateup_silu", "a", _F16)
+    _mat(w_gu, "gateup_silu", "w_gu", _F16)
+    m, k = a.shape
+    ffn = w_gu.shape[0] // 2
+    if w_gu.shape[1] != k or w_gu.shape[0] != 2 * ffn:
+        raise DttsError("gateup_silu: w_gu must be [2*ffn, k]")
+    y = torch.empty((m, ffn), dtype=_F32, device=a.device)
+    call("dtts_gemm_f16_gateup_silu", ptr(a), ptr(w_gu), ptr(y), m, k, ffn, stream_handle())
+    return y
+
+
+def swiglu_mul(gate, up):
+    """fused::swiglu_mul (crates/tts-nn/src/fused.rs:376-385), f32."""
+    _check(gate, "swiglu_mul", (_F32,), "gate")
+    _check(up, "swiglu_mul", (_F32,), "up")
+    if gate.shape != up.shape:
+        raise DttsError("swiglu_mul: shapes differ")
+    y = torch.empty_like(gate)
+    call("dtts_swiglu_mul_f32", ptr(gate), ptr(up), ptr(y), gate.numel(), stream_handle())
+    return y
+
+
+def q8_0_quantize(w):
+    """Host: f32 numpy [rows, k] -> uint8 [rows, k/32, 34] GGML Q8_0 blocks."""
+    import ctypes
+
+    import numpy as np
+
+    w = np.ascontiguousarray(w, np.float32)
+    rows, k = w.shape
+    out = np.empty((rows, k // 32, 34), np.uint8)
+    call("dtts_q8_0_quantize", ctypes.c_void_p(w.ctypes.data), ctypes.c_void_p(out.ctypes.data), rows, k)
+    return out
+
+
+def q8_0_dequantize(blocks, k):
+    """Device uint8 blocks [rows, k/32, 34] -> f32 [rows, k]."""
+    rows = blocks.shape[0]
+    w = torch.empty((rows, k), dtype=_F32, device=blocks.device)
+    call("dtts_q8_0_dequantize_f32", ptr(blocks), ptr(w), rows, k, stream_handle())
+    return w
+
+
+def q8_0_matmul(x, blocks, mode="w8a16"):
+    """QMatMul::forward on a Q8_0 weight [n, k]: x [m, k] f16 -> y [m, n] f32."""
+    _mat(x, "q8_0_matmul", "x", _F16)
+    m, k = x.shape
+    n = blocks.shape[0]
+    if blocks.dtype != torch.uint8 or not blocks.is_cuda or blocks.numel() != n * (k // 32) * 34:
+        raise DttsError("q8_0_matmul: blocks must be device uint8 [n, k/32, 34]")
+    y = torch.empty((m, n), dtype=_F32, device=x.device)
+    call("dtts_gemm_q8_0", ptr(x), ptr(blocks), ptr(y), m, k, n, {"w8a16": 0, "w8a8": 1}[mode], stream_handle())
+    return y

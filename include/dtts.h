@@ -197,6 +197,55 @@ int dtts_kv_append_f16(const dtts_f16 *k, const dtts_f16 *v, const int32_t *pos,
                        dtts_f16 *kcache, dtts_f16 *vcache, int64_t b, int64_t n_kv,
                        int64_t head_dim, int64_t cap, hipStream_t stream);
 
+/* ------------------------------------------------------------------ a12-a14 f16 projections */
+
+/* Decode-shape f16 GEMM, f32 accumulation and output: C[m, n] = A[m, k] . B. Replaces
+ * skinny::matmul / gemm_skinny_f16 + sum_splits_f32 (crates/tts-nn/src/skinny.rs:155-165,
+ * mtl.rs:1078-1150), which takes m <= 48, m % 8 == 0, k % 32 == 0, n % 64 == 0; the matrix-core
+ * kernel here takes m <= 64 (any), k % 64 == 0, n % 16 == 0, 16-byte aligned operands, and any
+ * other shape runs a direct kernel. Split-k partials are summed in a fixed order (deterministic).
+ *   dtts_gemm_f16_skinny: B = b_kn [k, n], the reference's own operand (Proj::Half's W_t,
+ *     crates/tts-nn/src/lib.rs:516-529);
+ *   dtts_gemm_f16_nt: B = w_nk^T with w_nk [n, k], the checkpoint's [out, in] layout, so no
+ *     load-time transpose is needed; the faster of the two. */
+int dtts_gemm_f16_skinny(const dtts_f16 *a, const dtts_f16 *b_kn, float *c, int64_t m, int64_t k,
+                         int64_t n, hipStream_t stream);
+int dtts_gemm_f16_nt(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k,
+                     int64_t n, hipStream_t stream);
+
+/* gate|up projection with SwiGLU fused: y[m, j] = silu(g) * u, g = A . Wg^T, u = A . Wu^T, where
+ * w_gu [2*ffn, k] holds gate's rows then up's (f16, [out, in]). Replaces
+ * swiglu_mul(gate.forward(x), up.forward(x)) at crates/qwen3tts/src/qwen3.rs:454-457. y f32. */
+int dtts_gemm_f16_gateup_silu(const dtts_f16 *a, const dtts_f16 *w_gu, float *y, int64_t m,
+                              int64_t k, int64_t ffn, hipStream_t stream);
+
+/* fused::swiglu_mul / SwigluMul (crates/tts-nn/src/fused.rs:289-385): y = (g / (1 + exp(-g))) * u,
+ * f32, n elements. */
+int dtts_swiglu_mul_f32(const float *g, const float *u, float *y, int64_t n, hipStream_t stream);
+
+/* ------------------------------------------------------------------ a15 Q8_0 */
+
+/* GGML block_q8_0 as candle stores a quantized [out, in] weight (QTensor::quantize_onto,
+ * crates/tts-nn/src/lib.rs:480-486): row n is k/32 consecutive 34-byte blocks {f16 d;
+ * int8 qs[32]}; w[n, c] = qs[n][c/32][c%32] * d[n][c/32]. */
+#define DTTS_Q8_W8A16 0 /* f16 activations times the exact int8 weights, scaled per block */
+#define DTTS_Q8_W8A8 1  /* activations quantized to Q8_0 per 32-block first (candle CPU's vec_dot) */
+
+/* Host: quantize f32 [rows, k] (k % 32 == 0) into blocks: d = amax/127, qs = round-half-away(x/d)
+ * with the f32 reciprocal, d stored as f16 (BlockQ8_0::from_float). blocks holds rows*k/32*34
+ * bytes. */
+int dtts_q8_0_quantize(const float *w, void *blocks, int64_t rows, int64_t k);
+
+/* Device: blocks -> f32 [rows, k] (the dequant index math, bit-exact). */
+int dtts_q8_0_dequantize_f32(const void *blocks, float *w, int64_t rows, int64_t k,
+                             hipStream_t stream);
+
+/* y[m, n] = x[m, k] . dequant(W)^T for the Q8_0 weight W [n, k]: replaces Proj::Quant's
+ * QMatMul::forward (crates/tts-nn/src/lib.rs:531). x f16 (16-byte aligned), y f32, m <= 64,
+ * n % 16 == 0, k % 32 == 0. mode: DTTS_Q8_W8A16 or DTTS_Q8_W8A8. */
+int dtts_gemm_q8_0(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k,
+                   int64_t n, int32_t mode, hipStream_t stream);
+
 /* ------------------------------------------------------------------ codec decoder stack */
 
 /* The qwen3tts codec's waveform stack on f16 channels-last activations, all lanes at once:

@@ -1,0 +1,87 @@
+"""Decode-shape f16 GEMMs, SwiGLU and Q8_0 projections (a12-a15) through the C ABI.
+
+Bars: f16 GEMM max-abs <= 2e-2 at unit-scale activations and max-rel (abs_and_rel) <= 1e-4
+against the oracle's f32-accumulated GEMM of the same f16 operands (the reference's own check,
+crates/tts-nn/src/skinny.rs:175-202, allows 2e-3 against candle); SwiGLU within 2e-6 of f64
+scaled by max(|g u|, 1) (fused.rs:2310-2322); Q8_0 dequant bit-exact; W8A8 max-rel <= 1e-5
+against the oracle's vec_dot restatement (same integer dots and scale products, different f32
+summation order); W8A16 max-abs <= 2e-2 and max-rel <= 1e-3 against f64 on the dequantized
+weights. Shapes: the reference test's, and configs 3 and 4.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dtts import ops, synth
+
+from _util import rel, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+SKINNY = [(48, 2048, 4096), (48, 2048, 6144), (48, 6144, 2048), (48, 1024, 3072), (40, 3072, 1024),
+          (32, 1024, 2048), (8, 1024, 4096),                        # skinny.rs:175-202
+          (48, 1024, 4096), (48, 3072, 1024),                       # config 3
+          (1, 1024, 1024), (64, 128, 48), (5, 100, 24), (3, 64, 16)]  # edges + the direct kernel
+
+
+def _ab(seed, m, k, n):
+    a = synth.f16_bits(synth.normal(seed, "a", (m, k)))
+    w = synth.f16_bits(synth.normal(seed, "w", (n, k), 0, 0.02))  # [out, in]
+    return a, w
+
+
+@pytest.mark.parametrize("m,k,n", SKINNY)
+def test_gemm_nt_and_kn_match_oracle(dev, m, k, n):
+    a, w = _ab(80, m, k, n)
+    b_kn = np.ascontiguousarray(w.T)
+    want = oracle.gemm_f16_f32acc(a, b_kn)
+    for got in (to_host(ops.matmul_nt(to_dev(a, dev), to_dev(w, dev))),
+                to_host(ops.skinny_matmul(to_dev(a, dev), to_dev(b_kn, dev)))):
+        ab, rl = rel(got, want)
+        assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
+
+
+@pytest.mark.parametrize("m,k,ffn", [(48, 1024, 3072), (8, 1024, 3072), (48, 2048, 6144), (3, 64, 16)])
+def test_gateup_silu_matches_oracle(dev, m, k, ffn):
+    a, w = _ab(81, m, k, 2 * ffn)
+    got = to_host(ops.gateup_silu(to_dev(a, dev), to_dev(w, dev)))
+    gu = oracle.gemm_f16_f32acc(a, np.ascontiguousarray(w.T))
+    want = oracle.swiglu_mul_f32(gu[:, :ffn].copy(), gu[:, ffn:].copy())
+    ab, rl = rel(got, want)
+    assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
+
+
+def test_swiglu_sweep_accuracy(dev):
+    n = 8 * 4096
+    gs = (-30.0 + 60.0 * (np.arange(n) % 4096) / 4095).astype(np.float32)
+    us = (-4.0 + 8.0 * (np.arange(n) % 4096) / 4095).astype(np.float32)
+    got = to_host(ops.swiglu_mul(to_dev(gs, dev), to_dev(us, dev)))
+    g64, u64 = gs.astype(np.float64), us.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(g64 * u64), 1.0)) < 2e-6
+
+
+Q8_SHAPES = [(m, k, n) for (k, n) in ((1024, 6144), (3072, 1024)) for m in (1, 8, 48)]
+
+
+@pytest.mark.parametrize("k,n", [(1024, 6144), (3072, 1024)])
+def test_q8_0_dequant_bit_exact(dev, k, n):
+    w = synth.normal(82, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    got = to_host(ops.q8_0_dequantize(torch.from_numpy(blocks).to(dev), k))
+    assert np.array_equal(got, oracle.q8_0_dequantize(blocks, k))
+
+
+@pytest.mark.parametrize("m,k,n", Q8_SHAPES)
+def test_q8_0_matmul(dev, m, k, n):
+    w = synth.normal(83, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    xb = synth.f16_bits(synth.normal(83, "x", (m, k)))
+    x = synth.from_f16_bits(xb)
+    xd, bd = to_dev(xb, dev), torch.from_numpy(blocks).to(dev)
+    got8 = to_host(ops.q8_0_matmul(xd, bd, "w8a8"))
+    assert rel(got8, oracle.q8_0_matmul_w8a8(x, blocks))[1] <= 1e-5
+    got16 = to_host(ops.q8_0_matmul(xd, bd, "w8a16"))
+    ab, rl = rel(got16, oracle.q8_0_matmul_f64(x, blocks))
+    assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)

@@ -1,0 +1,78 @@
+"""Pins the oracle's f16 GEMM, SwiGLU and Q8_0 restatements (float64, closed forms, exact cases),
+and checks the library's host Q8_0 quantizer against the oracle bit for bit."""
+import numpy as np
+import pytest
+
+import oracle
+from dtts import ops, synth
+
+
+def test_gemm_f16_oracle_matches_f64():
+    a = synth.f16_bits(synth.normal(70, "a", (48, 1024)))
+    b = synth.f16_bits(synth.normal(70, "b", (1024, 256), 0, 0.02))
+    got = oracle.gemm_f16_f32acc(a, b)
+    want = synth.from_f16_bits(a).astype(np.float64) @ synth.from_f16_bits(b).astype(np.float64)
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+    assert np.max(np.abs(oracle.gemm_f16_f64(a, b) - want)) < 1e-10
+
+
+def test_swiglu_oracle_matches_f64_sweep():
+    # crates/tts-nn/src/fused.rs:2310-2322: g over +-30, u over +-4, error / max(|g u|, 1) < 2e-6
+    n = 8 * 4096
+    gs = (-30.0 + 60.0 * (np.arange(n) % 4096) / 4095).astype(np.float32)
+    us = (-4.0 + 8.0 * (np.arange(n) % 4096) / 4095).astype(np.float32)
+    got = oracle.swiglu_mul_f32(gs, us)
+    g64, u64 = gs.astype(np.float64), us.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(g64 * u64), 1.0)) < 2e-6
+
+
+def _edge_weights():
+    w = synth.normal(71, "w", (6, 128), 0, 0.02)
+    w[1, :32] = 0.0                       # an all-zero block: d = 0, id = 0
+    w[2, :32] = np.linspace(-1, 1, 32)    # amax exactly at both ends
+    w[3, 32:64] = 0.5                     # constant block: every q = 127
+    w[4, :32] = np.arange(32) - 15.5      # halves land on x.5 boundaries
+    return w.astype(np.float32)
+
+
+def test_q8_0_oracle_closed_form_and_library_quantizer_agree():
+    w = _edge_weights()
+    blocks = oracle.q8_0_quantize(w)
+    assert blocks.shape == (6, 4, 34)
+    d = synth.from_f16_bits(blocks[..., :2].copy().view(np.uint16)[..., 0])
+    q = blocks[..., 2:].view(np.int8).astype(np.int32)
+    amax = np.abs(w.reshape(6, 4, 32)).max(-1)
+    assert np.array_equal(synth.f16_bits(amax / 127.0), blocks[..., :2].copy().view(np.uint16)[..., 0])
+    assert np.all(np.abs(q) <= 127)
+    assert np.all(q[1, 0] == 0) and d[1, 0] == 0.0
+    assert np.all(q[3, 1] == 127)
+    deq = oracle.q8_0_dequantize(blocks, 128)
+    assert np.array_equal(deq, (q * d[..., None]).reshape(6, 128).astype(np.float32))
+    assert np.all(np.abs(deq - w) <= np.repeat(d, 32, -1) * 0.5 + 1e-3 * np.abs(w) + 1e-9)
+    # the library's host quantizer writes the same bytes
+    assert np.array_equal(ops.q8_0_quantize(w), blocks)
+
+
+def test_q8_0_w8a8_is_exact_on_prequantized_activations():
+    # activations that are already Q8_0 values quantize to themselves, so the w8a8 result is the
+    # exact block dot up to the f32 scale products
+    k, n, m = 256, 32, 3
+    w = synth.normal(72, "w", (n, k), 0, 0.02)
+    blocks = oracle.q8_0_quantize(w)
+    qx = synth.randint(72, "qx", (m, k), -127, 127).astype(np.float32)
+    qx[:, ::32] = 127.0  # each block's amax is 127 * dx
+    dx = np.float32(0.03125)  # a power of two: d = amax/127 = dx exactly, 1/d exact
+    x = qx * dx
+    got = oracle.q8_0_matmul_w8a8(x, blocks)
+    want = oracle.q8_0_matmul_f64(x, blocks)
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-6
+
+
+def test_q8_0_w8a8_close_to_unquantized_activations():
+    w = synth.normal(73, "w", (64, 1024), 0, 0.02)
+    blocks = oracle.q8_0_quantize(w)
+    x = synth.from_f16_bits(synth.f16_bits(synth.normal(73, "x", (8, 1024))))
+    got = oracle.q8_0_matmul_w8a8(x, blocks)
+    want = oracle.q8_0_matmul_f64(x, blocks)
+    assert oracle.abs_and_rel(got, want)[1] < 2e-2  # activation quantization noise, ~1/254 per term
