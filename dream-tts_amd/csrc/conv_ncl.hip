@@ -1,0 +1,226 @@
+// Channel-major f32 conv1d (the reference's NCL route, crates/tts-nn/src/lib.rs:704-860) as an
+// implicit GEMM on the f32 matrix cores, and the tap-major im2col gather it replaces.
+//
+//   y[b, n, l] = act(bias[n] + res[b, n, l] + sum_t sum_c w[n, t*cin + c] * xs[b, c, l + t*dil - pad_left])
+//
+// xs is x or SnakeBeta(x) (full-precision sinf; f32 outputs are held to 1e-5). GEMM view per
+// lane: M = output channels, N = positions, K = (tap, channel). A workgroup owns 64 channels x
+// 128 positions; per 16-channel chunk it stages the dilated window of x (16 rows x
+// 128 + (k-1)*dil positions) and the 64 x k x 16 weight slice in LDS, then four waves (2 x 2)
+// run v_mfma_f32_32x32x2_f32, each tap reading the window at offset t*dil. The epilogue writes
+// straight from the accumulators: the 32 lanes of a C column are 32 consecutive positions.
+#include "conv.hpp"
+#include "snake.hpp"
+
+namespace dtts {
+namespace {
+
+struct NclParams {
+    const float *x, *w, *bias, *a_in, *r_in, *res;
+    float *y_pre, *y;
+    const float *a_out, *r_out;
+    int L, cin, cout, k, dil, pad_left, act;
+    int tiles_m, tiles_n, total, per_xcd;
+};
+
+constexpr int kBM = 64, kBN = 128, kKC = 16;
+
+template <int KMAX, int HMAX, bool SNAKE>
+__global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
+    constexpr int XW = kBN + HMAX;           // window positions per channel row
+    constexpr int WP = KMAX * kKC + 1;       // weight row pitch (floats); +1 spreads the banks
+    __shared__ float xs[kKC * XW];
+    __shared__ float ws[kBM * WP];
+    const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+    if (tile >= p.total) return;
+    const int m_tile = tile % p.tiles_m;  // output channels fastest: neighbours share the window
+    const int rest = tile / p.tiles_m;
+    const int n_tile = rest % p.tiles_n;
+    const int lane_idx = rest / p.tiles_n;
+    const int co0 = m_tile * kBM;
+    const int l0 = n_tile * kBN;
+    const int rows = kBN + (p.k - 1) * p.dil;
+    const int K = p.k * p.cin;
+    const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.cin * p.L;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int kh = lane >> 5, lr = lane & 31;
+
+    float16_t acc[2] = {float16_t{}, float16_t{}};
+    for (int c0 = 0; c0 < p.cin; c0 += kKC) {
+        for (int e = tid; e < kKC * rows; e += 256) {
+            const int ci = e / rows;
+            const int j = e - ci * rows;
+            const int s = l0 - p.pad_left + j;
+            float v = 0.0f;
+            if (s >= 0 && s < p.L) {
+                v = xl[static_cast<int64_t>(c0 + ci) * p.L + s];
+                if constexpr (SNAKE) v = snake_f32(v, p.a_in[c0 + ci], p.r_in[c0 + ci]);
+            }
+            xs[ci * XW + j] = v;
+        }
+        for (int e = tid; e < kBM * p.k * kKC; e += 256) {
+            const int m = e / (p.k * kKC);
+            const int q = e - m * (p.k * kKC);
+            const int t = q / kKC;
+            const int ci = q - t * kKC;
+            ws[m * WP + t * kKC + ci] = p.w[static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 + ci];
+        }
+        __syncthreads();
+        for (int t = 0; t < p.k; ++t) {
+            const float *wa = ws + (wm * 32 + lr) * WP + t * kKC + kh;
+            const float *xb = xs + kh * XW + wn * 64 + lr + t * p.dil;
+#pragma unroll
+            for (int ci = 0; ci < kKC; ci += 2) {
+                const float a = wa[ci];
+                const float b0 = xb[ci * XW];
+                const float b1 = xb[ci * XW + 32];
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b0, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b1, acc[1], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    const int64_t ybase = static_cast<int64_t>(lane_idx) * p.cout * p.L;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int pos = l0 + wn * 64 + j * 32 + lr;
+        if (pos >= p.L) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+            const int64_t off = ybase + static_cast<int64_t>(co) * p.L + pos;
+            float v = acc[j][r];
+            if (p.bias) v += p.bias[co];
+            if (p.res) v += p.res[off];
+            if (p.act == 1) v = tanhf(v);
+            if (p.y_pre) p.y_pre[off] = v;
+            if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
+            p.y[off] = v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void conv_ncl_f32_direct(NclParams p, int64_t total) {
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int l = static_cast<int>(e % p.L);
+        const int64_t bc = e / p.L;
+        const int co = static_cast<int>(bc % p.cout);
+        const int64_t b = bc / p.cout;
+        const float *xl = p.x + b * p.cin * p.L;
+        const float *wr = p.w + static_cast<int64_t>(co) * p.k * p.cin;
+        float acc = 0.0f;
+        for (int t = 0; t < p.k; ++t) {
+            const int s = l + t * p.dil - p.pad_left;
+            if (s < 0 || s >= p.L) continue;
+            for (int c = 0; c < p.cin; ++c) {
+                float v = xl[static_cast<int64_t>(c) * p.L + s];
+                if (p.a_in) v = snake_f32(v, p.a_in[c], p.r_in[c]);
+                acc += wr[t * p.cin + c] * v;
+            }
+        }
+        float v = acc;
+        if (p.bias) v += p.bias[co];
+        if (p.res) v += p.res[e];
+        if (p.act == 1) v = tanhf(v);
+        if (p.y_pre) p.y_pre[e] = v;
+        if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
+        p.y[e] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void im2col_kernel(const float *x, float *cols, int cin, int L, int k, int dil,
+                                                     int pad_left) {
+    const int64_t total = static_cast<int64_t>(k) * cin * L;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int l = static_cast<int>(e % L);
+        const int64_t row = e / L;  // t * cin + c
+        const int t = static_cast<int>(row / cin);
+        const int c = static_cast<int>(row - int64_t(t) * cin);
+        const int s = l + t * dil - pad_left;
+        cols[e] = (s >= 0 && s < L) ? x[static_cast<int64_t>(c) * L + s] : 0.0f;
+    }
+}
+
+template <int KMAX, int HMAX>
+hipError_t launch_ncl(NclParams p, int64_t lanes, bool snake, hipStream_t stream) {
+    p.tiles_m = p.cout / kBM;
+    p.tiles_n = (p.L + kBN - 1) / kBN;
+    const int64_t total = lanes * p.tiles_m * p.tiles_n;
+    p.total = static_cast<int>(total);
+    p.per_xcd = static_cast<int>((total + 7) / 8);
+    const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
+    if (snake)
+        conv_ncl_f32_mfma<KMAX, HMAX, true><<<grid, 256, 0, stream>>>(p);
+    else
+        conv_ncl_f32_mfma<KMAX, HMAX, false><<<grid, 256, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace dtts
+
+extern "C" int dtts_conv1d_ncl_f32_ex(const dtts_conv_desc *d, hipStream_t stream) {
+    const char *name = "dtts_conv1d_ncl_f32";
+    DTTS_REQUIRE(d, "%s: null descriptor", name);
+    DTTS_REQUIRE(d->lanes >= 0 && d->len >= 0 && d->cin > 0 && d->cout > 0 && d->k > 0 && d->dilation > 0 &&
+                     d->pad_left >= 0 && d->pad_left <= (d->k - 1) * d->dilation,
+                 "%s: bad shape or pad_left", name);
+    DTTS_REQUIRE(d->act == 0 || d->act == 1, "%s: act %d unknown", name, d->act);
+    if (d->lanes == 0 || d->len == 0) return DTTS_OK;
+    DTTS_REQUIRE(d->x && d->w && d->y, "%s: null x, w or y", name);
+    DTTS_REQUIRE((d->in_alpha == nullptr) == (d->in_brecip == nullptr) &&
+                     (d->out_alpha == nullptr) == (d->out_brecip == nullptr),
+                 "%s: snake alpha and brecip go together", name);
+    DTTS_REQUIRE(d->lanes * d->cout * d->len < (int64_t(1) << 40) && d->len < (int64_t(1) << 30) &&
+                     d->cin * d->k < (int64_t(1) << 30),
+                 "%s: shape too large", name);
+    dtts::NclParams p{};
+    p.x = static_cast<const float *>(d->x);
+    p.w = static_cast<const float *>(d->w);
+    p.bias = static_cast<const float *>(d->bias);
+    p.a_in = d->in_alpha;
+    p.r_in = d->in_brecip;
+    p.res = static_cast<const float *>(d->residual);
+    p.y_pre = static_cast<float *>(d->y_pre);
+    p.y = static_cast<float *>(d->y);
+    p.a_out = d->out_alpha;
+    p.r_out = d->out_brecip;
+    p.L = static_cast<int>(d->len);
+    p.cin = static_cast<int>(d->cin);
+    p.cout = static_cast<int>(d->cout);
+    p.k = static_cast<int>(d->k);
+    p.dil = static_cast<int>(d->dilation);
+    p.pad_left = static_cast<int>(d->pad_left);
+    p.act = d->act;
+    const int64_t halo = (d->k - 1) * d->dilation;
+    hipError_t e;
+    if (d->cin % dtts::kKC == 0 && d->cout % dtts::kBM == 0 && d->k <= 7 && halo <= 64) {
+        DTTS_REQUIRE(d->lanes * (d->cout / dtts::kBM) * ((d->len + dtts::kBN - 1) / dtts::kBN) < (int64_t(1) << 31),
+                     "%s: too many tiles", name);
+        if (d->k == 1)
+            e = dtts::launch_ncl<1, 0>(p, d->lanes, d->in_alpha != nullptr, stream);
+        else
+            e = dtts::launch_ncl<7, 64>(p, d->lanes, d->in_alpha != nullptr, stream);
+    } else {
+        const int64_t total = d->lanes * d->cout * d->len;
+        dtts::conv_ncl_f32_direct<<<dtts::grid_for(total, 256, 16), 256, 0, stream>>>(p, total);
+        e = hipGetLastError();
+    }
+    DTTS_HIP_CHECK(e, name);
+    return DTTS_OK;
+}
+
+extern "C" int dtts_im2col_tap_major_f32(const float *x, float *cols, int64_t cin, int64_t len, int64_t k,
+                                         int64_t dilation, int64_t pad_left, hipStream_t stream) {
+    DTTS_REQUIRE(cin > 0 && len >= 0 && k > 0 && dilation > 0 && pad_left >= 0, "dtts_im2col_tap_major_f32: bad shape");
+    if (len == 0) return DTTS_OK;
+    DTTS_REQUIRE(x && cols, "dtts_im2col_tap_major_f32: null pointer");
+    DTTS_REQUIRE(k * cin * len < (int64_t(1) << 40) && len < (int64_t(1) << 30) && k * cin < (int64_t(1) << 30),
+                 "dtts_im2col_tap_major_f32: shape too large");
+    dtts::im2col_kernel<<<dtts::grid_for(k * cin * len, 256), 256, 0, stream>>>(
+        x, cols, static_cast<int>(cin), static_cast<int>(len), static_cast<int>(k), static_cast<int>(dilation),
+        static_cast<int>(pad_left));
+    DTTS_LAUNCH_CHECK("dtts_im2col_tap_major_f32");
+    return DTTS_OK;
+}

@@ -72,6 +72,42 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
     return (y_pre, y) if want_pre else y
 
 
+def conv1d_ncl_f32(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, residual=None,
+                   snake_out=None, want_pre=False, out=None):
+    """The channel-major f32 conv (dtts_conv1d_ncl_f32_ex): x [lanes, cin, L] f32, w_tm
+    [cout, k*cin] f32 -> [lanes, cout, L]. centered_conv1d_gemm / causal_conv1d_gemm
+    (crates/tts-nn/src/lib.rs:704-767) with the neighbouring SnakeBeta and residual fused."""
+    name = "conv1d_ncl_f32"
+    lanes, cin, length = x.shape
+    cout = w_tm.shape[0]
+    _need(x, name, "x", torch.float32)
+    _need(w_tm, name, "w_tm", torch.float32, (cout, k * cin))
+    _need(bias, name, "bias", torch.float32, (cout,))
+    _need(residual, name, "residual", torch.float32, (lanes, cout, length))
+    y = torch.empty((lanes, cout, length), dtype=torch.float32, device=x.device) if out is None else out
+    y_pre = torch.empty_like(y) if want_pre else None
+    d = ConvDesc(lanes, length, cin, cout, k, dilation,
+                 (k - 1) * dilation if pad_left is None else pad_left,
+                 _p(x), _p(w_tm), _p(bias),
+                 _p(snake_in[0]) if snake_in else None, _p(snake_in[1]) if snake_in else None,
+                 _p(residual), _p(y_pre),
+                 _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
+                 _p(y), 0)
+    call("dtts_conv1d_ncl_f32_ex", ctypes.byref(d), stream_handle())
+    return (y_pre, y) if want_pre else y
+
+
+def im2col_tap_major(x, k, dilation, pad_left=None):
+    """im2col::im2col_tap_major / im2col_centered (crates/tts-nn/src/im2col.rs:150-166): one lane
+    [cin, L] f32 -> [k*cin, L]."""
+    _need(x, "im2col_tap_major", "x", torch.float32)
+    cin, length = x.shape
+    cols = torch.empty((k * cin, length), dtype=torch.float32, device=x.device)
+    call("dtts_im2col_tap_major_f32", _p(x), _p(cols), cin, length, k, dilation,
+         (k - 1) * dilation if pad_left is None else pad_left, stream_handle())
+    return cols
+
+
 def causal_conv1d(x, w_tm, bias, dilation):
     """nlc::causal_conv1d (crates/tts-nn/src/nlc.rs:70-132), w in tap-major [cout, k*cin]."""
     k = w_tm.shape[1] // x.shape[-1]

@@ -114,6 +114,25 @@ int dtts_snake_conv_residual_nlc_f16(const dtts_f16 *x, const dtts_f16 *w_tm, co
                                      int64_t len, int64_t cin, int64_t cout, int64_t k,
                                      hipStream_t stream);
 
+/* ------------------------------------------------------------------ a6/a7 channel-major f32 conv */
+
+/* The channel-major conv in f32: the same fused form as dtts_conv1d_nlc_f16_ex, with x
+ * [lanes, cin, len], residual / y_pre / y [lanes, cout, len], f32 everywhere (bias, weights
+ * [cout, k*cin] tap-major, snake parameters), SnakeBeta with full-precision sine, and no rounding
+ * between the fused steps. Replaces centered_conv1d_gemm / causal_conv1d_gemm /
+ * conv1d_gemm_whole (crates/tts-nn/src/lib.rs:704-860: im2col gather, w_tap @ cols, + bias),
+ * chunking included (it is exact there and needless here). pad_left = (k-1)*dilation is causal,
+ * (k-1)*dilation/2 the centred form. Tiled on the f32 matrix cores when cin % 16 == 0,
+ * cout % 64 == 0, k <= 7 and (k-1)*dilation <= 64; a direct kernel otherwise. */
+int dtts_conv1d_ncl_f32_ex(const dtts_conv_desc *desc, hipStream_t stream);
+
+/* im2col::im2col_tap_major / im2col_centered (crates/tts-nn/src/im2col.rs:47-166) for one lane:
+ * cols[(t*cin + c)*len + l] = x[c*len + l + t*dilation - pad_left], 0 outside [0, len). Bit-exact.
+ * The conv kernels never build this matrix; it is exported for parity and for callers that
+ * want it. */
+int dtts_im2col_tap_major_f32(const float *x, float *cols, int64_t cin, int64_t len, int64_t k,
+                              int64_t dilation, int64_t pad_left, hipStream_t stream);
+
 /* ------------------------------------------------------------------ weight layouts (host) */
 
 /* Host-side load-time rearrangements (the reference also does these on the host,
