@@ -72,6 +72,242 @@ def cpu_baseline(geo, weights, latent_np, budget_s=12.0, max_lanes=48):
                        f"per conv; polyphase transposed convs), {wall:.1f} s on {threads} threads")
 
 
+# ---------------------------------------------------------------- configs 1-4 (per-op lines)
+
+PEAK_TFLOPS_F32 = 157.3   # MI355X dense fp32 matrix
+
+
+def _time(fn, reps=20, warm=3):
+    """Mean ms per call between HIP events on torch's current stream (where libdtts launches)."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _graph_time(fn, reps=20, inner=1):
+    """Mean ms per call of `fn`, captured `inner` times back to back in one HIP graph and
+    replayed (the host launch cost leaves; what remains is the kernels' own time on the GPU)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(inner):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    return _time(g.replay, reps=reps, warm=2) / inner
+
+
+def _line(workload, metric, value, unit, ops_, extra=None):
+    d = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "higher_is_better": True,
+         "dtype": None, "data": "synthetic", "config": {"workload": workload}, "ops": ops_}
+    if extra:
+        d.update(extra)
+    return d
+
+
+def workload_cfg1(dev, args):
+    """Config 1: one residual unit [1, 512, 4800] f32, channel-major (f32 matrix cores)."""
+    import numpy as np
+    import torch
+
+    from dtts import nlc, synth
+    import oracle
+
+    c, length = 512, 4800
+    x = torch.from_numpy(synth.normal(0, "cfg1.x", (1, c, length))).to(dev)
+    a1 = synth.uniform(0, "cfg1.alpha1", (c,), 0.5, 1.5)
+    a2 = synth.uniform(0, "cfg1.alpha2", (c,), 0.5, 1.5)
+    f = lambda v: torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(dev)
+    w1 = f(oracle.tap_major_weight_f32(synth.kaiming_normal(0, "cfg1.w1", (c, c, 7), c * 7)))
+    w2 = f(oracle.tap_major_weight_f32(synth.kaiming_normal(0, "cfg1.w2", (c, c, 1), c)))
+    b1, b2 = f(synth.normal(0, "cfg1.b1", (c,), 0, 0.01)), f(synth.normal(0, "cfg1.b2", (c,), 0, 0.01))
+    s1, s2 = (f(a1), f(1.0 / a1)), (f(a2), f(1.0 / a2))
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    k7 = lambda: nlc.conv1d_ncl_f32(x, w1, b1, k=7, dilation=3, pad_left=9, snake_in=s1, snake_out=s2, out=h)
+    k1 = lambda: nlc.conv1d_ncl_f32(h, w2, b2, k=1, residual=x, out=y)
+    t7, t1 = _time(k7), _time(k1)
+    f7, f1 = 2.0 * c * c * 7 * length, 2.0 * c * c * length
+    by = 4.0 * c * length
+    ops_ = {"conv7_snake2": {"ms": t7, "tflops": f7 / t7 / 1e9, "frac_f32_peak": f7 / t7 / 1e9 / PEAK_TFLOPS_F32},
+            "conv1_residual": {"ms": t1, "tflops": f1 / t1 / 1e9, "gbs": 3 * by / t1 / 1e6}}
+    # CPU: the reference route on the oracle (snake pass, im2col + GEMM + bias, snake, GEMM, + x)
+    xn = synth.normal(0, "cfg1.x", (1, c, length))
+    w1n, w2n = w1.cpu().numpy(), w2.cpu().numpy()
+    t0 = time.perf_counter()
+    sn = oracle.snake_ncl_f32(xn, a1, (1.0 / a1).astype(np.float32))
+    hn = oracle.conv1d_ncl_gemm_f32(sn, w1n, b1.cpu().numpy(), 7, 3, 9)
+    hn = oracle.snake_ncl_f32(hn, a2, (1.0 / a2).astype(np.float32))
+    _ = oracle.conv1d_ncl_gemm_f32(hn, w2n, b2.cpu().numpy(), 1, 1, 0) + xn
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    return _line("config1: residual unit [1,512,4800] f32 NCL", "residual-unit ms (f32)", t7 + t1, "ms", ops_,
+                 {"higher_is_better": False, "dtype": "f32",
+                  "cpu_baseline": {"value": round(cpu_ms, 2), "unit": "ms", "kind": "port",
+                                   "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                                   "sample": "the whole unit through the oracle's im2col + GEMM route"}})
+
+
+def workload_cfg2(dev, args):
+    """Config 2: talker per-step norm/position ops at 48 lanes, f16 (latency-bound)."""
+    import numpy as np
+    import torch
+
+    from dtts import ops, synth
+
+    b, heads, n_kv, hd, cap = 48, 16, 8, 128, 2048
+    f16 = lambda v: torch.from_numpy(synth.f16_bits(v).view(np.int16)).view(torch.float16).to(dev)
+    hsd = f16(synth.normal(0, "cfg2.h", (b, 1, 1024)))
+    gam = f16(synth.uniform(0, "cfg2.gamma", (1024,), 0.9, 1.1))
+    q = f16(synth.normal(0, "cfg2.q", (b, heads, hd)))
+    k = f16(synth.normal(0, "cfg2.k", (b, n_kv, hd)))
+    v = f16(synth.normal(0, "cfg2.v", (b, n_kv, hd)))
+    qkv = f16(synth.normal(0, "cfg2.qkv", (b, (heads + 2 * n_kv) * hd)))
+    norms = torch.from_numpy(synth.uniform(0, "cfg2.norms", (2, hd), 0.5, 1.5)).to(dev)
+    c, s = ops.rope_table_f32(cap, hd, 1e6)
+    c, s = torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev)
+    pos = synth.randint(0, "cfg2.pos", (b,), 0, cap - 1).astype(np.int32)
+    kc = torch.zeros((b, n_kv, cap, hd), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    yq, yk, yh = torch.empty_like(q), torch.empty_like(k), torch.empty_like(hsd)
+    fns = {
+        "rms_norm_f16": (lambda: ops.rms_norm(hsd, gam, 1e-6, out=yh), 2 * 2 * b * 1024 + 2048),
+        "rope_q_f16": (lambda: ops.rope(q, c, s, pos, out=yq), 2 * 2 * q.numel() + 8 * b * hd // 2),
+        "rope_k_f16": (lambda: ops.rope(k, c, s, pos, out=yk), 2 * 2 * k.numel() + 8 * b * hd // 2),
+        "kv_append_f16": (lambda: ops.kv_append(k, v, pos, kc, vc), 2 * 2 * (k.numel() + v.numel())),
+        "qk_norm_rope_kv_append_f16": (lambda: ops.qk_norm_rope_kv_append(qkv, norms, c, s, pos, kc, vc, heads, 1e-6),
+                                       2 * qkv.numel() + 2 * b * heads * hd + 2 * 2 * b * n_kv * hd),
+    }
+    res = {}
+    for name, (fn, nbytes) in fns.items():
+        t = _graph_time(fn, reps=20, inner=100)
+        res[name] = {"us": t * 1e3, "gbs": nbytes / t / 1e6, "bytes": nbytes}
+    total = sum(r["us"] for r in res.values())
+    return _line("config2: talker step norm/RoPE/KV append, 48 lanes f16 (graph-replayed, launch-latency bound)",
+                 "per-step op time (us)", total, "us", res, {"higher_is_better": False, "dtype": "f16"})
+
+
+def workload_cfg3(dev, args):
+    """Config 3: Qwen3-talker-layer f16 projections at M=48, 28 distinct layers rotated."""
+    import torch
+
+    layers, m = 28, 48
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    w_qkv = [torch.randn((4096, 1024), device=dev, generator=gen).mul_(0.02).half() for _ in range(layers)]
+    w_gu = [torch.randn((6144, 1024), device=dev, generator=gen).mul_(0.02).half() for _ in range(layers)]
+    w_dn = [torch.randn((1024, 3072), device=dev, generator=gen).mul_(0.02).half() for _ in range(layers)]
+    x = torch.randn((m, 1024), device=dev, generator=gen).half()
+    hh = torch.randn((m, 3072), device=dev, generator=gen).half()
+    from dtts import ops
+
+    runs = {
+        "qkv_48x1024x4096": (lambda: [ops.matmul_nt(x, w) for w in w_qkv], 1024 * 4096),
+        "gateup_silu_48x1024x6144": (lambda: [ops.gateup_silu(x, w) for w in w_gu], 1024 * 6144),
+        "down_48x3072x1024": (lambda: [ops.matmul_nt(hh, w) for w in w_dn], 3072 * 1024),
+    }
+    res, tot_ms, tot_bytes = {}, 0.0, 0.0
+    for name, (fn, kn) in runs.items():
+        t = _graph_time(fn, reps=10) / layers
+        by = 2.0 * kn + 2.0 * m * (kn // (6144 if "gateup" in name else (4096 if "qkv" in name else 1024)))
+        fl = 2.0 * m * kn
+        res[name] = {"us_per_layer": t * 1e3, "gbs": 2.0 * kn / t / 1e6, "tflops": fl / t / 1e9}
+        tot_ms += t
+        tot_bytes += 2.0 * kn
+    return _line("config3: f16 decode projections M=48, 28 layers rotated (763 MB of weights), graph-replayed",
+                 "weight-streaming GB/s", tot_bytes / tot_ms / 1e6, "GB/s", res,
+                 {"dtype": "f16", "frac_hbm_peak": round(tot_bytes / tot_ms / 1e6 / PEAK_HBM_GBS, 4),
+                  "us_per_layer": round(tot_ms * 1e3, 2)})
+
+
+def workload_cfg4(dev, args):
+    """Config 4: Q8_0 GEMV/GEMM at M in {1, 8, 48}, K=1024 N=6144 and K=3072 N=1024."""
+    import numpy as np
+    import torch
+
+    from dtts import ops, synth
+
+    res = {}
+    for (k, n) in ((1024, 6144), (3072, 1024)):
+        w = synth.normal(0, f"cfg4.w{k}", (n, k), 0, 0.02)
+        blocks = torch.from_numpy(ops.q8_0_quantize(w)).to(dev)
+        copies = max(1, int(300e6 // blocks.numel()))  # rotate > the 256 MB MALL
+        sets = [blocks.clone() for _ in range(copies)]
+        for m in (1, 8, 48):
+            x = torch.from_numpy(synth.f16_bits(synth.normal(0, f"cfg4.x{m}", (m, k))).view(np.int16)).view(torch.float16).to(dev)
+            for mode in ("w8a16", "w8a8"):
+                t = _graph_time(lambda: [ops.q8_0_matmul(x, b, mode) for b in sets], reps=5) / copies
+                wb = 34.0 * n * k / 32
+                res[f"k{k}_n{n}_m{m}_{mode}"] = {"us": t * 1e3, "gbs": (wb + 2.0 * m * k + 4.0 * m * n) / t / 1e6,
+                                                 "tops": 2.0 * m * n * k / t / 1e9}
+        del sets
+    best = max(r["gbs"] for r in res.values())
+    return _line("config4: Q8_0 projections (GGML blocks), weights rotated past the MALL, graph-replayed",
+                 "best weight-streaming GB/s", best, "GB/s", res, {"dtype": "int8/f16"})
+
+
+# ---------------------------------------------------------------- rocprofv3 counter digest
+
+COPY_PROBE_BYTES = 1 << 30  # --copy-probe: a mul kernel reading and writing 1 GiB
+
+
+def pmc_summary(fetch_csv, write_csv, stages_json):
+    """Per-kernel HBM traffic of one decode from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE,
+    KiB per dispatch), each scaled by what its counter reads for the copy probe, next to the
+    algorithmic bytes of the same launches (dtts_codec_profile's accounting)."""
+    import csv
+
+    def rows(path, counter):
+        return [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+
+    def calib(rs):
+        probe = [float(r["Counter_Value"]) * 1024 for r in rs
+                 if "elementwise" in r["Kernel_Name"] and float(r["Counter_Value"]) * 1024 > COPY_PROBE_BYTES / 4]
+        if not probe:
+            raise SystemExit("pmc-summary: no copy-probe dispatch in " + fetch_csv)
+        return COPY_PROBE_BYTES / (sum(probe) / len(probe))
+
+    fr, wr = rows(fetch_csv, "FETCH_SIZE"), rows(write_csv, "WRITE_SIZE")
+    cf, cw = calib(fr), calib(wr)
+    stages = json.load(open(stages_json))["stages"]
+    dtts = lambda rs: [r for r in rs if "dtts::" in r["Kernel_Name"]]
+    fd, wd = dtts(fr), dtts(wr)
+    n = len(stages)
+    if len(fd) < n or len(wd) < n:
+        raise SystemExit("pmc-summary: fewer dtts dispatches than stages")
+    # the first n dispatches are the timed decode (steps=1, warmup=0), in stage order
+    out = {"fetch_scale": cf, "write_scale": cw, "kernels": {}, "stages": []}
+    for st, f, w in zip(stages, fd[:n], wd[:n]):
+        rd, wb = float(f["Counter_Value"]) * 1024 * cf, float(w["Counter_Value"]) * 1024 * cw
+        out["stages"].append({"name": st["name"], "kernel": st["kernel"], "fetch_bytes": rd, "write_bytes": wb,
+                              "alg_bytes": st["bytes"]})
+        k = out["kernels"].setdefault(st["kernel"], {"launches": 0, "fetch_bytes": 0.0, "write_bytes": 0.0,
+                                                     "alg_bytes": 0.0})
+        k["launches"] += 1
+        k["fetch_bytes"] += rd
+        k["write_bytes"] += wb
+        k["alg_bytes"] += st["bytes"]
+    for k in out["kernels"].values():
+        k["traffic_per_launch"] = (k["fetch_bytes"] + k["write_bytes"]) / k["launches"]
+        k["alg_per_launch"] = k["alg_bytes"] / k["launches"]
+        k["ratio"] = k["traffic_per_launch"] / k["alg_per_launch"]
+    return out
+
+
+WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,9 +318,19 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-runs", type=int, default=3)
     ap.add_argument("--stages-out", default=None, help="write the per-launch profile as JSON here")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "STAGES_JSON"),
+                    help="digest rocprofv3 FETCH_SIZE / WRITE_SIZE runs into per-kernel traffic (no GPU)")
+    ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "codec_config5_pmc.json"),
+                    help="per-kernel traffic from --pmc-summary, reported in roofline.traffic")
+    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "all"],
+                    help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -97,6 +343,11 @@ def main():
     from dtts import codec, synth
 
     dev = torch.device("cuda:0")
+    if args.workload != "cfg5":
+        for w in (["cfg1", "cfg2", "cfg3", "cfg4"] if args.workload == "all" else [args.workload]):
+            print(json.dumps(WORKLOADS[w](dev, args)), flush=True)
+        if args.workload != "all":
+            return
     geo = codec.CONFIG5
     t0 = time.perf_counter()
     w = codec.random_weights(geo, seed=0)
@@ -135,6 +386,11 @@ def main():
         roof = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s")
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
     roof["traffic"] = None
+    if os.path.exists(args.traffic_json):
+        tk = json.load(open(args.traffic_json))["kernels"].get(kname)
+        if tk:  # measured offline with rocprofv3 --pmc on this kernel (see --pmc-summary)
+            roof["traffic"] = round(tk["traffic_per_launch"])
+            roof["traffic_over_algorithmic"] = round(tk["ratio"], 3)
     roof["kernel"] = kname
     roof["launches_per_step"] = dom["launches"]
     roof["ms_per_launch"] = round(per_launch_ms, 4)
