@@ -153,9 +153,15 @@ namespace dtts {
 namespace {
 
 struct Stage {
+    bool ru;           // a fused residual unit (r) rather than one conv (d)
     dtts_conv_desc d;
+    dtts_ru_desc r;
     char name[32];
 };
+
+int run_stage(const Stage &st, hipStream_t stream) {
+    return st.ru ? residual_unit_nlc_f16(&st.r, stream) : conv1d_nlc_f16(&st.d, stream);
+}
 
 // The decode as a list of conv launches over the workspace's four buffers.
 int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes, int64_t frames,
@@ -178,9 +184,16 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
         return nullptr;
     };
     auto push = [&](const dtts_conv_desc &d, const char *fmt, long long a, long long b) {
-        Stage st;
+        Stage st{};
         st.d = d;
         snprintf(st.name, sizeof(st.name), fmt, a, b);
+        plan.push_back(st);
+    };
+    auto push_ru = [&](const dtts_ru_desc &r, long long a, long long b) {
+        Stage st{};
+        st.ru = true;
+        st.r = r;
+        snprintf(st.name, sizeof(st.name), "block%lld.unit%lld", a, b);
         plan.push_back(st);
     };
 
@@ -196,7 +209,25 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
     for (int64_t i = 0; i < g.n_blocks; ++i) {
         const dtts_codec_block &blk = w.blocks[i];
         const int64_t cin = g.channels[i], cout = g.channels[i + 1], rate = g.rates[i];
-        const bool wide = cout > kStoreSnakedAbove;
+        // residual units that fit one workgroup's channel width run fused (ru.hip); the others
+        // are two convs, and wide ones read a snaked copy of their input stored beside it
+        dtts_ru_desc probe{};
+        probe.channels = cout;
+        probe.k = g.ru_kernel;
+        probe.x = probe.w1 = probe.w2 = probe.b1 = probe.b2 = probe.y = buf[0];
+        const bool fused = [&] {
+            for (int j = 0; j < 3; ++j) {
+                probe.dilation = g.ru_dilations[j];
+                const dtts_codec_unit &un = blk.units[j];
+                probe.w1 = un.conv1_w;
+                probe.w2 = un.conv2_w;
+                probe.b1 = un.conv1_b;
+                probe.b2 = un.conv2_b;
+                if (!un.conv1_b || !un.conv2_b || !residual_unit_supported(&probe)) return false;
+            }
+            return true;
+        }();
+        const bool wide = !fused && cout > kStoreSnakedAbove;
         // TransConv: one causal conv of 2 taps over the snaked input, rate*cout phase columns
         char *u = pick(x, nullptr, nullptr);
         char *su = wide ? pick(x, u, nullptr) : nullptr;
@@ -210,7 +241,37 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
             push(d, "block%lld.up%.0lld", (long long)i, 0);
         }
         len *= rate;
-        for (int j = 0; j < 3; ++j) {
+        for (int j = 0; j < 3 && fused; ++j) {
+            const dtts_codec_unit &un = blk.units[j];
+            dtts_ru_desc r{};
+            r.lanes = lanes;
+            r.len = len;
+            r.channels = cout;
+            r.k = g.ru_kernel;
+            r.dilation = g.ru_dilations[j];
+            r.x = u;
+            r.act1_alpha = un.act1_alpha;
+            r.act1_brecip = un.act1_brecip;
+            r.w1 = un.conv1_w;
+            r.b1 = un.conv1_b;
+            r.act2_alpha = un.act2_alpha;
+            r.act2_brecip = un.act2_brecip;
+            r.w2 = un.conv2_w;
+            r.b2 = un.conv2_b;
+            char *y = pick(u, nullptr, nullptr);
+            r.y = y;
+            if (j == 2) {
+                const bool last = i + 1 == g.n_blocks;
+                r.out_alpha = last ? w.out_alpha : w.blocks[i + 1].act_alpha;
+                r.out_brecip = last ? w.out_brecip : w.blocks[i + 1].act_brecip;
+            }
+            push_ru(r, (long long)i, j);
+            if (j == 2)
+                x = y;  // snaked input of the next TransConv (or of the output conv)
+            else
+                u = y;
+        }
+        for (int j = 0; j < 3 && !fused; ++j) {
             const dtts_codec_unit &un = blk.units[j];
             char *h = pick(u, su, nullptr);
             {
@@ -265,7 +326,7 @@ extern "C" int dtts_codec_decode(const dtts_codec *c, const dtts_f16 *latent, dt
     int rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
     if (rc != DTTS_OK) return rc;
     for (const dtts::Stage &st : plan)
-        if ((rc = dtts::conv1d_nlc_f16(&st.d, stream)) != DTTS_OK) return rc;
+        if ((rc = dtts::run_stage(st, stream)) != DTTS_OK) return rc;
     return DTTS_OK;
 }
 
@@ -283,25 +344,38 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, d
     int status = DTTS_OK;
     hipError_t he = hipEventRecord(ev[0], stream);
     for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
-        status = dtts::conv1d_nlc_f16(&plan[i].d, stream);
+        status = dtts::run_stage(plan[i], stream);
         if (status == DTTS_OK) he = hipEventRecord(ev[i + 1], stream);
     }
     if (he == hipSuccess && status == DTTS_OK) he = hipEventSynchronize(ev.back());
     for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
-        const dtts_conv_desc &d = plan[i].d;
         dtts_codec_stage &s = stages[i];
         std::memset(&s, 0, sizeof(s));
         snprintf(s.name, sizeof(s.name), "%s", plan[i].name);
-        snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::conv_kernel_name(&d));
-        s.lanes = d.lanes;
-        s.len = d.len;
-        s.cin = d.cin;
-        s.cout = d.cout;
-        s.k = d.k;
-        s.dilation = d.dilation;
-        s.flops = 2.0 * d.lanes * d.len * d.cin * d.cout * d.k;
-        const double outs = (d.y_pre ? 2.0 : 1.0) + (d.residual ? 1.0 : 0.0);
-        s.bytes = 2.0 * d.lanes * d.len * (d.cin + d.cout * outs) + 2.0 * d.cout * d.k * d.cin;
+        if (plan[i].ru) {
+            const dtts_ru_desc &r = plan[i].r;
+            snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::residual_unit_kernel_name(&r));
+            s.lanes = r.lanes;
+            s.len = r.len;
+            s.cin = s.cout = r.channels;
+            s.k = r.k;
+            s.dilation = r.dilation;
+            const double c = static_cast<double>(r.channels);
+            s.flops = 2.0 * r.lanes * r.len * c * c * (r.k + 1);
+            s.bytes = 2.0 * r.lanes * r.len * c * (r.y_pre ? 3.0 : 2.0) + 2.0 * c * c * (r.k + 1);
+        } else {
+            const dtts_conv_desc &d = plan[i].d;
+            snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::conv_kernel_name(&d));
+            s.lanes = d.lanes;
+            s.len = d.len;
+            s.cin = d.cin;
+            s.cout = d.cout;
+            s.k = d.k;
+            s.dilation = d.dilation;
+            s.flops = 2.0 * d.lanes * d.len * d.cin * d.cout * d.k;
+            const double outs = (d.y_pre ? 2.0 : 1.0) + (d.residual ? 1.0 : 0.0);
+            s.bytes = 2.0 * d.lanes * d.len * (d.cin + d.cout * outs) + 2.0 * d.cout * d.k * d.cin;
+        }
         he = hipEventElapsedTime(&s.ms, ev[i], ev[i + 1]);
     }
     for (auto &e : ev) (void)hipEventDestroy(e);

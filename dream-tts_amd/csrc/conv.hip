@@ -15,219 +15,31 @@
 // Four waves split M (64 rows each) and cover all BN columns with 32x32x16 f16 MFMAs (f32
 // accumulate). The next chunk is prefetched into registers while the current one computes.
 // The epilogue goes through LDS so bias/residual/stores move 16 bytes per lane, coalesced.
-#include "conv.hpp"
-#include "snake.hpp"
+#include "conv_tile.hpp"
 
 namespace dtts {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kKC = 32;        // channels per chunk
-constexpr int kLDA = kKC + 8;  // LDS row pitch (halves); the 16-byte pad spreads the banks
+typedef ConvArgs ConvParams;
 
-struct ConvParams {
-    const half_t *x;
-    const half_t *w;
-    const half_t *bias;
-    const float *a_in;
-    const float *r_in;
-    const half_t *res;
-    half_t *y_pre;
-    half_t *y;
-    const float *a_out;
-    const float *r_out;
-    int L, cin, cout, k, dil, pad_left, act;
-    int tiles_m, tiles_n, total_tiles, tiles_per_xcd;
-};
-
-__device__ __forceinline__ float act_apply(float v, int act) {
-    return act == 1 ? tanhf(v) : v;
-}
-
-template <int BM, int BN, int KMAX, int HMAX, bool SNAKE_IN>
-__global__ __launch_bounds__(kThreads, 2) void conv_nlc_f16_mfma(ConvParams p) {
-    constexpr int WAVES = kThreads / 64;
-    constexpr int WTM = BM / WAVES;  // rows per wave
-    constexpr int TM = WTM / 32;
-    constexpr int TN = BN / 32;
-    constexpr int A_ROWS = BM + HMAX;
-    constexpr int A_HALVES = A_ROWS * kLDA;
-    constexpr int B_HALVES = KMAX * BN * kLDA;
-    constexpr int EPI_PITCH = BN + 4;  // floats
-    constexpr int EPI_FLOATS = WAVES * 32 * EPI_PITCH;
-    constexpr int MAIN_BYTES = (A_HALVES + B_HALVES) * 2;
-    constexpr int LDS_BYTES = MAIN_BYTES > EPI_FLOATS * 4 ? MAIN_BYTES : EPI_FLOATS * 4;
-    constexpr int A_SEGS = A_ROWS * (kKC / 8);
-    constexpr int A_PER_T = (A_SEGS + kThreads - 1) / kThreads;
-    constexpr int B_SEGS = KMAX * BN * (kKC / 8);
-    constexpr int B_PER_T = (B_SEGS + kThreads - 1) / kThreads;
-    static_assert(WTM % 32 == 0 && BN % 32 == 0, "tile shape");
-
-    __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
-    half_t *As = reinterpret_cast<half_t *>(smem);
-    half_t *Bs = As + A_HALVES;
-
-    // XCD-aware order: consecutive dispatch slots round-robin over the 8 XCDs, so block b runs on
-    // XCD b % 8; each XCD takes a contiguous range of (lane, m, n) tiles, N fastest, so the A
-    // window of an M tile is fetched into one L2 and reused by all of its N tiles there.
-    const int tile = (blockIdx.x & 7) * p.tiles_per_xcd + (blockIdx.x >> 3);
-    if (tile >= p.total_tiles) return;
-    const int n_tile = tile % p.tiles_n;
-    const int rest = tile / p.tiles_n;
-    const int m_tile = rest % p.tiles_m;
-    const int lane_idx = rest / p.tiles_m;
-    const int l0 = m_tile * BM;
-    const int n0 = n_tile * BN;
-    const int rows = BM + (p.k - 1) * p.dil;
-    const int win0 = l0 - p.pad_left;
-    const int K = p.k * p.cin;
+template <typename Cfg, bool SNAKE_IN>
+__global__ __launch_bounds__(Cfg::THREADS, 2) void conv_nlc_f16_mfma(ConvArgs p) {
+    constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_BYTES ? Cfg::MAIN_BYTES : Cfg::EPI_BYTES;
+    __shared__ __attribute__((aligned(16))) char smem[LDS];
+    int lane_idx, m_tile, n_tile;
+    if (!conv_tile_coords(p, lane_idx, m_tile, n_tile)) return;
+    const int l0 = m_tile * Cfg::BM;
+    const int n0 = n_tile * Cfg::BN;
     const half_t *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-
-    float16_t acc[TM][TN];
+    float16_t acc[Cfg::TM][Cfg::TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = float16_t{};
-
-    half8_t ra[A_PER_T];
-    half8_t rb[B_PER_T];
-    const int bsegs = p.k * BN * (kKC / 8);
-
-    auto load_chunk = [&](int c0) {
-#pragma unroll
-        for (int i = 0; i < A_PER_T; ++i) {
-            const int seg = tid + i * kThreads;
-            const int r = seg >> 2;
-            const int q = seg & 3;
-            half8_t v = half8_t{};
-            const int s = win0 + r;
-            if (seg < A_SEGS && r < rows && s >= 0 && s < p.L)
-                v = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + q * 8);
-            ra[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER_T; ++i) {
-            const int seg = tid + i * kThreads;
-            half8_t v = half8_t{};
-            if (seg < B_SEGS && seg < bsegs) {
-                const int row = seg >> 2;  // t * BN + n
-                const int q = seg & 3;
-                const int t = row / BN;
-                const int n = row - t * BN;
-                v = *reinterpret_cast<const half8_t *>(p.w + static_cast<int64_t>(n0 + n) * K + t * p.cin + c0 + q * 8);
-            }
-            rb[i] = v;
-        }
-    };
-
-    auto store_chunk = [&](int c0) {
-#pragma unroll
-        for (int i = 0; i < A_PER_T; ++i) {
-            const int seg = tid + i * kThreads;
-            if (seg < A_SEGS) {
-                const int r = seg >> 2;
-                const int q = seg & 3;
-                half8_t v = ra[i];
-                if constexpr (SNAKE_IN) {
-                    const int c = c0 + q * 8;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        v[j] = static_cast<half_t>(snake_f16out(static_cast<float>(v[j]), p.a_in[c + j], p.r_in[c + j]));
-                }
-                *reinterpret_cast<half8_t *>(As + r * kLDA + q * 8) = v;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < B_PER_T; ++i) {
-            const int seg = tid + i * kThreads;
-            if (seg < B_SEGS) {
-                const int row = seg >> 2;
-                const int q = seg & 3;
-                *reinterpret_cast<half8_t *>(Bs + row * kLDA + q * 8) = rb[i];
-            }
-        }
-    };
-
-    const int nchunks = p.cin / kKC;
-    const int arow0 = wave * WTM + (lane & 31);
-    const int koff = (lane >> 5) * 8;
-
-    load_chunk(0);
-    for (int c = 0; c < nchunks; ++c) {
-        store_chunk(c * kKC);
-        __syncthreads();
-        if (c + 1 < nchunks) load_chunk((c + 1) * kKC);
-        for (int t = 0; t < p.k; ++t) {
-            const half_t *at = As + (arow0 + t * p.dil) * kLDA + koff;
-            const half_t *bt = Bs + (t * BN + (lane & 31)) * kLDA + koff;
-#pragma unroll
-            for (int kk = 0; kk < kKC; kk += 16) {
-                half8_t af[TM], bf[TN];
-#pragma unroll
-                for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const half8_t *>(at + i * 32 * kLDA + kk);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const half8_t *>(bt + j * 32 * kLDA + kk);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-        }
-        __syncthreads();
-    }
-
-    // Epilogue, one 32-row block per wave at a time through the wave's own LDS region.
-    float *E = reinterpret_cast<float *>(smem) + wave * 32 * EPI_PITCH;
-    const int64_t ybase = static_cast<int64_t>(lane_idx) * p.L;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int mr = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                E[mr * EPI_PITCH + j * 32 + (lane & 31)] = acc[i][j][r];
-            }
-        __syncthreads();
-        constexpr int GROUPS = 32 * (BN / 8);
-        for (int g = lane; g < GROUPS; g += 64) {
-            const int mr = g / (BN / 8);
-            const int cg = g - mr * (BN / 8);
-            const int l = l0 + wave * WTM + i * 32 + mr;
-            if (l >= p.L) continue;
-            const int n = n0 + cg * 8;
-            const float4_t *src = reinterpret_cast<const float4_t *>(E + mr * EPI_PITCH + cg * 8);
-            const float4_t v0 = src[0], v1 = src[1];
-            float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            if (p.bias) {
-                const half8_t bb = *reinterpret_cast<const half8_t *>(p.bias + n);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] += static_cast<float>(bb[j]);
-            }
-            const int64_t off = (ybase + l) * p.cout + n;
-            if (p.res) {
-                const half8_t rr = *reinterpret_cast<const half8_t *>(p.res + off);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] += static_cast<float>(rr[j]);
-            }
-            half8_t h;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) h[j] = static_cast<half_t>(act_apply(v[j], p.act));
-            if (p.y_pre) *reinterpret_cast<half8_t *>(p.y_pre + off) = h;
-            if (p.a_out) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    h[j] = static_cast<half_t>(snake_f16out(static_cast<float>(h[j]), p.a_out[n + j], p.r_out[n + j]));
-            }
-            *reinterpret_cast<half8_t *>(p.y + off) = h;
-        }
-        __syncthreads();
-    }
+        for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
+    half_t *As = reinterpret_cast<half_t *>(smem);
+    conv_mainloop<Cfg, SNAKE_IN>(p, xl, l0, n0, As, As + Cfg::A_HALVES, acc);
+    conv_epilogue<Cfg>(acc, smem, static_cast<int64_t>(lane_idx) * p.L, l0, n0, p.L, p.cout, p.bias, p.res, p.y_pre,
+                       p.y, p.a_out, p.r_out, p.act);
 }
 
 // Any shape: one thread per output element, taps and channels looped directly. For shapes the
@@ -254,34 +66,34 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_direct(ConvParams p, int64_t
         float v = acc;
         if (p.bias) v += static_cast<float>(p.bias[n]);
         if (p.res) v += static_cast<float>(p.res[e]);
-        half_t h = static_cast<half_t>(act_apply(v, p.act));
+        half_t h = static_cast<half_t>(conv_act(v, p.act));
         if (p.y_pre) p.y_pre[e] = h;
         if (p.a_out) h = static_cast<half_t>(snake_f16out(static_cast<float>(h), p.a_out[n], p.r_out[n]));
         p.y[e] = h;
     }
 }
 
-template <int BM, int BN, int KMAX, int HMAX>
+template <typename Cfg>
 hipError_t launch_tiled(const ConvParams &p0, int64_t lanes, hipStream_t stream) {
     ConvParams p = p0;
-    p.tiles_m = (p.L + BM - 1) / BM;
-    p.tiles_n = p.cout / BN;
+    p.tiles_m = (p.L + Cfg::BM - 1) / Cfg::BM;
+    p.tiles_n = p.cout / Cfg::BN;
     const int64_t total = lanes * p.tiles_m * p.tiles_n;
     p.total_tiles = static_cast<int>(total);
     p.tiles_per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.tiles_per_xcd) * 8);
     if (p.a_in)
-        conv_nlc_f16_mfma<BM, BN, KMAX, HMAX, true><<<grid, kThreads, 0, stream>>>(p);
+        conv_nlc_f16_mfma<Cfg, true><<<grid, Cfg::THREADS, 0, stream>>>(p);
     else
-        conv_nlc_f16_mfma<BM, BN, KMAX, HMAX, false><<<grid, kThreads, 0, stream>>>(p);
+        conv_nlc_f16_mfma<Cfg, false><<<grid, Cfg::THREADS, 0, stream>>>(p);
     return hipGetLastError();
 }
 
 template <int KMAX, int HMAX>
 hipError_t launch_by_bn(const ConvParams &p, int64_t lanes, hipStream_t stream) {
-    if (p.cout % 96 == 0) return launch_tiled<256, 96, KMAX, HMAX>(p, lanes, stream);
-    if (p.cout % 64 == 0) return launch_tiled<256, 64, KMAX, HMAX>(p, lanes, stream);
-    return launch_tiled<256, 32, KMAX, HMAX>(p, lanes, stream);
+    if (p.cout % 96 == 0) return launch_tiled<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
+    if (p.cout % 64 == 0) return launch_tiled<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
+    return launch_tiled<ConvTile<256, 32, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
 }
 
 }  // namespace
@@ -305,7 +117,7 @@ Choice choose(const dtts_conv_desc *d) {
     const bool aligned16 = aligned(d->x, 16) && aligned(d->w, 16) && aligned(d->y, 16) &&
                            (!d->bias || aligned(d->bias, 16)) && (!d->residual || aligned(d->residual, 16)) &&
                            (!d->y_pre || aligned(d->y_pre, 16));
-    if (!aligned16 || d->cin % kKC != 0 || d->cout % 32 != 0 || d->k > 7) return c;
+    if (!aligned16 || d->cin % 32 != 0 || d->cout % 32 != 0 || d->k > 7) return c;
     if (d->k == 1) {
         c.kmax = 1;
         c.hmax = 0;
@@ -331,8 +143,8 @@ const char *conv_kernel_name(const dtts_conv_desc *d) {
     static thread_local char buf[64];
     const Choice c = choose(d);
     if (std::strcmp(c.path, "mfma") == 0)
-        snprintf(buf, sizeof(buf), "conv_nlc_f16_mfma<256, %d, %d, %d, %s>", c.bn, c.kmax, c.hmax,
-                 c.snake ? "true" : "false");
+        snprintf(buf, sizeof(buf), "conv_nlc_f16_mfma<dtts::ConvTile<256, %d, 4, 1, 32, %d, %d>, %s>", c.bn, c.kmax,
+                 c.hmax, c.snake ? "true" : "false");
     else
         snprintf(buf, sizeof(buf), "conv_nlc_f16_%s", c.path);
     return buf;

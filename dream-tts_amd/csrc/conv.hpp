@@ -13,6 +13,11 @@ const char *conv_path_name(const dtts_conv_desc *d);
 const char *conv_kernel_name(const dtts_conv_desc *d);
 int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream);
 
+// The fused residual unit (ru.hip).
+bool residual_unit_supported(const dtts_ru_desc *d);
+const char *residual_unit_kernel_name(const dtts_ru_desc *d);
+int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream);
+
 // The single-output-channel kernel (conv_narrow.hip).
 bool conv_narrow_eligible(const dtts_conv_desc *d);
 hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream);

@@ -36,6 +36,8 @@ SIGNATURES = {
     "dtts_causal_conv1d_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "dtts_snake_conv_residual_nlc_f16": [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _I64, _P],
+    "dtts_residual_unit_nlc_f16": [_P, _P],
+    "dtts_residual_unit_supported": [_P],
     "dtts_conv1d_ncl_f32_ex": [_P, _P],
     "dtts_im2col_tap_major_f32": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "dtts_tap_major_weight": [_P, _P, _I64, _I64, _I64, _I64],

@@ -120,7 +120,7 @@ class _Block(ctypes.Structure):
 
 
 class _Stage(ctypes.Structure):
-    _fields_ = [("name", ctypes.c_char * 32), ("kernel", ctypes.c_char * 64),
+    _fields_ = [("name", ctypes.c_char * 32), ("kernel", ctypes.c_char * 96),
                 ("lanes", ctypes.c_int64), ("len", ctypes.c_int64), ("cin", ctypes.c_int64),
                 ("cout", ctypes.c_int64), ("k", ctypes.c_int64), ("dilation", ctypes.c_int64),
                 ("flops", ctypes.c_double), ("bytes", ctypes.c_double), ("ms", ctypes.c_float)]

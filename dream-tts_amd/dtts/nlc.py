@@ -72,6 +72,30 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
     return (y_pre, y) if want_pre else y
 
 
+class RuDesc(ctypes.Structure):
+    _fields_ = [("lanes", ctypes.c_int64), ("len", ctypes.c_int64), ("channels", ctypes.c_int64),
+                ("k", ctypes.c_int64), ("dilation", ctypes.c_int64)] + [
+        (n, ctypes.c_void_p) for n in ("x", "act1_alpha", "act1_brecip", "w1", "b1", "act2_alpha",
+                                       "act2_brecip", "w2", "b2", "y_pre", "out_alpha", "out_brecip", "y")]
+
+
+def residual_unit(x, act1, w1_tm, b1, act2, w2_tm, b2, *, k, dilation, snake_out=None, want_pre=False):
+    """ResidualUnit::forward (crates/qwen3tts/src/codec.rs:215-229) in one launch:
+    x + conv_1(act2(conv_k(act1(x)))), optionally followed by the next SnakeBeta. x [lanes, L, C] f16."""
+    name = "residual_unit"
+    lanes, length, c = x.shape
+    _need(x, name, "x", torch.float16)
+    _need(w1_tm, name, "w1", torch.float16, (c, k * c))
+    _need(w2_tm, name, "w2", torch.float16, (c, c))
+    y = torch.empty_like(x)
+    y_pre = torch.empty_like(x) if want_pre else None
+    d = RuDesc(lanes, length, c, k, dilation, _p(x), _p(act1[0]), _p(act1[1]), _p(w1_tm), _p(b1),
+               _p(act2[0]), _p(act2[1]), _p(w2_tm), _p(b2), _p(y_pre),
+               _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None, _p(y))
+    call("dtts_residual_unit_nlc_f16", ctypes.byref(d), stream_handle())
+    return (y_pre, y) if want_pre else y
+
+
 def conv1d_ncl_f32(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, residual=None,
                    snake_out=None, want_pre=False, out=None):
     """The channel-major f32 conv (dtts_conv1d_ncl_f32_ex): x [lanes, cin, L] f32, w_tm

@@ -114,6 +114,35 @@ int dtts_snake_conv_residual_nlc_f16(const dtts_f16 *x, const dtts_f16 *w_tm, co
                                      int64_t len, int64_t cin, int64_t cout, int64_t k,
                                      hipStream_t stream);
 
+/* The codec's residual unit in one launch (ResidualUnit::forward, crates/qwen3tts/src/codec.rs:
+ * 215-229; nlc::snake_conv_residual, crates/tts-nn/src/nlc.rs:40-68, fuses its second half):
+ *
+ *   h  = f16(conv_k(SnakeBeta1(x)) + b1)     causal, pad (k-1)*dilation
+ *   h2 = f16(SnakeBeta2(h))
+ *   y_pre = f16(conv_1(h2) + b2 + x)
+ *   y  = f16(SnakeBeta_out(y_pre))           (y_pre itself when out_alpha == NULL)
+ *
+ * x, y, y_pre [lanes, len, channels] f16; w1 [C, k*C] and w2 [C, C] tap-major f16; b1, b2 f16;
+ * SnakeBeta parameters f32. h and h2 stay on chip: two activation passes instead of five. Taken
+ * for channels 96 and 192, k <= 7, (k-1)*dilation <= 64, 16-byte aligned x/y/y_pre/w1/w2/b2;
+ * anything else returns DTTS_ERR_UNSUPPORTED (compose two dtts_conv1d_nlc_f16_ex calls). */
+typedef struct dtts_ru_desc {
+    int64_t lanes, len, channels, k, dilation;
+    const void *x;
+    const float *act1_alpha, *act1_brecip;
+    const void *w1, *b1;
+    const float *act2_alpha, *act2_brecip;
+    const void *w2, *b2;
+    void *y_pre;
+    const float *out_alpha, *out_brecip;
+    void *y;
+} dtts_ru_desc;
+
+int dtts_residual_unit_nlc_f16(const dtts_ru_desc *desc, hipStream_t stream);
+
+/* 1 when dtts_residual_unit_nlc_f16 takes this descriptor, else 0 (no device work). */
+int dtts_residual_unit_supported(const dtts_ru_desc *desc);
+
 /* ------------------------------------------------------------------ a6/a7 channel-major f32 conv */
 
 /* The channel-major conv in f32: the same fused form as dtts_conv1d_nlc_f16_ex, with x
@@ -339,7 +368,7 @@ int dtts_codec_decode(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 
  * HIP events recorded on the stream around it. */
 typedef struct dtts_codec_stage {
     char name[32];    /* e.g. "block2.unit1.conv1" */
-    char kernel[64];  /* the HIP kernel that ran, as a profiler names it */
+    char kernel[96];  /* the HIP kernel that ran, as a profiler names it */
     int64_t lanes, len, cin, cout, k, dilation;
     double flops, bytes;
     float ms;

@@ -72,7 +72,8 @@ def test_codec_profile_covers_every_launch(dev):
     audio = torch.empty((2, 8 * geo.hop), dtype=torch.float16, device=dev)
     stages = model.profile(latent, out=audio)
     assert np.array_equal(to_host(audio), ref)
-    assert len(stages) == 1 + len(geo.rates) * 7 + 1
+    fused = [c in (96, 192) for c in geo.channels[1:]]  # residual units run as one kernel there
+    assert len(stages) == 2 + sum(1 + (3 if f else 6) for f in fused)
     assert all(s["ms"] > 0 for s in stages)
     assert stages[0]["name"] == "head" and stages[-1]["name"] == "out"
     assert sum(s["flops"] for s in stages) == pytest.approx(2 * 8 * geo.flops_per_frame(), rel=1e-9)

@@ -125,3 +125,34 @@ def test_conv_rejects_bad_shapes(dev):
         nlc.conv1d(x, w, None, k=7, dilation=1, pad_left=7)
     with pytest.raises(DttsError, match="shape"):
         nlc.conv1d(x, w[:, :100].contiguous(), None, k=7)
+
+
+@pytest.mark.parametrize("lanes,c,length,dil,out_snake", [(2, 96, 3000, 9, True), (3, 96, 700, 1, False),
+                                                           (2, 192, 1100, 3, True), (1, 192, 257, 9, False)])
+def test_fused_residual_unit_matches_composed_chain(dev, lanes, c, length, dil, out_snake):
+    """dtts_residual_unit_nlc_f16 against the oracle's unfused chain with the same f16 storage
+    points: h = conv7(snake1(x)); h2 = snake2(h); y = conv1(h2) + x; [snake_out(y)]."""
+    k = 7
+    x = synth.f16_bits(synth.normal(44, "x", (lanes, length, c)))
+    w1 = synth.f16_bits(synth.normal(44, "w1", (c, c, k), 0, np.sqrt(1.0 / (c * k))))
+    w2 = synth.f16_bits(synth.normal(44, "w2", (c, c, 1), 0, np.sqrt(1.0 / c)))
+    b1 = synth.f16_bits(synth.normal(44, "b1", (c,), 0, 0.01))
+    b2 = synth.f16_bits(synth.normal(44, "b2", (c,), 0, 0.01))
+    acts = [synth.uniform(44, f"a{i}", (c,), 0.5, 1.5) for i in range(3)]
+    pairs = [(a, (1.0 / a).astype(np.float32)) for a in acts]
+    dv = lambda p: (to_dev(p[0], dev), to_dev(p[1], dev))
+    y_pre, y = nlc.residual_unit(to_dev(x, dev), dv(pairs[0]), to_dev(nlc.tap_major_weight(w1), dev), to_dev(b1, dev),
+                                 dv(pairs[1]), to_dev(nlc.tap_major_weight(w2), dev), to_dev(b2, dev), k=k,
+                                 dilation=dil, snake_out=dv(pairs[2]) if out_snake else None, want_pre=True)
+    tap = lambda w: oracle.tap_weight_f32(synth.from_f16_bits(w)).astype(np.float16).view(np.uint16)
+    h = oracle.conv1d_nlc_f16(x, tap(w1), b1, dil, snake=pairs[0])
+    h2 = oracle.snake_nlc_f16(h, *pairs[1])
+    want = oracle.conv1d_nlc_f16(h2, tap(w2), b2, 1, res_bits=x)
+    got_pre = to_host(y_pre)
+    _close(got_pre, want)
+    g, w = synth.from_f16_bits(got_pre).astype(np.float64), synth.from_f16_bits(want).astype(np.float64)
+    assert np.sqrt(np.mean((g - w) ** 2)) < 1e-3 * np.sqrt(np.mean(w ** 2))
+    if out_snake:
+        assert f16_ulp_diff(to_host(y), oracle.snake_nlc_f16(got_pre, *pairs[2])) <= 1
+    else:
+        assert np.array_equal(to_host(y), got_pre)
