@@ -23,7 +23,7 @@ namespace {
 typedef ConvArgs ConvParams;
 
 template <typename Cfg, bool SNAKE_IN>
-__global__ __launch_bounds__(Cfg::THREADS, 2) void conv_nlc_f16_mfma(ConvArgs p) {
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(ConvArgs p) {
     constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_BYTES ? Cfg::MAIN_BYTES : Cfg::EPI_BYTES;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
     int lane_idx, m_tile, n_tile;
@@ -89,11 +89,25 @@ hipError_t launch_tiled(const ConvParams &p0, int64_t lanes, hipStream_t stream)
     return hipGetLastError();
 }
 
-template <int KMAX, int HMAX>
-hipError_t launch_by_bn(const ConvParams &p, int64_t lanes, hipStream_t stream) {
-    if (p.cout % 96 == 0) return launch_tiled<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
-    if (p.cout % 64 == 0) return launch_tiled<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
-    return launch_tiled<ConvTile<256, 32, 4, 1, 32, KMAX, HMAX>>(p, lanes, stream);
+template <typename Cfg>
+struct Tile {
+    typedef Cfg type;
+};
+
+// The one place a (taps, halo, cout) class is mapped to its tile: launches and kernel names both
+// go through it. f is called with Tile<Cfg>.
+template <int KMAX, int HMAX, typename F>
+auto with_tile(int cout, F &&f) {
+    if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>{});
+    if (cout % 64 == 0) return f(Tile<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>{});
+    return f(Tile<ConvTile<256, 32, 4, 1, 32, KMAX, HMAX>>{});
+}
+
+template <typename F>
+auto with_tile_k(int kmax, int cout, F &&f) {
+    if (kmax == 1) return with_tile<1, 0>(cout, f);
+    if (kmax == 2) return with_tile<2, 8>(cout, f);
+    return with_tile<7, 64>(cout, f);
 }
 
 }  // namespace
@@ -103,12 +117,12 @@ namespace {
 // Which kernel a descriptor runs on.
 struct Choice {
     const char *path;  // "narrow", "mfma" or "direct"
-    int bn, kmax, hmax;
+    int kmax, hmax;
     bool snake;
 };
 
 Choice choose(const dtts_conv_desc *d) {
-    Choice c{"direct", 0, 0, 0, d->in_alpha != nullptr};
+    Choice c{"direct", 0, 0, d->in_alpha != nullptr};
     if (conv_narrow_eligible(d)) {
         c.path = "narrow";
         return c;
@@ -131,7 +145,6 @@ Choice choose(const dtts_conv_desc *d) {
         return c;
     }
     c.path = "mfma";
-    c.bn = d->cout % 96 == 0 ? 96 : (d->cout % 64 == 0 ? 64 : 32);
     return c;
 }
 
@@ -140,11 +153,13 @@ Choice choose(const dtts_conv_desc *d) {
 const char *conv_path_name(const dtts_conv_desc *d) { return choose(d).path; }
 
 const char *conv_kernel_name(const dtts_conv_desc *d) {
-    static thread_local char buf[64];
+    static thread_local char buf[128];
     const Choice c = choose(d);
     if (std::strcmp(c.path, "mfma") == 0)
-        snprintf(buf, sizeof(buf), "conv_nlc_f16_mfma<dtts::ConvTile<256, %d, 4, 1, 32, %d, %d>, %s>", c.bn, c.kmax,
-                 c.hmax, c.snake ? "true" : "false");
+        with_tile_k(c.kmax, static_cast<int>(d->cout), [&](auto t) {
+            return tile_kernel_name<typename decltype(t)::type>(buf, sizeof(buf), "conv_nlc_f16_mfma",
+                                                                  c.snake ? ", true>" : ", false>");
+        });
     else
         snprintf(buf, sizeof(buf), "conv_nlc_f16_%s", c.path);
     return buf;
@@ -196,12 +211,9 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
-        if (ch.kmax == 1)
-            e = launch_by_bn<1, 0>(p, d->lanes, stream);
-        else if (ch.kmax == 2)
-            e = launch_by_bn<2, 8>(p, d->lanes, stream);
-        else
-            e = launch_by_bn<7, 64>(p, d->lanes, stream);
+        e = with_tile_k(ch.kmax, p.cout, [&](auto t) {
+            return launch_tiled<typename decltype(t)::type>(p, d->lanes, stream);
+        });
     } else {
         const int64_t total = d->lanes * d->len * d->cout;
         conv_nlc_f16_direct<<<grid_for(total, 256, 16), 256, 0, stream>>>(p, total);

@@ -7,35 +7,55 @@
 //      all k taps at row offsets t*dil (the im2col never exists, not even in LDS);
 //   B: w[n0 .. n0+BN, t*cin + c0 .. +KC] for every tap t.
 // Each wave owns (BM/WM) x (BN/WN) on 32x32x16 f16 MFMAs with f32 accumulation. The next chunk
-// is prefetched into registers while the current one computes. Row pitches are padded by 8
-// halves (16 bytes) so the 16-byte fragment reads of consecutive rows hit distinct banks.
+// is prefetched into registers while the current one computes, into a second LDS stage when the
+// tile has two (one barrier per chunk). Row pitches are padded by 8 halves (16 bytes) so the
+// 16-byte fragment reads of consecutive rows hit distinct banks.
 #pragma once
 
 #include "conv.hpp"
 #include "snake.hpp"
 
+// Halves of padding per LDS row of the A window and B tile (a multiple of 8 keeps the rows
+// 16-byte aligned for ds_read_b128).
+#ifndef DTTS_LDS_PAD
+#define DTTS_LDS_PAD 8
+#endif
+
 namespace dtts {
 
-template <int BM_, int BN_, int WM_, int WN_, int KC_, int KMAX_, int HMAX_>
+template <int BM_, int BN_, int WM_, int WN_, int KC_, int KMAX_, int HMAX_, int NBUF_ = 1>
 struct ConvTile {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KC = KC_, KMAX = KMAX_, HMAX = HMAX_;
+    static constexpr int NBUF = NBUF_;  // LDS stages: 2 overlaps staging chunk c+1 with computing chunk c
     static constexpr int THREADS = 64 * WM * WN;
     static constexpr int WTM = BM / WM, WTN = BN / WN;  // per-wave tile
     static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 blocks per wave
-    static constexpr int LDA = KC + 8;                  // LDS pitch (halves) of A and B rows
+    static constexpr int LDA = KC + DTTS_LDS_PAD;       // LDS pitch (halves) of A and B rows
     static constexpr int SEGS = KC / 8;                 // 16-byte segments per row chunk
     static constexpr int A_ROWS = BM + HMAX;
     static constexpr int A_HALVES = A_ROWS * LDA;
     static constexpr int B_HALVES = KMAX * BN * LDA;
-    static constexpr int MAIN_BYTES = (A_HALVES + B_HALVES) * 2;
+    static constexpr int STAGE_HALVES = A_HALVES + B_HALVES;
+    static constexpr int MAIN_BYTES = NBUF * STAGE_HALVES * 2;
     static constexpr int A_SEGS = A_ROWS * SEGS;
     static constexpr int A_PER_T = (A_SEGS + THREADS - 1) / THREADS;
     static constexpr int B_SEGS = KMAX * BN * SEGS;
     static constexpr int B_PER_T = (B_SEGS + THREADS - 1) / THREADS;
     static constexpr int EPI_PITCH = WTN + 4;  // floats, per-wave epilogue tile
     static constexpr int EPI_BYTES = WM * WN * 32 * EPI_PITCH * 4;
+    // workgroups per CU the register budget is sized for (two when two fit in LDS)
+    static constexpr int MIN_WG = (THREADS <= 256 && 2 * MAIN_BYTES <= 160 * 1024) ? 2 : 1;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC % 16 == 0, "tile shape");
 };
+
+// The demangled name of kernel<ConvTile<...>, ...> as profilers print it; `tail` closes the
+// template argument list (", true>", " >").
+template <typename Cfg>
+inline const char *tile_kernel_name(char *buf, size_t n, const char *kernel, const char *tail) {
+    snprintf(buf, n, "%s<dtts::ConvTile<%d, %d, %d, %d, %d, %d, %d, %d>%s", kernel, Cfg::BM, Cfg::BN, Cfg::WM, Cfg::WN,
+             Cfg::KC, Cfg::KMAX, Cfg::HMAX, Cfg::NBUF, tail);
+    return buf;
+}
 
 struct ConvArgs {
     const half_t *x;
@@ -108,7 +128,7 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
             rb[i] = v;
         }
     };
-    auto store_chunk = [&](int c0) {
+    auto store_chunk = [&](int c0, half_t *As, half_t *Bs) {
 #pragma unroll
         for (int i = 0; i < Cfg::A_PER_T; ++i) {
             const int seg = tid + i * Cfg::THREADS;
@@ -140,14 +160,10 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
     const int arow0 = wm * Cfg::WTM + (lane & 31);
     const int bcol0 = wn * Cfg::WTN + (lane & 31);
     const int koff = (lane >> 5) * 8;
-    load_chunk(0);
-    for (int c = 0; c < nchunks; ++c) {
-        store_chunk(c * Cfg::KC);
-        __syncthreads();
-        if (c + 1 < nchunks) load_chunk((c + 1) * Cfg::KC);
+    auto compute = [&](const half_t *A, const half_t *B) {
         for (int t = 0; t < p.k; ++t) {
-            const half_t *at = As + (arow0 + t * p.dil) * Cfg::LDA + koff;
-            const half_t *bt = Bs + (t * Cfg::BN + bcol0) * Cfg::LDA + koff;
+            const half_t *at = A + (arow0 + t * p.dil) * Cfg::LDA + koff;
+            const half_t *bt = B + (t * Cfg::BN + bcol0) * Cfg::LDA + koff;
 #pragma unroll
             for (int kk = 0; kk < Cfg::KC; kk += 16) {
                 half8_t af[Cfg::TM], bf[Cfg::TN];
@@ -162,7 +178,30 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
+    };
+    load_chunk(0);
+    if constexpr (Cfg::NBUF == 1) {
+        for (int c = 0; c < nchunks; ++c) {
+            store_chunk(c * Cfg::KC, As, Bs);
+            __syncthreads();
+            if (c + 1 < nchunks) load_chunk((c + 1) * Cfg::KC);
+            compute(As, Bs);
+            __syncthreads();
+        }
+    } else {
+        // stage c+1 is written while stage c is read; the one barrier per chunk also guarantees
+        // that the stage being overwritten was finished by every wave one chunk ago
+        store_chunk(0, As, Bs);
         __syncthreads();
+        for (int c = 0; c < nchunks; ++c) {
+            const int cur = c & 1;
+            half_t *Ac = As + cur * Cfg::STAGE_HALVES;
+            half_t *Bc = Bs + cur * Cfg::STAGE_HALVES;
+            if (c + 1 < nchunks) load_chunk((c + 1) * Cfg::KC);
+            compute(Ac, Bc);
+            if (c + 1 < nchunks) store_chunk((c + 1) * Cfg::KC, As + (cur ^ 1) * Cfg::STAGE_HALVES, Bs + (cur ^ 1) * Cfg::STAGE_HALVES);
+            __syncthreads();
+        }
     }
 }
 

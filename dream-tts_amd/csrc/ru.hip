@@ -26,7 +26,7 @@ struct RuArgs {
 };
 
 template <typename Cfg>
-__global__ __launch_bounds__(Cfg::THREADS, 2) void ru_nlc_f16(RuArgs q) {
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q) {
     constexpr int C = Cfg::BN;
     constexpr int HP = C + 8;  // h2 row pitch (halves)
     constexpr int H_BYTES = Cfg::BM * HP * 2;
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 2) void ru_nlc_f16(RuArgs q) {
 }
 
 typedef ConvTile<256, 96, 4, 1, 32, 7, 64> RuTile96;
-typedef ConvTile<128, 192, 2, 2, 16, 7, 64> RuTile192;
+typedef ConvTile<256, 192, 4, 2, 16, 7, 64, 2> RuTile192;
 
 template <typename Cfg>
 hipError_t launch_ru(RuArgs q, int64_t lanes, hipStream_t stream) {
@@ -120,8 +120,9 @@ bool residual_unit_supported(const dtts_ru_desc *d) {
 }
 
 const char *residual_unit_kernel_name(const dtts_ru_desc *d) {
-    return d->channels == 96 ? "ru_nlc_f16<dtts::ConvTile<256, 96, 4, 1, 32, 7, 64> >"
-                             : "ru_nlc_f16<dtts::ConvTile<128, 192, 2, 2, 16, 7, 64> >";
+    static thread_local char buf[128];
+    return d->channels == 96 ? tile_kernel_name<RuTile96>(buf, sizeof(buf), "ru_nlc_f16", " >")
+                             : tile_kernel_name<RuTile192>(buf, sizeof(buf), "ru_nlc_f16", " >");
 }
 
 int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream) {
