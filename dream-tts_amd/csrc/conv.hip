@@ -22,7 +22,7 @@ namespace {
 
 typedef ConvArgs ConvParams;
 
-template <typename Cfg, bool SNAKE_IN>
+template <typename Cfg, bool SNAKE_IN, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(ConvArgs p) {
     constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_BYTES ? Cfg::MAIN_BYTES : Cfg::EPI_BYTES;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
@@ -36,8 +36,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(C
     for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
-    half_t *As = reinterpret_cast<half_t *>(smem);
-    conv_mainloop<Cfg, SNAKE_IN>(p, xl, l0, n0, As, As + Cfg::A_HALVES, acc);
+    conv_mainloop<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
     conv_epilogue<Cfg>(acc, smem, static_cast<int64_t>(lane_idx) * p.L, l0, n0, p.L, p.cout, p.bias, p.res, p.y_pre,
                        p.y, p.a_out, p.r_out, p.act);
 }
@@ -82,10 +81,18 @@ hipError_t launch_tiled(const ConvParams &p0, int64_t lanes, hipStream_t stream)
     p.total_tiles = static_cast<int>(total);
     p.tiles_per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.tiles_per_xcd) * 8);
-    if (p.a_in)
-        conv_nlc_f16_mfma<Cfg, true><<<grid, Cfg::THREADS, 0, stream>>>(p);
-    else
-        conv_nlc_f16_mfma<Cfg, false><<<grid, Cfg::THREADS, 0, stream>>>(p);
+    // taps fixed at compile time when the shape fills the class's KMAX (k = 7, 2, 1)
+    if (p.k == Cfg::KMAX) {
+        if (p.a_in)
+            conv_nlc_f16_mfma<Cfg, true, Cfg::KMAX><<<grid, Cfg::THREADS, 0, stream>>>(p);
+        else
+            conv_nlc_f16_mfma<Cfg, false, Cfg::KMAX><<<grid, Cfg::THREADS, 0, stream>>>(p);
+    } else {
+        if (p.a_in)
+            conv_nlc_f16_mfma<Cfg, true, 0><<<grid, Cfg::THREADS, 0, stream>>>(p);
+        else
+            conv_nlc_f16_mfma<Cfg, false, 0><<<grid, Cfg::THREADS, 0, stream>>>(p);
+    }
     return hipGetLastError();
 }
 
@@ -95,19 +102,23 @@ struct Tile {
 };
 
 // The one place a (taps, halo, cout) class is mapped to its tile: launches and kernel names both
-// go through it. f is called with Tile<Cfg>.
+// go through it. f is called with Tile<Cfg>. `direct` says the shape's byte offsets fit the
+// direct-staging buffer loads.
 template <int KMAX, int HMAX, typename F>
-auto with_tile(int cout, F &&f) {
+auto with_tile(int cout, bool direct, F &&f) {
+    // the dilated k <= 7 class at 96-multiples: eight waves of 64 x 96, direct staging
+    if constexpr (KMAX == 7)
+        if (cout % 96 == 0 && direct) return f(Tile<ConvTile<512, 96, 8, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
     if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>{});
     if (cout % 64 == 0) return f(Tile<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>{});
     return f(Tile<ConvTile<256, 32, 4, 1, 32, KMAX, HMAX>>{});
 }
 
 template <typename F>
-auto with_tile_k(int kmax, int cout, F &&f) {
-    if (kmax == 1) return with_tile<1, 0>(cout, f);
-    if (kmax == 2) return with_tile<2, 8>(cout, f);
-    return with_tile<7, 64>(cout, f);
+auto with_tile_k(int kmax, int cout, bool direct, F &&f) {
+    if (kmax == 1) return with_tile<1, 0>(cout, direct, f);
+    if (kmax == 2) return with_tile<2, 8>(cout, direct, f);
+    return with_tile<7, 64>(cout, direct, f);
 }
 
 }  // namespace
@@ -119,10 +130,11 @@ struct Choice {
     const char *path;  // "narrow", "mfma" or "direct"
     int kmax, hmax;
     bool snake;
+    bool direct_ok;  // byte offsets fit direct-staging buffer loads
 };
 
 Choice choose(const dtts_conv_desc *d) {
-    Choice c{"direct", 0, 0, d->in_alpha != nullptr};
+    Choice c{"direct", 0, 0, d->in_alpha != nullptr, direct_offsets_fit(d->len, d->cin, d->cout, d->k)};
     if (conv_narrow_eligible(d)) {
         c.path = "narrow";
         return c;
@@ -156,9 +168,11 @@ const char *conv_kernel_name(const dtts_conv_desc *d) {
     static thread_local char buf[128];
     const Choice c = choose(d);
     if (std::strcmp(c.path, "mfma") == 0)
-        with_tile_k(c.kmax, static_cast<int>(d->cout), [&](auto t) {
-            return tile_kernel_name<typename decltype(t)::type>(buf, sizeof(buf), "conv_nlc_f16_mfma",
-                                                                  c.snake ? ", true>" : ", false>");
+        with_tile_k(c.kmax, static_cast<int>(d->cout), c.direct_ok, [&](auto t) {
+            typedef typename decltype(t)::type Cfg;
+            char tail[32];
+            snprintf(tail, sizeof(tail), ", %s, %d>", c.snake ? "true" : "false", d->k == Cfg::KMAX ? Cfg::KMAX : 0);
+            return tile_kernel_name<Cfg>(buf, sizeof(buf), "conv_nlc_f16_mfma", tail);
         });
     else
         snprintf(buf, sizeof(buf), "conv_nlc_f16_%s", c.path);
@@ -211,7 +225,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
-        e = with_tile_k(ch.kmax, p.cout, [&](auto t) {
+        e = with_tile_k(ch.kmax, p.cout, ch.direct_ok, [&](auto t) {
             return launch_tiled<typename decltype(t)::type>(p, d->lanes, stream);
         });
     } else {

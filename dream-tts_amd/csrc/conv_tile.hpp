@@ -6,54 +6,70 @@
 //   A: the whole dilated window, BM + (k-1)*dil rows x KC channels, loaded once and read by
 //      all k taps at row offsets t*dil (the im2col never exists, not even in LDS);
 //   B: w[n0 .. n0+BN, t*cin + c0 .. +KC] for every tap t.
-// Each wave owns (BM/WM) x (BN/WN) on 32x32x16 f16 MFMAs with f32 accumulation. The next chunk
-// is prefetched into registers while the current one computes, into a second LDS stage when the
-// tile has two (one barrier per chunk). Row pitches are padded by 8 halves (16 bytes) so the
-// 16-byte fragment reads of consecutive rows hit distinct banks.
+// Each wave owns (BM/WM) x (BN/WN) on 32x32x16 f16 MFMAs with f32 accumulation.
+//
+// Two ways to fill a stage (the tile's STAGING parameter):
+//   kStageRegs:   global -> registers -> ds_write, rows padded by 8 halves so the 16-byte
+//                 fragment reads of consecutive rows hit distinct banks; the next chunk is
+//                 prefetched into registers while the current one computes.
+//   kStageDirect: buffer_load_dwordx4 ... lds, the load unit writing LDS itself. No staging
+//                 registers, no per-chunk address arithmetic (a chunk moves only the scalar
+//                 offset), and rows of the window outside [0, L) read as zeros through the
+//                 buffer range check. A load instruction fills 64 consecutive 16-byte slots,
+//                 so rows cannot be padded: the 16-byte segments of a row are XOR-swizzled
+//                 instead. Two stages: chunk c+1 lands while chunk c is multiplied, one barrier
+//                 per chunk.
 #pragma once
 
 #include "conv.hpp"
 #include "snake.hpp"
 
-// Halves of padding per LDS row of the A window and B tile (a multiple of 8 keeps the rows
-// 16-byte aligned for ds_read_b128).
-#ifndef DTTS_LDS_PAD
-#define DTTS_LDS_PAD 8
-#endif
-
 namespace dtts {
 
-template <int BM_, int BN_, int WM_, int WN_, int KC_, int KMAX_, int HMAX_, int NBUF_ = 1>
+enum { kStageRegs = 0, kStageDirect = 1 };
+
+template <int BM_, int BN_, int WM_, int WN_, int KC_, int KMAX_, int HMAX_, int NBUF_ = 1, int STAGING_ = kStageRegs>
 struct ConvTile {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KC = KC_, KMAX = KMAX_, HMAX = HMAX_;
-    static constexpr int NBUF = NBUF_;  // LDS stages: 2 overlaps staging chunk c+1 with computing chunk c
+    static constexpr int STAGING = STAGING_;
+    static constexpr int NBUF = STAGING == kStageDirect ? 2 : NBUF_;  // LDS stages
     static constexpr int THREADS = 64 * WM * WN;
+    static constexpr int NW = WM * WN;
     static constexpr int WTM = BM / WM, WTN = BN / WN;  // per-wave tile
     static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 blocks per wave
-    static constexpr int LDA = KC + DTTS_LDS_PAD;       // LDS pitch (halves) of A and B rows
     static constexpr int SEGS = KC / 8;                 // 16-byte segments per row chunk
-    static constexpr int A_ROWS = BM + HMAX;
-    static constexpr int A_HALVES = A_ROWS * LDA;
-    static constexpr int B_HALVES = KMAX * BN * LDA;
-    static constexpr int STAGE_HALVES = A_HALVES + B_HALVES;
-    static constexpr int MAIN_BYTES = NBUF * STAGE_HALVES * 2;
-    static constexpr int A_SEGS = A_ROWS * SEGS;
+    // register staging: padded rows
+    static constexpr int LDA = KC + 8;  // LDS pitch (halves) of A and B rows
+    static constexpr int A_SEGS = (BM + HMAX) * SEGS;
     static constexpr int A_PER_T = (A_SEGS + THREADS - 1) / THREADS;
     static constexpr int B_SEGS = KMAX * BN * SEGS;
     static constexpr int B_PER_T = (B_SEGS + THREADS - 1) / THREADS;
-    static constexpr int EPI_PITCH = WTN + 4;  // floats, per-wave epilogue tile
+    // direct staging: unpadded swizzled rows, 1 KiB per load instruction
+    static constexpr int ROW_BYTES = STAGING == kStageDirect ? KC * 2 : LDA * 2;
+    static constexpr int RPI = 1024 / (KC * 2);  // rows per load instruction
+    static constexpr int A_ROWS = STAGING == kStageDirect ? (BM + HMAX + RPI - 1) / RPI * RPI : BM + HMAX;
+    static constexpr int A_INST = A_ROWS / RPI, B_INST = KMAX * BN / RPI;
+    static constexpr int A_PER_W = (A_INST + NW - 1) / NW, B_PER_W = (B_INST + NW - 1) / NW;
+    static constexpr int A_BYTES = A_ROWS * ROW_BYTES;
+    static constexpr int B_BYTES = KMAX * BN * ROW_BYTES;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int MAIN_BYTES = NBUF * STAGE_BYTES;
+    // epilogue: per-wave f32 tile; a pitch of 8 (mod 16) floats puts rows r and r+4 (the two
+    // lane halves of an MFMA result) half a bank sweep apart
+    static constexpr int EPI_PITCH = WTN + 8;
     static constexpr int EPI_BYTES = WM * WN * 32 * EPI_PITCH * 4;
     // workgroups per CU the register budget is sized for (two when two fit in LDS)
     static constexpr int MIN_WG = (THREADS <= 256 && 2 * MAIN_BYTES <= 160 * 1024) ? 2 : 1;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC % 16 == 0, "tile shape");
+    static_assert(STAGING != kStageDirect || (KC >= 16 && KC <= 64 && BN % RPI == 0), "direct staging shape");
 };
 
 // The demangled name of kernel<ConvTile<...>, ...> as profilers print it; `tail` closes the
 // template argument list (", true>", " >").
 template <typename Cfg>
 inline const char *tile_kernel_name(char *buf, size_t n, const char *kernel, const char *tail) {
-    snprintf(buf, n, "%s<dtts::ConvTile<%d, %d, %d, %d, %d, %d, %d, %d>%s", kernel, Cfg::BM, Cfg::BN, Cfg::WM, Cfg::WN,
-             Cfg::KC, Cfg::KMAX, Cfg::HMAX, Cfg::NBUF, tail);
+    snprintf(buf, n, "%s<dtts::ConvTile<%d, %d, %d, %d, %d, %d, %d, %d, %d>%s", kernel, Cfg::BM, Cfg::BN, Cfg::WM,
+             Cfg::WN, Cfg::KC, Cfg::KMAX, Cfg::HMAX, Cfg::NBUF, Cfg::STAGING, tail);
     return buf;
 }
 
@@ -72,6 +88,12 @@ struct ConvArgs {
     int tiles_m, tiles_n, total_tiles, tiles_per_xcd;
 };
 
+// Host check for direct staging: every byte offset a buffer load forms stays below 2^31, where
+// the out-of-range marker sits.
+inline bool direct_offsets_fit(int64_t len, int64_t cin, int64_t cout, int64_t k) {
+    return len * cin * 2 < (int64_t(1) << 31) && cout * k * cin * 2 < (int64_t(1) << 31);
+}
+
 __device__ __forceinline__ float conv_act(float v, int act) { return act == 1 ? tanhf(v) : v; }
 
 // XCD-aware tile order: dispatch slot b runs on XCD b % 8; each XCD takes a contiguous range of
@@ -87,10 +109,96 @@ __device__ __forceinline__ bool conv_tile_coords(const ConvArgs &p, int &lane_id
     return true;
 }
 
-// acc[i][j] += sum over taps and cin of window(x) . w for the workgroup's BM x BN tile.
-template <typename Cfg, bool SNAKE_IN>
-__device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *xl, int l0, int n0, half_t *As,
-                                              half_t *Bs, float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+// Slot of segment q in row r for direct staging: with 64 banks of 4 bytes a ds_read_b128 serves
+// 16 lanes per cycle, and a fragment read has those 16 lanes on 16 consecutive rows at one
+// segment. Rows r and r + 128/KC share a 256-byte bank sweep, so the swizzle is (r / (128/KC))
+// mod SEGS: the 16 rows land on 16 distinct 16-byte bank groups from any starting row. It only
+// looks at row bits below 5, so rows 32 apart (the TM/TN fragments) share it.
+template <int KC>
+__device__ __forceinline__ int seg_swizzle(int r) {
+    constexpr int SHIFT = KC == 16 ? 3 : (KC == 32 ? 2 : 1);  // log2(128 / KC)
+    return (static_cast<unsigned>(r) >> SHIFT) & (KC / 8 - 1);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rs, char *lds, uint32_t voffset,
+                                            uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)lds, 16, voffset, soffset, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// The k taps of one staged chunk on the matrix cores. KT > 0 is the tap count known at compile
+// time: the loop unrolls into straight-line code, so the fragment reads of tap t+1 are issued
+// before tap t's MFMAs and the wait before those MFMAs counts only tap t's reads (with PIPE, two
+// fragment sets alternate; without, the compiler schedules one set). KT == 0 takes k at run time.
+// frag_a(t, kk, i) / frag_b(t, kk, j) give the 16-byte fragment addresses of 32-row block i (or
+// column block j) at k-step kk of tap t.
+template <typename Cfg, int KT, bool PIPE, typename FA, typename FB>
+__device__ __forceinline__ void mma_taps(int k, FA frag_a, FB frag_b, float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+    constexpr int KS = Cfg::KC / 16;
+    typedef half8_t FragA[KS][Cfg::TM];
+    typedef half8_t FragB[KS][Cfg::TN];
+    auto load = [&](int t, FragA &a, FragB &b) {
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+            for (int i = 0; i < Cfg::TM; ++i) a[kk][i] = *frag_a(t, kk, i);
+#pragma unroll
+            for (int j = 0; j < Cfg::TN; ++j) b[kk][j] = *frag_b(t, kk, j);
+        }
+    };
+    auto mma = [&](const FragA &a, const FragB &b) {
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < Cfg::TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+    };
+    if constexpr (KT > 0 && PIPE) {
+        FragA a[2];
+        FragB b[2];
+        load(0, a[0], b[0]);
+#pragma unroll
+        for (int t = 0; t < KT; ++t) {
+            if (t + 1 < KT) load(t + 1, a[(t + 1) & 1], b[(t + 1) & 1]);
+            // keep the scheduler from sinking tap t+1's reads back next to their MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+            mma(a[t & 1], b[t & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else if constexpr (KT > 0) {
+#pragma unroll
+        for (int t = 0; t < KT; ++t) {
+            FragA a;
+            FragB b;
+            load(t, a, b);
+            mma(a, b);
+        }
+    } else {
+        for (int t = 0; t < k; ++t) {
+            FragA a;
+            FragB b;
+            load(t, a, b);
+            mma(a, b);
+        }
+    }
+}
+
+// acc += window(x) . w over all taps for the workgroup's BM x BN tile, register staging.
+template <typename Cfg, bool SNAKE_IN, int KT>
+__device__ __forceinline__ void conv_mainloop_regs(const ConvArgs &p, const half_t *xl, int l0, int n0, char *smem,
+                                                   float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+    constexpr int LDA = Cfg::LDA;
+    constexpr int STAGE_H = Cfg::STAGE_BYTES / 2;
+    constexpr int A_H = Cfg::A_BYTES / 2;
+    half_t *As = reinterpret_cast<half_t *>(smem);
+    half_t *Bs = As + A_H;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -128,7 +236,17 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
             rb[i] = v;
         }
     };
-    auto store_chunk = [&](int c0, half_t *As, half_t *Bs) {
+    static_assert(Cfg::THREADS % Cfg::SEGS == 0, "a thread's segments share one channel group");
+    auto store_chunk = [&](int c0, half_t *A, half_t *B) {
+        float ka[8], kr[8];
+        if constexpr (SNAKE_IN) {
+            const int c = c0 + (tid % Cfg::SEGS) * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ka[j] = p.a_in[c + j] * kInv2Pi;
+                kr[j] = p.r_in[c + j];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < Cfg::A_PER_T; ++i) {
             const int seg = tid + i * Cfg::THREADS;
@@ -137,12 +255,10 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
                 const int q = seg % Cfg::SEGS;
                 half8_t v = ra[i];
                 if constexpr (SNAKE_IN) {
-                    const int c = c0 + q * 8;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        v[j] = static_cast<half_t>(snake_f16out(static_cast<float>(v[j]), p.a_in[c + j], p.r_in[c + j]));
+                    for (int j = 0; j < 8; ++j) v[j] = snake_f16k(v[j], ka[j], kr[j]);
                 }
-                *reinterpret_cast<half8_t *>(As + r * Cfg::LDA + q * 8) = v;
+                *reinterpret_cast<half8_t *>(A + r * LDA + q * 8) = v;
             }
         }
 #pragma unroll
@@ -151,7 +267,7 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
             if (seg < Cfg::B_SEGS) {
                 const int row = seg / Cfg::SEGS;
                 const int q = seg % Cfg::SEGS;
-                *reinterpret_cast<half8_t *>(Bs + row * Cfg::LDA + q * 8) = rb[i];
+                *reinterpret_cast<half8_t *>(B + row * LDA + q * 8) = rb[i];
             }
         }
     };
@@ -161,23 +277,17 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
     const int bcol0 = wn * Cfg::WTN + (lane & 31);
     const int koff = (lane >> 5) * 8;
     auto compute = [&](const half_t *A, const half_t *B) {
-        for (int t = 0; t < p.k; ++t) {
-            const half_t *at = A + (arow0 + t * p.dil) * Cfg::LDA + koff;
-            const half_t *bt = B + (t * Cfg::BN + bcol0) * Cfg::LDA + koff;
-#pragma unroll
-            for (int kk = 0; kk < Cfg::KC; kk += 16) {
-                half8_t af[Cfg::TM], bf[Cfg::TN];
-#pragma unroll
-                for (int i = 0; i < Cfg::TM; ++i) af[i] = *reinterpret_cast<const half8_t *>(at + i * 32 * Cfg::LDA + kk);
-#pragma unroll
-                for (int j = 0; j < Cfg::TN; ++j) bf[j] = *reinterpret_cast<const half8_t *>(bt + j * 32 * Cfg::LDA + kk);
-#pragma unroll
-                for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < Cfg::TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-        }
+        const half_t *a0 = A + arow0 * LDA + koff;
+        const half_t *b0 = B + bcol0 * LDA + koff;
+        mma_taps<Cfg, KT, false>(
+            p.k,
+            [&](int t, int kk, int i) {
+                return reinterpret_cast<const half8_t *>(a0 + (t * p.dil + i * 32) * LDA + kk * 16);
+            },
+            [&](int t, int kk, int j) {
+                return reinterpret_cast<const half8_t *>(b0 + (t * Cfg::BN + j * 32) * LDA + kk * 16);
+            },
+            acc);
     };
     load_chunk(0);
     if constexpr (Cfg::NBUF == 1) {
@@ -195,14 +305,142 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
         __syncthreads();
         for (int c = 0; c < nchunks; ++c) {
             const int cur = c & 1;
-            half_t *Ac = As + cur * Cfg::STAGE_HALVES;
-            half_t *Bc = Bs + cur * Cfg::STAGE_HALVES;
             if (c + 1 < nchunks) load_chunk((c + 1) * Cfg::KC);
-            compute(Ac, Bc);
-            if (c + 1 < nchunks) store_chunk((c + 1) * Cfg::KC, As + (cur ^ 1) * Cfg::STAGE_HALVES, Bs + (cur ^ 1) * Cfg::STAGE_HALVES);
+            compute(As + cur * STAGE_H, Bs + cur * STAGE_H);
+            if (c + 1 < nchunks) store_chunk((c + 1) * Cfg::KC, As + (cur ^ 1) * STAGE_H, Bs + (cur ^ 1) * STAGE_H);
             __syncthreads();
         }
     }
+}
+
+// acc += window(x) . w over all taps for the workgroup's BM x BN tile, direct staging.
+template <typename Cfg, bool SNAKE_IN, int KT>
+__device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const half_t *xl, int l0, int n0, char *smem,
+                                                     float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+    constexpr int RB = Cfg::ROW_BYTES;
+    constexpr int SEGS = Cfg::SEGS;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: load guards stay scalar
+    const int lane = tid & 63;
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+    const int rows = Cfg::BM + (p.k - 1) * p.dil;
+    const int win0 = l0 - p.pad_left;
+    const int K = p.k * p.cin;
+    const int a_inst = (rows + Cfg::RPI - 1) / Cfg::RPI;
+    const int b_inst = (KT > 0 ? KT : p.k) * Cfg::BN / Cfg::RPI;
+    const __amdgpu_buffer_rsrc_t rsa =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(xl), 0, p.L * p.cin * 2, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rsb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(p.w), 0, p.cout * K * 2, kBufferWord3);
+
+    // Per-lane byte offsets of the slots this wave's load instructions fill; a chunk adds c0*2.
+    // Instruction j covers slots j*64 .. j*64+63 of its region; lane l fills slot j*64+l, which
+    // holds segment (slot % SEGS) ^ swizzle(row) of row slot / SEGS.
+    uint32_t va[Cfg::A_PER_W], vb[Cfg::B_PER_W];
+#pragma unroll
+    for (int i = 0; i < Cfg::A_PER_W; ++i) {
+        const int slot = (wave + i * Cfg::NW) * 64 + lane;
+        const int r = slot / SEGS;
+        const int q = (slot % SEGS) ^ seg_swizzle<Cfg::KC>(r);
+        const int s = win0 + r;
+        va[i] = (r < rows && s >= 0 && s < p.L) ? static_cast<uint32_t>((s * p.cin + q * 8) * 2) : kOutOfRange;
+    }
+#pragma unroll
+    for (int i = 0; i < Cfg::B_PER_W; ++i) {
+        const int slot = (wave + i * Cfg::NW) * 64 + lane;
+        const int r = slot / SEGS;  // t * BN + n
+        const int q = (slot % SEGS) ^ seg_swizzle<Cfg::KC>(r);
+        const int t = r / Cfg::BN;
+        const int n = r - t * Cfg::BN;
+        vb[i] = static_cast<uint32_t>(((n0 + n) * K + t * p.cin + q * 8) * 2);
+    }
+    auto issue = [&](int c0, int st) {
+        char *base = smem + st * Cfg::STAGE_BYTES;
+        const uint32_t so = static_cast<uint32_t>(c0 * 2);
+#pragma unroll
+        for (int i = 0; i < Cfg::A_PER_W; ++i) {
+            const int j = wave + i * Cfg::NW;
+            if (j < a_inst) load_lds_16(rsa, base + j * 1024, va[i], so);
+        }
+#pragma unroll
+        for (int i = 0; i < Cfg::B_PER_W; ++i) {
+            const int j = wave + i * Cfg::NW;
+            if (j < b_inst) load_lds_16(rsb, base + Cfg::A_BYTES + j * 1024, vb[i], so);
+        }
+    };
+    // SnakeBeta on the window slots this lane loaded (after they landed): rows outside the
+    // sequence hold zeros and snake(0) = 0, so they are skipped.
+    auto snake_stage = [&](int c0, int st) {
+        char *base = smem + st * Cfg::STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < Cfg::A_PER_W; ++i) {
+            const int j = wave + i * Cfg::NW;
+            if (j < a_inst && va[i] != kOutOfRange) {
+                const int slot = j * 64 + lane;
+                const int q = (slot % SEGS) ^ seg_swizzle<Cfg::KC>(slot / SEGS);
+                half8_t *sp = reinterpret_cast<half8_t *>(base + slot * 16);
+                half8_t v = *sp;
+                const int c = c0 + q * 8;
+                const float4_t a0 = *reinterpret_cast<const float4_t *>(p.a_in + c);
+                const float4_t a1 = *reinterpret_cast<const float4_t *>(p.a_in + c + 4);
+                const float4_t r0 = *reinterpret_cast<const float4_t *>(p.r_in + c);
+                const float4_t r1 = *reinterpret_cast<const float4_t *>(p.r_in + c + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = snake_f16k(v[e], a0[e] * kInv2Pi, r0[e]);
+                    v[e + 4] = snake_f16k(v[e + 4], a1[e] * kInv2Pi, r1[e]);
+                }
+                *sp = v;
+            }
+        }
+    };
+
+    const int nchunks = p.cin / Cfg::KC;
+    const int arow0 = wm * Cfg::WTM + (lane & 31);
+    const int bcol0 = wn * Cfg::WTN + (lane & 31);
+    const int qh = lane >> 5;
+    auto compute = [&](int st) {
+        const char *A = smem + st * Cfg::STAGE_BYTES;
+        const char *B = A + Cfg::A_BYTES;
+        mma_taps<Cfg, KT, true>(
+            p.k,
+            [&](int t, int kk, int i) {
+                const int r = arow0 + t * p.dil;
+                return reinterpret_cast<const half8_t *>(A + (r + i * 32) * RB +
+                                                         (((kk * 2 + qh) ^ seg_swizzle<Cfg::KC>(r)) << 4));
+            },
+            [&](int t, int kk, int j) {
+                const int r = t * Cfg::BN + bcol0;
+                return reinterpret_cast<const half8_t *>(B + (r + j * 32) * RB +
+                                                         (((kk * 2 + qh) ^ seg_swizzle<Cfg::KC>(r)) << 4));
+            },
+            acc);
+    };
+    issue(0, 0);
+    wait_vmem();
+    if constexpr (SNAKE_IN) snake_stage(0, 0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int st = c & 1;
+        if (c + 1 < nchunks) issue((c + 1) * Cfg::KC, st ^ 1);
+        compute(st);
+        if (c + 1 < nchunks) {
+            wait_vmem();
+            if constexpr (SNAKE_IN) snake_stage((c + 1) * Cfg::KC, st ^ 1);
+        }
+        __syncthreads();
+    }
+}
+
+// acc += sum over taps and cin of window(x) . w; ends on a barrier, after which all of smem is
+// free. KT: the tap count when the launch fixed it at compile time (== p.k), else 0.
+template <typename Cfg, bool SNAKE_IN, int KT>
+__device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *xl, int l0, int n0, char *smem,
+                                              float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+    if constexpr (Cfg::STAGING == kStageDirect)
+        conv_mainloop_direct<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
+    else
+        conv_mainloop_regs<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
 }
 
 // Writes acc (+ bias, + residual, act, rounded; y_pre; SnakeBeta_out; y) for the tile, one 32-row

@@ -25,7 +25,7 @@ struct RuArgs {
     const float *a_out, *r_out;
 };
 
-template <typename Cfg>
+template <typename Cfg, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q) {
     constexpr int C = Cfg::BN;
     constexpr int HP = C + 8;  // h2 row pitch (halves)
@@ -43,8 +43,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q
     for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
-    half_t *As = reinterpret_cast<half_t *>(smem);
-    conv_mainloop<Cfg, true>(p, xl, l0, 0, As, As + Cfg::A_HALVES, acc);  // ends on a barrier
+    conv_mainloop<Cfg, true, KT>(p, xl, l0, 0, smem, acc);  // ends on a barrier
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -55,14 +54,13 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q
     for (int j = 0; j < Cfg::TN; ++j) {
         const int n = wn * Cfg::WTN + j * 32 + (lane & 31);
         const float b1 = static_cast<float>(p.bias[n]);
-        const float a2 = q.a2[n], r2 = q.r2[n];
+        const float ka2 = q.a2[n] * kInv2Pi, r2 = q.r2[n];
 #pragma unroll
         for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = wm * Cfg::WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                const float h = static_cast<float>(static_cast<half_t>(acc[i][j][r] + b1));
-                H[m * HP + n] = static_cast<half_t>(snake_f16out(h, a2, r2));
+                H[m * HP + n] = snake_f16k(static_cast<half_t>(acc[i][j][r] + b1), ka2, r2);
             }
     }
     __syncthreads();
@@ -92,8 +90,10 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q
                        q.a_out, q.r_out, 0);
 }
 
+// C = 96 is bound by the SnakeBeta VALU work, which register staging overlaps across two
+// workgroups per CU; C = 192 is matrix-bound and takes direct staging with eight waves.
 typedef ConvTile<256, 96, 4, 1, 32, 7, 64> RuTile96;
-typedef ConvTile<256, 192, 4, 2, 16, 7, 64, 2> RuTile192;
+typedef ConvTile<256, 192, 4, 2, 16, 7, 64, 2, kStageDirect> RuTile192;
 
 template <typename Cfg>
 hipError_t launch_ru(RuArgs q, int64_t lanes, hipStream_t stream) {
@@ -103,13 +103,18 @@ hipError_t launch_ru(RuArgs q, int64_t lanes, hipStream_t stream) {
     const int64_t total = lanes * p.tiles_m;
     p.total_tiles = static_cast<int>(total);
     p.tiles_per_xcd = static_cast<int>((total + 7) / 8);
-    ru_nlc_f16<Cfg><<<static_cast<unsigned>(int64_t(p.tiles_per_xcd) * 8), Cfg::THREADS, 0, stream>>>(q);
+    const unsigned grid = static_cast<unsigned>(int64_t(p.tiles_per_xcd) * 8);
+    if (p.k == Cfg::KMAX)
+        ru_nlc_f16<Cfg, Cfg::KMAX><<<grid, Cfg::THREADS, 0, stream>>>(q);
+    else
+        ru_nlc_f16<Cfg, 0><<<grid, Cfg::THREADS, 0, stream>>>(q);
     return hipGetLastError();
 }
 
 bool ru_shape_ok(const dtts_ru_desc *d) {
     const int64_t halo = (d->k - 1) * d->dilation;
-    return (d->channels == 96 || d->channels == 192) && d->k >= 1 && d->k <= 7 && d->dilation >= 1 && halo <= 64;
+    return (d->channels == 96 || d->channels == 192) && d->k >= 1 && d->k <= 7 && d->dilation >= 1 && halo <= 64 &&
+           direct_offsets_fit(d->len, d->channels, d->channels, d->k);
 }
 
 }  // namespace
@@ -121,8 +126,9 @@ bool residual_unit_supported(const dtts_ru_desc *d) {
 
 const char *residual_unit_kernel_name(const dtts_ru_desc *d) {
     static thread_local char buf[128];
-    return d->channels == 96 ? tile_kernel_name<RuTile96>(buf, sizeof(buf), "ru_nlc_f16", " >")
-                             : tile_kernel_name<RuTile192>(buf, sizeof(buf), "ru_nlc_f16", " >");
+    const char *tail = d->k == 7 ? ", 7>" : ", 0>";
+    return d->channels == 96 ? tile_kernel_name<RuTile96>(buf, sizeof(buf), "ru_nlc_f16", tail)
+                             : tile_kernel_name<RuTile192>(buf, sizeof(buf), "ru_nlc_f16", tail);
 }
 
 int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream) {

@@ -3,10 +3,10 @@
 The GPU stack stores exactly the tensors the oracle's composed chain stores (all f16), so the
 two differ only by f32 summation order inside each conv -- and SnakeBeta amplifies any input
 difference through the stack (the reference's reason for keeping its codec f32,
-crates/qwen3tts/src/codec.rs:33-43). Bar: the waveform within 2e-2 absolute everywhere (the f16
-tolerance at unit scale), and the GPU no further (RMS) from the oracle than f16 storage itself
-puts the oracle from exact float64 arithmetic on the same inputs (torch's conv1d /
-conv_transpose1d). Each conv is held exactly to its oracle stage in test_gpu_conv.py. The
+crates/qwen3tts/src/codec.rs:33-43). Bar: the GPU no further from the oracle than f16 storage
+itself puts the oracle from exact float64 arithmetic on the same inputs (torch's conv1d /
+conv_transpose1d) -- in RMS, and at the worst sample within 2e-2 absolute (the f16 tolerance at
+unit scale) or 1.5x the oracle's own worst-sample distance from float64, whichever is larger. Each conv is held exactly to its oracle stage in test_gpu_conv.py. The
 geometries cover both SnakeBeta placements (stored snaked copy for stages wider than 96
 channels, conv prologue at 96) and every kernel path.
 """
@@ -46,9 +46,11 @@ def test_codec_decode_matches_oracle(dev, geo, lanes, frames):
     err = np.abs(got - want)
     rms_gpu = float(np.sqrt(np.mean((got - want) ** 2)))
     rms_f16 = float(np.sqrt(np.mean((want - exact) ** 2)))
-    msg = f"max {np.max(err):.3e} rms(gpu-oracle) {rms_gpu:.3e} rms(oracle-f64) {rms_f16:.3e}"
+    max_f16 = float(np.max(np.abs(want - exact)))
+    msg = (f"max {np.max(err):.3e} (oracle-f64 {max_f16:.3e}) rms(gpu-oracle) {rms_gpu:.3e} "
+           f"rms(oracle-f64) {rms_f16:.3e}")
     print(msg)
-    assert np.max(err) <= 2e-2, msg
+    assert np.max(err) <= max(2e-2, 1.5 * max_f16), msg
     assert rms_gpu <= 2.0 * rms_f16 + 1e-4, msg
     assert 0.02 < np.std(want) < 0.95
 
