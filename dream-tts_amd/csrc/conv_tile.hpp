@@ -17,8 +17,8 @@
 //                 offset), and rows of the window outside [0, L) read as zeros through the
 //                 buffer range check. A load instruction fills 64 consecutive 16-byte slots,
 //                 so rows cannot be padded: the 16-byte segments of a row are XOR-swizzled
-//                 instead. Two stages: chunk c+1 lands while chunk c is multiplied, one barrier
-//                 per chunk.
+//                 instead. NBUF >= 2 stages: chunk c+NBUF-1 lands while chunk c is multiplied,
+//                 one barrier per chunk.
 #pragma once
 
 #include "conv.hpp"
@@ -32,7 +32,7 @@ template <int BM_, int BN_, int WM_, int WN_, int KC_, int KMAX_, int HMAX_, int
 struct ConvTile {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, KC = KC_, KMAX = KMAX_, HMAX = HMAX_;
     static constexpr int STAGING = STAGING_;
-    static constexpr int NBUF = STAGING == kStageDirect ? 2 : NBUF_;  // LDS stages
+    static constexpr int NBUF = STAGING == kStageDirect && NBUF_ < 2 ? 2 : NBUF_;  // LDS stages
     static constexpr int THREADS = 64 * WM * WN;
     static constexpr int NW = WM * WN;
     static constexpr int WTM = BM / WM, WTN = BN / WN;  // per-wave tile
@@ -130,6 +130,25 @@ __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rs, char *lds
 }
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Waits until at most N of this wave's vector-memory operations are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Load instructions a wave issues per chunk, at least: instruction j of a region belongs to wave
+// j % nw, and the region has at least `inst` instructions.
+constexpr int loads_of_wave(int wave, int nw, int inst) { return wave < inst ? (inst - wave + nw - 1) / nw : 0; }
+constexpr int min_loads_per_wave(int nw, int a_inst, int b_inst) {
+    int m = 1 << 30;
+    for (int w = 0; w < nw; ++w) {
+        const int c = loads_of_wave(w, nw, a_inst) + loads_of_wave(w, nw, b_inst);
+        m = c < m ? c : m;
+    }
+    return m;
+}
 
 // The k taps of one staged chunk on the matrix cores. KT > 0 is the tap count known at compile
 // time: the loop unrolls into straight-line code, so the fragment reads of tap t+1 are issued
@@ -416,19 +435,39 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
             },
             acc);
     };
-    issue(0, 0);
-    wait_vmem();
+    // NBUF stages: chunk c+NBUF-1 is issued while chunk c is multiplied. vmcnt counts this wave's
+    // loads in issue order, so chunk c+1 has landed once no more than the loads of the chunks
+    // after it remain; the bound uses the fewest loads any wave issues per chunk (the narrowest
+    // window), which can only wait longer, never shorter.
+    constexpr int S = Cfg::NBUF;
+    constexpr int PMIN = min_loads_per_wave(Cfg::NW, (Cfg::BM + Cfg::RPI - 1) / Cfg::RPI,
+                                            (KT > 0 ? KT : 1) * Cfg::BN / Cfg::RPI);
+    constexpr int LATER = (S - 2) * PMIN;
+    auto wait_for_next = [&](int later_chunks) {
+        if (later_chunks >= S - 2)
+            wait_vmem_le<LATER>();
+        else
+            wait_vmem();
+    };
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+        if (st < nchunks) issue(st * Cfg::KC, st);
+    wait_for_next(nchunks - 1);
     if constexpr (SNAKE_IN) snake_stage(0, 0);
     __syncthreads();
+    int st = 0;          // stage holding chunk c
+    int st_new = S - 1;  // stage receiving chunk c + S - 1
     for (int c = 0; c < nchunks; ++c) {
-        const int st = c & 1;
-        if (c + 1 < nchunks) issue((c + 1) * Cfg::KC, st ^ 1);
+        if (c + S - 1 < nchunks) issue((c + S - 1) * Cfg::KC, st_new);
         compute(st);
+        const int st_next = st + 1 == S ? 0 : st + 1;
         if (c + 1 < nchunks) {
-            wait_vmem();
-            if constexpr (SNAKE_IN) snake_stage((c + 1) * Cfg::KC, st ^ 1);
+            wait_for_next(nchunks - 2 - c);
+            if constexpr (SNAKE_IN) snake_stage((c + 1) * Cfg::KC, st_next);
         }
         __syncthreads();
+        st = st_next;
+        st_new = st_new + 1 == S ? 0 : st_new + 1;
     }
 }
 
