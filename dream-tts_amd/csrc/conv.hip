@@ -24,7 +24,7 @@ typedef ConvArgs ConvParams;
 
 template <typename Cfg, bool SNAKE_IN, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(ConvArgs p) {
-    constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_BYTES ? Cfg::MAIN_BYTES : Cfg::EPI_BYTES;
+    constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_TOTAL ? Cfg::MAIN_BYTES : Cfg::EPI_TOTAL;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
     int lane_idx, m_tile, n_tile;
     if (!conv_tile_coords(p, lane_idx, m_tile, n_tile)) return;

@@ -58,6 +58,7 @@ struct ConvTile {
     // lane halves of an MFMA result) half a bank sweep apart
     static constexpr int EPI_PITCH = WTN + 8;
     static constexpr int EPI_BYTES = WM * WN * 32 * EPI_PITCH * 4;
+    static constexpr int EPI_TOTAL = EPI_BYTES + BN * 8;  // + the output SnakeBeta table (a/2pi, r)
     // workgroups per CU the register budget is sized for (two when two fit in LDS)
     static constexpr int MIN_WG = (THREADS <= 256 && 2 * MAIN_BYTES <= 160 * 1024) ? 2 : 1;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC % 16 == 0, "tile shape");
@@ -482,22 +483,56 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
         conv_mainloop_regs<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
 }
 
+// Orders this wave's LDS accesses before and after it (the LDS executes one wave's instructions
+// in issue order, so lanes then see each other's earlier writes; the fence stops the compiler
+// from moving accesses across).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // Writes acc (+ bias, + residual, act, rounded; y_pre; SnakeBeta_out; y) for the tile, one 32-row
 // block per wave at a time through the wave's own LDS region (16-byte coalesced rows). `ld` is the
 // output row length (cout), `n0` the tile's first output channel, `lmax` the lane's length.
+// The block's residual and bias vectors are loaded before the block is staged, so their latency
+// overlaps the staging; the staging region is private to the wave, so only the first block waits
+// for the workgroup (smem may still be read by other waves before that).
 template <typename Cfg>
 __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
                                               int l0, int n0, int lmax, int ld, const half_t *bias, const half_t *res,
                                               half_t *y_pre, half_t *y, const float *a_out, const float *r_out,
                                               int act) {
+    constexpr int CG = Cfg::WTN / 8;     // 8-channel groups per wave row
+    constexpr int NG = 32 * CG / 64;     // groups per lane per 32-row block
+    static_assert((32 * CG) % 64 == 0, "a 32-row block splits evenly over the lanes");
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     float *E = reinterpret_cast<float *>(smem) + wave * 32 * Cfg::EPI_PITCH;
     const int nw = n0 + wn * Cfg::WTN;
+    float *tab = reinterpret_cast<float *>(smem + Cfg::EPI_BYTES);  // [BN] a/2pi, then [BN] r
+    __syncthreads();
+    if (a_out) {
+        for (int c = threadIdx.x; c < Cfg::BN; c += Cfg::THREADS) {
+            tab[c] = a_out[n0 + c] * kInv2Pi;
+            tab[Cfg::BN + c] = r_out[n0 + c];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < Cfg::TM; ++i) {
-        __syncthreads();
+        const int lb = l0 + wm * Cfg::WTM + i * 32;
+        half8_t rr[NG], bb[NG];
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            const int g = lane + 64 * u;
+            const int mr = g / CG, cg = g - (g / CG) * CG;
+            const int n = nw + cg * 8;
+            rr[u] = half8_t{};
+            bb[u] = half8_t{};
+            if (res && lb + mr < lmax) rr[u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + n);
+            if (bias) bb[u] = *reinterpret_cast<const half8_t *>(bias + n);
+        }
+        if (i > 0) wave_lds_order();  // the wave's reads of block i-1 precede these writes
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j)
 #pragma unroll
@@ -505,36 +540,38 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
                 const int mr = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
                 E[mr * Cfg::EPI_PITCH + j * 32 + (lane & 31)] = acc[i][j][r];
             }
-        __syncthreads();
-        constexpr int CG = Cfg::WTN / 8;
-        for (int g = lane; g < 32 * CG; g += 64) {
-            const int mr = g / CG;
-            const int cg = g - mr * CG;
-            const int l = l0 + wm * Cfg::WTM + i * 32 + mr;
+        if (i == 0 && a_out)
+            __syncthreads();  // the snake table is written by the whole workgroup
+        else
+            wave_lds_order();
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            const int g = lane + 64 * u;
+            const int mr = g / CG, cg = g - (g / CG) * CG;
+            const int l = lb + mr;
             if (l >= lmax) continue;
             const int n = nw + cg * 8;
             const float4_t *src = reinterpret_cast<const float4_t *>(E + mr * Cfg::EPI_PITCH + cg * 8);
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            if (bias) {
-                const half8_t bb = *reinterpret_cast<const half8_t *>(bias + n);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) v[q] += static_cast<float>(bb[q]);
-            }
+            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[u][q])) + static_cast<float>(rr[u][q]);
             const int64_t off = (row0 + l) * ld + n;
-            if (res) {
-                const half8_t rr = *reinterpret_cast<const half8_t *>(res + off);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) v[q] += static_cast<float>(rr[q]);
-            }
             half8_t h;
 #pragma unroll
             for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], act));
             if (y_pre) *reinterpret_cast<half8_t *>(y_pre + off) = h;
             if (a_out) {
+                const int c = n - n0;
+                const float4_t ka0 = *reinterpret_cast<const float4_t *>(tab + c);
+                const float4_t ka1 = *reinterpret_cast<const float4_t *>(tab + c + 4);
+                const float4_t kr0 = *reinterpret_cast<const float4_t *>(tab + Cfg::BN + c);
+                const float4_t kr1 = *reinterpret_cast<const float4_t *>(tab + Cfg::BN + c + 4);
 #pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    h[q] = static_cast<half_t>(snake_f16out(static_cast<float>(h[q]), a_out[n + q], r_out[n + q]));
+                for (int q = 0; q < 4; ++q) {
+                    h[q] = snake_f16k(h[q], ka0[q], kr0[q]);
+                    h[q + 4] = snake_f16k(h[q + 4], ka1[q], kr1[q]);
+                }
             }
             *reinterpret_cast<half8_t *>(y + off) = h;
         }

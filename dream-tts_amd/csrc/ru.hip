@@ -30,7 +30,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q
     constexpr int C = Cfg::BN;
     constexpr int HP = C + 8;  // h2 row pitch (halves)
     constexpr int H_BYTES = Cfg::BM * HP * 2;
-    constexpr int LDS0 = Cfg::MAIN_BYTES > Cfg::EPI_BYTES ? Cfg::MAIN_BYTES : Cfg::EPI_BYTES;
+    constexpr int LDS0 = Cfg::MAIN_BYTES > Cfg::EPI_TOTAL ? Cfg::MAIN_BYTES : Cfg::EPI_TOTAL;
     constexpr int LDS = LDS0 > H_BYTES ? LDS0 : H_BYTES;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
     const ConvArgs &p = q.c1;
