@@ -101,11 +101,12 @@ struct Tile {
     typedef Cfg type;
 };
 
-// The one place a (taps, halo, length, cout) class is mapped to its tile: launches and kernel
+// The one place a (taps, halo, length, cin, cout) class is mapped to its tile: launches and kernel
 // names both go through it. f is called with Tile<Cfg>. `direct` says the shape's byte offsets
-// fit the direct-staging buffer loads.
+// fit the direct-staging buffer loads. Every tile needs cin % KC == 0 (the caller guarantees
+// cin % 32 == 0) and cout % BN == 0.
 template <int KMAX, int HMAX, typename F>
-auto with_tile(int len, int cout, bool direct, F &&f) {
+auto with_tile(int len, int cin, int cout, bool direct, F &&f) {
     if (direct) {
         // k <= 7 (dilated) at 96-multiples: eight waves of 64 x 96; short sequences take 256-row
         // tiles (two workgroups per CU) so the last tile of a lane is not mostly padding
@@ -113,12 +114,14 @@ auto with_tile(int len, int cout, bool direct, F &&f) {
             if (cout % 96 == 0 && len >= 1024) return f(Tile<ConvTile<512, 96, 8, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
             if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 16, KMAX, HMAX, 2, kStageDirect>>{});
         }
-        // k = 2 (the transposed convs) and k = 1 at 192-multiples: 256 x 192 over eight waves,
-        // three or four stages in flight (a chunk holds little matrix work at one or two taps)
+        // k = 2 (the transposed convs) and k = 1 at 192-multiples: 256 x 192 over eight waves. A
+        // chunk holds little matrix work at one or two taps, so k = 2 keeps three stages in flight
+        // and k = 1 takes 64-channel chunks (half the barriers per output)
         if constexpr (KMAX == 2)
             if (cout % 192 == 0) return f(Tile<ConvTile<256, 192, 4, 2, 32, KMAX, HMAX, 3, kStageDirect>>{});
         if constexpr (KMAX == 1)
-            if (cout % 192 == 0) return f(Tile<ConvTile<256, 192, 4, 2, 32, KMAX, HMAX, 4, kStageDirect>>{});
+            if (cout % 192 == 0 && cin % 64 == 0)
+                return f(Tile<ConvTile<256, 192, 4, 2, 64, KMAX, HMAX, 2, kStageDirect>>{});
     }
     if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>{});
     if (cout % 64 == 0) return f(Tile<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>{});
@@ -126,10 +129,10 @@ auto with_tile(int len, int cout, bool direct, F &&f) {
 }
 
 template <typename F>
-auto with_tile_k(int kmax, int len, int cout, bool direct, F &&f) {
-    if (kmax == 1) return with_tile<1, 0>(len, cout, direct, f);
-    if (kmax == 2) return with_tile<2, 8>(len, cout, direct, f);
-    return with_tile<7, 64>(len, cout, direct, f);
+auto with_tile_k(int kmax, int len, int cin, int cout, bool direct, F &&f) {
+    if (kmax == 1) return with_tile<1, 0>(len, cin, cout, direct, f);
+    if (kmax == 2) return with_tile<2, 8>(len, cin, cout, direct, f);
+    return with_tile<7, 64>(len, cin, cout, direct, f);
 }
 
 }  // namespace
@@ -179,7 +182,8 @@ const char *conv_kernel_name(const dtts_conv_desc *d) {
     static thread_local char buf[128];
     const Choice c = choose(d);
     if (std::strcmp(c.path, "mfma") == 0)
-        with_tile_k(c.kmax, static_cast<int>(d->len), static_cast<int>(d->cout), c.direct_ok, [&](auto t) {
+        with_tile_k(c.kmax, static_cast<int>(d->len), static_cast<int>(d->cin), static_cast<int>(d->cout), c.direct_ok,
+                    [&](auto t) {
             typedef typename decltype(t)::type Cfg;
             char tail[32];
             snprintf(tail, sizeof(tail), ", %s, %d>", c.snake ? "true" : "false", d->k == Cfg::KMAX ? Cfg::KMAX : 0);
@@ -236,7 +240,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
-        e = with_tile_k(ch.kmax, p.L, p.cout, ch.direct_ok, [&](auto t) {
+        e = with_tile_k(ch.kmax, p.L, p.cin, p.cout, ch.direct_ok, [&](auto t) {
             return launch_tiled<typename decltype(t)::type>(p, d->lanes, stream);
         });
     } else {

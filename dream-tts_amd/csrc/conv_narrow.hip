@@ -13,6 +13,7 @@ namespace {
 constexpr int kBM = 256;
 constexpr int kMaxCin = 128;
 constexpr int kMaxHalo = 64;
+constexpr int kMaxVec = (kBM + kMaxHalo) * (kMaxCin / 8) / 256;  // window vectors per thread, at most
 
 struct NarrowParams {
     const half_t *x;
@@ -39,20 +40,35 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
     const int cv = p.cin / 8;  // 16-byte vectors per row
     const half_t *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
     for (int i = threadIdx.x; i < p.k * p.cin; i += 256) wsh[i] = p.w[i];
-    for (int v = threadIdx.x; v < rows * cv; v += 256) {
-        const int r = v / cv;
-        const int q = v - r * cv;
-        const int s = l0 - p.pad_left + r;
-        half8_t h = half8_t{};
-        if (s >= 0 && s < p.L) {
-            h = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + q * 8);
+    // every 16-byte vector of the window is loaded before any is stored, so the loads' latencies
+    // overlap instead of adding up
+    const int nvec = rows * cv;
+    half8_t buf[kMaxVec];
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int v = threadIdx.x + i * 256;
+        buf[i] = half8_t{};
+        if (v < nvec) {
+            const int r = v / cv;
+            const int s = l0 - p.pad_left + r;
+            if (s >= 0 && s < p.L)
+                buf[i] = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + (v - r * cv) * 8);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int v = threadIdx.x + i * 256;
+        if (v < nvec) {
+            const int r = v / cv;
+            const int q = v - r * cv;
+            half8_t h = buf[i];
             if (p.a_in) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     h[j] = static_cast<half_t>(snake_f16out(static_cast<float>(h[j]), p.a_in[q * 8 + j], p.r_in[q * 8 + j]));
             }
+            *reinterpret_cast<half8_t *>(win + r * pitch + q * 8) = h;
         }
-        *reinterpret_cast<half8_t *>(win + r * pitch + q * 8) = h;
     }
     __syncthreads();
     const int l = l0 + threadIdx.x;

@@ -49,6 +49,8 @@ def _close(got_bits, want_bits, tol=2e-2):
     (3, 96, 96, 700, 7, 9), (2, 192, 192, 513, 7, 3), (2, 384, 384, 300, 7, 1),   # codec RU shapes
     (2, 768, 768, 250, 1, 1), (2, 1024, 1536, 250, 7, 1),                         # RU k1, head conv
     (2, 64, 64, 100, 7, 2), (2, 32, 32, 65, 3, 4),                                 # BN 64 / 32 tiles
+    (2, 96, 384, 300, 1, 1), (1, 160, 192, 257, 1, 1),                             # cin off the 64-chunk tile
+    (1, 384, 192, 1500, 2, 1), (2, 96, 192, 300, 7, 3),                            # k=2 and k=7 at 192 columns
 ])
 def test_causal_conv_matches_oracle(dev, lanes, cin, cout, length, k, dil):
     x, w, wb, b = _case(40, lanes, length, cin, cout, k)
