@@ -1,110 +1,442 @@
 // The codec's residual unit as one kernel (ResidualUnit::forward, crates/qwen3tts/src/codec.rs:
 // 215-229):
 //
-//   h  = f16(conv_k,dil(SnakeBeta1(u)) + b1)          conv1, the tile main loop
-//   h2 = f16(SnakeBeta2(h))                           epilogue 1, into LDS
-//   y  = f16(conv_1(h2) + b2 + u)                     conv2 on the matrix cores from LDS
-//   out = y, and/or f16(SnakeBeta_next(y))            epilogue 2
+//   h  = f16(conv_k,dil(SnakeBeta1(u)) + b1)          conv1, the chunked main loop
+//   h2 = f16(SnakeBeta2(h))                           in registers
+//   y  = f16(conv_1(h2) + b2 + u)                     conv2, from registers
+//   out = y, and/or f16(SnakeBeta_next(y))
 //
 // A workgroup owns BM positions x all C channels, so the k=1 conv's whole reduction (C) is in the
-// workgroup after conv1: h and h2 never reach HBM. Per unit the activation traffic drops from
-// five passes (read u; write h; read h; read u; write y) to two (read u with its halo, write y),
-// and every value rounded to f16 here is one the unfused chain stores. W2 (C x C) is read as
-// MFMA B fragments straight from L2.
+// workgroup after conv1: h and h2 never reach HBM. Per unit the activation traffic is two passes
+// (read u with its halo, write y) instead of the unfused chain's five, and every value rounded
+// to f16 here is one the unfused chain stores.
+//
+// The matrix products are computed transposed, D[channel][position] = W . X^T, so the MFMA result
+// a lane holds is one position x 16 channels (four runs of four consecutive channels). That makes
+// conv2 free of any data movement: the f16-packed h2 values of a lane are exactly the B operand
+// conv2 needs at that position, provided conv2's reduction index runs over the channels in the
+// same order -- so the A operand (W2) is read in that order, two 8-byte pieces per fragment.
+// The epilogues work on four consecutive channels per access, and the biases start the
+// accumulators.
+//
+// Main loop, per KC-channel chunk: the dilated window of u (BM + (k-1)*dil rows) is loaded into
+// registers one chunk ahead, SnakeBeta'd in f32 (fma_mix reads the f16 directly) and written to
+// LDS while the previous chunk is on the matrix cores; W1's slice for the chunk goes straight
+// from memory to LDS (buffer_load ... lds), XOR-swizzled rows. Two LDS stages, one barrier per
+// chunk.
 #include "conv_tile.hpp"
 
 namespace dtts {
 namespace {
 
 struct RuArgs {
-    ConvArgs c1;        // conv1: x = u, w = w1, bias = b1, a_in/r_in = act1; cin = cout = C
-    const half_t *u;    // the residual
-    const float *a2, *r2;
-    const half_t *w2, *b2;
+    const half_t *u;    // [lanes, L, C]: the input and the residual
+    const half_t *w1;   // [C, k*C] tap-major
+    const half_t *w2;   // [C, C]
+    const half_t *b1, *b2;
+    const float *a1, *r1, *a2, *r2, *a_out, *r_out;
     half_t *y_pre, *y;
-    const float *a_out, *r_out;
+    int L, k, dil, pad_left;
+    int tiles_m, total_tiles, tiles_per_xcd;
 };
+
+// C channels; a wave owns WP positions x all C channels; NW waves; KC channels per chunk.
+template <int C_, int WP_, int NW_, int KC_>
+struct RuCfg {
+    static constexpr int C = C_, WP = WP_, NW = NW_, KC = KC_;
+    static constexpr int BM = WP * NW;  // positions per workgroup
+    static constexpr int THREADS = 64 * NW;
+    static constexpr int TM = WP / 32;  // 32-position blocks per wave
+    static constexpr int TN = C / 32;   // 32-channel blocks
+    static constexpr int KMAX = 7, HMAX = 64;
+    static constexpr int CHUNKS = C / KC;
+    // window: BM + HMAX rows x KC halves, rows padded by 8 halves (16 consecutive rows at one
+    // 16-byte segment then hit 16 distinct 4-bank groups)
+    static constexpr int ROWS = BM + HMAX;
+    static constexpr int SEGS = KC / 8;
+    static constexpr int APITCH = KC + 8;
+    static constexpr int A_BYTES = ROWS * APITCH * 2;
+    static constexpr int A_SEGS = ROWS * SEGS;
+    static constexpr int A_PER_T = (A_SEGS + THREADS - 1) / THREADS;
+    // W1 slice: KMAX * C rows (tap-major, t * C + channel) x KC halves, direct loads of 1 KiB
+    static constexpr int RPI = 1024 / (KC * 2);
+    static constexpr int B_BYTES = KMAX * C * KC * 2;
+    static constexpr int B_INST = KMAX * C / RPI;
+    static constexpr int B_PER_W = (B_INST + NW - 1) / NW;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int TAB_BYTES = 8 * C * 4;
+    static constexpr int LDS = 2 * STAGE + TAB_BYTES;
+    static constexpr int MIN_WG = 2 * LDS <= 160 * 1024 ? 2 : 1;
+    // W2 in LDS for conv2, written once the main loop is done (both stages are free then):
+    // rows padded to C + 8 halves (16 consecutive rows at one 16-byte column hit distinct banks)
+    static constexpr int W2_PITCH = C + 8;
+    static constexpr int W2_SEGS = C * C / 8;
+    static constexpr int W2_PER_T = (W2_SEGS + THREADS - 1) / THREADS;
+    static_assert(C % 32 == 0 && C % KC == 0 && WP % 32 == 0 && KC == 16, "residual-unit tile shape");
+    static_assert(THREADS % SEGS == 0, "a thread's window segments share one channel group");
+    static_assert((KMAX * C) % RPI == 0 && RPI % 32 == 0, "whole direct-load instructions per tap");
+    static_assert(C * W2_PITCH * 2 <= 2 * STAGE, "W2 fits the stages");
+};
+
+// C = 96: two 32-position blocks per wave, two workgroups per CU. C = 192: one block per wave
+// (96 accumulator registers either way), eight waves, one workgroup per CU.
+typedef RuCfg<96, 64, 4, 16> RuTile96;
+typedef RuCfg<192, 32, 8, 16> RuTile192;
+
+typedef _Float16 half4_v __attribute__((ext_vector_type(4)));
+
+// SnakeBeta on an f16 value with ka = alpha / 2pi: the product reads the f16 directly (fma_mix),
+// the sine takes revolutions after the fract reduction, and the result is rounded once to f16.
+__device__ __forceinline__ half_t snake_h(half_t x, float ka, float r) {
+    const float t = __builtin_fmaf(static_cast<float>(x), ka, 0.0f);
+    const float s = __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(t));
+    return static_cast<half_t>(__builtin_fmaf(r, s * s, static_cast<float>(x)));
+}
 
 template <typename Cfg, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q) {
-    constexpr int C = Cfg::BN;
-    constexpr int HP = C + 8;  // h2 row pitch (halves)
-    constexpr int H_BYTES = Cfg::BM * HP * 2;
-    constexpr int LDS0 = Cfg::MAIN_BYTES > Cfg::EPI_TOTAL ? Cfg::MAIN_BYTES : Cfg::EPI_TOTAL;
-    constexpr int LDS = LDS0 > H_BYTES ? LDS0 : H_BYTES;
-    __shared__ __attribute__((aligned(16))) char smem[LDS];
-    const ConvArgs &p = q.c1;
-    int lane_idx, m_tile, n_tile;
-    if (!conv_tile_coords(p, lane_idx, m_tile, n_tile)) return;
+    constexpr int C = Cfg::C, KC = Cfg::KC, SEGS = Cfg::SEGS, TM = Cfg::TM, TN = Cfg::TN, NW = Cfg::NW;
+    constexpr int APITCH = Cfg::APITCH;
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
+    const int tile = (blockIdx.x & 7) * q.tiles_per_xcd + (blockIdx.x >> 3);
+    if (tile >= q.total_tiles) return;
+    const int m_tile = tile % q.tiles_m;
+    const int lane_idx = tile / q.tiles_m;
     const int l0 = m_tile * Cfg::BM;
-    const half_t *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
-    float16_t acc[Cfg::TM][Cfg::TN];
-#pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
-    conv_mainloop<Cfg, true, KT>(p, xl, l0, 0, smem, acc);  // ends on a barrier
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
+    const int k = KT > 0 ? KT : q.k;
+    const int rows = Cfg::BM + (k - 1) * q.dil;
+    const int win0 = l0 - q.pad_left;
+    const half_t *ul = q.u + static_cast<int64_t>(lane_idx) * q.L * C;
 
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-    half_t *H = reinterpret_cast<half_t *>(smem);
-    // epilogue 1: h = f16(acc + b1), h2 = f16(SnakeBeta2(h)) -> H[row][channel]
+    // per-channel constants: ka1 r1 b1 ka2 r2 b2 ka_out r_out, f32
+    float *tab = reinterpret_cast<float *>(smem + 2 * Cfg::STAGE);
+    for (int c = tid; c < C; c += Cfg::THREADS) {
+        tab[c] = q.a1[c] * kInv2Pi;
+        tab[C + c] = q.r1[c];
+        tab[2 * C + c] = static_cast<float>(q.b1[c]);
+        tab[3 * C + c] = q.a2[c] * kInv2Pi;
+        tab[4 * C + c] = q.r2[c];
+        tab[5 * C + c] = static_cast<float>(q.b2[c]);
+        if (q.a_out) {
+            tab[6 * C + c] = q.a_out[c] * kInv2Pi;
+            tab[7 * C + c] = q.r_out[c];
+        }
+    }
+
+    // window segments of this thread: s = tid + i * THREADS -> row s / SEGS, segment tid % SEGS.
+    // Where the last round of segments runs past the window, a thread takes the segment of a
+    // thread that has one (same channel group) and stores the same value there: every load, snake
+    // and store is unconditional, so no branch splits the main loop's scheduling regions. Rows
+    // outside the window or the sequence read zeros through the buffer range check.
+    constexpr int LAST = Cfg::A_SEGS - (Cfg::A_PER_T - 1) * Cfg::THREADS;  // segments of the last round
+    static_assert(LAST > 0 && LAST % SEGS == 0, "window segment rounds");
+    const __amdgpu_buffer_rsrc_t rsu =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(ul), 0, q.L * C * 2, kBufferWord3);
+    const int qd = tid % SEGS;
+    uint32_t va[Cfg::A_PER_T];
+    int arow[Cfg::A_PER_T];
 #pragma unroll
-    for (int j = 0; j < Cfg::TN; ++j) {
-        const int n = wn * Cfg::WTN + j * 32 + (lane & 31);
-        const float b1 = static_cast<float>(p.bias[n]);
-        const float ka2 = q.a2[n] * kInv2Pi, r2 = q.r2[n];
+    for (int i = 0; i < Cfg::A_PER_T; ++i) {
+        const int s = i + 1 < Cfg::A_PER_T ? tid + i * Cfg::THREADS : (Cfg::A_PER_T - 1) * Cfg::THREADS + tid % LAST;
+        const int r = s / SEGS;
+        const int src = win0 + r;
+        arow[i] = r;
+        va[i] = (r < rows && src >= 0 && src < q.L) ? static_cast<uint32_t>((src * C + qd * 8) * 2) : kOutOfRange;
+    }
+    typedef half8_t WinRegs[Cfg::A_PER_T];
+    auto win_load = [&](WinRegs &R, int c0) {
 #pragma unroll
-        for (int i = 0; i < Cfg::TM; ++i)
+        for (int i = 0; i < Cfg::A_PER_T; ++i)
+            R[i] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rsu, va[i], c0 * 2, 0));
+    };
+    // SnakeBeta on the window registers, element g of the chunk (vector g / 8, lane element g % 8),
+    // in place; the per-channel constants of the thread's channel group come from the table
+    struct SnakeK {
+        float4_t ka0, ka1, r0, r1;
+    };
+    auto snake_consts = [&](int c0) {
+        const int c = c0 + qd * 8;
+        return SnakeK{*reinterpret_cast<const float4_t *>(tab + c), *reinterpret_cast<const float4_t *>(tab + c + 4),
+                      *reinterpret_cast<const float4_t *>(tab + C + c), *reinterpret_cast<const float4_t *>(tab + C + c + 4)};
+    };
+    auto snake_elems = [&](WinRegs &R, const SnakeK &kk, int g0, int g1) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = wm * Cfg::WTM + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                H[m * HP + n] = snake_f16k(static_cast<half_t>(acc[i][j][r] + b1), ka2, r2);
+        for (int g = g0; g < g1; ++g) {
+            const int i = g >> 3, e = g & 7;
+            R[i][e] = snake_h(R[i][e], e < 4 ? kk.ka0[e & 3] : kk.ka1[e & 3], e < 4 ? kk.r0[e & 3] : kk.r1[e & 3]);
+        }
+    };
+    auto win_write = [&](const WinRegs &R, char *stage) {
+#pragma unroll
+        for (int i = 0; i < Cfg::A_PER_T; ++i)
+            *reinterpret_cast<half8_t *>(stage + arow[i] * APITCH * 2 + qd * 16) = R[i];
+    };
+    auto win_store = [&](WinRegs &R, int c0, char *stage) {
+        const SnakeK kk = snake_consts(c0);
+        snake_elems(R, kk, 0, 8 * Cfg::A_PER_T);
+        win_write(R, stage);
+    };
+
+    // W1 slice of a chunk, straight to LDS: instruction j fills slots j*64 .. j*64+63; slot ->
+    // row slot / SEGS (= t * C + channel), segment (slot % SEGS) ^ swizzle(row)
+    const int K = k * C;
+    const __amdgpu_buffer_rsrc_t rsw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(q.w1), 0, C * K * 2, kBufferWord3);
+    const int b_inst = k * C / Cfg::RPI;
+    uint32_t vb[Cfg::B_PER_W];
+#pragma unroll
+    for (int i = 0; i < Cfg::B_PER_W; ++i) {
+        const int slot = (wave + i * NW) * 64 + lane;
+        const int r = slot / SEGS;
+        const int qq = (slot % SEGS) ^ seg_swizzle<KC>(r);
+        const int t = r / C;
+        const int n = r - t * C;
+        vb[i] = static_cast<uint32_t>((n * K + t * C + qq * 8) * 2);
+    }
+    auto w_issue = [&](int c0, char *stage) {
+        char *base = stage + Cfg::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < Cfg::B_PER_W; ++i) {
+            const int j = wave + i * NW;
+            if (j < b_inst) load_lds_16(rsw, base + j * 1024, vb[i], static_cast<uint32_t>(c0 * 2));
+        }
+    };
+
+    // accumulators start at b1: acc[i][j][4g + e] is channel 32j + 8g + 4hf + e at position
+    // 32i + l32 of the wave's block
+    float16_t acc[TM][TN];
+    __syncthreads();  // the table
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4_t b = *reinterpret_cast<const float4_t *>(tab + 2 * C + 32 * j + 8 * g + 4 * hf);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = b[e];
+        }
+
+    // fragments: window (B operand) rows wave*WP + 32i + l32 + t*dil, halves hf*8; W1 (A operand)
+    // rows t*C + 32j + l32, segment hf ^ swizzle
+    const int prow = wave * Cfg::WP + l32;
+    // hook(t) runs in the same scheduling region as tap t's MFMAs, so its VALU work issues in
+    // their shadow
+    auto compute = [&](const char *stage, auto &&hook) {
+        const char *A = stage;
+        const char *B = stage + Cfg::A_BYTES;
+        auto frag_x = [&](int t, int i) {
+            return *reinterpret_cast<const half8_t *>(A + (prow + 32 * i + t * q.dil) * APITCH * 2 + hf * 16);
+        };
+        auto frag_w = [&](int t, int j) {
+            const int r = t * C + 32 * j + l32;
+            return *reinterpret_cast<const half8_t *>(B + r * (KC * 2) + ((hf ^ seg_swizzle<KC>(r)) << 4));
+        };
+        if constexpr (KT > 0) {
+            half8_t fx[2][TM], fw[2][TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) fx[0][i] = frag_x(0, i);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) fw[0][j] = frag_w(0, j);
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+                if (t + 1 < KT) {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) fx[(t + 1) & 1][i] = frag_x(t + 1, i);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) fw[(t + 1) & 1][j] = frag_w(t + 1, j);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[t & 1][j], fx[t & 1][i], acc[i][j], 0, 0, 0);
+                hook(t);
+                // one MFMA, then a few VALU instructions (the hook's), in turn
+#pragma unroll
+                for (int m = 0; m < TM * TN; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            for (int t = 0; t < k; ++t) {
+                half8_t fx[TM], fw[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) fx[i] = frag_x(t, i);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) fw[j] = frag_w(t, j);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[j], fx[i], acc[i][j], 0, 0, 0);
+            }
+            hook(-1);
+        }
+    };
+
+    // Pipeline. Chunk c computes from stage c & 1. During chunk c: W1 of chunk c+1 streams into
+    // stage (c+1) & 1, the window of chunk c+2 into registers, and the registers holding chunk
+    // c+1's window are snaked into stage (c+1) & 1. Stage (c+1) & 1 was last read by chunk c-1,
+    // which every wave finished before the barrier that closed it.
+    char *stage[2] = {smem, smem + Cfg::STAGE};
+    WinRegs R[2];
+    // W2 [C][C] in 16-byte segments (8 input channels of one output channel), loaded during the
+    // last chunk and stored in the A-fragment order conv2 reads (see below)
+    half8_t w2r[Cfg::W2_PER_T];
+    auto w2_load = [&] {
+#pragma unroll
+        for (int i = 0; i < Cfg::W2_PER_T; ++i) {
+            const int sg = tid + i * Cfg::THREADS;
+            if (Cfg::W2_SEGS % Cfg::THREADS == 0 || sg < Cfg::W2_SEGS)
+                w2r[i] = *reinterpret_cast<const half8_t *>(q.w2 + sg * 8);
+        }
+    };
+    w_issue(0, stage[0]);
+    win_load(R[0], 0);
+    if (Cfg::CHUNKS > 1) win_load(R[1], KC);
+    wait_vmem();
+    win_store(R[0], 0, stage[0]);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < Cfg::CHUNKS; ++c) {
+        const int cur = c & 1, nxt = cur ^ 1;
+        if (c + 1 < Cfg::CHUNKS) w_issue((c + 1) * KC, stage[nxt]);
+        if (c + 2 < Cfg::CHUNKS) win_load(R[cur], (c + 2) * KC);
+        if (c + 1 == Cfg::CHUNKS) w2_load();
+        if (c + 1 < Cfg::CHUNKS) {
+            // the window of chunk c+1 (loaded a chunk ago; the compiler waits for those registers)
+            // is snaked in the shadow of chunk c's MFMAs
+            const SnakeK kk = snake_consts((c + 1) * KC);
+            constexpr int NE = 8 * Cfg::A_PER_T;
+            compute(stage[cur], [&](int t) {
+                if constexpr (KT > 0) {
+                    snake_elems(R[nxt], kk, t * NE / KT, (t + 1) * NE / KT);
+                } else {
+                    if (t < 0) snake_elems(R[nxt], kk, 0, NE);
+                }
+            });
+        } else {
+            compute(stage[cur], [](int) {});
+        }
+        // W1 of chunk c+1 has landed (only the newest window loads may be in flight)
+        if (c + 2 < Cfg::CHUNKS)
+            wait_vmem_le<Cfg::A_PER_T>();
+        else if (c + 1 < Cfg::CHUNKS)
+            wait_vmem();
+        if (c + 1 < Cfg::CHUNKS) win_write(R[nxt], stage[nxt]);
+        __syncthreads();
+    }
+
+    // the residual rows of this lane's positions, four channels per load (consumed at the end)
+    half4_v ures[TM][TN][4];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int pos = l0 + prow + 32 * i;
+        const half_t *urow = ul + static_cast<int64_t>(pos < q.L ? pos : 0) * C + 4 * hf;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) ures[i][j][g] = *reinterpret_cast<const half4_v *>(urow + 32 * j + 8 * g);
+    }
+    // W2 into LDS, permuted within each 16-channel group so that one 16-byte read is an A
+    // fragment: row co holds, at 16kk + 8h + 4m + e, W2[co][16kk + 8m + 4h + e]
+    half_t *W2s = reinterpret_cast<half_t *>(smem);
+#pragma unroll
+    for (int i = 0; i < Cfg::W2_PER_T; ++i) {
+        const int sg = tid + i * Cfg::THREADS;
+        if (Cfg::W2_SEGS % Cfg::THREADS == 0 || sg < Cfg::W2_SEGS) {
+            const int co = sg / (C / 8), s8 = sg % (C / 8);  // channels 8*s8 .. +8: kk = s8/2, m = s8&1
+            half_t *dst = W2s + co * Cfg::W2_PITCH + 16 * (s8 >> 1) + 4 * (s8 & 1);
+            const half8_t v = w2r[i];
+            *reinterpret_cast<half4_v *>(dst) = half4_v{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<half4_v *>(dst + 8) = half4_v{v[4], v[5], v[6], v[7]};
+        }
+    }
+
+    // h2 = f16(SnakeBeta2(f16(acc))), packed as conv2's B fragments: fragment kk of position block
+    // i holds channels 16kk + {0..3, 8..11} + 4hf, in that order
+    half8_t h2[TM][C / 16];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int ch = 32 * j + 8 * g + 4 * hf;
+            const float4_t ka = *reinterpret_cast<const float4_t *>(tab + 3 * C + ch);
+            const float4_t rr = *reinterpret_cast<const float4_t *>(tab + 4 * C + ch);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    h2[i][2 * j + (g >> 1)][(g & 1) * 4 + e] = snake_h(static_cast<half_t>(acc[i][j][4 * g + e]), ka[e], rr[e]);
+        }
+
+    // conv2: acc = b2 + W2 . h2, reduction over the channels in the fragments' order
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4_t b = *reinterpret_cast<const float4_t *>(tab + 5 * C + 32 * j + 8 * g + 4 * hf);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = b[e];
+        }
+    __syncthreads();  // W2 in LDS
+    const half_t *w2l = W2s + l32 * Cfg::W2_PITCH + 8 * hf;
+#pragma unroll
+    for (int kk = 0; kk < C / 16; ++kk)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const half8_t a = *reinterpret_cast<const half8_t *>(w2l + 32 * j * Cfg::W2_PITCH + 16 * kk);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, h2[i][kk], acc[i][j], 0, 0, 0);
+        }
+
+    // y = f16(acc + u), y_pre, SnakeBeta_out: four consecutive channels per access
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int pos = l0 + prow + 32 * i;
+        if (pos >= q.L) continue;
+        const int64_t rowoff = (static_cast<int64_t>(lane_idx) * q.L + pos) * C;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int ch = 32 * j + 8 * g + 4 * hf;
+                const half4_v uu = ures[i][j][g];
+                half4_v yv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    yv[e] = static_cast<half_t>(__builtin_fmaf(static_cast<float>(uu[e]), 1.0f, acc[i][j][4 * g + e]));
+                if (q.y_pre) *reinterpret_cast<half4_v *>(q.y_pre + rowoff + ch) = yv;
+                if (q.a_out) {
+                    const float4_t ka = *reinterpret_cast<const float4_t *>(tab + 6 * C + ch);
+                    const float4_t rr = *reinterpret_cast<const float4_t *>(tab + 7 * C + ch);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) yv[e] = snake_h(yv[e], ka[e], rr[e]);
+                }
+                *reinterpret_cast<half4_v *>(q.y + rowoff + ch) = yv;
             }
     }
-    __syncthreads();
-    // conv2 (k = 1): acc = H[rows] . W2^T over K = C
-#pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
-    const int koff = (lane >> 5) * 8;
-    const half_t *ha = H + (wm * Cfg::WTM + (lane & 31)) * HP + koff;
-    const half_t *wb = q.w2 + static_cast<int64_t>(wn * Cfg::WTN + (lane & 31)) * C + koff;
-#pragma unroll 2
-    for (int kk = 0; kk < C; kk += 16) {
-        half8_t af[Cfg::TM], bf[Cfg::TN];
-#pragma unroll
-        for (int j = 0; j < Cfg::TN; ++j) bf[j] = *reinterpret_cast<const half8_t *>(wb + j * 32 * C + kk);
-#pragma unroll
-        for (int i = 0; i < Cfg::TM; ++i) af[i] = *reinterpret_cast<const half8_t *>(ha + i * 32 * HP + kk);
-#pragma unroll
-        for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-            for (int j = 0; j < Cfg::TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    // epilogue 2 (starts with a barrier, so H is no longer read when E overwrites it)
-    conv_epilogue<Cfg>(acc, smem, static_cast<int64_t>(lane_idx) * p.L, l0, 0, p.L, C, q.b2, q.u, q.y_pre, q.y,
-                       q.a_out, q.r_out, 0);
 }
-
-// C = 96 is bound by the SnakeBeta VALU work, which register staging overlaps across two
-// workgroups per CU; C = 192 is matrix-bound and takes direct staging with eight waves.
-typedef ConvTile<256, 96, 4, 1, 32, 7, 64> RuTile96;
-typedef ConvTile<256, 192, 4, 2, 16, 7, 64, 2, kStageDirect> RuTile192;
 
 template <typename Cfg>
 hipError_t launch_ru(RuArgs q, int64_t lanes, hipStream_t stream) {
-    ConvArgs &p = q.c1;
-    p.tiles_m = (p.L + Cfg::BM - 1) / Cfg::BM;
-    p.tiles_n = 1;
-    const int64_t total = lanes * p.tiles_m;
-    p.total_tiles = static_cast<int>(total);
-    p.tiles_per_xcd = static_cast<int>((total + 7) / 8);
-    const unsigned grid = static_cast<unsigned>(int64_t(p.tiles_per_xcd) * 8);
-    if (p.k == Cfg::KMAX)
+    q.tiles_m = (q.L + Cfg::BM - 1) / Cfg::BM;
+    const int64_t total = lanes * q.tiles_m;
+    q.total_tiles = static_cast<int>(total);
+    q.tiles_per_xcd = static_cast<int>((total + 7) / 8);
+    const unsigned grid = static_cast<unsigned>(int64_t(q.tiles_per_xcd) * 8);
+    if (q.k == Cfg::KMAX)
         ru_nlc_f16<Cfg, Cfg::KMAX><<<grid, Cfg::THREADS, 0, stream>>>(q);
     else
         ru_nlc_f16<Cfg, 0><<<grid, Cfg::THREADS, 0, stream>>>(q);
@@ -117,18 +449,24 @@ bool ru_shape_ok(const dtts_ru_desc *d) {
            direct_offsets_fit(d->len, d->channels, d->channels, d->k);
 }
 
+template <typename Cfg>
+const char *ru_name(char *buf, size_t n, int k) {
+    snprintf(buf, n, "ru_nlc_f16<dtts::(anonymous namespace)::RuCfg<%d, %d, %d, %d>, %d>", Cfg::C, Cfg::WP, Cfg::NW,
+             Cfg::KC, k == Cfg::KMAX ? Cfg::KMAX : 0);
+    return buf;
+}
+
 }  // namespace
 
 bool residual_unit_supported(const dtts_ru_desc *d) {
-    return d && ru_shape_ok(d) && aligned(d->x, 16) && aligned(d->w1, 16) && aligned(d->w2, 16) && aligned(d->b1, 2) &&
-           aligned(d->b2, 16) && aligned(d->y, 16) && (!d->y_pre || aligned(d->y_pre, 16));
+    return d && ru_shape_ok(d) && aligned(d->x, 16) && aligned(d->w1, 16) && aligned(d->w2, 8) && aligned(d->b1, 2) &&
+           aligned(d->b2, 2) && aligned(d->y, 8) && (!d->y_pre || aligned(d->y_pre, 8));
 }
 
 const char *residual_unit_kernel_name(const dtts_ru_desc *d) {
     static thread_local char buf[128];
-    const char *tail = d->k == 7 ? ", 7>" : ", 0>";
-    return d->channels == 96 ? tile_kernel_name<RuTile96>(buf, sizeof(buf), "ru_nlc_f16", tail)
-                             : tile_kernel_name<RuTile192>(buf, sizeof(buf), "ru_nlc_f16", tail);
+    const int k = static_cast<int>(d->k);
+    return d->channels == 96 ? ru_name<RuTile96>(buf, sizeof(buf), k) : ru_name<RuTile192>(buf, sizeof(buf), k);
 }
 
 int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream) {
@@ -148,26 +486,23 @@ int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream) {
     }
     DTTS_REQUIRE(d->len < (int64_t(1) << 30) && d->lanes * d->len < (int64_t(1) << 36), "%s: shape too large", name);
     RuArgs q{};
-    ConvArgs &p = q.c1;
-    p.x = reinterpret_cast<const half_t *>(d->x);
-    p.w = reinterpret_cast<const half_t *>(d->w1);
-    p.bias = reinterpret_cast<const half_t *>(d->b1);
-    p.a_in = d->act1_alpha;
-    p.r_in = d->act1_brecip;
-    p.L = static_cast<int>(d->len);
-    p.cin = p.cout = static_cast<int>(d->channels);
-    p.k = static_cast<int>(d->k);
-    p.dil = static_cast<int>(d->dilation);
-    p.pad_left = static_cast<int>((d->k - 1) * d->dilation);
     q.u = reinterpret_cast<const half_t *>(d->x);
+    q.w1 = reinterpret_cast<const half_t *>(d->w1);
+    q.w2 = reinterpret_cast<const half_t *>(d->w2);
+    q.b1 = reinterpret_cast<const half_t *>(d->b1);
+    q.b2 = reinterpret_cast<const half_t *>(d->b2);
+    q.a1 = d->act1_alpha;
+    q.r1 = d->act1_brecip;
     q.a2 = d->act2_alpha;
     q.r2 = d->act2_brecip;
-    q.w2 = reinterpret_cast<const half_t *>(d->w2);
-    q.b2 = reinterpret_cast<const half_t *>(d->b2);
-    q.y_pre = reinterpret_cast<half_t *>(d->y_pre);
-    q.y = reinterpret_cast<half_t *>(d->y);
     q.a_out = d->out_alpha;
     q.r_out = d->out_brecip;
+    q.y_pre = reinterpret_cast<half_t *>(d->y_pre);
+    q.y = reinterpret_cast<half_t *>(d->y);
+    q.L = static_cast<int>(d->len);
+    q.k = static_cast<int>(d->k);
+    q.dil = static_cast<int>(d->dilation);
+    q.pad_left = static_cast<int>((d->k - 1) * d->dilation);
     const hipError_t e = d->channels == 96 ? launch_ru<RuTile96>(q, d->lanes, stream) : launch_ru<RuTile192>(q, d->lanes, stream);
     DTTS_HIP_CHECK(e, name);
     return DTTS_OK;
