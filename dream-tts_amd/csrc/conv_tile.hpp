@@ -152,9 +152,9 @@ constexpr int min_loads_per_wave(int nw, int a_inst, int b_inst) {
 }
 
 // The k taps of one staged chunk on the matrix cores. KT > 0 is the tap count known at compile
-// time: the loop unrolls into straight-line code, so the fragment reads of tap t+1 are issued
-// before tap t's MFMAs and the wait before those MFMAs counts only tap t's reads (with PIPE, two
-// fragment sets alternate; without, the compiler schedules one set). KT == 0 takes k at run time.
+// time: the loop unrolls into straight-line code, and with PIPE two fragment sets alternate: tap
+// t+1's reads are interleaved with tap t's MFMAs, and the wait before an MFMA counts only tap t's
+// reads (without PIPE, the compiler schedules one set). KT == 0 takes k at run time.
 // frag_a(t, kk, i) / frag_b(t, kk, j) give the 16-byte fragment addresses of 32-row block i (or
 // column block j) at k-step kk of tap t.
 template <typename Cfg, int KT, bool PIPE, typename FA, typename FB>
@@ -187,9 +187,14 @@ __device__ __forceinline__ void mma_taps(int k, FA frag_a, FB frag_b, float16_t 
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
             if (t + 1 < KT) load(t + 1, a[(t + 1) & 1], b[(t + 1) & 1]);
-            // keep the scheduler from sinking tap t+1's reads back next to their MFMAs
-            __builtin_amdgcn_sched_barrier(0);
             mma(a[t & 1], b[t & 1]);
+            // tap t+1's fragment reads go out one at a time between tap t's MFMAs, so the LDS
+            // queue and the matrix pipe stay busy together
+#pragma unroll
+            for (int m = 0; m < KS * Cfg::TM * Cfg::TN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     } else if constexpr (KT > 0) {
@@ -511,6 +516,23 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
     float *E = reinterpret_cast<float *>(smem) + wave * 32 * Cfg::EPI_PITCH;
     const int nw = n0 + wn * Cfg::WTN;
     float *tab = reinterpret_cast<float *>(smem + Cfg::EPI_BYTES);  // [BN] a/2pi, then [BN] r
+    // every block's residual and bias vectors are requested up front, so their latency overlaps
+    // the barrier, the table fill and the staging of the blocks before them
+    half8_t rr[Cfg::TM][NG], bb[Cfg::TM][NG];
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i) {
+        const int lb = l0 + wm * Cfg::WTM + i * 32;
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            const int g = lane + 64 * u;
+            const int mr = g / CG, cg = g - (g / CG) * CG;
+            const int n = nw + cg * 8;
+            rr[i][u] = half8_t{};
+            bb[i][u] = half8_t{};
+            if (res && lb + mr < lmax) rr[i][u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + n);
+            if (bias) bb[i][u] = *reinterpret_cast<const half8_t *>(bias + n);
+        }
+    }
     __syncthreads();
     if (a_out) {
         for (int c = threadIdx.x; c < Cfg::BN; c += Cfg::THREADS) {
@@ -521,17 +543,6 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
 #pragma unroll
     for (int i = 0; i < Cfg::TM; ++i) {
         const int lb = l0 + wm * Cfg::WTM + i * 32;
-        half8_t rr[NG], bb[NG];
-#pragma unroll
-        for (int u = 0; u < NG; ++u) {
-            const int g = lane + 64 * u;
-            const int mr = g / CG, cg = g - (g / CG) * CG;
-            const int n = nw + cg * 8;
-            rr[u] = half8_t{};
-            bb[u] = half8_t{};
-            if (res && lb + mr < lmax) rr[u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + n);
-            if (bias) bb[u] = *reinterpret_cast<const half8_t *>(bias + n);
-        }
         if (i > 0) wave_lds_order();  // the wave's reads of block i-1 precede these writes
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j)
@@ -555,7 +566,7 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[u][q])) + static_cast<float>(rr[u][q]);
+            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[i][u][q])) + static_cast<float>(rr[i][u][q]);
             const int64_t off = (row0 + l) * ld + n;
             half8_t h;
 #pragma unroll
