@@ -24,8 +24,7 @@ typedef ConvArgs ConvParams;
 
 template <typename Cfg, bool SNAKE_IN, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(ConvArgs p) {
-    constexpr int LDS = Cfg::MAIN_BYTES > Cfg::EPI_TOTAL ? Cfg::MAIN_BYTES : Cfg::EPI_TOTAL;
-    __shared__ __attribute__((aligned(16))) char smem[LDS];
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
     int lane_idx, m_tile, n_tile;
     if (!conv_tile_coords(p, lane_idx, m_tile, n_tile)) return;
     const int l0 = m_tile * Cfg::BM;
@@ -36,9 +35,10 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(C
     for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = float16_t{};
+    conv_snake_table<Cfg>(smem, n0, p.a_out, p.r_out);
     conv_mainloop<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
     conv_epilogue<Cfg>(acc, smem, static_cast<int64_t>(lane_idx) * p.L, l0, n0, p.L, p.cout, p.bias, p.res, p.y_pre,
-                       p.y, p.a_out, p.r_out, p.act);
+                       p.y, p.a_out, p.act);
 }
 
 // Any shape: one thread per output element, taps and channels looped directly. For shapes the
@@ -114,11 +114,12 @@ auto with_tile(int len, int cin, int cout, bool direct, F &&f) {
             if (cout % 96 == 0 && len >= 1024) return f(Tile<ConvTile<512, 96, 8, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
             if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 16, KMAX, HMAX, 2, kStageDirect>>{});
         }
-        // k = 2 (the transposed convs) and k = 1 at 192-multiples: 256 x 192 over eight waves. A
-        // chunk holds little matrix work at one or two taps, so k = 2 keeps three stages in flight
-        // and k = 1 takes 64-channel chunks (half the barriers per output)
+        // k = 2 (the transposed convs): 256 x 96 over four waves, two workgroups per CU (their
+        // epilogues and prologues overlap the other's main loop). k = 1 at 192-multiples: 256 x 192
+        // over eight waves with 64-channel chunks (a chunk holds little matrix work at one tap;
+        // this halves the barriers per output)
         if constexpr (KMAX == 2)
-            if (cout % 192 == 0) return f(Tile<ConvTile<256, 192, 4, 2, 32, KMAX, HMAX, 3, kStageDirect>>{});
+            if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
         if constexpr (KMAX == 1)
             if (cout % 192 == 0 && cin % 64 == 0)
                 return f(Tile<ConvTile<256, 192, 4, 2, 64, KMAX, HMAX, 2, kStageDirect>>{});

@@ -1,12 +1,13 @@
-// The channels-last implicit-GEMM conv tile shared by the conv kernel and the fused residual
-// unit: the staged dilated window, the MFMA main loop, and the LDS-staged epilogue.
+// The channels-last implicit-GEMM conv tile: the staged dilated window, the MFMA main loop, and
+// the epilogue.
 //
 // GEMM view per lane: M = positions, N = output channels, K = k*cin tap-major. A workgroup of
 // WM x WN waves owns BM positions x BN channels. Per KC-channel chunk it stages, in LDS:
 //   A: the whole dilated window, BM + (k-1)*dil rows x KC channels, loaded once and read by
 //      all k taps at row offsets t*dil (the im2col never exists, not even in LDS);
 //   B: w[n0 .. n0+BN, t*cin + c0 .. +KC] for every tap t.
-// Each wave owns (BM/WM) x (BN/WN) on 32x32x16 f16 MFMAs with f32 accumulation.
+// Each wave owns (BM/WM) x (BN/WN) on 32x32x16 f16 MFMAs with f32 accumulation, computed
+// transposed (weights as the A operand): a lane's result is one position x 16 channels.
 //
 // Two ways to fill a stage (the tile's STAGING parameter):
 //   kStageRegs:   global -> registers -> ds_write, rows padded by 8 halves so the 16-byte
@@ -54,13 +55,18 @@ struct ConvTile {
     static constexpr int B_BYTES = KMAX * BN * ROW_BYTES;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
     static constexpr int MAIN_BYTES = NBUF * STAGE_BYTES;
-    // epilogue: per-wave f32 tile; a pitch of 8 (mod 16) floats puts rows r and r+4 (the two
-    // lane halves of an MFMA result) half a bank sweep apart
-    static constexpr int EPI_PITCH = WTN + 8;
-    static constexpr int EPI_BYTES = WM * WN * 32 * EPI_PITCH * 4;
-    static constexpr int EPI_TOTAL = EPI_BYTES + BN * 8;  // + the output SnakeBeta table (a/2pi, r)
-    // workgroups per CU the register budget is sized for (two when two fit in LDS)
-    static constexpr int MIN_WG = (THREADS <= 256 && 2 * MAIN_BYTES <= 160 * 1024) ? 2 : 1;
+    // epilogue: each wave stages a 32-row block of its results in f32 through LDS (the stages are
+    // free by then); a row pitch of 4 (mod 64) floats keeps the 16-byte writes of 16 consecutive
+    // rows on distinct banks
+    static constexpr int EPI_PITCH = WTN + 4;
+    static constexpr int EPI_BYTES = NW * 32 * EPI_PITCH * 4;
+    // the output SnakeBeta table (a/2pi, r per channel of the tile) sits after both
+    static constexpr int TAB_OFFSET = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+    static constexpr int LDS_BYTES = TAB_OFFSET + BN * 8;
+    // workgroups per CU the register budget is sized for: as many as fit in LDS, at most three
+    // (two when the accumulators alone take 96 registers: three would spill)
+    static constexpr int WG_BY_LDS = (160 * 1024) / LDS_BYTES;
+    static constexpr int MIN_WG = THREADS > 256 ? 1 : (WG_BY_LDS >= 3 && TM * TN <= 4 ? 3 : (WG_BY_LDS >= 2 ? 2 : 1));
     static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC % 16 == 0, "tile shape");
     static_assert(STAGING != kStageDirect || (KC >= 16 && KC <= 64 && BN % RPI == 0), "direct staging shape");
 };
@@ -178,7 +184,7 @@ __device__ __forceinline__ void mma_taps(int k, FA frag_a, FB frag_b, float16_t 
             for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
                 for (int j = 0; j < Cfg::TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk][i], b[kk][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[kk][j], a[kk][i], acc[i][j], 0, 0, 0);
     };
     if constexpr (KT > 0 && PIPE) {
         FragA a[2];
@@ -488,6 +494,18 @@ __device__ __forceinline__ void conv_mainloop(const ConvArgs &p, const half_t *x
         conv_mainloop_regs<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
 }
 
+// Fills the output SnakeBeta table (a/2pi and r for the tile's BN channels) after the stages and
+// the epilogue's staging area; the main loop's barriers make it visible before the epilogue.
+template <typename Cfg>
+__device__ __forceinline__ void conv_snake_table(char *smem, int n0, const float *a_out, const float *r_out) {
+    if (!a_out) return;
+    float *tab = reinterpret_cast<float *>(smem + Cfg::TAB_OFFSET);
+    for (int c = threadIdx.x; c < Cfg::BN; c += Cfg::THREADS) {
+        tab[c] = a_out[n0 + c] * kInv2Pi;
+        tab[Cfg::BN + c] = r_out[n0 + c];
+    }
+}
+
 // Orders this wave's LDS accesses before and after it (the LDS executes one wave's instructions
 // in issue order, so lanes then see each other's earlier writes; the fence stops the compiler
 // from moving accesses across).
@@ -497,28 +515,32 @@ __device__ __forceinline__ void wave_lds_order() {
 }
 
 // Writes acc (+ bias, + residual, act, rounded; y_pre; SnakeBeta_out; y) for the tile, one 32-row
-// block per wave at a time through the wave's own LDS region (16-byte coalesced rows). `ld` is the
-// output row length (cout), `n0` the tile's first output channel, `lmax` the lane's length.
-// The block's residual and bias vectors are loaded before the block is staged, so their latency
-// overlaps the staging; the staging region is private to the wave, so only the first block waits
-// for the workgroup (smem may still be read by other waves before that).
+// block per wave at a time through the wave's own LDS region. The products are transposed
+// (D[channel][position]): a lane holds one position and runs of four consecutive channels, which
+// go to LDS as 16-byte writes; rows then come back 8 channels per lane, so bias, residual and the
+// stores move 16 coalesced bytes per lane. The whole tile's residual and bias vectors are
+// requested up front. `ld` is the output row length (cout), `n0` the tile's first output
+// channel, `lmax` the lane's length. Called after the main loop's closing barrier (smem free).
 template <typename Cfg>
 __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
                                               int l0, int n0, int lmax, int ld, const half_t *bias, const half_t *res,
-                                              half_t *y_pre, half_t *y, const float *a_out, const float *r_out,
-                                              int act) {
-    constexpr int CG = Cfg::WTN / 8;     // 8-channel groups per wave row
-    constexpr int NG = 32 * CG / 64;     // groups per lane per 32-row block
+                                              half_t *y_pre, half_t *y, const float *a_out, int act) {
+    constexpr int CG = Cfg::WTN / 8;  // 8-channel groups per wave row
+    constexpr int NG = 32 * CG / 64;  // groups per lane per 32-row block
     static_assert((32 * CG) % 64 == 0, "a 32-row block splits evenly over the lanes");
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
+    const int l32 = lane & 31, hf = lane >> 5;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     float *E = reinterpret_cast<float *>(smem) + wave * 32 * Cfg::EPI_PITCH;
     const int nw = n0 + wn * Cfg::WTN;
-    float *tab = reinterpret_cast<float *>(smem + Cfg::EPI_BYTES);  // [BN] a/2pi, then [BN] r
-    // every block's residual and bias vectors are requested up front, so their latency overlaps
-    // the barrier, the table fill and the staging of the blocks before them
-    half8_t rr[Cfg::TM][NG], bb[Cfg::TM][NG];
+    const float *tab = reinterpret_cast<const float *>(smem + Cfg::TAB_OFFSET);
+    half8_t rr[Cfg::TM][NG], bb[NG];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        const int cg = (lane + 64 * u) % CG;
+        bb[u] = bias ? *reinterpret_cast<const half8_t *>(bias + nw + cg * 8) : half8_t{};
+    }
 #pragma unroll
     for (int i = 0; i < Cfg::TM; ++i) {
         const int lb = l0 + wm * Cfg::WTM + i * 32;
@@ -526,18 +548,9 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
         for (int u = 0; u < NG; ++u) {
             const int g = lane + 64 * u;
             const int mr = g / CG, cg = g - (g / CG) * CG;
-            const int n = nw + cg * 8;
             rr[i][u] = half8_t{};
-            bb[i][u] = half8_t{};
-            if (res && lb + mr < lmax) rr[i][u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + n);
-            if (bias) bb[i][u] = *reinterpret_cast<const half8_t *>(bias + n);
-        }
-    }
-    __syncthreads();
-    if (a_out) {
-        for (int c = threadIdx.x; c < Cfg::BN; c += Cfg::THREADS) {
-            tab[c] = a_out[n0 + c] * kInv2Pi;
-            tab[Cfg::BN + c] = r_out[n0 + c];
+            if (res && lb + mr < lmax)
+                rr[i][u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + nw + cg * 8);
         }
     }
 #pragma unroll
@@ -547,14 +560,10 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
 #pragma unroll
         for (int j = 0; j < Cfg::TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int mr = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                E[mr * Cfg::EPI_PITCH + j * 32 + (lane & 31)] = acc[i][j][r];
-            }
-        if (i == 0 && a_out)
-            __syncthreads();  // the snake table is written by the whole workgroup
-        else
-            wave_lds_order();
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4_t *>(E + l32 * Cfg::EPI_PITCH + 32 * j + 8 * g + 4 * hf) =
+                    float4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        wave_lds_order();
 #pragma unroll
         for (int u = 0; u < NG; ++u) {
             const int g = lane + 64 * u;
@@ -566,7 +575,7 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[i][u][q])) + static_cast<float>(rr[i][u][q]);
+            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[u][q])) + static_cast<float>(rr[i][u][q]);
             const int64_t off = (row0 + l) * ld + n;
             half8_t h;
 #pragma unroll
@@ -587,7 +596,6 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             *reinterpret_cast<half8_t *>(y + off) = h;
         }
     }
-    __syncthreads();
 }
 
 }  // namespace dtts
