@@ -181,6 +181,13 @@ def workload_cfg2(dev, args):
     kc = torch.zeros((b, n_kv, cap, hd), dtype=torch.float16, device=dev)
     vc = torch.zeros_like(kc)
     yq, yk, yh = torch.empty_like(q), torch.empty_like(k), torch.empty_like(hsd)
+    qa = torch.from_numpy(synth.normal(0, "cfg2.qa", (b, n_kv, heads // n_kv, hd), 0, 0.1)).to(dev)
+    ya = torch.empty_like(qa)
+    kc.copy_(torch.from_numpy(synth.normal(0, "cfg2.kc", (b, n_kv, cap, hd))).half())
+    vc.copy_(torch.from_numpy(synth.normal(0, "cfg2.vc", (b, n_kv, cap, hd))).half())
+    span = pos.astype(np.int32) + 1
+    wsa = torch.empty(ops.decode_attention_workspace_bytes(b, n_kv, heads // n_kv, hd, int(span.max())),
+                      dtype=torch.uint8, device=dev)
     fns = {
         "rms_norm_f16": (lambda: ops.rms_norm(hsd, gam, 1e-6, out=yh), 2 * 2 * b * 1024 + 2048),
         "rope_q_f16": (lambda: ops.rope(q, c, s, pos, out=yq), 2 * 2 * q.numel() + 8 * b * hd // 2),
@@ -188,13 +195,17 @@ def workload_cfg2(dev, args):
         "kv_append_f16": (lambda: ops.kv_append(k, v, pos, kc, vc), 2 * 2 * (k.numel() + v.numel())),
         "qk_norm_rope_kv_append_f16": (lambda: ops.qk_norm_rope_kv_append(qkv, norms, c, s, pos, kc, vc, heads, 1e-6),
                                        2 * qkv.numel() + 2 * b * heads * hd + 2 * 2 * b * n_kv * hd),
+        # each lane attends to its positions 0..pos (the cache read once per kv head)
+        "decode_attention_f16": (lambda: ops.decode_attention(qa, kc, vc, span, out=ya, workspace=wsa),
+                                 int(2 * 2 * n_kv * hd * span.sum()) + 2 * 4 * qa.numel()),
     }
     res = {}
     for name, (fn, nbytes) in fns.items():
         t = _graph_time(fn, reps=20, inner=100)
         res[name] = {"us": t * 1e3, "gbs": nbytes / t / 1e6, "bytes": nbytes}
     total = sum(r["us"] for r in res.values())
-    return _line("config2: talker step norm/RoPE/KV append, 48 lanes f16 (graph-replayed, launch-latency bound)",
+    return _line("config2: talker step norm/RoPE/KV append and decode attention over the cache, 48 lanes f16 "
+                 "(graph-replayed; all but attention launch-latency bound)",
                  "per-step op time (us)", total, "us", res, {"higher_is_better": False, "dtype": "f16"})
 
 

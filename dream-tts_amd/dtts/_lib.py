@@ -55,6 +55,9 @@ SIGNATURES = {
                                         _I64, _I64, _F32, _P],
     "dtts_kv_append_f32": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_kv_append_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_decode_attention_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],
+    "dtts_decode_attention_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
+    "dtts_decode_attention_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
     "dtts_gemm_f16_skinny": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_gemm_f16_nt": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_gemm_f16_gateup_silu": [_P, _P, _P, _I64, _I64, _I64, _P],
@@ -70,7 +73,8 @@ SIGNATURES = {
     "dtts_codec_profile": [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _I32, _P],
 }
 _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
-             "dtts_codec_hop": ctypes.c_int64, "dtts_codec_workspace_bytes": ctypes.c_size_t}
+             "dtts_codec_hop": ctypes.c_int64, "dtts_codec_workspace_bytes": ctypes.c_size_t,
+             "dtts_decode_attention_workspace_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

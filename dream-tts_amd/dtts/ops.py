@@ -152,6 +152,44 @@ def kv_append(k, v, pos, k_cache, v_cache):
     call(fn, ptr(k), ptr(v), pp, ptr(k_cache), ptr(v_cache), b, n_kv, hd, k_cache.shape[2], stream_handle())
 
 
+# ---------------------------------------------------------------- f-1 decode attention
+
+def decode_attention(q, k, v, span, window_start=0, out=None, workspace=None):
+    """attn::decode_attention (crates/tts-nn/src/attn.rs:18-73): q [b, n_kv, gqa, D] f32 (scale
+    folded in), caches k, v [b, n_kv, cap, D] (f16 or f32, read in place) -> [b, n_kv, gqa, D] f32
+    over positions [window_start, span). span and window_start are one int for the whole batch,
+    as in the reference, or one per lane. `workspace` (a device byte tensor of at least
+    decode_attention_workspace_bytes) lets long spans split over workgroups; allocated here when
+    not given."""
+    import numpy as np
+
+    _check(q, "decode_attention", (_F32,), "q")
+    _check(k, "decode_attention", (_F16, _F32), "k")
+    _check(v, "decode_attention", (k.dtype,), "v")
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise DttsError(f"decode_attention: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    b, n_kv, gqa, hd = q.shape
+    if tuple(k.shape[:2]) != (b, n_kv) or k.shape[3] != hd:
+        raise DttsError(f"decode_attention: cache {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    sp, spp = _pos_array(np.broadcast_to(np.asarray(span, np.int32), (b,)), b, "decode_attention")
+    ws, wsp = _pos_array(np.broadcast_to(np.asarray(window_start, np.int32), (b,)), b, "decode_attention")
+    y = torch.empty_like(q) if out is None else out
+    if workspace is None:
+        need = decode_attention_workspace_bytes(b, n_kv, gqa, hd, int(np.max(sp - ws)) if b else 0)
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    fn = "dtts_decode_attention_f16" if k.dtype == _F16 else "dtts_decode_attention_f32"
+    call(fn, ptr(q), ptr(k), ptr(v), ptr(y), b, n_kv, gqa, hd, k.shape[2], spp, wsp, ptr(workspace),
+         workspace.numel(), stream_handle())
+    return y
+
+
+def decode_attention_workspace_bytes(b, n_kv, gqa, head_dim, max_window):
+    """Workspace bytes decode_attention splits spans of up to max_window positions with."""
+    from ._lib import lib as _l
+
+    return int(_l().dtts_decode_attention_workspace_bytes(b, n_kv, gqa, head_dim, max_window))
+
+
 # ---------------------------------------------------------------- a12-a15 projections
 
 def _mat(t, name, what, dtype):

@@ -245,6 +245,33 @@ int dtts_kv_append_f16(const dtts_f16 *k, const dtts_f16 *v, const int32_t *pos,
                        dtts_f16 *kcache, dtts_f16 *vcache, int64_t b, int64_t n_kv,
                        int64_t head_dim, int64_t cap, hipStream_t stream);
 
+/* ------------------------------------------------------------------ f-1 decode attention */
+
+/* Decode attention reading the KV cache in place: replaces attn::decode_attention
+ * (crates/tts-nn/src/attn.rs:18-73), whose CPU path (Scores, softmax_last_dim, Weighted:
+ * attn.rs:85-126, 62, 189-226) defines the result. q [b, n_kv, gqa, D] f32 with any scale already
+ * folded in; caches [b, n_kv, cap, D] (f16, or f32 for the _f32 form); out [b, n_kv, gqa, D] f32,
+ * caller-allocated: out[b, h, g, :] = sum_p softmax_p(q[b,h,g] . k[b,h,p]) v[b,h,p] over
+ * p in [window_start[b], span[b]). span and window_start are HOST int32[b] arrays (window_start
+ * may be NULL: 0); the reference's one span and window start per batch are the case of equal
+ * entries. Checked before anything is enqueued: span <= cap (attn.rs:31), window_start < span.
+ * D in {64, 128}, gqa in {1, 2, 4, 8}, b <= 256. The caches are only read.
+ * workspace (device, 16-byte aligned) may be NULL; given at least
+ * dtts_decode_attention_workspace_bytes(b, n_kv, gqa, D, max_b(span - window_start)) bytes, long
+ * spans are split over several workgroups and merged by a second launch (the reference has no
+ * such argument: its op allocates; a shim passes a cached buffer). Bytes needed are 0 when no
+ * window exceeds 256 positions. */
+size_t dtts_decode_attention_workspace_bytes(int64_t b, int64_t n_kv, int64_t gqa,
+                                             int64_t head_dim, int64_t max_window);
+int dtts_decode_attention_f16(const float *q, const dtts_f16 *kcache, const dtts_f16 *vcache,
+                              float *out, int64_t b, int64_t n_kv, int64_t gqa, int64_t head_dim,
+                              int64_t cap, const int32_t *span, const int32_t *window_start,
+                              void *workspace, size_t ws_bytes, hipStream_t stream);
+int dtts_decode_attention_f32(const float *q, const float *kcache, const float *vcache, float *out,
+                              int64_t b, int64_t n_kv, int64_t gqa, int64_t head_dim, int64_t cap,
+                              const int32_t *span, const int32_t *window_start, void *workspace,
+                              size_t ws_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------ a12-a14 f16 projections */
 
 /* Decode-shape f16 GEMM, f32 accumulation and output: C[m, n] = A[m, k] . B. Replaces

@@ -339,6 +339,23 @@ def kv_append_f16(k_bits, v_bits, pos, kcache, vcache):
 
 # ---------------------------------------------------------------- GEMMs
 
+def decode_attention_f32(q, k, v, span, window_start=0):
+    """attn::decode_attention's CPU path (crates/tts-nn/src/attn.rs:18-73, 85-126, 189-226).
+    q [b, n_kv, gqa, D] f32; caches [b, n_kv, cap, D] as f16 bit patterns (uint16) or f32; span
+    and window_start one int or one per lane. Returns [b, n_kv, gqa, D] f32."""
+    q = _f32(q)
+    b, n_kv, gqa, hd = q.shape
+    kv_f16 = 1 if np.asarray(k).dtype == np.uint16 else 0
+    k = _u16(k) if kv_f16 else _f32(k)
+    v = _u16(v) if kv_f16 else _f32(v)
+    sp = np.ascontiguousarray(np.broadcast_to(np.asarray(span, np.int32), (b,)))
+    ws = np.ascontiguousarray(np.broadcast_to(np.asarray(window_start, np.int32), (b,)))
+    out = np.empty_like(q)
+    lib().or_decode_attention_f32(_ptr(q), _ptr(k), _ptr(v), ctypes.c_int(kv_f16), _ptr(out), _I64(b), _I64(n_kv),
+                                  _I64(gqa), _I64(hd), _I64(k.shape[2]), _ptr(sp), _ptr(ws))
+    return out
+
+
 def gemm_f16_f32acc(a_bits, b_kn_bits):
     a, b = _u16(a_bits), _u16(b_kn_bits)
     m, k = a.shape

@@ -661,6 +661,55 @@ void or_kv_append_f16(const uint16_t *k, const uint16_t *v, const int32_t *pos,
         }
 }
 
+/* ------------------------------------------------------------------ f-1 decode attention */
+
+/* attn::decode_attention's CPU path (crates/tts-nn/src/attn.rs:18-73): Scores::cpu_fwd
+ * (attn.rs:85-126: -inf outside [window_start, span), else the d-ordered f32 dot q.k with f16
+ * cache values widened), candle_nn::ops::softmax_last_dim (called at attn.rs:62; candle-nn 0.10.2,
+ * not vendored: max over the row, exp(x - max), their sum in order, each divided by the sum), and
+ * Weighted::cpu_fwd (attn.rs:189-226: dst[d] += p * v[p][d] in position order over [0, span)).
+ * q [b, n_kv, gqa, D]; caches [b, n_kv, cap, D] as f16 bits (kv_f16 = 1) or f32; span and
+ * window start per lane. */
+static float or_cache_at(const void *c, int kv_f16, int64_t i) {
+    return kv_f16 ? or_f16_to_f32(((const uint16_t *)c)[i]) : ((const float *)c)[i];
+}
+
+void or_decode_attention_f32(const float *q, const void *kc, const void *vc, int kv_f16, float *out,
+                             int64_t b, int64_t n_kv, int64_t gqa, int64_t hd, int64_t cap,
+                             const int32_t *span, const int32_t *wstart) {
+#pragma omp parallel for schedule(static)
+    for (int64_t bh = 0; bh < b * n_kv; ++bh) {
+        const int64_t bi = bh / n_kv;
+        const int64_t sp = span[bi], ws = wstart ? wstart[bi] : 0;
+        float *sc = (float *)malloc(sizeof(float) * (size_t)(sp > 0 ? sp : 1));
+        for (int64_t g = 0; g < gqa; ++g) {
+            const float *qr = q + (bh * gqa + g) * hd;
+            for (int64_t p = 0; p < sp; ++p) {
+                if (p < ws) {
+                    sc[p] = -INFINITY;
+                    continue;
+                }
+                float acc = 0.0f;
+                for (int64_t d = 0; d < hd; ++d) acc += qr[d] * or_cache_at(kc, kv_f16, (bh * cap + p) * hd + d);
+                sc[p] = acc;
+            }
+            float mx = -INFINITY;
+            for (int64_t p = 0; p < sp; ++p) mx = sc[p] > mx ? sc[p] : mx;
+            float sum = 0.0f;
+            for (int64_t p = 0; p < sp; ++p) {
+                sc[p] = expf(sc[p] - mx);
+                sum += sc[p];
+            }
+            for (int64_t p = 0; p < sp; ++p) sc[p] /= sum;
+            float *o = out + (bh * gqa + g) * hd;
+            for (int64_t d = 0; d < hd; ++d) o[d] = 0.0f;
+            for (int64_t p = 0; p < sp; ++p)
+                for (int64_t d = 0; d < hd; ++d) o[d] += sc[p] * or_cache_at(vc, kv_f16, (bh * cap + p) * hd + d);
+        }
+        free(sc);
+    }
+}
+
 /* ------------------------------------------------------------------ a12-a14 */
 
 /* `[m,k] f16 x [k,n] f16 -> [m,n] f32` with f32 accumulation in k order: the arithmetic

@@ -107,6 +107,11 @@ void or_kv_append_f16(const uint16_t *k, const uint16_t *v, const int32_t *pos,
                       uint16_t *kcache, uint16_t *vcache, int64_t b, int64_t n_kv,
                       int64_t head_dim, int64_t cap);
 
+/* ---- f-1 decode attention over the KV cache ---- */
+void or_decode_attention_f32(const float *q, const void *kc, const void *vc, int kv_f16, float *out,
+                             int64_t b, int64_t n_kv, int64_t gqa, int64_t hd, int64_t cap,
+                             const int32_t *span, const int32_t *wstart);
+
 /* ---- a12-a14 f16 projections ---- */
 void or_gemm_f16_f32acc(const uint16_t *a, const uint16_t *b_kn, float *c, int64_t m, int64_t k,
                         int64_t n);
