@@ -223,10 +223,15 @@ def workload_cfg3(dev, args):
     hh = torch.randn((m, 3072), device=dev, generator=gen).half()
     from dtts import ops
 
+    ws = torch.empty(max(ops.gemm_workspace_bytes(m, 1024, 4096), ops.gemm_workspace_bytes(m, 1024, 3072, True),
+                         ops.gemm_workspace_bytes(m, 3072, 1024), 1), dtype=torch.uint8, device=dev)
+    y_qkv = torch.empty((m, 4096), dtype=torch.float32, device=dev)
+    y_gu = torch.empty((m, 3072), dtype=torch.float32, device=dev)
+    y_dn = torch.empty((m, 1024), dtype=torch.float32, device=dev)
     runs = {
-        "qkv_48x1024x4096": (lambda: [ops.matmul_nt(x, w) for w in w_qkv], 1024 * 4096),
-        "gateup_silu_48x1024x6144": (lambda: [ops.gateup_silu(x, w) for w in w_gu], 1024 * 6144),
-        "down_48x3072x1024": (lambda: [ops.matmul_nt(hh, w) for w in w_dn], 3072 * 1024),
+        "qkv_48x1024x4096": (lambda: [ops.matmul_nt(x, w, ws, y_qkv) for w in w_qkv], 1024 * 4096),
+        "gateup_silu_48x1024x6144": (lambda: [ops.gateup_silu(x, w, ws, y_gu) for w in w_gu], 1024 * 6144),
+        "down_48x3072x1024": (lambda: [ops.matmul_nt(hh, w, ws, y_dn) for w in w_dn], 3072 * 1024),
     }
     res, tot_ms, tot_bytes = {}, 0.0, 0.0
     for name, (fn, kn) in runs.items():

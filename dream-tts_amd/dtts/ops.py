@@ -210,19 +210,32 @@ def skinny_matmul(a, b):
     return c
 
 
-def matmul_nt(a, w):
-    """[m, k] f16 x [n, k]^T f16 -> [m, n] f32 (Proj::Half on the checkpoint's [out, in] weight)."""
+def gemm_workspace_bytes(m, k, n, gateup=False):
+    """Workspace bytes matmul_nt (gateup=False, n outputs) or gateup_silu (n = ffn) split k with."""
+    from ._lib import lib as _l
+
+    return int(_l().dtts_gemm_f16_workspace_bytes(m, k, n, 1 if gateup else 0))
+
+
+def _workspace(t, nbytes):
+    return t if t is not None else torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+
+
+def matmul_nt(a, w, workspace=None, out=None):
+    """[m, k] f16 x [n, k]^T f16 -> [m, n] f32 (Proj::Half on the checkpoint's [out, in] weight).
+    `workspace`: a device byte tensor of gemm_workspace_bytes(m, k, n) (allocated when not given)."""
     _mat(a, "matmul_nt", "a", _F16)
     _mat(w, "matmul_nt", "w", _F16)
     m, k = a.shape
     if w.shape[1] != k:
         raise DttsError(f"matmul_nt: {k} != {w.shape[1]}")
-    c = torch.empty((m, w.shape[0]), dtype=_F32, device=a.device)
-    call("dtts_gemm_f16_nt", ptr(a), ptr(w), ptr(c), m, k, w.shape[0], stream_handle())
+    c = torch.empty((m, w.shape[0]), dtype=_F32, device=a.device) if out is None else out
+    ws = _workspace(workspace, gemm_workspace_bytes(m, k, w.shape[0]))
+    call("dtts_gemm_f16_nt", ptr(a), ptr(w), ptr(c), m, k, w.shape[0], ptr(ws), ws.numel(), stream_handle())
     return c
 
 
-def gateup_silu(a, w_gu):
+def gateup_silu(a, w_gu, workspace=None, out=None):
     """silu(a . Wg^T) * (a . Wu^T), w_gu [2*ffn, k] = gate rows then up rows; f32 [m, ffn]."""
     _mat(a, "gateup_silu", "a", _F16)
     _mat(w_gu, "gateup_silu", "w_gu", _F16)
@@ -230,8 +243,9 @@ def gateup_silu(a, w_gu):
     ffn = w_gu.shape[0] // 2
     if w_gu.shape[1] != k or w_gu.shape[0] != 2 * ffn:
         raise DttsError("gateup_silu: w_gu must be [2*ffn, k]")
-    y = torch.empty((m, ffn), dtype=_F32, device=a.device)
-    call("dtts_gemm_f16_gateup_silu", ptr(a), ptr(w_gu), ptr(y), m, k, ffn, stream_handle())
+    y = torch.empty((m, ffn), dtype=_F32, device=a.device) if out is None else out
+    ws = _workspace(workspace, gemm_workspace_bytes(m, k, ffn, True))
+    call("dtts_gemm_f16_gateup_silu", ptr(a), ptr(w_gu), ptr(y), m, k, ffn, ptr(ws), ws.numel(), stream_handle())
     return y
 
 

@@ -282,17 +282,23 @@ int dtts_decode_attention_f32(const float *q, const float *kcache, const float *
  *   dtts_gemm_f16_skinny: B = b_kn [k, n], the reference's own operand (Proj::Half's W_t,
  *     crates/tts-nn/src/lib.rs:516-529);
  *   dtts_gemm_f16_nt: B = w_nk^T with w_nk [n, k], the checkpoint's [out, in] layout, so no
- *     load-time transpose is needed; the faster of the two. */
+ *     load-time transpose is needed; the faster of the two. Its workspace (device, 16-byte
+ *     aligned; NULL allowed) lets a projection with few output columns split k over
+ *     workgroups as well, the splits' partials summed in split order by a second launch: give
+ *     at least dtts_gemm_f16_workspace_bytes(m, k, n, 0) bytes (0 when no split is needed). */
 int dtts_gemm_f16_skinny(const dtts_f16 *a, const dtts_f16 *b_kn, float *c, int64_t m, int64_t k,
                          int64_t n, hipStream_t stream);
+size_t dtts_gemm_f16_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t gateup);
 int dtts_gemm_f16_nt(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k,
-                     int64_t n, hipStream_t stream);
+                     int64_t n, void *workspace, size_t ws_bytes, hipStream_t stream);
 
 /* gate|up projection with SwiGLU fused: y[m, j] = silu(g) * u, g = A . Wg^T, u = A . Wu^T, where
  * w_gu [2*ffn, k] holds gate's rows then up's (f16, [out, in]). Replaces
- * swiglu_mul(gate.forward(x), up.forward(x)) at crates/qwen3tts/src/qwen3.rs:454-457. y f32. */
+ * swiglu_mul(gate.forward(x), up.forward(x)) at crates/qwen3tts/src/qwen3.rs:454-457. y f32.
+ * Workspace as for dtts_gemm_f16_nt, sized by dtts_gemm_f16_workspace_bytes(m, k, ffn, 1). */
 int dtts_gemm_f16_gateup_silu(const dtts_f16 *a, const dtts_f16 *w_gu, float *y, int64_t m,
-                              int64_t k, int64_t ffn, hipStream_t stream);
+                              int64_t k, int64_t ffn, void *workspace, size_t ws_bytes,
+                              hipStream_t stream);
 
 /* fused::swiglu_mul / SwigluMul (crates/tts-nn/src/fused.rs:289-385): y = (g / (1 + exp(-g))) * u,
  * f32, n elements. */

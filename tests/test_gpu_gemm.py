@@ -42,6 +42,25 @@ def test_gemm_nt_and_kn_match_oracle(dev, m, k, n):
         assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
 
 
+@pytest.mark.parametrize("m,k,n,gateup", [(48, 3072, 1024, False), (40, 6144, 1024, False), (48, 3072, 512, True),
+                                           (8, 8192, 256, False)])
+def test_gemm_k_split_over_workgroups_matches_single_pass(dev, m, k, n, gateup):
+    """Few output columns: with a workspace, k splits over workgroups too and a second launch sums
+    the splits in order; without one, each column group's workgroup takes all of k."""
+    need = ops.gemm_workspace_bytes(m, k, n, gateup)
+    assert need > 0
+    a, w = _ab(82, m, k, 2 * n if gateup else n)
+    ad, wd = to_dev(a, dev), to_dev(w, dev)
+    fn = ops.gateup_silu if gateup else ops.matmul_nt
+    split = to_host(fn(ad, wd, torch.empty(need, dtype=torch.uint8, device=dev)))
+    single = to_host(fn(ad, wd, torch.empty(1, dtype=torch.uint8, device=dev)))
+    gu = oracle.gemm_f16_f32acc(a, np.ascontiguousarray(w.T))
+    want = oracle.swiglu_mul_f32(gu[:, :n].copy(), gu[:, n:].copy()) if gateup else gu
+    for got in (split, single):
+        ab, rl = rel(got, want)
+        assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
+
+
 @pytest.mark.parametrize("m,k,ffn", [(48, 1024, 3072), (8, 1024, 3072), (48, 2048, 6144), (3, 64, 16)])
 def test_gateup_silu_matches_oracle(dev, m, k, ffn):
     a, w = _ab(81, m, k, 2 * ffn)
