@@ -76,6 +76,10 @@ struct RuCfg {
     static_assert(THREADS % SEGS == 0, "a thread's window segments share one channel group");
     static_assert((KMAX * C) % RPI == 0 && RPI % 32 == 0, "whole direct-load instructions per tap");
     static_assert(C * W2_PITCH * 2 <= 2 * STAGE, "W2 fits the stages");
+    // output staging: a 32-row block per wave, rows of C + 4 halves (an odd multiple of 4 bytes
+    // over 64 banks puts the 8-byte writes of 32 consecutive rows on distinct bank pairs)
+    static constexpr int OPITCH = C + 4;
+    static_assert(NW * 32 * OPITCH * 2 <= 2 * STAGE, "output staging fits the stages");
 };
 
 // C = 96: two 32-position blocks per wave, two workgroups per CU. C = 192: one block per wave
@@ -401,31 +405,62 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, h2[i][kk], acc[i][j], 0, 0, 0);
         }
 
-    // y = f16(acc + u), y_pre, SnakeBeta_out: four consecutive channels per access
+    // y = f16(acc + u), y_pre, SnakeBeta_out. The values are made in the transposed layout (a
+    // lane: one position, runs of four channels) and go out through the wave's own LDS block, so
+    // every store moves 16 coalesced bytes of a row (a store of the 8-byte runs would touch 32
+    // rows per instruction). The stages are free once every wave's conv2 has read W2.
+    __syncthreads();
+    half_t *O = reinterpret_cast<half_t *>(smem) + wave * 32 * Cfg::OPITCH;
+    constexpr int RSEG = C / 8;                 // 16-byte segments per row
+    constexpr int NSEG = 32 * RSEG / 64;        // per lane per 32-row block
+    static_assert((32 * RSEG) % 64 == 0, "row segments split evenly over the lanes");
+    auto flush = [&](int i, half_t *dst) {      // the block's rows from O to dst, 16 bytes a lane
+        wave_lds_order();
+        // four segments in flight at a time: the values of the block are still live here
+#pragma unroll 1
+        for (int u0 = 0; u0 < NSEG; u0 += 4) {
+#pragma unroll
+            for (int u = u0; u < u0 + 4 && u < NSEG; ++u) {
+                const int sgi = lane + 64 * u;
+                const int r = sgi / RSEG, c8 = sgi - (sgi / RSEG) * RSEG;
+                const int pos = l0 + wave * Cfg::WP + 32 * i + r;
+                const half8_t v = *reinterpret_cast<const half8_t *>(O + r * Cfg::OPITCH + c8 * 8);
+                if (pos < q.L)
+                    *reinterpret_cast<half8_t *>(dst + (static_cast<int64_t>(lane_idx) * q.L + pos) * C + c8 * 8) = v;
+            }
+        }
+        wave_lds_order();  // the reads precede the next block's writes
+    };
+    // y_pre = f16(acc + u) of run (i, j, g), and y = SnakeBeta_out(y_pre) (or y_pre)
+    auto y_run = [&](int i, int j, int g, bool snake) {
+        const half4_v uu = ures[i][j][g];
+        half4_v yv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            yv[e] = static_cast<half_t>(__builtin_fmaf(static_cast<float>(uu[e]), 1.0f, acc[i][j][4 * g + e]));
+        if (snake) {
+            const int ch = 32 * j + 8 * g + 4 * hf;
+            const float4_t ka = *reinterpret_cast<const float4_t *>(tab + 6 * C + ch);
+            const float4_t rr = *reinterpret_cast<const float4_t *>(tab + 7 * C + ch);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) yv[e] = snake_h(yv[e], ka[e], rr[e]);
+        }
+        *reinterpret_cast<half4_v *>(O + l32 * Cfg::OPITCH + 32 * j + 8 * g + 4 * hf) = yv;
+    };
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-        const int pos = l0 + prow + 32 * i;
-        if (pos >= q.L) continue;
-        const int64_t rowoff = (static_cast<int64_t>(lane_idx) * q.L + pos) * C;
+        if (q.y_pre) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) y_run(i, j, g, false);
+            flush(i, q.y_pre);
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int ch = 32 * j + 8 * g + 4 * hf;
-                const half4_v uu = ures[i][j][g];
-                half4_v yv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    yv[e] = static_cast<half_t>(__builtin_fmaf(static_cast<float>(uu[e]), 1.0f, acc[i][j][4 * g + e]));
-                if (q.y_pre) *reinterpret_cast<half4_v *>(q.y_pre + rowoff + ch) = yv;
-                if (q.a_out) {
-                    const float4_t ka = *reinterpret_cast<const float4_t *>(tab + 6 * C + ch);
-                    const float4_t rr = *reinterpret_cast<const float4_t *>(tab + 7 * C + ch);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) yv[e] = snake_h(yv[e], ka[e], rr[e]);
-                }
-                *reinterpret_cast<half4_v *>(q.y + rowoff + ch) = yv;
-            }
+            for (int g = 0; g < 4; ++g) y_run(i, j, g, q.a_out != nullptr);
+        flush(i, q.y);
     }
 }
 
