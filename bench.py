@@ -273,6 +273,53 @@ def workload_cfg4(dev, args):
                  "best weight-streaming GB/s", best, "GB/s", res, {"dtype": "int8/f16"})
 
 
+def workload_stack(dev, args):
+    """Row f-2: one decode step of the talker (28 layers) and of the code predictor (5 layers) at 48
+    lanes, each lane at its own position, f16 weights and caches, eager and graph-replayed."""
+    import numpy as np
+    import torch
+
+    from dtts import stack, synth
+
+    lanes = 48
+    res = {}
+    best = None
+    for name, geo, cap in (("talker", stack.TALKER, 2048), ("predictor", stack.PREDICTOR, 17)):
+        from dataclasses import replace
+
+        geo = replace(geo, capacity=cap)
+        layers, fn = stack.random_device_weights(geo, dev, seed=0)
+        st = stack.Stack(geo, layers, fn, dev)
+        state = st.new_state(lanes, cap)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1)
+        for t in state.k + state.v:
+            t.copy_(torch.randn(t.shape, generator=gen, device=dev))
+        x = torch.randn((lanes, geo.dim), generator=gen, device=dev)
+        out = torch.empty_like(x)
+        pos = synth.randint(0, f"stack.{name}.pos", (lanes,), 0, cap - 1).astype(np.int32)
+        ws = st.workspace(lanes, cap)
+        t_eager = _time(lambda: st.decode(x, state, pos, out=out, workspace=ws), reps=10)
+        t_graph = _time(lambda: st.decode(x, state, pos, out=out, graph=True, workspace=ws), reps=20)
+        if not torch.isfinite(out).all():
+            raise SystemExit(f"bench: non-finite {name} output")
+        wbytes = geo.layers * geo.weight_bytes_per_layer()
+        kv = geo.layers * 2 * 2 * geo.n_kv * geo.head_dim * int((pos.astype(np.int64) + 1).sum())
+        res[name] = {"layers": geo.layers, "cap": cap, "ms_graph": round(t_graph, 4), "ms_eager": round(t_eager, 4),
+                     "tokens_per_s": round(lanes / (t_graph / 1e3), 1), "weight_bytes": wbytes, "kv_bytes": kv,
+                     "gbs": round((wbytes + kv) / t_graph / 1e6, 1),
+                     "us_per_layer": round(t_graph * 1e3 / geo.layers, 2)}
+        if best is None:
+            best = res[name]
+        del st, state, layers
+        torch.cuda.empty_cache()
+    return _line("row f-2: decoder-stack decode step, 48 lanes at per-lane positions (talker 28 layers, cap 2048; "
+                 "code predictor 5 layers), f16 weights and KV cache, one HIP graph per step",
+                 "talker decode tokens/s at 48 lanes", best["tokens_per_s"], "tokens/s", res,
+                 {"dtype": "f16 weights / f32 activations",
+                  "frac_hbm_peak": round(best["gbs"] / PEAK_HBM_GBS, 4)})
+
+
 # ---------------------------------------------------------------- rocprofv3 counter digest
 
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: a mul kernel reading and writing 1 GiB
@@ -321,7 +368,8 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
     return out
 
 
-WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4}
+WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
+             "stack": workload_stack}
 
 
 def main():
@@ -338,8 +386,9 @@ def main():
                     help="digest rocprofv3 FETCH_SIZE / WRITE_SIZE runs into per-kernel traffic (no GPU)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "codec_config5_pmc.json"),
                     help="per-kernel traffic from --pmc-summary, reported in roofline.traffic")
-    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "all"],
-                    help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops")
+    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "cfg5", "all"],
+                    help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops; stack "
+                         "times the decoder-stack decode step")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -360,7 +409,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.workload != "cfg5":
-        for w in (["cfg1", "cfg2", "cfg3", "cfg4"] if args.workload == "all" else [args.workload]):
+        for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack"] if args.workload == "all" else [args.workload]):
             print(json.dumps(WORKLOADS[w](dev, args)), flush=True)
         if args.workload != "all":
             return

@@ -1,260 +1,9 @@
-// Decode attention over the KV cache in place (attn::decode_attention,
-// crates/tts-nn/src/attn.rs:18-73; the CPU path it is held to is Scores, softmax_last_dim and
-// Weighted, attn.rs:85-126, 62, 189-226).
-//
-//   q     [b, n_kv, gqa, D] f32, any scale already folded in
-//   cache [b, n_kv, cap, D] f16 or f32 (k and v)
-//   out   [b, n_kv, gqa, D] f32
-//   lane i attends to positions [window_start[i], span[i]); the reference's single span and
-//   window start are the case where every lane has the same ones
-//
-// One workgroup per (lane, kv head): the cache rows of the span are read once, for all gqa query
-// heads that share them. The span is split over groups of 16 lanes (4 per wave), each group
-// taking every G-th position; a lane of a group owns D/16 dimensions: the score is a 16-lane
-// shuffle reduction, and each group keeps a running softmax state (max m, sum l, weighted sum of
-// v) updated position by position (online softmax). The groups' states are combined through LDS
-// at the end: out = sum_k acc_k e^(m_k - M) / sum_k l_k e^(m_k - M), M the largest m_k. This is
-// the reference's exp(s - max) / sum weighting, regrouped; its K and V traffic is one pass.
-// HBM-bound: 2 * D * (span - window_start) cache bytes per (lane, kv head).
-//
-// Long spans are split (flash-decoding): with a workspace, each workgroup takes kChunk positions
-// of one (lane, kv head) and leaves its combined state (its max, its sum, its weighted v sum) in
-// the workspace, and a second kernel merges a lane's chunks the same way. Without one, a
-// workgroup takes the whole span.
-#include <cmath>
-
-#include "common.hpp"
+// Decode attention entry points: host-side checks and the launch plan; the kernels are in
+// attn.hpp.
+#include "attn.hpp"
 
 namespace dtts {
 namespace {
-
-constexpr int kAttnMaxLanes = 256;
-
-struct Spans {
-    int32_t lo[kAttnMaxLanes];  // window start
-    int32_t hi[kAttnMaxLanes];  // span (exclusive end)
-};
-
-template <typename T>
-struct CacheRow;  // D/16 consecutive elements of one cache row, as f32
-
-template <>
-struct CacheRow<half_t> {
-    template <int E>
-    __device__ __forceinline__ static void load(const half_t *p, float (&out)[E]) {
-        static_assert(E == 8 || E == 4, "row slice");
-        if constexpr (E == 8) {
-            const half8_t v = *reinterpret_cast<const half8_t *>(p);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) out[e] = static_cast<float>(v[e]);
-        } else {
-            const half4_t v = *reinterpret_cast<const half4_t *>(p);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) out[e] = static_cast<float>(v[e]);
-        }
-    }
-};
-
-template <>
-struct CacheRow<float> {
-    template <int E>
-    __device__ __forceinline__ static void load(const float *p, float (&out)[E]) {
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            const float4_t v = *reinterpret_cast<const float4_t *>(p + e);
-            out[e] = v[0];
-            out[e + 1] = v[1];
-            out[e + 2] = v[2];
-            out[e + 3] = v[3];
-        }
-    }
-};
-
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-constexpr int kChunk = 256;  // positions per workgroup when a span is split
-
-// Chunks of a lane's window [lo, hi) when split.
-__device__ __host__ inline int chunks_of(int lo, int hi) { return (hi - lo + kChunk - 1) / kChunk; }
-
-// T: cache element type; D: head dim (64 or 128); GQA: query heads per kv head; NW: waves.
-// part == nullptr: blockIdx.y is 0 and the workgroup writes out. Otherwise blockIdx.y is a chunk
-// of kChunk positions, and the workgroup writes its state to part (rows of D + 2 floats: the
-// weighted v sum, the weight sum, the max score) at [(bh * max_chunks + chunk) * GQA + g].
-template <typename T, int D, int GQA, int NW>
-__global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, const T *kc, const T *vc, float *out,
-                                                              float *part, int max_chunks, int n_kv, int cap,
-                                                              Spans sp) {
-    constexpr int E = D / 16;     // dimensions per lane
-    constexpr int G = NW * 4;     // position groups
-    constexpr int UNROLL = 4;     // positions whose rows are in flight per group
-    __shared__ float sm_m[G][GQA], sm_l[G][GQA];
-    __shared__ __attribute__((aligned(16))) float sm_acc[G][GQA][D];
-    const int bh = blockIdx.x;  // lane * n_kv + kv head
-    const int lane_idx = bh / n_kv;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int grp = wave * 4 + ((tid & 63) >> 4);
-    const int j = tid & 15;
-    int lo = sp.lo[lane_idx], hi = sp.hi[lane_idx];
-    if (part) {
-        if (static_cast<int>(blockIdx.y) >= chunks_of(lo, hi)) return;  // the whole workgroup
-        lo += blockIdx.y * kChunk;
-        hi = hi < lo + kChunk ? hi : lo + kChunk;
-    }
-
-    float qv[GQA][E];
-#pragma unroll
-    for (int g = 0; g < GQA; ++g) {
-        const float *qp = q + (static_cast<int64_t>(bh) * GQA + g) * D + j * E;
-#pragma unroll
-        for (int e = 0; e < E; ++e) qv[g][e] = qp[e];
-    }
-    float m[GQA], l[GQA], acc[GQA][E];
-#pragma unroll
-    for (int g = 0; g < GQA; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[g][e] = 0.0f;
-    }
-    const T *kb = kc + static_cast<int64_t>(bh) * cap * D + j * E;
-    const T *vb = vc + static_cast<int64_t>(bh) * cap * D + j * E;
-    auto step = [&](const float (&kr)[E], const float (&vr)[E]) {
-#pragma unroll
-        for (int g = 0; g < GQA; ++g) {
-            float s = 0.0f;
-#pragma unroll
-            for (int e = 0; e < E; ++e) s += qv[g][e] * kr[e];
-            s = group16_sum(s);
-            const float mn = fmaxf(m[g], s);
-            const float c = __builtin_expf(m[g] - mn);  // 0 on the group's first position
-            const float w = __builtin_expf(s - mn);
-            l[g] = l[g] * c + w;
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[g][e] = acc[g][e] * c + w * vr[e];
-            m[g] = mn;
-        }
-    };
-    // UNROLL positions of the group at a time: their K and V rows are all requested before the
-    // first is used (the group's 16 lanes read 16 * E contiguous elements per row)
-    int p = lo + grp;
-    for (; p + (UNROLL - 1) * G < hi; p += UNROLL * G) {
-        float kr[UNROLL][E], vr[UNROLL][E];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            CacheRow<T>::load(kb + static_cast<int64_t>(p + u * G) * D, kr[u]);
-            CacheRow<T>::load(vb + static_cast<int64_t>(p + u * G) * D, vr[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) step(kr[u], vr[u]);
-    }
-    for (; p < hi; p += G) {
-        float kr[E], vr[E];
-        CacheRow<T>::load(kb + static_cast<int64_t>(p) * D, kr);
-        CacheRow<T>::load(vb + static_cast<int64_t>(p) * D, vr);
-        step(kr, vr);
-    }
-
-    // combine the groups' states
-#pragma unroll
-    for (int g = 0; g < GQA; ++g) {
-#pragma unroll
-        for (int e = 0; e < E; e += 4)
-            *reinterpret_cast<float4_t *>(&sm_acc[grp][g][j * E + e]) =
-                float4_t{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
-        if (j == 0) {
-            sm_m[grp][g] = m[g];
-            sm_l[grp][g] = l[g];
-        }
-    }
-    __syncthreads();
-    for (int t = tid; t < GQA * D; t += NW * 64) {
-        const int g = t / D, d = t - (t / D) * D;
-        float mx = -INFINITY;
-#pragma unroll 4
-        for (int k = 0; k < G; ++k) mx = fmaxf(mx, sm_m[k][g]);
-        float den = 0.0f, num = 0.0f;
-#pragma unroll 4
-        for (int k = 0; k < G; ++k) {
-            const float f = __builtin_expf(sm_m[k][g] - mx);  // 0 for groups that saw no position
-            den += sm_l[k][g] * f;
-            num += sm_acc[k][g][d] * f;
-        }
-        if (part) {
-            float *pr = part + ((static_cast<int64_t>(bh) * max_chunks + blockIdx.y) * GQA + g) * (D + 2);
-            pr[d] = num;
-            if (d == 0) {
-                pr[D] = den;
-                pr[D + 1] = mx;
-            }
-        } else {
-            out[(static_cast<int64_t>(bh) * GQA + g) * D + d] = num / den;
-        }
-    }
-}
-
-// Merges the chunk states of each (lane, kv head): out = sum_c num_c e^(m_c - M) / sum_c den_c
-// e^(m_c - M), M the largest m_c, chunks in order.
-template <int D, int GQA>
-__global__ __launch_bounds__(256) void decode_attn_merge(const float *part, float *out, int max_chunks, int n_kv,
-                                                         Spans sp) {
-    const int bh = blockIdx.x;
-    const int lane_idx = bh / n_kv;
-    const int nch = chunks_of(sp.lo[lane_idx], sp.hi[lane_idx]);
-    for (int t = threadIdx.x; t < GQA * D; t += 256) {
-        const int g = t / D, d = t - (t / D) * D;
-        const float *pr = part + (static_cast<int64_t>(bh) * max_chunks * GQA + g) * (D + 2);
-        const int64_t stride = static_cast<int64_t>(GQA) * (D + 2);
-        float mx = -INFINITY;
-        for (int c = 0; c < nch; ++c) mx = fmaxf(mx, pr[c * stride + D + 1]);
-        float num = 0.0f, den = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-            const float f = __builtin_expf(pr[c * stride + D + 1] - mx);
-            num += pr[c * stride + d] * f;
-            den += pr[c * stride + D] * f;
-        }
-        out[(static_cast<int64_t>(bh) * GQA + g) * D + d] = num / den;
-    }
-}
-
-template <typename T, int D, int GQA>
-hipError_t launch_gqa(const float *q, const T *kc, const T *vc, float *out, float *part, int max_chunks, int64_t b,
-                      int64_t n_kv, int64_t cap, const Spans &sp, hipStream_t stream) {
-    const unsigned grid = static_cast<unsigned>(b * n_kv);
-    if (!part) {
-        decode_attn_kernel<T, D, GQA, 4><<<grid, 256, 0, stream>>>(q, kc, vc, out, nullptr, 0, static_cast<int>(n_kv),
-                                                                  static_cast<int>(cap), sp);
-        return hipGetLastError();
-    }
-    decode_attn_kernel<T, D, GQA, 4><<<dim3(grid, max_chunks), 256, 0, stream>>>(
-        q, kc, vc, out, part, max_chunks, static_cast<int>(n_kv), static_cast<int>(cap), sp);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    decode_attn_merge<D, GQA><<<grid, 256, 0, stream>>>(part, out, max_chunks, static_cast<int>(n_kv), sp);
-    return hipGetLastError();
-}
-
-template <typename T, int D>
-hipError_t launch_d(const float *q, const T *kc, const T *vc, float *out, float *part, int max_chunks, int64_t b,
-                    int64_t n_kv, int64_t gqa, int64_t cap, const Spans &sp, hipStream_t stream) {
-    switch (gqa) {
-        case 1: return launch_gqa<T, D, 1>(q, kc, vc, out, part, max_chunks, b, n_kv, cap, sp, stream);
-        case 2: return launch_gqa<T, D, 2>(q, kc, vc, out, part, max_chunks, b, n_kv, cap, sp, stream);
-        case 4: return launch_gqa<T, D, 4>(q, kc, vc, out, part, max_chunks, b, n_kv, cap, sp, stream);
-        default: return launch_gqa<T, D, 8>(q, kc, vc, out, part, max_chunks, b, n_kv, cap, sp, stream);
-    }
-}
-
-size_t workspace_bytes(int64_t b, int64_t n_kv, int64_t gqa, int64_t head_dim, int64_t max_window) {
-    if (b <= 0 || n_kv <= 0 || gqa <= 0 || head_dim <= 0 || max_window <= kChunk) return 0;
-    const int64_t chunks = (max_window + kChunk - 1) / kChunk;
-    return static_cast<size_t>(b * n_kv * chunks * gqa * (head_dim + 2)) * sizeof(float);
-}
 
 template <typename T>
 int decode_attention(const char *name, const float *q, const T *kc, const T *vc, float *out, int64_t b, int64_t n_kv,
@@ -273,7 +22,7 @@ int decode_attention(const char *name, const float *q, const T *kc, const T *vc,
                  name);
     DTTS_REQUIRE(aligned(q, 16) && aligned(kc, 16) && aligned(vc, 16) && aligned(out, 4), "%s: misaligned operand",
                  name);
-    Spans sp{};
+    HostSpans sp{};
     int64_t max_window = 0;
     for (int64_t i = 0; i < b; ++i) {
         const int32_t lo = window_start ? window_start[i] : 0;
@@ -281,12 +30,12 @@ int decode_attention(const char *name, const float *q, const T *kc, const T *vc,
                      (long long)cap);
         DTTS_REQUIRE(lo >= 0 && lo < span[i], "%s: lane %lld attends to the empty range [%d, %d)", name,
                      (long long)i, lo, span[i]);
-        sp.lo[i] = lo;
-        sp.hi[i] = span[i];
+        sp.sp.lo[i] = lo;
+        sp.sp.hi[i] = span[i];
         max_window = span[i] - lo > max_window ? span[i] - lo : max_window;
     }
     // split the spans when a workspace holds every chunk's state (and there is more than one)
-    const size_t need = workspace_bytes(b, n_kv, gqa, head_dim, max_window);
+    const size_t need = attn_workspace_bytes(b, n_kv, gqa, head_dim, max_window);
     float *part = nullptr;
     int max_chunks = 0;
     if (need > 0 && workspace && ws_bytes >= need) {
@@ -294,9 +43,7 @@ int decode_attention(const char *name, const float *q, const T *kc, const T *vc,
         part = static_cast<float *>(workspace);
         max_chunks = static_cast<int>((max_window + kChunk - 1) / kChunk);
     }
-    const hipError_t e =
-        head_dim == 128 ? launch_d<T, 128>(q, kc, vc, out, part, max_chunks, b, n_kv, gqa, cap, sp, stream)
-                        : launch_d<T, 64>(q, kc, vc, out, part, max_chunks, b, n_kv, gqa, cap, sp, stream);
+    const hipError_t e = launch_attention(q, kc, vc, out, part, max_chunks, b, n_kv, gqa, head_dim, cap, sp, stream);
     DTTS_HIP_CHECK(e, name);
     return DTTS_OK;
 }
@@ -306,7 +53,7 @@ int decode_attention(const char *name, const float *q, const T *kc, const T *vc,
 
 extern "C" size_t dtts_decode_attention_workspace_bytes(int64_t b, int64_t n_kv, int64_t gqa, int64_t head_dim,
                                                          int64_t max_window) {
-    return dtts::workspace_bytes(b, n_kv, gqa, head_dim, max_window);
+    return dtts::attn_workspace_bytes(b, n_kv, gqa, head_dim, max_window);
 }
 
 extern "C" int dtts_decode_attention_f16(const float *q, const dtts_f16 *kcache, const dtts_f16 *vcache, float *out,

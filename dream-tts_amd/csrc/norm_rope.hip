@@ -1,72 +1,11 @@
-// Per-step norm and position ops of the decode layer: RMSNorm, half-split RoPE, the fused
-// QK-norm + RoPE + KV-cache append, and the plain KV append.
-//
-// These are latency-bound at decode shapes (48 lanes): one wave per row (or per (lane, head)),
-// 16-byte loads, a wave-wide shuffle reduction, and no LDS. Per-lane positions come from the
-// host, are checked against the cache capacity before anything is enqueued, and travel in the
-// kernel arguments.
-//
-// Rounding: floating-point contraction is off for this file, so o = x1*c - x2*s rounds each
-// product before the subtraction, as the reference's CPU path does (hipcc would otherwise fuse
-// them into an FMA). f32 -> f16 stores round to nearest-even.
-#include <cmath>
-
-#include "common.hpp"
+// Per-step norm and position ops of the decode layer: the entry points, the plain RoPE and KV
+// append kernels. RMSNorm and the fused QK-norm + RoPE + append kernels are in norm_rope.hpp.
+#include "norm_rope.hpp"
 
 #pragma clang fp contract(off)
 
 namespace dtts {
 namespace {
-
-constexpr int kMaxLanes = 256;
-
-struct Positions {
-    int32_t p[kMaxLanes];
-};
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// ---------------------------------------------------------------- RMSNorm
-
-// One wave per row; lane j owns elements j, j+64, ...
-
-template <typename T>
-__global__ __launch_bounds__(256) void rms_norm_kernel(const T *x, const T *gamma, T *y, int rows, int dim, float eps) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const T *xr = x + static_cast<int64_t>(row) * dim;
-    T *yr = y + static_cast<int64_t>(row) * dim;
-    float ss = 0.0f;
-    for (int i = lane; i < dim; i += 64) {
-        const float v = static_cast<float>(xr[i]);
-        ss += v * v;
-    }
-    ss = wave_sum(ss);
-    const float m = sqrtf(ss / static_cast<float>(dim) + eps);
-    if constexpr (sizeof(T) == 2) {
-        // candle's f16 form: m rounded to f16, then (x / m) and (* gamma) each rounded to f16
-        const float mh = static_cast<float>(static_cast<half_t>(m));
-        for (int i = lane; i < dim; i += 64) {
-            const float q = static_cast<float>(static_cast<half_t>(static_cast<float>(xr[i]) / mh));
-            yr[i] = static_cast<half_t>(q * static_cast<float>(gamma[i]));
-        }
-    } else {
-        for (int i = lane; i < dim; i += 64) yr[i] = (xr[i] / m) * gamma[i];
-    }
-}
-
-// ---------------------------------------------------------------- RoPE
-
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
-    const float a = x1 * c, b = x2 * s, e = x2 * c, f = x1 * s;
-    o1 = a - b;
-    o2 = e + f;
-}
 
 // x, y [rows, heads, D]; thread per (row, head, i < D/2).
 template <typename T>
@@ -79,72 +18,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const T *x, const float *cos_
         const int64_t rh = e / half;
         const int row = static_cast<int>(rh / heads);
         const int64_t base = rh * hd;
-        const int p = pos.p[row];
+        const int p = pos.at(row);
         const float c = cos_t[static_cast<int64_t>(p) * half + i];
         const float s = sin_t[static_cast<int64_t>(p) * half + i];
         float o1, o2;
         rope_pair(static_cast<float>(x[base + i]), static_cast<float>(x[base + i + half]), c, s, o1, o2);
         y[base + i] = static_cast<T>(o1);
         y[base + i + half] = static_cast<T>(o2);
-    }
-}
-
-// ---------------------------------------------------------------- QK-norm + RoPE + append
-
-// One wave per (lane b, head h) with h < heads (query) or heads <= h < heads + n_kv (key; the
-// wave also writes v). Lane j holds dims j and j + 64 when D = 128 (any even D <= 128: lane j
-// holds pair j < D/2).
-template <typename T>
-__global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float *norms, const float *cos_t,
-                                                      const float *sin_t, Positions pos, T *q_out, float *k_out,
-                                                      half_t *kc, half_t *vc, int b, int heads, int n_kv, int hd,
-                                                      int cap, float eps) {
-    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int per = heads + n_kv;
-    if (wid >= b * per) return;
-    const int bi = wid / per;
-    const int h = wid - bi * per;
-    const int half = hd / 2;
-    const int width = (heads + 2 * n_kv) * hd;
-    const T *row = qkv + static_cast<int64_t>(bi) * width;
-    const T *src = row + h * hd;
-    const bool is_q = h < heads;
-    const float *w = norms + (is_q ? 0 : hd);
-    const bool act = lane < half;
-    float x1 = 0.0f, x2 = 0.0f;
-    if (act) {
-        x1 = static_cast<float>(src[lane]);
-        x2 = static_cast<float>(src[lane + half]);
-    }
-    float ss = wave_sum(x1 * x1 + x2 * x2);
-    const float m = sqrtf(ss / static_cast<float>(hd) + eps);
-    if (!act) return;
-    // candle's rms_norm: (x / m) * w
-    const float y1 = (x1 / m) * w[lane];
-    const float y2 = (x2 / m) * w[lane + half];
-    const int p = pos.p[bi];
-    const float c = cos_t[static_cast<int64_t>(p) * half + lane];
-    const float s = sin_t[static_cast<int64_t>(p) * half + lane];
-    float o1, o2;
-    rope_pair(y1, y2, c, s, o1, o2);
-    if (is_q) {
-        T *dq = q_out + (static_cast<int64_t>(bi) * heads + h) * hd;
-        dq[lane] = static_cast<T>(o1);
-        dq[lane + half] = static_cast<T>(o2);
-        return;
-    }
-    const int kh = h - heads;
-    const int64_t dst = ((static_cast<int64_t>(bi) * n_kv + kh) * cap + p) * hd;
-    kc[dst + lane] = static_cast<half_t>(o1);
-    kc[dst + lane + half] = static_cast<half_t>(o2);
-    const T *vs = row + (heads + n_kv + kh) * hd;
-    vc[dst + lane] = static_cast<half_t>(static_cast<float>(vs[lane]));
-    vc[dst + lane + half] = static_cast<half_t>(static_cast<float>(vs[lane + half]));
-    if (k_out) {
-        float *fk = k_out + (static_cast<int64_t>(bi) * n_kv + kh) * hd;
-        fk[lane] = o1;
-        fk[lane + half] = o2;
     }
 }
 
@@ -219,10 +99,10 @@ int qk_rope(const char *name, const T *qkv, const float *norms, const float *cos
     int rc = load_positions(name, pos, b, cap < table_len ? cap : table_len, p);
     if (rc != DTTS_OK) return rc;
     const int64_t waves = b * (heads + n_kv);
-    qk_rope_kernel<T><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
+    qk_rope_kernel<T, Positions><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
         qkv, norms, cos_t, sin_t, p, q_out, k_out, reinterpret_cast<half_t *>(kc), reinterpret_cast<half_t *>(vc),
         static_cast<int>(b), static_cast<int>(heads), static_cast<int>(n_kv), static_cast<int>(hd),
-        static_cast<int>(cap), eps);
+        static_cast<int>(cap), eps, 1.0f);
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

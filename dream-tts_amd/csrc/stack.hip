@@ -1,0 +1,340 @@
+// One decode step of a Qwen3 decoder stack (Stack::forward at t = 1, crates/qwen3tts/src/
+// qwen3.rs:294-467) over all layers, every lane at its own position:
+//
+//   h = x
+//   per layer:  a = f16(rms_norm(h, attn_norm))                      rms kernel
+//               qkv = a . Wqkv^T                    (f32)             NT GEMM
+//               q, cache[pos] <- QK-norm, RoPE, append (or RoPE, q*s)  qk-rope kernel
+//               o = f16(attention(q, cache[window .. pos]))           decode attention
+//               h += (o . Wo^T) * attn_scale                          NT GEMM, residual epilogue
+//               a = f16(rms_norm(h, ffn_norm))                        rms kernel
+//               t = f16(silu(a . Wg^T) * (a . Wu^T))                  NT GEMM, gate|up epilogue
+//               h += (t . Wdown^T) * mlp_scale                        NT GEMM, residual epilogue
+//   out = rms_norm(h, norm)
+//
+// The f16 roundings are the reference's own: Proj::forward casts its input to f16
+// (crates/tts-nn/src/lib.rs:517), so the kernel producing a projection's input stores it in f16
+// directly. Everything else is f32, as the reference's f32 activations are.
+//
+// Decode is launch-bound (8 to 12 small launches per layer), so the step can be captured once
+// into a HIP graph and replayed: every kernel reads the lanes' positions from a device array
+// that a one-block kernel fills from the kernel arguments before each replay, and the attention
+// grid is sized for the longest window the cache allows (workgroups past a lane's window
+// return at once). The graph is kept until a call brings other pointers or sizes.
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "attn.hpp"
+#include "gemm_nt.hpp"
+#include "norm_rope.hpp"
+
+struct dtts_stack {
+    dtts_stack_geometry geo;
+    std::vector<dtts_stack_layer> layers;
+    const float *final_norm = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;  // [capacity, head_dim / 2]
+    int32_t *pos = nullptr;                    // [256] device positions of the step being run
+    // the captured step
+    hipStream_t capture_stream = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<const void *> key;
+};
+
+namespace dtts {
+namespace {
+
+constexpr int kStackMaxLanes = 64;  // the NT GEMM's row limit
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+__global__ __launch_bounds__(256) void set_positions(Positions p, int32_t *dst, int n) {
+    if (static_cast<int>(threadIdx.x) < n) dst[threadIdx.x] = p.p[threadIdx.x];
+}
+
+// Row-wise RMSNorm of the stack: f32 in, the f16 input of the next projection out (or the
+// final f32 output), optionally copying x into the residual stream h first (layer 0).
+// One wave per row; 4 rows per workgroup.
+template <typename TO>
+__global__ __launch_bounds__(256) void stack_norm(const float *x, const float *gamma, TO *y, float *copy, int rows,
+                                                  int dim, float eps) {
+#pragma clang fp contract(off)
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + static_cast<int64_t>(row) * dim;
+    TO *yr = y + static_cast<int64_t>(row) * dim;
+    float ss = 0.0f;
+    for (int i = lane; i < dim; i += 64) {
+        const float v = xr[i];
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    const float m = sqrtf(ss / static_cast<float>(dim) + eps);
+    for (int i = lane; i < dim; i += 64) {
+        const float v = xr[i];
+        yr[i] = static_cast<TO>((v / m) * gamma[i]);
+        if (copy) copy[static_cast<int64_t>(row) * dim + i] = v;
+    }
+}
+
+struct Plan {  // workspace carve-up for one (lanes, cap)
+    size_t h, a16, t16, qkv, q, gemm_part, attn_part, total;
+    size_t gemm_bytes, attn_bytes;
+    int max_window;
+};
+
+Plan plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t cap) {
+    Plan p{};
+    const int64_t qw = g.heads * g.head_dim, kvw = g.n_kv * g.head_dim;
+    const int64_t aw = g.dim > qw ? g.dim : qw;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    p.h = take(sizeof(float) * lanes * g.dim);
+    p.a16 = take(2 * lanes * aw);
+    p.t16 = take(2 * lanes * g.ffn);
+    p.qkv = take(sizeof(float) * lanes * (qw + 2 * kvw));
+    p.q = take(sizeof(float) * lanes * qw);
+    size_t gb = nt_workspace_bytes(lanes, g.dim, qw + 2 * kvw, 0);
+    const size_t gb2[3] = {nt_workspace_bytes(lanes, qw, g.dim, 2), nt_workspace_bytes(lanes, g.dim, 2 * g.ffn, 1),
+                           nt_workspace_bytes(lanes, g.ffn, g.dim, 2)};
+    for (size_t v : gb2) gb = v > gb ? v : gb;
+    p.gemm_bytes = gb;
+    p.gemm_part = take(gb);
+    const int64_t win = g.window > 0 && g.window < cap ? g.window : cap;
+    p.max_window = static_cast<int>(win);
+    p.attn_bytes = attn_workspace_bytes(lanes, g.n_kv, g.heads / g.n_kv, g.head_dim, win);
+    p.attn_part = take(p.attn_bytes);
+    p.total = off;
+    return p;
+}
+
+template <int MODE>
+hipError_t gemm_nt_launch(const half_t *a, const half_t *w, float *c, half_t *c16, const float *scale, int m, int k,
+                          int n, void *part, size_t part_bytes, hipStream_t stream) {
+    GemmParams p{};
+    p.a = a;
+    p.w = w;
+    p.c = c;
+    p.c16 = c16;
+    p.scale = scale;
+    p.m = m;
+    p.k = k;
+    p.n = n;
+    return launch_nt<MODE>(p, (m + 15) / 16, part, part_bytes, stream);
+}
+
+#define STACK_STEP(expr)                          \
+    do {                                          \
+        const hipError_t e_ = (expr);             \
+        if (e_ != hipSuccess) return e_;          \
+    } while (0)
+
+// Enqueues the step (after the positions are on the device).
+hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const dtts_stack_cache *caches, int lanes,
+                        int cap, char *ws, const Plan &pl, hipStream_t stream) {
+    const dtts_stack_geometry &g = s.geo;
+    const int dim = static_cast<int>(g.dim), hd = static_cast<int>(g.head_dim);
+    const int heads = static_cast<int>(g.heads), n_kv = static_cast<int>(g.n_kv), ffn = static_cast<int>(g.ffn);
+    const int qw = heads * hd, qkvw = (heads + 2 * n_kv) * hd;
+    const int gqa = heads / n_kv;
+    float *h = reinterpret_cast<float *>(ws + pl.h);
+    half_t *a16 = reinterpret_cast<half_t *>(ws + pl.a16);
+    half_t *t16 = reinterpret_cast<half_t *>(ws + pl.t16);
+    float *qkv = reinterpret_cast<float *>(ws + pl.qkv);
+    float *q = reinterpret_cast<float *>(ws + pl.q);
+    void *gpart = pl.gemm_bytes ? ws + pl.gemm_part : nullptr;
+    float *apart = pl.attn_bytes ? reinterpret_cast<float *>(ws + pl.attn_part) : nullptr;
+    const int max_chunks = apart ? (pl.max_window + kChunk - 1) / kChunk : 0;
+    const unsigned norm_grid = static_cast<unsigned>((lanes + 3) / 4);
+    const float qscale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
+    const DevSpans spans{s.pos, static_cast<int>(g.window)};
+    for (int64_t li = 0; li < g.layers; ++li) {
+        const dtts_stack_layer &L = s.layers[li];
+        const float *hin = li == 0 ? x : h;
+        stack_norm<half_t><<<norm_grid, 256, 0, stream>>>(hin, L.attn_norm, a16, li == 0 ? h : nullptr, lanes, dim,
+                                                          g.eps);
+        STACK_STEP(hipGetLastError());
+        STACK_STEP(gemm_nt_launch<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, lanes, dim,
+                                     qkvw, gpart, pl.gemm_bytes, stream));
+        const int waves = lanes * (heads + n_kv);
+        qk_rope_kernel<float, DevPositions><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
+            qkv, g.qk_norm ? L.qk_norms : nullptr, s.cos_t, s.sin_t, DevPositions{s.pos}, q, nullptr,
+            reinterpret_cast<half_t *>(caches[li].k), reinterpret_cast<half_t *>(caches[li].v), lanes, heads, n_kv,
+            hd, cap, g.eps, qscale);
+        STACK_STEP(hipGetLastError());
+        STACK_STEP(launch_attention(q, reinterpret_cast<const half_t *>(caches[li].k),
+                                    reinterpret_cast<const half_t *>(caches[li].v), a16, apart, max_chunks, lanes,
+                                    n_kv, gqa, hd, cap, spans, stream));
+        STACK_STEP(gemm_nt_launch<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr,
+                                     g.layer_scale ? L.attn_scale : nullptr, lanes, qw, dim, gpart, pl.gemm_bytes,
+                                     stream));
+        stack_norm<half_t><<<norm_grid, 256, 0, stream>>>(h, L.ffn_norm, a16, nullptr, lanes, dim, g.eps);
+        STACK_STEP(hipGetLastError());
+        STACK_STEP(gemm_nt_launch<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, lanes,
+                                     dim, 2 * ffn, gpart, pl.gemm_bytes, stream));
+        STACK_STEP(gemm_nt_launch<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr,
+                                     g.layer_scale ? L.mlp_scale : nullptr, lanes, ffn, dim, gpart, pl.gemm_bytes,
+                                     stream));
+    }
+    stack_norm<float><<<norm_grid, 256, 0, stream>>>(h, s.final_norm, out, nullptr, lanes, dim, g.eps);
+    return hipGetLastError();
+}
+
+bool tiles_ok(int64_t lanes, int64_t k, int64_t n, int mode) {
+    const int64_t cols = mode == 1 ? n / 2 : n;
+    return lanes <= 64 && k % 64 == 0 && cols % 16 == 0 &&
+           pick_nt_split(cols / 16, mode == 1 ? 2 : 1, k, false).ks > 0;
+}
+
+}  // namespace
+}  // namespace dtts
+
+using dtts::half_t;
+
+extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stack_layer *layers,
+                                 const float *final_norm, dtts_stack **out) {
+    DTTS_REQUIRE(geo && layers && final_norm && out, "dtts_stack_create: null argument");
+    *out = nullptr;
+    const dtts_stack_geometry &g = *geo;
+    DTTS_REQUIRE(g.layers > 0 && g.dim > 0 && g.heads > 0 && g.n_kv > 0 && g.ffn > 0 && g.capacity > 0,
+                 "dtts_stack_create: bad geometry (layers %lld, dim %lld, heads %lld, n_kv %lld, ffn %lld, "
+                 "capacity %lld)",
+                 (long long)g.layers, (long long)g.dim, (long long)g.heads, (long long)g.n_kv, (long long)g.ffn,
+                 (long long)g.capacity);
+    DTTS_REQUIRE(g.head_dim == 64 || g.head_dim == 128, "dtts_stack_create: head_dim %lld (64 or 128 supported)",
+                 (long long)g.head_dim);
+    DTTS_REQUIRE(g.heads % g.n_kv == 0, "dtts_stack_create: %lld heads over %lld kv heads", (long long)g.heads,
+                 (long long)g.n_kv);
+    const int64_t gqa = g.heads / g.n_kv;
+    DTTS_REQUIRE(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8, "dtts_stack_create: gqa %lld (1, 2, 4 or 8)",
+                 (long long)gqa);
+    DTTS_REQUIRE(g.window >= 0 && g.eps >= 0.0f && g.rope_base > 0.0, "dtts_stack_create: bad window, eps or base");
+    const int64_t qw = g.heads * g.head_dim, qkvw = (g.heads + 2 * g.n_kv) * g.head_dim;
+    DTTS_REQUIRE(dtts::tiles_ok(dtts::kStackMaxLanes, g.dim, qkvw, 0) && dtts::tiles_ok(dtts::kStackMaxLanes, qw, g.dim, 2) &&
+                     dtts::tiles_ok(dtts::kStackMaxLanes, g.dim, 2 * g.ffn, 1) &&
+                     dtts::tiles_ok(dtts::kStackMaxLanes, g.ffn, g.dim, 2),
+                 "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of 64");
+    DTTS_REQUIRE(g.capacity < (int64_t(1) << 24) && g.dim * g.ffn < (int64_t(1) << 31) && qkvw * g.dim < (int64_t(1) << 31),
+                 "dtts_stack_create: geometry too large");
+    for (int64_t i = 0; i < g.layers; ++i) {
+        const dtts_stack_layer &L = layers[i];
+        DTTS_REQUIRE(L.attn_norm && L.ffn_norm && L.wqkv && L.wo && L.w_gateup && L.wdown,
+                     "dtts_stack_create: layer %lld incomplete", (long long)i);
+        DTTS_REQUIRE(!g.qk_norm || L.qk_norms, "dtts_stack_create: layer %lld has no qk_norms", (long long)i);
+        DTTS_REQUIRE(!g.layer_scale || (L.attn_scale && L.mlp_scale), "dtts_stack_create: layer %lld has no scales",
+                     (long long)i);
+        DTTS_REQUIRE(dtts::aligned(L.wqkv, 16) && dtts::aligned(L.wo, 16) && dtts::aligned(L.w_gateup, 16) &&
+                         dtts::aligned(L.wdown, 16),
+                     "dtts_stack_create: layer %lld projection weights not 16-byte aligned", (long long)i);
+    }
+    dtts_stack *s = new (std::nothrow) dtts_stack();
+    DTTS_REQUIRE(s, "dtts_stack_create: out of host memory");
+    s->geo = g;
+    s->layers.assign(layers, layers + g.layers);
+    s->final_norm = final_norm;
+    const int64_t half = g.head_dim / 2;
+    std::vector<float> c(static_cast<size_t>(g.capacity * half)), sn(c.size());
+    int rc = dtts_rope_table_f32(g.capacity, g.head_dim, g.rope_base, c.data(), sn.data());
+    hipError_t e = hipSuccess;
+    if (rc == DTTS_OK) {
+        e = hipMalloc(&s->cos_t, sizeof(float) * c.size());
+        if (e == hipSuccess) e = hipMalloc(&s->sin_t, sizeof(float) * c.size());
+        if (e == hipSuccess) e = hipMalloc(&s->pos, sizeof(int32_t) * 256);
+        if (e == hipSuccess) e = hipMemcpy(s->cos_t, c.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(s->sin_t, sn.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice);
+    }
+    if (rc != DTTS_OK || e != hipSuccess) {
+        dtts_stack_destroy(s);
+        if (e != hipSuccess) dtts::set_error("dtts_stack_create: %s", hipGetErrorString(e));
+        return rc != DTTS_OK ? rc : DTTS_ERR_HIP;
+    }
+    *out = s;
+    return DTTS_OK;
+}
+
+extern "C" void dtts_stack_destroy(dtts_stack *s) {
+    if (!s) return;
+    if (s->exec) (void)hipGraphExecDestroy(s->exec);
+    if (s->capture_stream) (void)hipStreamDestroy(s->capture_stream);
+    if (s->cos_t) (void)hipFree(s->cos_t);
+    if (s->sin_t) (void)hipFree(s->sin_t);
+    if (s->pos) (void)hipFree(s->pos);
+    delete s;
+}
+
+extern "C" size_t dtts_stack_workspace_bytes(const dtts_stack *s, int64_t lanes, int64_t cap) {
+    if (!s || lanes <= 0 || lanes > dtts::kStackMaxLanes || cap <= 0) return 0;
+    return dtts::plan_of(s->geo, lanes, cap).total;
+}
+
+extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, const dtts_stack_cache *caches,
+                                 int64_t lanes, int64_t cap, const int32_t *pos, void *workspace, size_t ws_bytes,
+                                 int32_t flags, hipStream_t stream) {
+    const char *name = "dtts_stack_decode";
+    DTTS_REQUIRE(s, "%s: null stack", name);
+    DTTS_REQUIRE(lanes >= 0 && lanes <= dtts::kStackMaxLanes, "%s: %lld lanes (1 to %d)", name, (long long)lanes,
+                 dtts::kStackMaxLanes);
+    DTTS_REQUIRE((flags & ~DTTS_STACK_GRAPH) == 0, "%s: unknown flags 0x%x", name, static_cast<unsigned>(flags));
+    if (lanes == 0) return DTTS_OK;
+    const dtts_stack_geometry &g = s->geo;
+    DTTS_REQUIRE(cap > 0 && cap <= g.capacity, "%s: cache capacity %lld outside (0, %lld] (the RoPE table)", name,
+                 (long long)cap, (long long)g.capacity);
+    DTTS_REQUIRE(lanes * g.n_kv * cap * g.head_dim < (int64_t(1) << 40), "%s: caches too large", name);
+    DTTS_REQUIRE(x && out && caches && pos && workspace, "%s: null pointer", name);
+    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(out, 16) && dtts::aligned(workspace, 256),
+                 "%s: x and out must be 16-byte aligned, the workspace 256-byte aligned", name);
+    for (int64_t i = 0; i < g.layers; ++i)
+        DTTS_REQUIRE(caches[i].k && caches[i].v && dtts::aligned(caches[i].k, 16) && dtts::aligned(caches[i].v, 16),
+                     "%s: layer %lld cache missing or misaligned", name, (long long)i);
+    const dtts::Plan pl = dtts::plan_of(g, lanes, cap);
+    DTTS_REQUIRE(ws_bytes >= pl.total, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, pl.total);
+    dtts::Positions p{};
+    for (int64_t i = 0; i < lanes; ++i) {
+        // Stack::forward refuses start + t > capacity (crates/qwen3tts/src/qwen3.rs:303-309)
+        DTTS_REQUIRE(pos[i] >= 0 && pos[i] < cap, "%s: lane %lld position %d exceeds cache capacity %lld", name,
+                     (long long)i, pos[i], (long long)cap);
+        p.p[i] = pos[i];
+    }
+    dtts::set_positions<<<1, 256, 0, stream>>>(p, s->pos, static_cast<int>(lanes));
+    DTTS_LAUNCH_CHECK(name);
+    char *ws = static_cast<char *>(workspace);
+    if (!(flags & DTTS_STACK_GRAPH)) {
+        DTTS_HIP_CHECK(dtts::enqueue_step(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, pl,
+                                          stream),
+                       name);
+        return DTTS_OK;
+    }
+    std::vector<const void *> key = {x, out, workspace, reinterpret_cast<const void *>(lanes),
+                                     reinterpret_cast<const void *>(cap), reinterpret_cast<const void *>(ws_bytes)};
+    for (int64_t i = 0; i < g.layers; ++i) {
+        key.push_back(caches[i].k);
+        key.push_back(caches[i].v);
+    }
+    if (!s->exec || key != s->key) {
+        if (s->exec) {
+            DTTS_HIP_CHECK(hipGraphExecDestroy(s->exec), name);
+            s->exec = nullptr;
+        }
+        if (!s->capture_stream) DTTS_HIP_CHECK(hipStreamCreateWithFlags(&s->capture_stream, hipStreamNonBlocking), name);
+        DTTS_HIP_CHECK(hipStreamBeginCapture(s->capture_stream, hipStreamCaptureModeThreadLocal), name);
+        const hipError_t le =
+            dtts::enqueue_step(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, pl,
+                               s->capture_stream);
+        hipGraph_t graph = nullptr;
+        const hipError_t ee = hipStreamEndCapture(s->capture_stream, &graph);
+        hipError_t ie = hipSuccess;
+        if (le == hipSuccess && ee == hipSuccess) ie = hipGraphInstantiate(&s->exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        DTTS_HIP_CHECK(le, name);
+        DTTS_HIP_CHECK(ee, name);
+        DTTS_HIP_CHECK(ie, name);
+        s->key = key;
+    }
+    DTTS_HIP_CHECK(hipGraphLaunch(s->exec, stream), name);
+    return DTTS_OK;
+}

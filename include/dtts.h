@@ -272,6 +272,71 @@ int dtts_decode_attention_f32(const float *q, const float *kcache, const float *
                               const int32_t *span, const int32_t *window_start, void *workspace,
                               size_t ws_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------ f-2 decoder stack step */
+
+/* One decode step (t = 1) of a Qwen3 decoder stack over all its layers: replaces Stack::forward
+ * (crates/qwen3tts/src/qwen3.rs:294-467) on its decode path with f16 weights (Proj::Half) and an
+ * f16 KV cache: per layer rms_norm, the fused QKV projection, QK-norm + RoPE + cache append (or
+ * RoPE and q * 1/sqrt(head_dim) without QK-norm), decode attention over the cache (the last
+ * `window` positions when set), the output projection added to the residual stream (times
+ * attn_scale with LayerScale), rms_norm, gate|up with SiLU*mul, the down projection added to
+ * the residual stream (times mlp_scale); then the final rms_norm. Activations are f32 as in the
+ * reference, each projection's input rounded to f16 as Proj::forward casts it
+ * (crates/tts-nn/src/lib.rs:517). Geometries: the talker (dim 2048, 28 layers, 16/8 heads, D 128,
+ * ffn 6144), the code predictor (dim 1024, 5 layers, ffn 3072) and the codec's windowed
+ * transformer (dim 512, 8 layers, 16/16 heads, D 64, LayerScale, window 72) all fit. */
+typedef struct dtts_stack_geometry {
+    int64_t dim, layers, heads, n_kv, head_dim, ffn;
+    float eps;
+    double rope_base;
+    int32_t qk_norm, layer_scale; /* Geometry's flags (qwen3.rs:16-28) */
+    int64_t window;               /* sliding window in positions; 0 = none */
+    int64_t capacity;             /* RoPE table length (Stack::load's capacity); caches may be shorter */
+} dtts_stack_geometry;
+
+/* Device pointers, kept (not copied) by dtts_stack_create; norms and scales f32, projections f16
+ * in the checkpoint's [out, in] layout, 16-byte aligned. */
+typedef struct dtts_stack_layer {
+    const float *attn_norm, *ffn_norm; /* [dim] */
+    const dtts_f16 *wqkv;              /* [(heads + 2 n_kv) head_dim, dim]: q, k, v rows (Layer::load's cat) */
+    const dtts_f16 *wo;                /* [dim, heads head_dim] */
+    const dtts_f16 *w_gateup;          /* [2 ffn, dim]: gate rows, then up rows */
+    const dtts_f16 *wdown;             /* [dim, ffn] */
+    const float *qk_norms;             /* [2, head_dim]: q's weight times 1/sqrt(head_dim), then k's (qk_norm) */
+    const float *attn_scale, *mlp_scale; /* [dim] (layer_scale) */
+} dtts_stack_layer;
+
+/* One layer's cache (State's Cache, qwen3.rs:122-126): k and v [lanes, n_kv, cap, head_dim] f16. */
+typedef struct dtts_stack_cache {
+    dtts_f16 *k, *v;
+} dtts_stack_cache;
+
+typedef struct dtts_stack dtts_stack;
+
+/* Checks the geometry and weights, builds the RoPE table (rope_table_f32, crates/tts-nn/src/
+ * lib.rs:1178-1205) on the current device. */
+int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stack_layer *layers, const float *final_norm,
+                      dtts_stack **out);
+void dtts_stack_destroy(dtts_stack *stack);
+
+/* Device scratch bytes for a step of `lanes` lanes over caches of capacity `cap`. */
+size_t dtts_stack_workspace_bytes(const dtts_stack *stack, int64_t lanes, int64_t cap);
+
+#define DTTS_STACK_GRAPH 1 /* capture the step's launches once into a HIP graph and replay it */
+
+/* x [lanes, dim] f32 (the embedded tokens) -> out [lanes, dim] f32 (the normed hidden state);
+ * caches[layers]: layer i's k and v, written at each lane's position and read over its window;
+ * pos a HOST int32[lanes], each < cap (checked before anything is enqueued, as Stack::forward
+ * refuses start + t > capacity). lanes <= 64. The reference advances one position for the whole
+ * batch; a position per lane is the batched-decode generalisation. With DTTS_STACK_GRAPH the
+ * launches are captured on the first call and replayed while x, out, the caches, lanes, cap and
+ * the workspace stay the same (any change captures again). Calls on one stack must be ordered
+ * (one stream at a time), as the reference's device-global encoder is (crates/tts-nn/src/
+ * lib.rs:76-83). */
+int dtts_stack_decode(dtts_stack *stack, const float *x, float *out, const dtts_stack_cache *caches, int64_t lanes,
+                      int64_t cap, const int32_t *pos, void *workspace, size_t ws_bytes, int32_t flags,
+                      hipStream_t stream);
+
 /* ------------------------------------------------------------------ a12-a14 f16 projections */
 
 /* Decode-shape f16 GEMM, f32 accumulation and output: C[m, n] = A[m, k] . B. Replaces

@@ -381,6 +381,59 @@ def swiglu_mul_f32(g, u):
     return y
 
 
+# ---------------------------------------------------------------- decoder stack step
+
+def _proj_f16(x, w_out_in):
+    """Proj::Half's forward on the decode path (crates/tts-nn/src/lib.rs:514-524): x cast to f16,
+    times the f16 weight, f32 accumulation and output. w is [out, in] f32 (rounded to f16 here)."""
+    return gemm_f16_f32acc(f32_to_f16(x), np.ascontiguousarray(f32_to_f16(w_out_in).T))
+
+
+def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
+    """Stack::forward at t = 1 (crates/qwen3tts/src/qwen3.rs:294-467) with f16 weights and f16
+    caches, each lane at its own position. geo: an object with the Geometry fields (dim, layers,
+    heads, n_kv, head_dim, ffn, eps, rope_base, qk_norm, layer_scale, window, capacity); layers:
+    dicts of checkpoint-layout f32 weights (wq, wk, wv, wo, gate, up, down [out, in]; attn_norm,
+    ffn_norm; q_norm, k_norm; attn_scale, mlp_scale); x [b, dim] f32; kcaches / vcaches: per
+    layer uint16 [b, n_kv, cap, head_dim], updated in place; pos int32[b]. Returns the final
+    rms_norm of the residual stream, [b, dim] f32."""
+    b = x.shape[0]
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw = heads * hd, n_kv * hd
+    pos = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (b,)))
+    cos_t, sin_t = rope_table_f32(geo.capacity, hd, geo.rope_base)  # Stack::load (qwen3.rs:240)
+    span = pos + 1
+    # the window start of the decode branch (qwen3.rs:409-412)
+    wstart = np.where(span > geo.window, span - geo.window, 0).astype(np.int32) if geo.window else np.zeros(b, np.int32)
+    h = _f32(x).copy()
+    for li, L in enumerate(layers):
+        normed = rms_norm_f32(h, L["attn_norm"], geo.eps)                             # :339
+        qkv = _proj_f16(normed, np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0))  # :340, :69-77
+        if geo.qk_norm:                                                               # :343-357
+            s = np.float32(1.0 / np.sqrt(np.float64(hd)))
+            norms = np.stack([_f32(L["q_norm"]) * s, _f32(L["k_norm"])])              # :78-91
+            q, _ = qk_norm_rope_append_f32(qkv, norms, cos_t, sin_t, pos, kcaches[li], vcaches[li],
+                                           heads, n_kv, geo.eps)
+        else:                                                                         # :358-400
+            q = rope_halfsplit_f32(qkv[:, :qw].reshape(b, heads, hd), cos_t, sin_t, pos)
+            k = rope_halfsplit_f32(qkv[:, qw:qw + kvw].reshape(b, n_kv, hd), cos_t, sin_t, pos)
+            kv_append_f32(k, qkv[:, qw + kvw:].reshape(b, n_kv, hd), pos, kcaches[li], vcaches[li])
+            q = q * np.float32(1.0 / np.sqrt(np.float64(hd)))                         # :404-408
+        attn = decode_attention_f32(q.reshape(b, n_kv, heads // n_kv, hd), kcaches[li], vcaches[li],
+                                    span, wstart).reshape(b, qw)                      # :413-414
+        o = _proj_f16(attn, L["wo"])                                                  # :446
+        if geo.layer_scale:
+            o = o * _f32(L["attn_scale"])                                             # :447-450
+        h = h + o                                                                     # :451
+        normed = rms_norm_f32(h, L["ffn_norm"], geo.eps)                              # :453
+        tail = swiglu_mul_f32(_proj_f16(normed, L["gate"]), _proj_f16(normed, L["up"]))  # :454-457
+        mlp = _proj_f16(tail, L["down"])                                              # :458
+        if geo.layer_scale:
+            mlp = mlp * _f32(L["mlp_scale"])                                          # :459-462
+        h = h + mlp                                                                   # :463
+    return rms_norm_f32(h, final_norm, geo.eps)                                       # :466
+
+
 def q8_0_quantize(w):
     w = _f32(w)
     rows, k = w.shape

@@ -1,0 +1,102 @@
+"""Shared pieces of the decoder-stack tests: small geometries, seeded inputs, and an independent
+float64 restatement of Stack::forward's decode step (crates/qwen3tts/src/qwen3.rs:294-467) in
+numpy, with the reference's f16 roundings at the same points (projection inputs, weights, cache
+entries) and everything else in float64."""
+from dataclasses import replace
+
+import numpy as np
+
+from dtts import stack, synth
+
+SMALL = stack.Geometry(dim=256, layers=2, heads=4, n_kv=2, head_dim=128, ffn=512, capacity=64)
+# no QK-norm, LayerScale, a sliding window, D = 64, one query head per kv head
+WINDOWED = stack.Geometry(dim=128, layers=2, heads=4, n_kv=4, head_dim=64, ffn=256, eps=1e-5,
+                          rope_base=10_000.0, qk_norm=False, layer_scale=True, window=5, capacity=32)
+
+
+def with_layers(geo, n):
+    return replace(geo, layers=n)
+
+
+def inputs(geo, seed, lanes, cap, fill=True):
+    """x [lanes, dim] f32 and per-layer caches (uint16 f16 bits), pre-filled with N(0,1) history
+    when fill is set."""
+    x = synth.normal(seed, "stack.x", (lanes, geo.dim))
+    shape = (lanes, geo.n_kv, cap, geo.head_dim)
+    kc, vc = [], []
+    for i in range(geo.layers):
+        if fill:
+            kc.append(synth.f16_bits(synth.normal(seed, f"stack.k{i}", shape)))
+            vc.append(synth.f16_bits(synth.normal(seed, f"stack.v{i}", shape)))
+        else:
+            kc.append(np.zeros(shape, np.uint16))
+            vc.append(np.zeros(shape, np.uint16))
+    return x, kc, vc
+
+
+def _h(a):
+    """Round to f16 (numpy's conversion is round-to-nearest-even) and back, in float64."""
+    return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
+
+
+def _rms(x, g, eps):
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * g
+
+
+def _rope(x, pos, geo):
+    half = geo.head_dim // 2
+    i = np.arange(half, dtype=np.float64)
+    freq = 1.0 / geo.rope_base ** (2.0 * i / geo.head_dim)
+    ph = pos[:, None, None].astype(np.float64) * freq  # [b, 1, half]
+    c, s = np.cos(ph), np.sin(ph)
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], -1)
+
+
+def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
+    """Returns (out [b, dim] float64, kc, vc) with the caches as new uint16 arrays."""
+    b = x.shape[0]
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw, gqa = heads * hd, n_kv * hd, heads // n_kv
+    pos = np.broadcast_to(np.asarray(pos, np.int64), (b,))
+    kc = [k.copy() for k in kc]
+    vc = [v.copy() for v in vc]
+    h = np.asarray(x, np.float64)
+    for li, L in enumerate(layers):
+        a = _h(_rms(h, L["attn_norm"], geo.eps))
+        wqkv = _h(np.concatenate([L["wq"], L["wk"], L["wv"]], 0))
+        qkv = a @ wqkv.T
+        q = qkv[:, :qw].reshape(b, heads, hd)
+        k = qkv[:, qw:qw + kvw].reshape(b, n_kv, hd)
+        v = qkv[:, qw + kvw:].reshape(b, n_kv, hd)
+        if geo.qk_norm:
+            q = _rms(q, np.float64(L["q_norm"]) / np.sqrt(hd), geo.eps)
+            k = _rms(k, L["k_norm"], geo.eps)
+        q, k = _rope(q, pos, geo), _rope(k, pos, geo)
+        if not geo.qk_norm:
+            q = q / np.sqrt(hd)
+        for i in range(b):
+            kc[li][i, :, pos[i]] = synth.f16_bits(k[i])
+            vc[li][i, :, pos[i]] = synth.f16_bits(v[i])
+        att = np.empty((b, heads, hd))
+        for i in range(b):
+            hi = pos[i] + 1
+            lo = hi - geo.window if geo.window and hi > geo.window else 0
+            kk = synth.from_f16_bits(kc[li][i, :, lo:hi]).astype(np.float64)  # [n_kv, n, hd]
+            vv = synth.from_f16_bits(vc[li][i, :, lo:hi]).astype(np.float64)
+            qg = q[i].reshape(n_kv, gqa, hd)
+            s = np.einsum("hgd,hnd->hgn", qg, kk)
+            e = np.exp(s - s.max(-1, keepdims=True))
+            att[i] = np.einsum("hgn,hnd->hgd", e / e.sum(-1, keepdims=True), vv).reshape(heads, hd)
+        o = _h(att.reshape(b, qw)) @ _h(L["wo"]).T
+        if geo.layer_scale:
+            o = o * L["attn_scale"]
+        h = h + o
+        a = _h(_rms(h, L["ffn_norm"], geo.eps))
+        g, u = a @ _h(L["gate"]).T, a @ _h(L["up"]).T
+        t = _h(g / (1.0 + np.exp(-g)) * u)
+        m = t @ _h(L["down"]).T
+        if geo.layer_scale:
+            m = m * L["mlp_scale"]
+        h = h + m
+    return _rms(h, final_norm, geo.eps), kc, vc
