@@ -97,6 +97,9 @@ __global__ __launch_bounds__(1024) void gemm_skinny_nt(GemmParams p) {
         arow[mb] = row < p.m;
         ar[mb] = p.a + static_cast<int64_t>(arow[mb] ? row : 0) * p.k + k0 + g * 16;
     }
+    // keep every weight load ahead of the first MFMA (the scheduler would otherwise sink them
+    // next to their uses, leaving a few requests in flight per wave)
+    __builtin_amdgcn_sched_barrier(0);
     float4v acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -146,21 +149,23 @@ __global__ __launch_bounds__(1024) void gemm_skinny_nt(GemmParams p) {
     }
 }
 
-// Sums the k splits' partials in split order (deterministic), then the mode's store.
+// Sums the k splits' partials in split order (deterministic), then the mode's store; four
+// output columns per thread (every caller has output widths that are multiples of 16).
 template <int MODE>
 __global__ __launch_bounds__(256) void gemm_merge_splits(GemmParams p, int ysplit) {
-    const int cols = MODE == 1 ? p.n / 2 : p.n;
-    const int64_t total = static_cast<int64_t>(p.m) * cols;
+    const int c4n = (MODE == 1 ? p.n / 2 : p.n) / 4;
+    const int64_t total = static_cast<int64_t>(p.m) * c4n;
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
-        const int64_t row = e / cols;
-        const int col = static_cast<int>(e - row * cols);
-        float s0 = 0.f, s1 = 0.f;
+        const int64_t row = e / c4n;
+        const int col = static_cast<int>(e - row * c4n) * 4;
+        float4v s0 = float4v{0.f, 0.f, 0.f, 0.f}, s1 = float4v{0.f, 0.f, 0.f, 0.f};
         for (int y = 0; y < ysplit; ++y) {
             const float *pr = p.part + (static_cast<int64_t>(y) * p.m + row) * p.n + col;
-            s0 += pr[0];
-            if constexpr (MODE == 1) s1 += pr[p.n / 2];
+            s0 += *reinterpret_cast<const float4v *>(pr);
+            if constexpr (MODE == 1) s1 += *reinterpret_cast<const float4v *>(pr + p.n / 2);
         }
-        gemm_store<MODE>(p, row, col, s0, s1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gemm_store<MODE>(p, row, col + i, s0[i], s1[i]);
     }
 }
 
@@ -190,12 +195,170 @@ NtSplit pick_nt_split(int64_t groups, int nb, int64_t k, bool can_split) {
     return most;
 }
 
-size_t nt_workspace_bytes(int64_t m, int64_t k, int64_t n, int mode) {
+// ---------------------------------------------------------------- the A-sharing kernel
+//
+// Workgroup (x, y) = 4 waves: 64 weight rows (output columns; for gate|up, 32 gate rows and the
+// matching 32 up rows) times the k range [y * KR, (y + 1) * KR), KR = NC * 64. The activation
+// slab A[0:m, k range] is read once per workgroup with coalesced 16-byte loads and kept in LDS,
+// where all four waves read their fragments: per workgroup A costs m/64 of the weight bytes
+// instead of m/16 when every wave fetches its own. Each wave holds its 16 weight rows x KR in
+// registers, every load issued before the first MFMA. With one k range the workgroup applies
+// the epilogue; with several (gridDim.y > 1) it writes its partial tile to p.part
+// [gridDim.y][m][n] and the ranges are summed in order afterwards, by gemm_merge_splits or by
+// the consuming kernel.
+constexpr int kLdsMaxTiles = 1 << 16;
+
+template <int MB, int NC, int MODE>
+__global__ __launch_bounds__(256) void gemm_lds_nt(GemmParams p) {
+    constexpr int KR = NC * 64;
+    constexpr int PITCH = KR + 8;  // halves; 16 bytes of padding spread the fragment reads over banks
+    constexpr int TP = 64 + 4;     // f32 pitch of the 64-column tile
+    extern __shared__ __attribute__((aligned(16))) half_t als[];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int g = lane >> 4, r = lane & 15;
+    const int kb = blockIdx.y * KR;
+    // A slab: MB*16 rows x KR/8 16-byte segments over 256 threads (rows >= m are zero)
+    constexpr int SEGS = MB * 16 * (KR / 8);
+    constexpr int APT = SEGS / 256;
+    static_assert(SEGS % 256 == 0, "slab segments");
+    half8_t av[APT];
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        const int sg = t + i * 256;
+        const int row = sg / (KR / 8), seg = sg % (KR / 8);
+        av[i] = row < p.m ? *reinterpret_cast<const half8_t *>(p.a + static_cast<int64_t>(row) * p.k + kb + seg * 8)
+                          : half8_t{};
+    }
+    int wrow;  // the weight row this lane streams
+    if constexpr (MODE == 1)
+        wrow = (wave < 2 ? 0 : p.n / 2) + blockIdx.x * 32 + (wave & 1) * 16 + r;
+    else
+        wrow = blockIdx.x * 64 + wave * 16 + r;
+    const half_t *wr = p.w + static_cast<int64_t>(wrow) * p.k + kb + g * 16;
+    half8_t b[NC][2];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        b[c][0] = *reinterpret_cast<const half8_t *>(wr + c * 64);
+        b[c][1] = *reinterpret_cast<const half8_t *>(wr + c * 64 + 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first wait
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        const int sg = t + i * 256;
+        const int row = sg / (KR / 8), seg = sg % (KR / 8);
+        *reinterpret_cast<half8_t *>(als + row * PITCH + seg * 8) = av[i];
+    }
+    __syncthreads();
+    float4v acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = float4v{0.f, 0.f, 0.f, 0.f};
+    const half_t *ab = als + r * PITCH + g * 16;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const half8_t a0 = *reinterpret_cast<const half8_t *>(ab + mb * 16 * PITCH + c * 64);
+            const half8_t a1 = *reinterpret_cast<const half8_t *>(ab + mb * 16 * PITCH + c * 64 + 8);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[c][0], acc[mb], 0, 0, 0);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[c][1], acc[mb], 0, 0, 0);
+        }
+    // the 64-column tile, f32, through LDS (the slab is no longer read)
+    __syncthreads();
+    float *tile = reinterpret_cast<float *>(als);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tile[(mb * 16 + g * 4 + i) * TP + wave * 16 + r] = acc[mb][i];
+    __syncthreads();
+    // tile column tc -> output column: gate|up tiles hold gate columns 0..31 then up columns
+    auto gcol = [&](int tc) {
+        if constexpr (MODE == 1) return (tc < 32 ? 0 : p.n / 2) + blockIdx.x * 32 + (tc & 31);
+        return blockIdx.x * 64 + tc;
+    };
+    constexpr int OUTC = MODE == 1 ? 32 : 64;  // output columns of the tile
+    if (gridDim.y > 1) {  // this range's partial tile, 4 columns per thread
+        for (int e = t; e < p.m * 16; e += 256) {
+            const int row = e >> 4, c4 = (e & 15) * 4;
+            *reinterpret_cast<float4v *>(p.part + (static_cast<int64_t>(blockIdx.y) * p.m + row) * p.n + gcol(c4)) =
+                *reinterpret_cast<const float4v *>(tile + row * TP + c4);
+        }
+        return;
+    }
+    for (int e = t; e < p.m * OUTC; e += 256) {
+        const int row = e / OUTC, oc = e - (e / OUTC) * OUTC;
+        const float s0 = tile[row * TP + oc];
+        const float s1 = MODE == 1 ? tile[row * TP + oc + 32] : 0.f;
+        gemm_store<MODE>(p, row, MODE == 1 ? blockIdx.x * 32 + oc : gcol(oc), s0, s1);
+    }
+}
+
+// The A-sharing kernel's plan: NC chunks of 64 k per workgroup (8 when that still gives ~192
+// workgroups or more, else 4; 2 when k is an odd multiple of 128), ys = k / (NC * 64) ranges.
+// Needs m <= 64, k % 128 == 0 and 64 output columns per tile (32 for gate|up). nc == 0: not
+// applicable.
+struct LdsPlan {
+    int nc, ys, tiles;
+};
+
+inline LdsPlan pick_lds(int64_t m, int64_t k, int64_t n, int mode) {
+    const int64_t per = mode == 1 ? 32 : 64;
+    const int64_t cols = mode == 1 ? n / 2 : n;
+    if (m <= 0 || m > 64 || k % 128 != 0 || cols % per != 0 || cols / per > kLdsMaxTiles) return LdsPlan{0, 0, 0};
+    const int64_t tiles = cols / per;
+    const int nc = k % 256 != 0 ? 2 : (k % 512 == 0 && tiles * (k / 512) >= 192) ? 8 : 4;
+    return LdsPlan{nc, static_cast<int>(k / (nc * 64)), static_cast<int>(tiles)};
+}
+
+inline size_t lds_partial_bytes(const LdsPlan &pl, int64_t m, int64_t n) {
+    return pl.nc > 0 && pl.ys > 1 ? static_cast<size_t>(pl.ys) * m * n * sizeof(float) : 0;
+}
+
+// merge == false leaves the partial tiles for the consumer to sum (the stack step does).
+template <int MODE>
+hipError_t launch_lds_nt(const GemmParams &p0, const LdsPlan &pl, void *workspace, hipStream_t stream,
+                         bool merge = true) {
+    GemmParams p = p0;
+    p.part = pl.ys > 1 ? static_cast<float *>(workspace) : nullptr;
+    const int mb = (p.m + 15) / 16;
+    const size_t slab = static_cast<size_t>(mb) * 16 * (pl.nc * 64 + 8) * 2;
+    const size_t tile = static_cast<size_t>(mb) * 16 * 68 * 4;
+    const size_t lds = slab > tile ? slab : tile;
+    const dim3 grid(static_cast<unsigned>(pl.tiles), static_cast<unsigned>(pl.ys));
+#define DTTS_LDS_NT(MB_)                                                                         \
+    if (pl.nc == 8)                                                                               \
+        gemm_lds_nt<MB_, 8, MODE><<<grid, 256, lds, stream>>>(p);                                 \
+    else if (pl.nc == 4)                                                                          \
+        gemm_lds_nt<MB_, 4, MODE><<<grid, 256, lds, stream>>>(p);                                 \
+    else                                                                                          \
+        gemm_lds_nt<MB_, 2, MODE><<<grid, 256, lds, stream>>>(p);
+    switch (mb) {
+        case 1: DTTS_LDS_NT(1) break;
+        case 2: DTTS_LDS_NT(2) break;
+        case 3: DTTS_LDS_NT(3) break;
+        default: DTTS_LDS_NT(4) break;
+    }
+#undef DTTS_LDS_NT
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || pl.ys == 1 || !merge) return e;
+    const int64_t outs = int64_t(p.m) * (MODE == 1 ? p.n / 2 : p.n) / 4;
+    gemm_merge_splits<MODE><<<grid_for(outs, 256, 4), 256, 0, stream>>>(p, pl.ys);
+    return hipGetLastError();
+}
+
+// Workspace for a projection: the A-sharing kernel's partial tiles when it applies, else the
+// per-wave kernel's split partials.
+inline size_t wave_kernel_workspace_bytes(int64_t m, int64_t k, int64_t n, int mode) {
     if (m <= 0 || m > 64 || k % 64 != 0 || (mode == 1 ? n / 2 : n) % 16 != 0) return 0;
     const int nb = mode == 1 ? 2 : 1;
     const int64_t groups = (mode == 1 ? n / 2 : n) / 16;
     const NtSplit sp = pick_nt_split(groups, nb, k, true);
     return sp.ks > 0 && sp.ysplit > 1 ? static_cast<size_t>(sp.ysplit) * m * n * sizeof(float) : 0;
+}
+
+size_t nt_workspace_bytes(int64_t m, int64_t k, int64_t n, int mode) {
+    const LdsPlan pl = pick_lds(m, k, n, mode);
+    if (pl.nc > 0) return lds_partial_bytes(pl, m, n);
+    return wave_kernel_workspace_bytes(m, k, n, mode);
 }
 
 template <int MB, int MODE>
@@ -215,10 +378,16 @@ hipError_t launch_nt_mb(const GemmParams &p, dim3 grid, unsigned threads, size_t
 
 template <int MODE>
 hipError_t launch_nt(const GemmParams &p0, int mb_blocks, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    const LdsPlan pl = pick_lds(p0.m, p0.k, p0.n, MODE);
+    if (pl.nc > 0) {
+        const size_t need = lds_partial_bytes(pl, p0.m, p0.n);
+        if (need == 0 || (workspace && ws_bytes >= need && aligned(workspace, 16)))
+            return launch_lds_nt<MODE>(p0, pl, workspace, stream);
+    }
     GemmParams p = p0;
     const int nb = MODE == 1 ? 2 : 1;
     const int64_t groups = MODE == 1 ? p.n / 2 / 16 : p.n / 16;
-    const size_t need = nt_workspace_bytes(p.m, p.k, p.n, MODE);
+    const size_t need = wave_kernel_workspace_bytes(p.m, p.k, p.n, MODE);
     const bool split_ok = need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16);
     const NtSplit sp = pick_nt_split(groups, nb, p.k, split_ok);
     p.ks = sp.ks;
@@ -235,7 +404,7 @@ hipError_t launch_nt(const GemmParams &p0, int mb_blocks, void *workspace, size_
         default: e = launch_nt_mb<4, MODE>(p, grid, threads, lds, sp.nc, stream); break;
     }
     if (e != hipSuccess || !p.part) return e;
-    const int64_t outs = int64_t(p.m) * (MODE == 1 ? p.n / 2 : p.n);
+    const int64_t outs = int64_t(p.m) * (MODE == 1 ? p.n / 2 : p.n) / 4;
     gemm_merge_splits<MODE><<<grid_for(outs, 256, 4), 256, 0, stream>>>(p, sp.ysplit);
     return hipGetLastError();
 }

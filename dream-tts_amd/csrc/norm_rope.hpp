@@ -84,12 +84,13 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 // wave also writes v). Lane j holds dims j and j + 64 when D = 128 (any even D <= 128: lane j
 // holds pair j < D/2). norms == nullptr skips the QK-norm (layers without it); q_scale then
 // multiplies the roped q (Stack::forward's q * 1/sqrt(D) for such layers, crates/qwen3tts/src/
-// qwen3.rs:404-408), and is 1 otherwise. P: Positions or DevPositions.
+// qwen3.rs:404-408), and is 1 otherwise. P: Positions or DevPositions. ys > 1: qkv is the sum,
+// in order, of ys partial arrays ystride elements apart (a projection's k-split partials).
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float *norms, const float *cos_t,
                                                       const float *sin_t, P pos, T *q_out, float *k_out,
                                                       half_t *kc, half_t *vc, int b, int heads, int n_kv, int hd,
-                                                      int cap, float eps, float q_scale) {
+                                                      int cap, float eps, float q_scale, int ys, int64_t ystride) {
 #pragma clang fp contract(off)
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -103,10 +104,15 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
     const T *src = row + h * hd;
     const bool is_q = h < heads;
     const bool act = lane < half;
+    auto ld = [&](const T *q) {
+        float v = static_cast<float>(q[0]);
+        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
+        return v;
+    };
     float x1 = 0.0f, x2 = 0.0f;
     if (act) {
-        x1 = static_cast<float>(src[lane]);
-        x2 = static_cast<float>(src[lane + half]);
+        x1 = ld(src + lane);
+        x2 = ld(src + lane + half);
     }
     float ss = wave_sum(x1 * x1 + x2 * x2);
     const float m = sqrtf(ss / static_cast<float>(hd) + eps);
@@ -137,8 +143,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
     kc[dst + lane] = static_cast<half_t>(o1);
     kc[dst + lane + half] = static_cast<half_t>(o2);
     const T *vs = row + (heads + n_kv + kh) * hd;
-    vc[dst + lane] = static_cast<half_t>(static_cast<float>(vs[lane]));
-    vc[dst + lane + half] = static_cast<half_t>(static_cast<float>(vs[lane + half]));
+    vc[dst + lane] = static_cast<half_t>(ld(vs + lane));
+    vc[dst + lane + half] = static_cast<half_t>(ld(vs + lane + half));
     if (k_out) {
         float *fk = k_out + (static_cast<int64_t>(bi) * n_kv + kh) * hd;
         fk[lane] = o1;

@@ -52,29 +52,99 @@ __global__ __launch_bounds__(256) void set_positions(Positions p, int32_t *dst, 
     if (static_cast<int>(threadIdx.x) < n) dst[threadIdx.x] = p.p[threadIdx.x];
 }
 
-// Row-wise RMSNorm of the stack: f32 in, the f16 input of the next projection out (or the
-// final f32 output), optionally copying x into the residual stream h first (layer 0).
-// One wave per row; 4 rows per workgroup.
-template <typename TO>
-__global__ __launch_bounds__(256) void stack_norm(const float *x, const float *gamma, TO *y, float *copy, int rows,
-                                                  int dim, float eps) {
+// A projection's output as its consumer reads it: the value itself (ys == 1), or ys partial
+// arrays `stride` floats apart, summed in order (the projection's k ranges).
+struct Partials {
+    const float *p;
+    int ys;
+    int64_t stride;
+};
+
+// Row-wise RMSNorm of the stack, f32 in, the f16 input of the next projection out (or the final
+// f32 output). When `add` is set, the row first takes the residual update of the projection that
+// precedes it: x + (sum of add's partials) * scale (LayerScale, or 1), rounded as the reference
+// rounds h + attn; the updated row is written to h. Layer 0 copies x into h the same way (add
+// unset, h set). One workgroup per row; each thread holds NV float4 of the row (every load of the
+// row in flight at once); the sum of squares is reduced over the wave, then over the four waves
+// through LDS.
+template <typename TO, int NV>
+__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const float *scale, float *h,
+                                                  const float *gamma, TO *y, int dim, float eps) {
 #pragma clang fp contract(off)
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float *xr = x + static_cast<int64_t>(row) * dim;
-    TO *yr = y + static_cast<int64_t>(row) * dim;
+    __shared__ float part[4];
+    const int row = blockIdx.x;
+    const int t = threadIdx.x;
+    const int64_t ro = static_cast<int64_t>(row) * dim;
+    float4_t v[NV], gm[NV];
     float ss = 0.0f;
-    for (int i = lane; i < dim; i += 64) {
-        const float v = xr[i];
-        ss += v * v;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = (i * 256 + t) * 4;
+        const float4_t z = float4_t{0.f, 0.f, 0.f, 0.f};
+        v[i] = e < dim ? *reinterpret_cast<const float4_t *>(x + ro + e) : z;
+        gm[i] = e < dim ? *reinterpret_cast<const float4_t *>(gamma + e) : z;
+        if (add.p && e < dim) {
+            float4_t u = *reinterpret_cast<const float4_t *>(add.p + ro + e);
+            for (int k = 1; k < add.ys; ++k) u += *reinterpret_cast<const float4_t *>(add.p + k * add.stride + ro + e);
+            if (scale) {
+                const float4_t sc = *reinterpret_cast<const float4_t *>(scale + e);
+                u = u * sc;
+            }
+            v[i] = v[i] + u;
+        }
     }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
     ss = wave_sum(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
     const float m = sqrtf(ss / static_cast<float>(dim) + eps);
-    for (int i = lane; i < dim; i += 64) {
-        const float v = xr[i];
-        yr[i] = static_cast<TO>((v / m) * gamma[i]);
-        if (copy) copy[static_cast<int64_t>(row) * dim + i] = v;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = (i * 256 + t) * 4;
+        if (e >= dim) continue;
+        TO *yo = y + ro + e;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) yo[j] = static_cast<TO>((v[i][j] / m) * gm[i][j]);
+        if (h) *reinterpret_cast<float4_t *>(h + ro + e) = v[i];
+    }
+}
+
+// dim % 4 == 0 and dim <= 8192 (checked at create)
+template <typename TO>
+hipError_t launch_norm(const float *x, Partials add, const float *scale, float *h, const float *gamma, TO *y, int rows,
+                       int dim, float eps, hipStream_t stream) {
+    const int nv = (dim + 1023) / 1024;
+    if (nv <= 1)
+        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+    else if (nv <= 2)
+        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+    else if (nv <= 4)
+        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+    else
+        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+    return hipGetLastError();
+}
+
+// t = f16(silu(g) * u) from the gate|up projection's partials (gate columns, then up columns, ys
+// arrays of [rows, 2 * ffn]); four columns per thread.
+__global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t, int rows, int ffn) {
+    const int c4n = ffn / 4;
+    const int64_t total = static_cast<int64_t>(rows) * c4n;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t row = e / c4n;
+        const int col = static_cast<int>(e - row * c4n) * 4;
+        const float *pr = gu.p + row * 2 * ffn + col;
+        float4_t g = *reinterpret_cast<const float4_t *>(pr), u = *reinterpret_cast<const float4_t *>(pr + ffn);
+        for (int k = 1; k < gu.ys; ++k) {
+            g += *reinterpret_cast<const float4_t *>(pr + k * gu.stride);
+            u += *reinterpret_cast<const float4_t *>(pr + k * gu.stride + ffn);
+        }
+        half4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = static_cast<half_t>(silu_mul(g[j], u[j]));
+        *reinterpret_cast<half4_t *>(t + row * ffn + col) = o;
     }
 }
 
@@ -99,10 +169,14 @@ Plan plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t cap) {
     p.t16 = take(2 * lanes * g.ffn);
     p.qkv = take(sizeof(float) * lanes * (qw + 2 * kvw));
     p.q = take(sizeof(float) * lanes * qw);
-    size_t gb = nt_workspace_bytes(lanes, g.dim, qw + 2 * kvw, 0);
-    const size_t gb2[3] = {nt_workspace_bytes(lanes, qw, g.dim, 2), nt_workspace_bytes(lanes, g.dim, 2 * g.ffn, 1),
-                           nt_workspace_bytes(lanes, g.ffn, g.dim, 2)};
-    for (size_t v : gb2) gb = v > gb ? v : gb;
+    // one partial region serves every projection: each one's partials are summed by its consumer
+    // before the next projection runs
+    size_t gb = 0;
+    const int64_t shapes[4][3] = {{g.dim, qw + 2 * kvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}};
+    for (const auto &sh : shapes) {
+        const size_t v = lds_partial_bytes(pick_lds(lanes, sh[0], sh[1], static_cast<int>(sh[2])), lanes, sh[1]);
+        gb = v > gb ? v : gb;
+    }
     p.gemm_bytes = gb;
     p.gemm_part = take(gb);
     const int64_t win = g.window > 0 && g.window < cap ? g.window : cap;
@@ -113,9 +187,13 @@ Plan plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t cap) {
     return p;
 }
 
+// One projection of the step on the A-sharing kernel. With several k ranges it leaves the
+// partials in `part` and returns them for the consumer to sum; with one it applies its own
+// epilogue (c, c16, scale) and returns the plain output (`plain`, or {} for the residual form,
+// whose result is already in h).
 template <int MODE>
-hipError_t gemm_nt_launch(const half_t *a, const half_t *w, float *c, half_t *c16, const float *scale, int m, int k,
-                          int n, void *part, size_t part_bytes, hipStream_t stream) {
+hipError_t stack_gemm(const half_t *a, const half_t *w, float *c, half_t *c16, const float *scale, int m, int k, int n,
+                      float *part, const float *plain, Partials &out, hipStream_t stream) {
     GemmParams p{};
     p.a = a;
     p.w = w;
@@ -125,7 +203,9 @@ hipError_t gemm_nt_launch(const half_t *a, const half_t *w, float *c, half_t *c1
     p.m = m;
     p.k = k;
     p.n = n;
-    return launch_nt<MODE>(p, (m + 15) / 16, part, part_bytes, stream);
+    const LdsPlan pl = pick_lds(m, k, n, MODE);
+    out = pl.ys > 1 ? Partials{part, pl.ys, static_cast<int64_t>(m) * n} : Partials{plain, 1, 0};
+    return launch_lds_nt<MODE>(p, pl, part, stream, false);
 }
 
 #define STACK_STEP(expr)                          \
@@ -147,49 +227,51 @@ hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const d
     half_t *t16 = reinterpret_cast<half_t *>(ws + pl.t16);
     float *qkv = reinterpret_cast<float *>(ws + pl.qkv);
     float *q = reinterpret_cast<float *>(ws + pl.q);
-    void *gpart = pl.gemm_bytes ? ws + pl.gemm_part : nullptr;
+    float *gpart = pl.gemm_bytes ? reinterpret_cast<float *>(ws + pl.gemm_part) : nullptr;
     float *apart = pl.attn_bytes ? reinterpret_cast<float *>(ws + pl.attn_part) : nullptr;
     const int max_chunks = apart ? (pl.max_window + kChunk - 1) / kChunk : 0;
-    const unsigned norm_grid = static_cast<unsigned>((lanes + 3) / 4);
     const float qscale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
     const DevSpans spans{s.pos, static_cast<int>(g.window)};
+    Partials pending{};             // the previous layer's down projection, not yet in h
+    const float *pending_scale = nullptr;
     for (int64_t li = 0; li < g.layers; ++li) {
         const dtts_stack_layer &L = s.layers[li];
-        const float *hin = li == 0 ? x : h;
-        stack_norm<half_t><<<norm_grid, 256, 0, stream>>>(hin, L.attn_norm, a16, li == 0 ? h : nullptr, lanes, dim,
-                                                          g.eps);
-        STACK_STEP(hipGetLastError());
-        STACK_STEP(gemm_nt_launch<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, lanes, dim,
-                                     qkvw, gpart, pl.gemm_bytes, stream));
+        // h = x (layer 0) or h + the previous layer's MLP output; a = f16(rms_norm(h))
+        STACK_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a16, lanes, dim, g.eps, stream));
+        Partials r{};
+        STACK_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, lanes, dim, qkvw,
+                                 gpart, qkv, r, stream));
         const int waves = lanes * (heads + n_kv);
         qk_rope_kernel<float, DevPositions><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
-            qkv, g.qk_norm ? L.qk_norms : nullptr, s.cos_t, s.sin_t, DevPositions{s.pos}, q, nullptr,
+            r.p, g.qk_norm ? L.qk_norms : nullptr, s.cos_t, s.sin_t, DevPositions{s.pos}, q, nullptr,
             reinterpret_cast<half_t *>(caches[li].k), reinterpret_cast<half_t *>(caches[li].v), lanes, heads, n_kv,
-            hd, cap, g.eps, qscale);
+            hd, cap, g.eps, qscale, r.ys, r.stride);
         STACK_STEP(hipGetLastError());
         STACK_STEP(launch_attention(q, reinterpret_cast<const half_t *>(caches[li].k),
                                     reinterpret_cast<const half_t *>(caches[li].v), a16, apart, max_chunks, lanes,
                                     n_kv, gqa, hd, cap, spans, stream));
-        STACK_STEP(gemm_nt_launch<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr,
-                                     g.layer_scale ? L.attn_scale : nullptr, lanes, qw, dim, gpart, pl.gemm_bytes,
-                                     stream));
-        stack_norm<half_t><<<norm_grid, 256, 0, stream>>>(h, L.ffn_norm, a16, nullptr, lanes, dim, g.eps);
-        STACK_STEP(hipGetLastError());
-        STACK_STEP(gemm_nt_launch<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, lanes,
-                                     dim, 2 * ffn, gpart, pl.gemm_bytes, stream));
-        STACK_STEP(gemm_nt_launch<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr,
-                                     g.layer_scale ? L.mlp_scale : nullptr, lanes, ffn, dim, gpart, pl.gemm_bytes,
-                                     stream));
+        const float *attn_scale = g.layer_scale ? L.attn_scale : nullptr;
+        STACK_STEP(stack_gemm<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr, attn_scale, lanes, qw, dim,
+                                 gpart, nullptr, r, stream));
+        // h += attn * attn_scale (when the projection left partials); a = f16(rms_norm(h))
+        STACK_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, lanes, dim, g.eps, stream));
+        STACK_STEP(stack_gemm<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, lanes, dim,
+                                 2 * ffn, gpart, nullptr, r, stream));
+        if (r.p) {
+            stack_gateup_merge<<<grid_for(int64_t(lanes) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, lanes, ffn);
+            STACK_STEP(hipGetLastError());
+        }
+        const float *mlp_scale = g.layer_scale ? L.mlp_scale : nullptr;
+        STACK_STEP(stack_gemm<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr, mlp_scale, lanes, ffn, dim,
+                                 gpart, nullptr, pending, stream));
+        pending_scale = mlp_scale;
     }
-    stack_norm<float><<<norm_grid, 256, 0, stream>>>(h, s.final_norm, out, nullptr, lanes, dim, g.eps);
-    return hipGetLastError();
+    // h + the last MLP output, then the final norm
+    return launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, lanes, dim, g.eps,
+                       stream);
 }
 
-bool tiles_ok(int64_t lanes, int64_t k, int64_t n, int mode) {
-    const int64_t cols = mode == 1 ? n / 2 : n;
-    return lanes <= 64 && k % 64 == 0 && cols % 16 == 0 &&
-           pick_nt_split(cols / 16, mode == 1 ? 2 : 1, k, false).ks > 0;
-}
+bool tiles_ok(int64_t k, int64_t n, int mode) { return pick_lds(kStackMaxLanes, k, n, mode).nc > 0; }
 
 }  // namespace
 }  // namespace dtts
@@ -215,10 +297,11 @@ extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stac
                  (long long)gqa);
     DTTS_REQUIRE(g.window >= 0 && g.eps >= 0.0f && g.rope_base > 0.0, "dtts_stack_create: bad window, eps or base");
     const int64_t qw = g.heads * g.head_dim, qkvw = (g.heads + 2 * g.n_kv) * g.head_dim;
-    DTTS_REQUIRE(dtts::tiles_ok(dtts::kStackMaxLanes, g.dim, qkvw, 0) && dtts::tiles_ok(dtts::kStackMaxLanes, qw, g.dim, 2) &&
-                     dtts::tiles_ok(dtts::kStackMaxLanes, g.dim, 2 * g.ffn, 1) &&
-                     dtts::tiles_ok(dtts::kStackMaxLanes, g.ffn, g.dim, 2),
-                 "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of 64");
+    DTTS_REQUIRE(dtts::tiles_ok(g.dim, qkvw, 0) && dtts::tiles_ok(qw, g.dim, 2) && dtts::tiles_ok(g.dim, 2 * g.ffn, 1) &&
+                     dtts::tiles_ok(g.ffn, g.dim, 2),
+                 "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of 128");
+    DTTS_REQUIRE(g.dim % 4 == 0 && g.dim <= 8192, "dtts_stack_create: dim %lld (a multiple of 4, at most 8192)",
+                 (long long)g.dim);
     DTTS_REQUIRE(g.capacity < (int64_t(1) << 24) && g.dim * g.ffn < (int64_t(1) << 31) && qkvw * g.dim < (int64_t(1) << 31),
                  "dtts_stack_create: geometry too large");
     for (int64_t i = 0; i < g.layers; ++i) {
@@ -228,10 +311,13 @@ extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stac
         DTTS_REQUIRE(!g.qk_norm || L.qk_norms, "dtts_stack_create: layer %lld has no qk_norms", (long long)i);
         DTTS_REQUIRE(!g.layer_scale || (L.attn_scale && L.mlp_scale), "dtts_stack_create: layer %lld has no scales",
                      (long long)i);
+        DTTS_REQUIRE(dtts::aligned(L.attn_norm, 16) && dtts::aligned(L.ffn_norm, 16),
+                     "dtts_stack_create: layer %lld norm weights not 16-byte aligned", (long long)i);
         DTTS_REQUIRE(dtts::aligned(L.wqkv, 16) && dtts::aligned(L.wo, 16) && dtts::aligned(L.w_gateup, 16) &&
                          dtts::aligned(L.wdown, 16),
                      "dtts_stack_create: layer %lld projection weights not 16-byte aligned", (long long)i);
     }
+    DTTS_REQUIRE(dtts::aligned(final_norm, 16), "dtts_stack_create: final norm weight not 16-byte aligned");
     dtts_stack *s = new (std::nothrow) dtts_stack();
     DTTS_REQUIRE(s, "dtts_stack_create: out of host memory");
     s->geo = g;

@@ -75,7 +75,7 @@ def test_stack_create_and_decode_check_arguments_on_the_host():
     g.ffn = 500
     rc = lib.dtts_stack_create(ctypes.byref(g), ctypes.cast(layers, ctypes.c_void_p), ctypes.c_void_p(16),
                                ctypes.byref(handle))
-    assert rc == -1 and b"multiples of 64" in lib.dtts_last_error()
+    assert rc == -1 and b"multiples of 128" in lib.dtts_last_error()
     assert lib.dtts_stack_workspace_bytes(None, 4, 16) == 0
     pos = np.zeros(4, np.int32)
     rc = lib.dtts_stack_decode(None, None, None, None, 4, 16, pos.ctypes.data_as(ctypes.c_void_p), None, 0, 0, None)

@@ -128,5 +128,5 @@ def test_stack_rejects_bad_arguments(dev):
         assert not t.any(), "a rejected call wrote the cache"
     with pytest.raises(DttsError, match="heads"):
         stack.Stack(replace(geo, heads=3), layers, fn, dev)
-    with pytest.raises(DttsError, match="multiples of 64"):
+    with pytest.raises(DttsError, match="multiples of 128"):
         stack.Stack(replace(geo, ffn=500), stack.random_weights(replace(geo, ffn=500), 95)[0], fn, dev)
