@@ -104,9 +104,16 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
     const T *src = row + h * hd;
     const bool is_q = h < heads;
     const bool act = lane < half;
-    auto ld = [&](const T *q) {
-        float v = static_cast<float>(q[0]);
-        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
+    auto ld = [&](const T *q) {  // the first 8 partials requested together, summed in order
+        float w[8];
+#pragma unroll
+        for (int y = 0; y < 8; ++y)
+            if (y < ys) w[y] = static_cast<float>(q[y * ystride]);
+        float v = w[0];
+#pragma unroll
+        for (int y = 1; y < 8; ++y)
+            if (y < ys) v += w[y];
+        for (int y = 8; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
         return v;
     };
     float x1 = 0.0f, x2 = 0.0f;

@@ -60,6 +60,22 @@ struct Partials {
     int64_t stride;
 };
 
+// The ordered sum of ys partial float4s `stride` floats apart: the first U requested together,
+// then summed in order (a plain loop would wait for each load before issuing the next).
+template <int U>
+__device__ __forceinline__ float4_t sum_parts(const float *p, int ys, int64_t stride) {
+    float4_t v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+        if (k < ys) v[k] = *reinterpret_cast<const float4_t *>(p + k * stride);
+    float4_t u = v[0];
+#pragma unroll
+    for (int k = 1; k < U; ++k)
+        if (k < ys) u += v[k];
+    for (int k = U; k < ys; ++k) u += *reinterpret_cast<const float4_t *>(p + k * stride);
+    return u;
+}
+
 // Row-wise RMSNorm of the stack, f32 in, the f16 input of the next projection out (or the final
 // f32 output). When `add` is set, the row first takes the residual update of the projection that
 // precedes it: x + (sum of add's partials) * scale (LayerScale, or 1), rounded as the reference
@@ -84,8 +100,7 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
         v[i] = e < dim ? *reinterpret_cast<const float4_t *>(x + ro + e) : z;
         gm[i] = e < dim ? *reinterpret_cast<const float4_t *>(gamma + e) : z;
         if (add.p && e < dim) {
-            float4_t u = *reinterpret_cast<const float4_t *>(add.p + ro + e);
-            for (int k = 1; k < add.ys; ++k) u += *reinterpret_cast<const float4_t *>(add.p + k * add.stride + ro + e);
+            float4_t u = sum_parts<12>(add.p + ro + e, add.ys, add.stride);
             if (scale) {
                 const float4_t sc = *reinterpret_cast<const float4_t *>(scale + e);
                 u = u * sc;
@@ -136,11 +151,7 @@ __global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t
         const int64_t row = e / c4n;
         const int col = static_cast<int>(e - row * c4n) * 4;
         const float *pr = gu.p + row * 2 * ffn + col;
-        float4_t g = *reinterpret_cast<const float4_t *>(pr), u = *reinterpret_cast<const float4_t *>(pr + ffn);
-        for (int k = 1; k < gu.ys; ++k) {
-            g += *reinterpret_cast<const float4_t *>(pr + k * gu.stride);
-            u += *reinterpret_cast<const float4_t *>(pr + k * gu.stride + ffn);
-        }
+        const float4_t g = sum_parts<8>(pr, gu.ys, gu.stride), u = sum_parts<8>(pr + ffn, gu.ys, gu.stride);
         half4_t o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = static_cast<half_t>(silu_mul(g[j], u[j]));
