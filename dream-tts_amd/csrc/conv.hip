@@ -38,7 +38,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_nlc_f16_mfma(C
     conv_snake_table<Cfg>(smem, n0, p.a_out, p.r_out);
     conv_mainloop<Cfg, SNAKE_IN, KT>(p, xl, l0, n0, smem, acc);
     conv_epilogue<Cfg>(acc, smem, static_cast<int64_t>(lane_idx) * p.L, l0, n0, p.L, p.cout, p.bias, p.res, p.y_pre,
-                       p.y, p.a_out, p.act);
+                       p.y, p.a_out, p.act, p.scale);
 }
 
 // Any shape: one thread per output element, taps and channels looped directly. For shapes the
@@ -62,9 +62,8 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_direct(ConvParams p, int64_t
                 acc += xv * static_cast<float>(wr[c]);
             }
         }
-        float v = acc;
-        if (p.bias) v += static_cast<float>(p.bias[n]);
-        if (p.res) v += static_cast<float>(p.res[e]);
+        const float v = conv_sum(acc, p.bias ? static_cast<float>(p.bias[n]) : 0.0f, p.scale, n,
+                                 p.res ? static_cast<float>(p.res[e]) : 0.0f);
         half_t h = static_cast<half_t>(conv_act(v, p.act));
         if (p.y_pre) p.y_pre[e] = h;
         if (p.a_out) h = static_cast<half_t>(snake_f16out(static_cast<float>(h), p.a_out[n], p.r_out[n]));
@@ -150,7 +149,7 @@ struct Choice {
 
 Choice choose(const dtts_conv_desc *d) {
     Choice c{"direct", 0, 0, d->in_alpha != nullptr, direct_offsets_fit(d->len, d->cin, d->cout, d->k)};
-    if (conv_narrow_eligible(d)) {
+    if (conv_narrow_eligible(d) && d->act <= 1 && !d->out_scale) {
         c.path = "narrow";
         return c;
     }
@@ -206,7 +205,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     DTTS_REQUIRE(d->pad_left <= (d->k - 1) * d->dilation,
                  "%s: pad_left %lld exceeds the receptive field (k-1)*dil = %lld", name,
                  (long long)d->pad_left, (long long)((d->k - 1) * d->dilation));
-    DTTS_REQUIRE(d->act == 0 || d->act == 1, "%s: act %d unknown", name, d->act);
+    DTTS_REQUIRE(d->act >= 0 && d->act <= 2, "%s: act %d unknown", name, d->act);
     if (d->lanes == 0 || d->len == 0) return DTTS_OK;
     DTTS_REQUIRE(d->x && d->w && d->y, "%s: null x, w or y", name);
     DTTS_REQUIRE((d->in_alpha == nullptr) == (d->in_brecip == nullptr), "%s: in_alpha and in_brecip go together", name);
@@ -233,6 +232,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     p.dil = static_cast<int>(d->dilation);
     p.pad_left = static_cast<int>(d->pad_left);
     p.act = d->act;
+    p.scale = d->out_scale;
 
     const Choice ch = choose(d);
     hipError_t e;

@@ -91,6 +91,7 @@ struct ConvArgs {
     half_t *y;
     const float *a_out;
     const float *r_out;
+    const float *scale;  // [cout] factor on (sum + bias) before the residual, or null
     int L, cin, cout, k, dil, pad_left, act;
     int tiles_m, tiles_n, total_tiles, tiles_per_xcd;
 };
@@ -101,7 +102,21 @@ inline bool direct_offsets_fit(int64_t len, int64_t cin, int64_t cout, int64_t k
     return len * cin * 2 < (int64_t(1) << 31) && cout * k * cin * 2 < (int64_t(1) << 31);
 }
 
-__device__ __forceinline__ float conv_act(float v, int act) { return act == 1 ? tanhf(v) : v; }
+// act 1: tanh; act 2: GELU, erf form (0.5 v (1 + erf(v / sqrt 2))).
+__device__ __forceinline__ float conv_act(float v, int act) {
+    if (act == 1) return tanhf(v);
+    if (act == 2) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    return v;
+}
+
+// The epilogue's sum for one element: (acc + bias), times the channel's scale when there is one,
+// plus the residual; each step rounded in f32 (no contraction), as the reference's separate ops.
+__device__ __forceinline__ float conv_sum(float acc, float bias, const float *scale, int n, float res) {
+#pragma clang fp contract(off)
+    float t = acc + bias;
+    if (scale) t = t * scale[n];
+    return t + res;
+}
 
 // XCD-aware tile order: dispatch slot b runs on XCD b % 8; each XCD takes a contiguous range of
 // (lane, m, n) tiles, N fastest, so an M tile's window is fetched into one L2 and reused by its
@@ -524,7 +539,8 @@ __device__ __forceinline__ void wave_lds_order() {
 template <typename Cfg>
 __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
                                               int l0, int n0, int lmax, int ld, const half_t *bias, const half_t *res,
-                                              half_t *y_pre, half_t *y, const float *a_out, int act) {
+                                              half_t *y_pre, half_t *y, const float *a_out, int act,
+                                              const float *scale) {
     constexpr int CG = Cfg::WTN / 8;  // 8-channel groups per wave row
     constexpr int NG = 32 * CG / 64;  // groups per lane per 32-row block
     static_assert((32 * CG) % 64 == 0, "a 32-row block splits evenly over the lanes");
@@ -575,7 +591,8 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = (v[q] + static_cast<float>(bb[u][q])) + static_cast<float>(rr[i][u][q]);
+            for (int q = 0; q < 8; ++q)
+                v[q] = conv_sum(v[q], static_cast<float>(bb[u][q]), scale, n + q, static_cast<float>(rr[i][u][q]));
             const int64_t off = (row0 + l) * ld + n;
             half8_t h;
 #pragma unroll

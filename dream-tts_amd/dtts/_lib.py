@@ -58,6 +58,8 @@ SIGNATURES = {
     "dtts_decode_attention_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],
     "dtts_decode_attention_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
     "dtts_decode_attention_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
+    "dtts_rvq_lookup_sum_f16": [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "dtts_depthwise_layernorm_nlc_f16": [_P, _P, _P, _P, _P, _F32, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],

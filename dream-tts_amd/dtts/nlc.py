@@ -22,7 +22,7 @@ class ConvDesc(ctypes.Structure):
         ("in_alpha", ctypes.c_void_p), ("in_brecip", ctypes.c_void_p),
         ("residual", ctypes.c_void_p), ("y_pre", ctypes.c_void_p),
         ("out_alpha", ctypes.c_void_p), ("out_brecip", ctypes.c_void_p),
-        ("y", ctypes.c_void_p), ("act", ctypes.c_int32),
+        ("y", ctypes.c_void_p), ("act", ctypes.c_int32), ("out_scale", ctypes.c_void_p),
     ]
 
 
@@ -40,12 +40,13 @@ def _need(t, name, what, dtype, shape=None):
 
 
 def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, residual=None,
-           snake_out=None, want_pre=False, act=None, out=None):
+           snake_out=None, want_pre=False, act=None, scale=None, out=None):
     """The general fused channels-last conv (dtts_conv1d_nlc_f16_ex).
 
     x [lanes, L, cin] f16, w_tm [cout, k*cin] f16, bias [cout] f16. snake_in / snake_out are
-    (alpha, brecip) f32 pairs applied to the input as loaded / to the rounded output. Returns y,
-    or (y_pre, y) when want_pre."""
+    (alpha, brecip) f32 pairs applied to the input as loaded / to the rounded output. act: None,
+    "tanh" or "gelu"; scale: f32 [cout] on (sum + bias) before the residual. Returns y, or
+    (y_pre, y) when want_pre."""
     name = "nlc.conv1d"
     if x.dim() != 3:
         raise DttsError(f"{name}: x must be [lanes, L, cin]")
@@ -55,6 +56,7 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
     _need(w_tm, name, "w_tm", torch.float16, (cout, k * cin))
     _need(bias, name, "bias", torch.float16, (cout,))
     _need(residual, name, "residual", torch.float16, (lanes, length, cout))
+    _need(scale, name, "scale", torch.float32, (cout,))
     for pair, what, c in ((snake_in, "snake_in", cin), (snake_out, "snake_out", cout)):
         if pair is not None:
             for t in pair:
@@ -67,7 +69,7 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
                  _p(snake_in[0]) if snake_in else None, _p(snake_in[1]) if snake_in else None,
                  _p(residual), _p(y_pre),
                  _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
-                 _p(y), {None: 0, "tanh": 1}[act])
+                 _p(y), {None: 0, "tanh": 1, "gelu": 2}[act], _p(scale))
     call("dtts_conv1d_nlc_f16_ex", ctypes.byref(d), stream_handle())
     return (y_pre, y) if want_pre else y
 

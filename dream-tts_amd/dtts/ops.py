@@ -291,3 +291,35 @@ def q8_0_matmul(x, blocks, mode="w8a16"):
     y = torch.empty((m, n), dtype=_F32, device=x.device)
     call("dtts_gemm_q8_0", ptr(x), ptr(blocks), ptr(y), m, k, n, {"w8a16": 0, "w8a8": 1}[mode], stream_handle())
     return y
+
+
+# ---------------------------------------------------------------- codec front half
+
+def rvq_lookup_sum(codes, codebooks, n_first, out=None):
+    """Rvq::decode's lookups for both quantizer stacks (dtts_rvq_lookup_sum_f16): codes [rows,
+    n_books] int32, codebooks [n_books, size, dim] f32 (folded) -> [rows, 2*dim] f16."""
+    name = "rvq_lookup_sum"
+    _check(codes, name, (torch.int32,), "codes")
+    _check(codebooks, name, (torch.float32,), "codebooks")
+    rows, n_books = codes.shape
+    nb, size, dim = codebooks.shape
+    if nb != n_books:
+        raise DttsError(f"{name}: {n_books} codes per row for {nb} codebooks")
+    y = torch.empty((rows, 2 * dim), dtype=torch.float16, device=codes.device) if out is None else out
+    call("dtts_rvq_lookup_sum_f16", ptr(codes), ptr(codebooks), n_books, n_first, size, dim, ptr(y), rows,
+         stream_handle())
+    return y
+
+
+def depthwise_layernorm(x, taps, bias, ln_weight, ln_bias, eps, out=None):
+    """ConvNext's depthwise causal conv + LayerNorm (dtts_depthwise_layernorm_nlc_f16): x [lanes,
+    L, C] f16, taps [C, k] f32, the rest [C] f32."""
+    name = "depthwise_layernorm"
+    _check(x, name, (torch.float16,), "x")
+    for t, what in ((taps, "taps"), (bias, "bias"), (ln_weight, "ln_weight"), (ln_bias, "ln_bias")):
+        _check(t, name, (torch.float32,), what)
+    lanes, length, c = x.shape
+    y = torch.empty_like(x) if out is None else out
+    call("dtts_depthwise_layernorm_nlc_f16", ptr(x), ptr(taps), ptr(bias), ptr(ln_weight), ptr(ln_bias),
+         float(eps), ptr(y), lanes, length, c, taps.shape[1], stream_handle())
+    return y

@@ -83,7 +83,10 @@ int dtts_snake_nlc_f16(const dtts_f16 *x, const float *alpha, const float *breci
  * lib.rs:630-635), not NlcConv's [k*cin, cout]: both GEMM operands then run along K, which is
  * what the matrix cores consume. dtts_tap_weight_to_tap_major converts. x, w_tm, y, bias,
  * residual and y_pre must be 16-byte aligned for the matrix-core kernel; other shapes or
- * alignments take a direct (slow, exact-semantics) kernel. act: 0 none, 1 tanh. */
+ * alignments take a direct (slow, exact-semantics) kernel. act: 0 none, 1 tanh, 2 GELU
+ * (erf form, gelu_exact, crates/tts-nn/src/lib.rs:1129-1131). With out_scale the sum is
+ *   s[l, n] = residual[l, n] + out_scale[n] * (bias[n] + sum ...), the scaled term rounded in
+ * f32 before the add. */
 typedef struct dtts_conv_desc {
     int64_t lanes, len, cin, cout, k, dilation, pad_left;
     const void *x;          /* [lanes, len, cin] */
@@ -97,6 +100,8 @@ typedef struct dtts_conv_desc {
     const float *out_brecip;
     void *y;                /* [lanes, len, cout] */
     int32_t act;
+    const float *out_scale; /* [cout] factor on (sum + bias) before the residual is added, or NULL:
+                               y = residual + scale * (bias + sum), ConvNeXt's gamma and LayerScale */
 } dtts_conv_desc;
 
 int dtts_conv1d_nlc_f16_ex(const dtts_conv_desc *desc, hipStream_t stream);
@@ -336,6 +341,29 @@ size_t dtts_stack_workspace_bytes(const dtts_stack *stack, int64_t lanes, int64_
 int dtts_stack_decode(dtts_stack *stack, const float *x, float *out, const dtts_stack_cache *caches, int64_t lanes,
                       int64_t cap, const int32_t *pos, void *workspace, size_t ws_bytes, int32_t flags,
                       hipStream_t stream);
+
+/* ------------------------------------------------------------------ f-3 codec front half */
+
+/* Rvq::decode's lookups (crates/qwen3tts/src/codec.rs:296-313) for both quantizer stacks at
+ * once: out[r] = [sum_{b < n_first} books[b][codes[r, b]] | sum_{b >= n_first} books[b][codes[r, b]]],
+ * each sum in codebook order in f32, stored f16. codes [rows, n_books] int32 (device); books
+ * [n_books, book_size, dim] f32, already divided by the clamped cluster usage as Rvq::load folds
+ * them (codec.rs:275-282); out [rows, 2 * dim]. The two output projections are then one conv
+ * (k = 1) over the concatenated width: Ws and Wa side by side along the input channels. Codes
+ * outside [0, book_size) are clamped on the device (the reference's index_select refuses them;
+ * callers with host codes check them first, as the front-half driver does). */
+int dtts_rvq_lookup_sum_f16(const int32_t *codes, const float *codebooks, int64_t n_books, int64_t n_first,
+                            int64_t book_size, int64_t dim, dtts_f16 *out, int64_t rows, hipStream_t stream);
+
+/* ConvNext::forward's depthwise conv and LayerNorm (codec.rs:186-188): per lane and channel c,
+ *   h[l, c] = sum_{t < k} x[l - (k-1) + t, c] * taps[c, t] + bias[c]   (zero before the start;
+ *             nlc::depthwise, crates/tts-nn/src/nlc.rs:236-256)
+ *   y[l, :] = (h - mean) / sqrt(var + eps) * ln_weight + ln_bias       (layer_norm, lib.rs:1006-1035)
+ * x, y [lanes, len, channels] f16 (not in place), taps [channels, k] f32 (the [C, 1, k] weight),
+ * bias, ln_weight, ln_bias [channels] f32. channels % 8 == 0, <= 2048; k <= 64. */
+int dtts_depthwise_layernorm_nlc_f16(const dtts_f16 *x, const float *taps, const float *bias,
+                                     const float *ln_weight, const float *ln_bias, float eps, dtts_f16 *y,
+                                     int64_t lanes, int64_t len, int64_t channels, int64_t k, hipStream_t stream);
 
 /* ------------------------------------------------------------------ a12-a14 f16 projections */
 

@@ -188,7 +188,9 @@ def conv1d_nlc_f64(x, w_tap, bias, dil, pad_left=None, snake=None, res=None):
 
 
 def conv1d_nlc_f16(x_bits, w_tap_bits, bias_bits, dil, pad_left=None, snake=None, res_bits=None,
-                   act_tanh=False):
+                   act_tanh=False, act=None, scale=None):
+    """f16 storage, f32 accumulation. act: None, "tanh" or "gelu" (act_tanh=True is "tanh");
+    scale: f32 [cout] applied to (sum + bias) before the residual."""
     x, w = _u16(x_bits), _u16(w_tap_bits)
     lanes, length, cin = x.shape
     cout = w.shape[-1]
@@ -196,12 +198,22 @@ def conv1d_nlc_f16(x_bits, w_tap_bits, bias_bits, dil, pad_left=None, snake=None
     if pad_left is None:
         pad_left = (k - 1) * dil
     a, r = (None, None) if snake is None else (_f32(snake[0]), _f32(snake[1]))
-    b, rs = _u16(bias_bits), _u16(res_bits)
+    b, rs, sc = _u16(bias_bits), _u16(res_bits), _f32(scale)
+    code = {None: 0, "tanh": 1, "gelu": 2}["tanh" if act_tanh else act]
     y = np.empty((lanes, length, cout), np.uint16)
-    lib().or_conv1d_nlc_f16(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
-                            _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),
-                            _I64(pad_left), ctypes.c_int32(1 if act_tanh else 0))
+    lib().or_conv1d_nlc_f16_ex(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
+                               _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),
+                               _I64(pad_left), ctypes.c_int32(code), _ptr(sc))
     return y
+
+
+def gelu_erf(x):
+    """gelu_exact's formula in f32 with the C library's erf, elementwise over x (f32)."""
+    x = _f32(x)
+    f = lib().or_gelu_erf
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_float]
+    return np.array([f(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
 
 
 def conv_transpose1d_causal_f64(x, w_iok, bias, stride):
@@ -378,6 +390,32 @@ def swiglu_mul_f32(g, u):
     g, u = _f32(g), _f32(u)
     y = np.empty_like(g)
     lib().or_swiglu_mul_f32(_ptr(g), _ptr(u), _ptr(y), _I64(g.size))
+    return y
+
+
+# ---------------------------------------------------------------- codec front half
+
+def rvq_lookup_sum_f16(codes, books, n_first):
+    """codes [rows, n_books] int32, books [n_books, size, dim] f32 -> [rows, 2*dim] f16 bits."""
+    codes = np.ascontiguousarray(codes, np.int32)
+    books = _f32(books)
+    rows, n_books = codes.shape
+    _, size, dim = books.shape
+    out = np.empty((rows, 2 * dim), np.uint16)
+    lib().or_rvq_lookup_sum_f16(_ptr(codes), _ptr(books), _I64(n_books), _I64(n_first), _I64(size), _I64(dim),
+                                _ptr(out), _I64(rows))
+    return out
+
+
+def depthwise_layernorm_f16(x_bits, taps, bias, ln_w, ln_b, eps):
+    """x [lanes, L, C] f16 bits; taps [C, K] f32 -> [lanes, L, C] f16 bits."""
+    x = _u16(x_bits)
+    lanes, length, c = x.shape
+    taps = _f32(taps)
+    y = np.empty_like(x)
+    lib().or_depthwise_layernorm_f16(_ptr(x), _ptr(taps), _ptr(_f32(bias)), _ptr(_f32(ln_w)), _ptr(_f32(ln_b)),
+                                     ctypes.c_float(eps), _ptr(y), _I64(lanes), _I64(length), _I64(c),
+                                     _I64(taps.shape[1]))
     return y
 
 

@@ -270,10 +270,16 @@ void or_conv1d_nlc_f64(const double *x, const double *w_tap, const double *bias,
  * value an unfused snake_beta_nlc f16 pass would have stored); products accumulate in f32;
  * bias then residual are added in f32 and the sum is rounded once. `act_tanh` applies tanh
  * before that rounding (the decoder's output conv). */
-void or_conv1d_nlc_f16(const uint16_t *x, const uint16_t *w_tap, const uint16_t *bias,
-                       const float *alpha, const float *brecip, const uint16_t *res,
-                       uint16_t *y, int64_t lanes, int64_t len, int64_t cin, int64_t cout,
-                       int64_t k, int64_t dil, int64_t pad_left, int32_t act_tanh) {
+/* gelu_exact (crates/tts-nn/src/lib.rs:1129-1131; CPU op cpu.rs:173-191): 0.5 x (1 + erf(x /
+ * sqrt 2)). erf here is the C library's; the reference's CPU path evaluates a clamped rational
+ * approximation of erf (cpu.rs:10-26) that agrees with it to ~1e-7 absolute. */
+float or_gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+void or_conv1d_nlc_f16_ex(const uint16_t *x, const uint16_t *w_tap, const uint16_t *bias,
+                          const float *alpha, const float *brecip, const uint16_t *res,
+                          uint16_t *y, int64_t lanes, int64_t len, int64_t cin, int64_t cout,
+                          int64_t k, int64_t dil, int64_t pad_left, int32_t act,
+                          const float *scale) {
     float *wf = (float *)malloc(sizeof(float) * (size_t)(k * cin * cout));
     for (int64_t i = 0; i < k * cin * cout; ++i) wf[i] = or_f16_to_f32(w_tap[i]);
 #pragma omp parallel
@@ -304,8 +310,10 @@ void or_conv1d_nlc_f16(const uint16_t *x, const uint16_t *w_tap, const uint16_t 
                 for (int64_t co = 0; co < cout; ++co) {
                     float v = acc[co];
                     if (bias) v += or_f16_to_f32(bias[co]);
+                    if (scale) v = v * scale[co];  /* ConvNeXt's gamma (codec.rs:193) */
                     if (rr) v += or_f16_to_f32(rr[co]);
-                    if (act_tanh) v = tanhf(v);
+                    if (act == 1) v = tanhf(v);
+                    if (act == 2) v = or_gelu_erf(v);
                     yr[co] = or_f32_to_f16(v);
                 }
             }
@@ -313,6 +321,14 @@ void or_conv1d_nlc_f16(const uint16_t *x, const uint16_t *w_tap, const uint16_t 
         free(xs);
     }
     free(wf);
+}
+
+void or_conv1d_nlc_f16(const uint16_t *x, const uint16_t *w_tap, const uint16_t *bias,
+                       const float *alpha, const float *brecip, const uint16_t *res,
+                       uint16_t *y, int64_t lanes, int64_t len, int64_t cin, int64_t cout,
+                       int64_t k, int64_t dil, int64_t pad_left, int32_t act_tanh) {
+    or_conv1d_nlc_f16_ex(x, w_tap, bias, alpha, brecip, res, y, lanes, len, cin, cout, k, dil,
+                         pad_left, act_tanh ? 1 : 0, NULL);
 }
 
 /* ------------------------------------------------------------------ a5 transposed conv */
@@ -856,4 +872,60 @@ void or_abs_and_rel(const float *a, const float *b, int64_t n, float *abs_out, f
     }
     *abs_out = mx;
     *rel_out = sc > 0.0f ? mx / sc : 0.0f;
+}
+
+/* ------------------------------------------------------------------ f-3 codec front half */
+
+/* Rvq::decode's lookups (crates/qwen3tts/src/codec.rs:296-313): per row, the picked codebook rows
+ * summed in codebook order (sum = q0; sum = sum + q1; ...) in f32, for books [0, n_first) and
+ * [n_first, n_books) side by side, each rounded to f16. */
+void or_rvq_lookup_sum_f16(const int32_t *codes, const float *books, int64_t n_books, int64_t n_first,
+                           int64_t size, int64_t dim, uint16_t *out, int64_t rows) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int half = 0; half < 2; ++half) {
+            const int64_t b0 = half ? n_first : 0, b1 = half ? n_books : n_first;
+            for (int64_t d = 0; d < dim; ++d) {
+                float s = 0.0f;
+                for (int64_t b = b0; b < b1; ++b) {
+                    const float v = books[(b * size + codes[r * n_books + b]) * dim + d];
+                    s = b == b0 ? v : s + v;
+                }
+                out[r * 2 * dim + half * dim + d] = or_f32_to_f16(s);
+            }
+        }
+}
+
+/* ConvNext's depthwise conv and LayerNorm (codec.rs:186-188): nlc::depthwise (crates/tts-nn/src/
+ * nlc.rs:236-256: left zero padding of k-1, taps accumulated oldest first, then the bias) and
+ * layer_norm_plain (lib.rs:1030-1035: mean, centred, mean of squares, divide by sqrt(var + eps))
+ * times the weight plus the bias (lib.rs:1020). f16 in and out, f32 inside. */
+void or_depthwise_layernorm_f16(const uint16_t *x, const float *taps, const float *bias, const float *lnw,
+                                const float *lnb, float eps, uint16_t *y, int64_t lanes, int64_t len,
+                                int64_t C, int64_t K) {
+    float *h = (float *)malloc(sizeof(float) * (size_t)C);
+    for (int64_t b = 0; b < lanes; ++b)
+        for (int64_t l = 0; l < len; ++l) {
+            for (int64_t c = 0; c < C; ++c) {
+                float acc = 0.0f;
+                for (int64_t t = 0; t < K; ++t) {
+                    const int64_t s = l - (K - 1) + t;
+                    const float xv = s >= 0 ? or_f16_to_f32(x[(b * len + s) * C + c]) : 0.0f;
+                    const float term = xv * taps[c * K + t];
+                    acc = t == 0 ? term : acc + term;
+                }
+                h[c] = acc + bias[c];
+            }
+            float mean = 0.0f;
+            for (int64_t c = 0; c < C; ++c) mean += h[c];
+            mean /= (float)C;
+            float var = 0.0f;
+            for (int64_t c = 0; c < C; ++c) {
+                h[c] = h[c] - mean;
+                var += h[c] * h[c];
+            }
+            var /= (float)C;
+            const float den = sqrtf(var + eps);
+            for (int64_t c = 0; c < C; ++c) y[(b * len + l) * C + c] = or_f32_to_f16((h[c] / den) * lnw[c] + lnb[c]);
+        }
+    free(h);
 }

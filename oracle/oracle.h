@@ -57,6 +57,12 @@ void or_conv1d_nlc_f64(const double *x, const double *w_tap, const double *bias,
                        const double *alpha, const double *brecip, const double *res, double *y,
                        int64_t lanes, int64_t len, int64_t cin, int64_t cout, int64_t k,
                        int64_t dil, int64_t pad_left);
+float or_gelu_erf(float x);
+void or_conv1d_nlc_f16_ex(const uint16_t *x, const uint16_t *w_tap, const uint16_t *bias,
+                          const float *alpha, const float *brecip, const uint16_t *res,
+                          uint16_t *y, int64_t lanes, int64_t len, int64_t cin, int64_t cout,
+                          int64_t k, int64_t dil, int64_t pad_left, int32_t act,
+                          const float *scale);
 void or_conv1d_nlc_f16(const uint16_t *x, const uint16_t *w_tap, const uint16_t *bias,
                        const float *alpha, const float *brecip, const uint16_t *res,
                        uint16_t *y, int64_t lanes, int64_t len, int64_t cin, int64_t cout,
@@ -133,4 +139,10 @@ void or_abs_and_rel(const float *a, const float *b, int64_t n, float *abs_out, f
 #ifdef __cplusplus
 }
 #endif
+void or_rvq_lookup_sum_f16(const int32_t *codes, const float *books, int64_t n_books, int64_t n_first,
+                           int64_t size, int64_t dim, uint16_t *out, int64_t rows);
+void or_depthwise_layernorm_f16(const uint16_t *x, const float *taps, const float *bias, const float *lnw,
+                                const float *lnb, float eps, uint16_t *y, int64_t lanes, int64_t len,
+                                int64_t C, int64_t K);
+
 #endif
