@@ -12,19 +12,23 @@
 //                   mean, then the variance of the centred values; lib.rs:1006-1035), one wave
 //                   per position.
 //
-// Both are HBM-bound gathers: the lookup reads n_books rows of `dim` f32 per frame and writes
-// 2 * dim f16; depthwise+LN reads its k input rows (the earlier k-1 mostly from cache, as
-// neighbouring positions share them) and writes one row.
-#include "common.hpp"
+//   RMSNorm rows   rms_norm over channels-last rows for the windowed transformer: f16 in, f32
+//                   arithmetic, one rounding out (the reference runs it in f32).
+//   SwiGLU rows    silu(gate) * up from a [rows, 2 * ffn] gate|up projection, f16 out.
+//   window attn    Stack::forward's prefill branch (crates/qwen3tts/src/qwen3.rs:420-443) for a
+//                   sliding window: RoPE on q and k as they are loaded, scores = q.k * scale,
+//                   the causal window mask of causal_window_mask (lib.rs:1210-1224: key j is
+//                   visible to query i when i - window < j <= i), softmax, weighted v.
+//
+// The lookup, depthwise+LN, the norm and SwiGLU are HBM-bound passes: the lookup reads n_books
+// rows of `dim` f32 per frame and writes 2 * dim f16; depthwise+LN reads its k input rows (the
+// earlier k-1 mostly from cache, as neighbouring positions share them) and writes one row.
+#include "norm_rope.hpp"
 
 namespace dtts {
 namespace {
 
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum64(float v) { return wave_sum(v); }
 
 // Thread per (row, 4 output dims). codes [rows, n_books] int32 (clamped into the codebook; the
 // entry point checks them on the host when it is given host codes); books [n_books, size, dim]
@@ -114,6 +118,162 @@ __global__ __launch_bounds__(256) void depthwise_ln_kernel(const half_t *x, cons
     }
 }
 
+// One wave per row: x f16 [rows, C] -> y f16, y = (x / sqrt(mean(x^2) + eps)) * gamma in f32.
+__global__ __launch_bounds__(256) void rms_rows_kernel(const half_t *x, const float *gamma, half_t *y, int64_t rows,
+                                                       int C, float eps) {
+#pragma clang fp contract(off)
+    const int64_t row = blockIdx.x * int64_t(4) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const half_t *xr = x + row * C;
+    float ss = 0.0f;
+    for (int c = lane * 8; c < C; c += 512) {
+        const half8_t v = *reinterpret_cast<const half8_t *>(xr + c);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ss += static_cast<float>(v[q]) * static_cast<float>(v[q]);
+    }
+    const float m = sqrtf(wave_sum(ss) / static_cast<float>(C) + eps);
+    for (int c = lane * 8; c < C; c += 512) {
+        const half8_t v = *reinterpret_cast<const half8_t *>(xr + c);
+        half8_t o;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] = static_cast<half_t>((static_cast<float>(v[q]) / m) * gamma[c + q]);
+        *reinterpret_cast<half8_t *>(y + row * C + c) = o;
+    }
+}
+
+// gu [rows, 2 * ffn] f16 (gate columns, then up columns) -> t [rows, ffn] f16 = silu(g) * u.
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const half_t *gu, half_t *t, int64_t rows, int ffn) {
+    const int q8 = ffn / 8;
+    const int64_t total = rows * q8;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t row = e / q8;
+        const int c = static_cast<int>(e - row * q8) * 8;
+        const half8_t g = *reinterpret_cast<const half8_t *>(gu + row * 2 * ffn + c);
+        const half8_t u = *reinterpret_cast<const half8_t *>(gu + row * 2 * ffn + ffn + c);
+        half8_t o;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float gv = static_cast<float>(g[q]);
+            o[q] = static_cast<half_t>((gv / (1.0f + expf(-gv))) * static_cast<float>(u[q]));
+        }
+        *reinterpret_cast<half8_t *>(t + row * ffn + c) = o;
+    }
+}
+
+// Windowed causal attention over a sequence, D = 64. Workgroup = (64-query block, query head,
+// lane); 4 threads per query, each taking every 4th key of the query's window with an online
+// softmax (running max, sum and weighted v), combined over the 4 at the end. The block's keys
+// ([first query - window + 1, last query]) are staged in LDS once: k roped in f32 (the
+// reference keeps roped k in f32), v as stored. q is roped in registers; scores are scaled
+// after the dot product, as the prefill branch scales the scores.
+constexpr int kWinMax = 192;
+constexpr int kQBlock = 64;
+
+__global__ __launch_bounds__(256) void window_attn_kernel(const half_t *qkv, const float *cos_t, const float *sin_t,
+                                                          half_t *out, int T, int heads, int n_kv, int window,
+                                                          float scale) {
+#pragma clang fp contract(off)
+    constexpr int D = 64, HALF = 32;
+    constexpr int RMAX = kQBlock + kWinMax - 1;
+    __shared__ __attribute__((aligned(16))) float Ks[RMAX][D];
+    __shared__ __attribute__((aligned(16))) half_t Vs[RMAX][D];
+    const int l0 = blockIdx.x * kQBlock;
+    const int h = blockIdx.y;
+    const int lane_idx = blockIdx.z;
+    const int kh = h / (heads / n_kv);
+    const int width = (heads + 2 * n_kv) * D;
+    const half_t *base = qkv + static_cast<int64_t>(lane_idx) * T * width;
+    const int kbase = l0 - window + 1 > 0 ? l0 - window + 1 : 0;
+    const int kend = l0 + kQBlock < T ? l0 + kQBlock : T;  // exclusive
+    const int nrows = kend - kbase;
+    // stage k (roped, f32) and v: one thread per (row, rotation pair)
+    for (int e = threadIdx.x; e < nrows * HALF; e += 256) {
+        const int r = e / HALF, i = e - (e / HALF) * HALF;
+        const int j = kbase + r;
+        const half_t *kr = base + static_cast<int64_t>(j) * width + (heads + kh) * D;
+        float o1, o2;
+        rope_pair(static_cast<float>(kr[i]), static_cast<float>(kr[i + HALF]), cos_t[j * HALF + i], sin_t[j * HALF + i],
+                  o1, o2);
+        Ks[r][i] = o1;
+        Ks[r][i + HALF] = o2;
+        const half_t *vr = base + static_cast<int64_t>(j) * width + (heads + n_kv + kh) * D;
+        Vs[r][i] = vr[i];
+        Vs[r][i + HALF] = vr[i + HALF];
+    }
+    const int qi = threadIdx.x >> 2, sub = threadIdx.x & 3;
+    const int p = l0 + qi;
+    float q[D];
+    if (p < T) {
+        const half_t *qr = base + static_cast<int64_t>(p) * width + h * D;
+#pragma unroll
+        for (int i = 0; i < HALF; ++i)
+            rope_pair(static_cast<float>(qr[i]), static_cast<float>(qr[i + HALF]), cos_t[p * HALF + i],
+                      sin_t[p * HALF + i], q[i], q[i + HALF]);
+    }
+    __syncthreads();
+    if (p >= T) return;  // (no barrier follows)
+    const int jlo = p - window + 1 > 0 ? p - window + 1 : 0;
+    float m = -INFINITY, l = 0.0f, acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    for (int j = jlo + sub; j <= p; j += 4) {
+        const float *kr = Ks[j - kbase];
+        float s = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; d += 4) {
+            const float4_t kv = *reinterpret_cast<const float4_t *>(kr + d);
+            s += q[d] * kv[0];
+            s += q[d + 1] * kv[1];
+            s += q[d + 2] * kv[2];
+            s += q[d + 3] * kv[3];
+        }
+        s = s * scale;
+        const float mn = fmaxf(m, s);
+        const float c = __builtin_expf(m - mn);
+        const float w = __builtin_expf(s - mn);
+        l = l * c + w;
+        const half_t *vr = Vs[j - kbase];
+#pragma unroll
+        for (int d = 0; d < D; d += 8) {
+            const half8_t vv = *reinterpret_cast<const half8_t *>(vr + d);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[d + u] = acc[d + u] * c + w * static_cast<float>(vv[u]);
+        }
+        m = mn;
+    }
+    // combine the 4 threads of the query (adjacent lanes)
+    float mx = m;
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    const float f = m == -INFINITY ? 0.0f : __builtin_expf(m - mx);
+    float ls = l * f;
+    ls += __shfl_xor(ls, 1, 64);
+    ls += __shfl_xor(ls, 2, 64);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        float a = acc[d] * f;
+        a += __shfl_xor(a, 1, 64);
+        a += __shfl_xor(a, 2, 64);
+        acc[d] = a;
+    }
+    // thread `sub` stores dims [16 sub, 16 sub + 16); the branches keep acc's indices constant
+    // (a register array indexed at run time would be moved to LDS)
+    half_t *o = out + (static_cast<int64_t>(lane_idx) * T + p) * heads * D + h * D + sub * 16;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+        if (sub != s4) continue;
+        half8_t o0, o1;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            o0[u] = static_cast<half_t>(acc[s4 * 16 + u] / ls);
+            o1[u] = static_cast<half_t>(acc[s4 * 16 + 8 + u] / ls);
+        }
+        *reinterpret_cast<half8_t *>(o) = o0;
+        *reinterpret_cast<half8_t *>(o + 8) = o1;
+    }
+}
+
 }  // namespace
 }  // namespace dtts
 
@@ -166,6 +326,63 @@ extern "C" int dtts_depthwise_layernorm_nlc_f16(const dtts_f16 *x, const float *
         dtts::depthwise_ln_kernel<2><<<grid, 256, 0, stream>>>(xh, taps, bias, ln_weight, ln_bias, yh, rows, L, C, K, eps);
     else
         dtts::depthwise_ln_kernel<4><<<grid, 256, 0, stream>>>(xh, taps, bias, ln_weight, ln_bias, yh, rows, L, C, K, eps);
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
+extern "C" int dtts_rms_norm_rows_f16(const dtts_f16 *x, const float *gamma, dtts_f16 *y, int64_t rows, int64_t dim,
+                                      float eps, hipStream_t stream) {
+    const char *name = "dtts_rms_norm_rows_f16";
+    DTTS_REQUIRE(rows >= 0 && dim > 0 && dim % 8 == 0 && dim < (1 << 24), "%s: bad shape (%lld, %lld): dim a multiple of 8",
+                 name, (long long)rows, (long long)dim);
+    if (rows == 0) return DTTS_OK;
+    DTTS_REQUIRE(x && gamma && y, "%s: null pointer", name);
+    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(y, 16), "%s: x and y must be 16-byte aligned", name);
+    DTTS_REQUIRE(rows < (int64_t(1) << 40), "%s: too many rows", name);
+    dtts::rms_rows_kernel<<<static_cast<unsigned>((rows + 3) / 4), 256, 0, stream>>>(
+        reinterpret_cast<const half_t *>(x), gamma, reinterpret_cast<half_t *>(y), rows, static_cast<int>(dim), eps);
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
+extern "C" int dtts_swiglu_rows_f16(const dtts_f16 *gate_up, dtts_f16 *y, int64_t rows, int64_t ffn, hipStream_t stream) {
+    const char *name = "dtts_swiglu_rows_f16";
+    DTTS_REQUIRE(rows >= 0 && ffn > 0 && ffn % 8 == 0 && ffn < (1 << 24), "%s: bad shape (%lld, %lld)", name,
+                 (long long)rows, (long long)ffn);
+    if (rows == 0) return DTTS_OK;
+    DTTS_REQUIRE(gate_up && y, "%s: null pointer", name);
+    DTTS_REQUIRE(dtts::aligned(gate_up, 16) && dtts::aligned(y, 16), "%s: misaligned operand", name);
+    dtts::swiglu_rows_kernel<<<dtts::grid_for(rows * (ffn / 8), 256), 256, 0, stream>>>(
+        reinterpret_cast<const half_t *>(gate_up), reinterpret_cast<half_t *>(y), rows, static_cast<int>(ffn));
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
+extern "C" int dtts_window_attention_prefill_f16(const dtts_f16 *qkv, const float *cos_t, const float *sin_t,
+                                                 int64_t table_len, dtts_f16 *out, int64_t lanes, int64_t len,
+                                                 int64_t heads, int64_t n_kv, int64_t head_dim, int64_t window,
+                                                 float scale, hipStream_t stream) {
+    const char *name = "dtts_window_attention_prefill_f16";
+    DTTS_REQUIRE(lanes >= 0 && len >= 0 && heads > 0 && n_kv > 0 && heads % n_kv == 0,
+                 "%s: bad shape (lanes %lld, len %lld, heads %lld, n_kv %lld)", name, (long long)lanes, (long long)len,
+                 (long long)heads, (long long)n_kv);
+    DTTS_REQUIRE(head_dim == 64, "%s: head_dim %lld (64 supported)", name, (long long)head_dim);
+    DTTS_REQUIRE(window >= 1 && window <= dtts::kWinMax, "%s: window %lld (1 to %d)", name, (long long)window,
+                 dtts::kWinMax);
+    if (lanes == 0 || len == 0) return DTTS_OK;
+    DTTS_REQUIRE(qkv && cos_t && sin_t && out, "%s: null pointer", name);
+    DTTS_REQUIRE(len <= table_len, "%s: %lld positions exceed the RoPE table (%lld)", name, (long long)len,
+                 (long long)table_len);
+    DTTS_REQUIRE(dtts::aligned(qkv, 16) && dtts::aligned(out, 16), "%s: misaligned operand", name);
+    DTTS_REQUIRE(lanes < 65536 && heads < 65536 && len < (int64_t(1) << 30) &&
+                     lanes * len * (heads + 2 * n_kv) * head_dim < (int64_t(1) << 40),
+                 "%s: shape too large", name);
+    const dim3 grid(static_cast<unsigned>((len + dtts::kQBlock - 1) / dtts::kQBlock), static_cast<unsigned>(heads),
+                    static_cast<unsigned>(lanes));
+    dtts::window_attn_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const half_t *>(qkv), cos_t, sin_t,
+                                                       reinterpret_cast<half_t *>(out), static_cast<int>(len),
+                                                       static_cast<int>(heads), static_cast<int>(n_kv),
+                                                       static_cast<int>(window), scale);
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

@@ -60,6 +60,13 @@ SIGNATURES = {
     "dtts_decode_attention_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
     "dtts_rvq_lookup_sum_f16": [_P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "dtts_depthwise_layernorm_nlc_f16": [_P, _P, _P, _P, _P, _F32, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_rms_norm_rows_f16": [_P, _P, _P, _I64, _I64, _F32, _P],
+    "dtts_swiglu_rows_f16": [_P, _P, _I64, _I64, _P],
+    "dtts_window_attention_prefill_f16": [_P, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P],
+    "dtts_codec_front_create": [_P, _P, _P],
+    "dtts_codec_front_destroy": [_P],
+    "dtts_codec_front_workspace_bytes": [_P, _I64, _I64],
+    "dtts_codec_front_decode": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
@@ -83,7 +90,8 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_codec_hop": ctypes.c_int64, "dtts_codec_workspace_bytes": ctypes.c_size_t,
              "dtts_decode_attention_workspace_bytes": ctypes.c_size_t,
              "dtts_gemm_f16_workspace_bytes": ctypes.c_size_t, "dtts_stack_destroy": None,
-             "dtts_stack_workspace_bytes": ctypes.c_size_t}
+             "dtts_stack_workspace_bytes": ctypes.c_size_t, "dtts_codec_front_destroy": None,
+             "dtts_codec_front_workspace_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

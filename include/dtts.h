@@ -365,6 +365,90 @@ int dtts_depthwise_layernorm_nlc_f16(const dtts_f16 *x, const float *taps, const
                                      const float *ln_weight, const float *ln_bias, float eps, dtts_f16 *y,
                                      int64_t lanes, int64_t len, int64_t channels, int64_t k, hipStream_t stream);
 
+/* RMSNorm over f16 rows with f32 arithmetic and one rounding out (rms_norm, crates/tts-nn/src/
+ * lib.rs:1000-1003, on the f32 activations the codec transformer runs in); gamma f32 [dim]. */
+int dtts_rms_norm_rows_f16(const dtts_f16 *x, const float *gamma, dtts_f16 *y, int64_t rows, int64_t dim,
+                           float eps, hipStream_t stream);
+
+/* y[r, j] = silu(gu[r, j]) * gu[r, ffn + j] (fused::swiglu_mul, crates/tts-nn/src/fused.rs:298-320,
+ * on a gate|up projection's [rows, 2 ffn] output), f16 in and out, f32 inside. ffn % 8 == 0. */
+int dtts_swiglu_rows_f16(const dtts_f16 *gate_up, dtts_f16 *y, int64_t rows, int64_t ffn, hipStream_t stream);
+
+/* Stack::forward's prefill attention (crates/qwen3tts/src/qwen3.rs:420-443) over whole
+ * sequences with a sliding window and no QK-norm (the codec transformer, codec.rs:337-349):
+ * q and k half-split-roped at their positions 0..len-1 (cos/sin [table_len, D/2], rope_table_f32),
+ * scores (q . k) * scale, key j visible to query i when i - window < j <= i (causal_window_mask,
+ * lib.rs:1210-1224), softmax, weighted v. qkv [lanes, len, (heads + 2 n_kv) D] f16 (q heads, k
+ * heads, v heads); out [lanes, len, heads D] f16. D = 64, 1 <= window <= 192, len <= table_len. */
+int dtts_window_attention_prefill_f16(const dtts_f16 *qkv, const float *cos_t, const float *sin_t, int64_t table_len,
+                                      dtts_f16 *out, int64_t lanes, int64_t len, int64_t heads, int64_t n_kv,
+                                      int64_t head_dim, int64_t window, float scale, hipStream_t stream);
+
+/* The codec's front half (Codec::forward up to the waveform stack, crates/qwen3tts/src/codec.rs:
+ * 401-424): codes -> RVQ lookups and output projections (Rvq::decode, codec.rs:296-313) -> causal
+ * pre_conv -> input projection -> the sliding-window transformer (Stack::forward's prefill over
+ * the chunk, with LayerScale) -> output projection -> per upsampling ratio, a transposed conv
+ * (kernel = stride) and a ConvNeXt block (codec.rs:160-196). Output: the latent the waveform
+ * stack (dtts_codec_decode) takes, [lanes, frames * prod(up_ratios), latent_dim] f16. Every
+ * activation is f16 in HBM with f32 arithmetic inside each kernel (the reference runs this half
+ * in f32); projections are channels-last convs with k = 1. */
+#define DTTS_FRONT_MAX_LAYERS 16
+#define DTTS_FRONT_MAX_UP 4
+
+typedef struct dtts_codec_front_geometry {
+    int64_t n_books, n_first, book_size, book_dim; /* 16, 1, 2048, 256 (cfg.rs codec: QUANTIZERS...) */
+    int64_t codebook_dim;                         /* 512: the width the two stacks are summed at */
+    int64_t latent_dim, pre_kernel;               /* 1024, 3 */
+    int64_t tf_dim, tf_layers, tf_heads, tf_n_kv, tf_head_dim, tf_ffn, tf_window; /* 512, 8, 16, 16, 64, 1024, 72 */
+    float tf_eps;                                 /* 1e-5 */
+    double tf_rope_base;                          /* 1e4 */
+    int64_t n_up, up_ratios[DTTS_FRONT_MAX_UP];   /* 2, {2, 2} */
+    int64_t dw_kernel;                            /* 7 */
+    float ln_eps;                                 /* 1e-6 */
+    int64_t max_frames;                           /* RoPE table length: frames per call at most */
+} dtts_codec_front_geometry;
+
+/* Device pointers, kept by dtts_codec_front_create. Projections are f16 [out, in]; norms and
+ * scales f32. */
+typedef struct dtts_codec_front_layer {
+    const float *attn_norm, *attn_scale, *ffn_norm, *mlp_scale; /* [tf_dim] */
+    const dtts_f16 *wqkv;     /* [(heads + 2 n_kv) D, tf_dim]: q, k, v rows */
+    const dtts_f16 *wo;       /* [tf_dim, heads D] */
+    const dtts_f16 *w_gateup; /* [2 ffn, tf_dim]: gate rows, then up rows */
+    const dtts_f16 *wdown;    /* [tf_dim, ffn] */
+} dtts_codec_front_layer;
+
+typedef struct dtts_codec_front_up {
+    const dtts_f16 *up_w, *up_b; /* the transposed conv: dtts_transpose_tap_major_weight's layout for
+                                    kernel = stride = r ([r C, C]), bias repeated r times */
+    const float *dw_taps, *dw_bias, *ln_weight, *ln_bias; /* [C, dw_kernel], [C] x 3 */
+    const dtts_f16 *pw1_w, *pw1_b, *pw2_w, *pw2_b;        /* [4C, C], [4C], [C, 4C], [C] */
+    const float *gamma;                                   /* [C] */
+} dtts_codec_front_up;
+
+typedef struct dtts_codec_front_weights {
+    const float *codebooks;        /* [n_books, book_size, book_dim] f32, embedding_sum / clamp(usage) */
+    const dtts_f16 *out_proj;      /* [codebook_dim, 2 book_dim]: semantic then acoustic output_proj */
+    const dtts_f16 *pre_w, *pre_b; /* [latent, pre_kernel codebook_dim] tap-major, [latent] */
+    const dtts_f16 *in_w, *in_b;   /* [tf_dim, latent], [tf_dim] */
+    dtts_codec_front_layer layers[DTTS_FRONT_MAX_LAYERS];
+    const float *tf_norm;          /* [tf_dim] */
+    const dtts_f16 *out_w, *out_b; /* [latent, tf_dim], [latent] */
+    dtts_codec_front_up up[DTTS_FRONT_MAX_UP];
+} dtts_codec_front_weights;
+
+typedef struct dtts_codec_front dtts_codec_front;
+
+int dtts_codec_front_create(const dtts_codec_front_geometry *geo, const dtts_codec_front_weights *weights,
+                            dtts_codec_front **out);
+void dtts_codec_front_destroy(dtts_codec_front *front);
+size_t dtts_codec_front_workspace_bytes(const dtts_codec_front *front, int64_t lanes, int64_t frames);
+
+/* codes [lanes, frames, n_books] int32 on the HOST (Codec::forward's frames; checked against
+ * book_size before anything is enqueued, then staged into the workspace) -> latent f16. */
+int dtts_codec_front_decode(const dtts_codec_front *front, const int32_t *codes, dtts_f16 *latent, int64_t lanes,
+                            int64_t frames, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------ a12-a14 f16 projections */
 
 /* Decode-shape f16 GEMM, f32 accumulation and output: C[m, n] = A[m, k] . B. Replaces

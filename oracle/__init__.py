@@ -419,6 +419,33 @@ def depthwise_layernorm_f16(x_bits, taps, bias, ln_w, ln_b, eps):
     return y
 
 
+def window_attention_prefill_f16(qkv_bits, cos_t, sin_t, heads, n_kv, head_dim, window, scale):
+    """qkv [lanes, T, (heads + 2 n_kv) D] f16 bits -> [lanes, T, heads D] f16 bits."""
+    qkv = _u16(qkv_bits)
+    lanes, length, _ = qkv.shape
+    out = np.empty((lanes, length, heads * head_dim), np.uint16)
+    lib().or_window_attention_prefill_f16(_ptr(qkv), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), _ptr(out), _I64(lanes),
+                                          _I64(length), _I64(heads), _I64(n_kv), _I64(head_dim), _I64(window),
+                                          ctypes.c_float(scale))
+    return out
+
+
+def rms_norm_rows_f16(x_bits, gamma, eps):
+    x = _u16(x_bits)
+    dim = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_rms_norm_rows_f16(_ptr(x), _ptr(_f32(gamma)), _ptr(y), _I64(x.size // dim), _I64(dim), ctypes.c_float(eps))
+    return y
+
+
+def swiglu_rows_f16(gu_bits):
+    gu = _u16(gu_bits)
+    ffn = gu.shape[-1] // 2
+    y = np.empty(gu.shape[:-1] + (ffn,), np.uint16)
+    lib().or_swiglu_rows_f16(_ptr(gu), _ptr(y), _I64(gu.size // (2 * ffn)), _I64(ffn))
+    return y
+
+
 # ---------------------------------------------------------------- decoder stack step
 
 def _proj_f16(x, w_out_in):

@@ -929,3 +929,80 @@ void or_depthwise_layernorm_f16(const uint16_t *x, const float *taps, const floa
         }
     free(h);
 }
+
+/* Stack::forward's prefill attention (crates/qwen3tts/src/qwen3.rs:420-443) over one sequence
+ * per lane with a sliding window, no QK-norm (the codec transformer's form, qwen3.rs:358-400):
+ * q and k half-split-roped in f32 at their positions (candle_nn::rotary_emb::rope as called at
+ * qwen3.rs:384-387), scores = (q . k) * scale (qwen3.rs:433-436), the mask of causal_window_mask
+ * (lib.rs:1210-1224), softmax_last_dim (max, exp(s - max), in-order sum, divide), then probs . v.
+ * qkv [lanes, T, (heads + 2 n_kv) D] f16 (q heads, k heads, v heads); out [lanes, T, heads D] f16. */
+void or_window_attention_prefill_f16(const uint16_t *qkv, const float *cos_t, const float *sin_t,
+                                     uint16_t *out, int64_t lanes, int64_t T, int64_t heads, int64_t n_kv,
+                                     int64_t D, int64_t window, float scale) {
+    const int64_t width = (heads + 2 * n_kv) * D, half = D / 2, gqa = heads / n_kv;
+    float *k = (float *)malloc(sizeof(float) * (size_t)(T * D));
+    float *q = (float *)malloc(sizeof(float) * (size_t)D);
+    float *xin = (float *)malloc(sizeof(float) * (size_t)D);
+    float *p = (float *)malloc(sizeof(float) * (size_t)T);
+    for (int64_t b = 0; b < lanes; ++b)
+        for (int64_t h = 0; h < heads; ++h) {
+            const int64_t kh = h / gqa;
+            for (int64_t j = 0; j < T; ++j) {
+                const uint16_t *kr = qkv + (b * T + j) * width + (heads + kh) * D;
+                for (int64_t d = 0; d < D; ++d) xin[d] = or_f16_to_f32(kr[d]);
+                rope_row(xin, cos_t + j * half, sin_t + j * half, k + j * D, half);
+            }
+            for (int64_t i = 0; i < T; ++i) {
+                const uint16_t *qr = qkv + (b * T + i) * width + h * D;
+                for (int64_t d = 0; d < D; ++d) xin[d] = or_f16_to_f32(qr[d]);
+                rope_row(xin, cos_t + i * half, sin_t + i * half, q, half);
+                const int64_t lo = i + 1 > window ? i + 1 - window : 0;
+                float mx = -INFINITY;
+                for (int64_t j = lo; j <= i; ++j) {
+                    float s = 0.0f;
+                    for (int64_t d = 0; d < D; ++d) s += q[d] * k[j * D + d];
+                    p[j] = s * scale;
+                    mx = p[j] > mx ? p[j] : mx;
+                }
+                float sum = 0.0f;
+                for (int64_t j = lo; j <= i; ++j) {
+                    p[j] = expf(p[j] - mx);
+                    sum += p[j];
+                }
+                for (int64_t j = lo; j <= i; ++j) p[j] = p[j] / sum;
+                for (int64_t d = 0; d < D; ++d) {
+                    float o = 0.0f;
+                    for (int64_t j = lo; j <= i; ++j)
+                        o += p[j] * or_f16_to_f32(qkv[(b * T + j) * width + (heads + n_kv + kh) * D + d]);
+                    out[(b * T + i) * heads * D + h * D + d] = or_f32_to_f16(o);
+                }
+            }
+        }
+    free(k);
+    free(q);
+    free(xin);
+    free(p);
+}
+
+/* rms_norm over f16 rows in f32 (lib.rs:1000-1003 on f32 activations), one rounding out. */
+void or_rms_norm_rows_f16(const uint16_t *x, const float *gamma, uint16_t *y, int64_t rows, int64_t dim,
+                          float eps) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float ss = 0.0f;
+        for (int64_t i = 0; i < dim; ++i) {
+            const float v = or_f16_to_f32(x[r * dim + i]);
+            ss += v * v;
+        }
+        const float m = sqrtf(ss / (float)dim + eps);
+        for (int64_t i = 0; i < dim; ++i) y[r * dim + i] = or_f32_to_f16((or_f16_to_f32(x[r * dim + i]) / m) * gamma[i]);
+    }
+}
+
+/* silu(gate) * up (fused::swiglu_mul, crates/tts-nn/src/fused.rs:298-320) over f16 [rows, 2 ffn]. */
+void or_swiglu_rows_f16(const uint16_t *gu, uint16_t *y, int64_t rows, int64_t ffn) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t j = 0; j < ffn; ++j) {
+            const float g = or_f16_to_f32(gu[r * 2 * ffn + j]), u = or_f16_to_f32(gu[r * 2 * ffn + ffn + j]);
+            y[r * ffn + j] = or_f32_to_f16((g / (1.0f + expf(-g))) * u);
+        }
+}

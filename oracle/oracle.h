@@ -145,4 +145,11 @@ void or_depthwise_layernorm_f16(const uint16_t *x, const float *taps, const floa
                                 const float *lnb, float eps, uint16_t *y, int64_t lanes, int64_t len,
                                 int64_t C, int64_t K);
 
+void or_window_attention_prefill_f16(const uint16_t *qkv, const float *cos_t, const float *sin_t,
+                                     uint16_t *out, int64_t lanes, int64_t T, int64_t heads, int64_t n_kv,
+                                     int64_t D, int64_t window, float scale);
+void or_rms_norm_rows_f16(const uint16_t *x, const float *gamma, uint16_t *y, int64_t rows, int64_t dim,
+                          float eps);
+void or_swiglu_rows_f16(const uint16_t *gu, uint16_t *y, int64_t rows, int64_t ffn);
+
 #endif

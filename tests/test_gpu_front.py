@@ -78,3 +78,87 @@ def test_front_ops_reject_bad_arguments(dev):
     codes = torch.zeros((3, 4), dtype=torch.int32, device=dev)
     with pytest.raises(DttsError, match="codes per row"):
         ops.rvq_lookup_sum(codes, torch.zeros((5, 8, 4), device=dev), 1)
+
+
+def _rows_close(got, want, ulp_frac=2.0 ** -10, abs_tol=1e-4):
+    g = synth.from_f16_bits(got).astype(np.float64)
+    w = synth.from_f16_bits(want).astype(np.float64)
+    bad = np.abs(g - w) > np.abs(w) * ulp_frac + abs_tol
+    assert not bad.any(), f"{int(bad.sum())} elements off, worst {np.max(np.abs(g - w)):.3e}"
+
+
+def test_rms_rows_and_swiglu_rows(dev):
+    x = synth.f16_bits(synth.normal(34, "x", (97, 512)))
+    g = synth.uniform(34, "g", (512,), 0.9, 1.1)
+    got = to_host(ops_rms_rows(to_dev(x, dev), to_dev(g, dev), 1e-5))
+    _rows_close(got, oracle.rms_norm_rows_f16(x, g, 1e-5), abs_tol=1e-5)
+    gu = synth.f16_bits(synth.normal(34, "gu", (53, 2 * 1024)))
+    y = torch.empty((53, 1024), dtype=torch.float16, device=dev)
+    from dtts._lib import call, ptr, stream_handle
+    gud = to_dev(gu, dev)  # held: a temporary's memory could be reused before the kernel runs
+    call("dtts_swiglu_rows_f16", ptr(gud), ptr(y), 53, 1024, stream_handle())
+    _rows_close(to_host(y), oracle.swiglu_rows_f16(gu), abs_tol=1e-6)
+
+
+def ops_rms_rows(x, g, eps):
+    from dtts._lib import call, ptr, stream_handle
+    y = torch.empty_like(x)
+    call("dtts_rms_norm_rows_f16", ptr(x), ptr(g), ptr(y), x.shape[0], x.shape[1], float(eps), stream_handle())
+    return y
+
+
+@pytest.mark.parametrize("lanes,length,heads,n_kv,window", [(2, 325, 16, 16, 72), (3, 70, 4, 2, 5), (1, 200, 8, 8, 192),
+                                                            (2, 1, 16, 16, 72)])
+def test_window_attention_matches_oracle(dev, lanes, length, heads, n_kv, window):
+    from dtts._lib import call, ptr, stream_handle
+    hd = 64
+    qkv = synth.f16_bits(synth.normal(35, "qkv", (lanes, length, (heads + 2 * n_kv) * hd)))
+    cos_t, sin_t = oracle.rope_table_f32(max(length, 8), hd, 1e4)
+    scale = float(np.float32(1 / 8))
+    out = torch.empty((lanes, length, heads * hd), dtype=torch.float16, device=dev)
+    qd, cd, sd = to_dev(qkv, dev), to_dev(cos_t, dev), to_dev(sin_t, dev)  # held until the kernel has run
+    call("dtts_window_attention_prefill_f16", ptr(qd), ptr(cd), ptr(sd), cos_t.shape[0], ptr(out), lanes, length,
+         heads, n_kv, hd, window, scale, stream_handle())
+    torch.cuda.synchronize()
+    want = oracle.window_attention_prefill_f16(qkv, cos_t, sin_t, heads, n_kv, hd, window, scale)
+    _rows_close(to_host(out), want, abs_tol=2e-4)
+
+
+def test_front_decode_tiny_matches_oracle(dev):
+    from dtts import codec_front
+    from oracle import codec_front as ofront
+    from _front_ref import TINY
+    hw = codec_front.random_weights(TINY, 36)
+    codes = synth.randint(36, "codes", (3, 17, TINY.n_books), 0, TINY.book_size - 1)
+    front = codec_front.CodecFront(TINY, hw, dev)
+    got = to_host(front.decode(codes))
+    want = ofront.decode_f16(TINY, hw, codes)
+    g, w = synth.from_f16_bits(got), synth.from_f16_bits(want)
+    from _util import rel
+    assert rel(g, w)[1] < 2e-3, rel(g, w)
+
+
+def test_front_decode_codec_geometry(dev):
+    """The Qwen3-TTS codec's own widths (16 books, latent 1024, 8 layers at 512, window 72, ratios
+    2 and 2), 2 lanes x 90 frames (the window bites) against the oracle chain."""
+    from dtts import codec_front
+    from oracle import codec_front as ofront
+    geo = codec_front.CODEC
+    hw = codec_front.random_weights(geo, 37)
+    codes = synth.randint(37, "codes", (2, 90, geo.n_books), 0, geo.book_size - 1)
+    front = codec_front.CodecFront(geo, hw, dev)
+    got = to_host(front.decode(codes))
+    want = ofront.decode_f16(geo, hw, codes)
+    from _util import rel
+    assert got.shape == (2, 360, 1024)
+    assert rel(synth.from_f16_bits(got), synth.from_f16_bits(want))[1] < 5e-3
+
+
+def test_front_decode_rejects_bad_codes(dev):
+    from dtts import codec_front
+    from _front_ref import TINY
+    front = codec_front.CodecFront(TINY, codec_front.random_weights(TINY, 38), dev)
+    codes = np.zeros((1, 4, TINY.n_books), np.int32)
+    codes[0, 2, 1] = TINY.book_size
+    with pytest.raises(DttsError, match="outside"):
+        front.decode(codes)
