@@ -320,6 +320,55 @@ def workload_stack(dev, args):
                   "frac_hbm_peak": round(best["gbs"] / PEAK_HBM_GBS, 4)})
 
 
+def workload_front(dev, args):
+    """Row f-3: the codec's front half (split RVQ, pre_conv, 8-layer windowed transformer, two
+    TransConv + ConvNeXt stages) over 48 lanes x 325 code frames (one Codec::decode window each),
+    and Codec::decode of one 3000-frame document (10 windows as lanes) through the front half and
+    the waveform stack to f32 audio."""
+    import numpy as np
+    import torch
+
+    from dtts import codec, codec_front, synth
+
+    geo = codec_front.CODEC
+    hw = codec_front.random_weights(geo, 0)
+    front = codec_front.CodecFront(geo, hw, dev)
+    lanes, frames = 48, codec_front.CHUNK_FRAMES + codec_front.CHUNK_LEFT_CONTEXT
+    codes = synth.randint(0, "front.codes", (lanes, frames, geo.n_books), 0, geo.book_size - 1).astype(np.int32)
+    latent = torch.empty((lanes, frames * geo.upsample, geo.latent_dim), dtype=torch.float16, device=dev)
+    front.workspace(lanes, frames)
+    t_front = _time(lambda: front.decode(codes, out=latent), reps=10)
+    if not torch.isfinite(latent.float()).all():
+        raise SystemExit("bench: non-finite latent")
+    wave = codec.Codec(codec.CONFIG5, codec.random_weights(codec.CONFIG5, seed=0), dev)
+    spf = geo.upsample * codec.CONFIG5.hop
+    n_doc = 3000
+    doc = synth.randint(0, "front.doc", (n_doc, geo.n_books), 0, geo.book_size - 1).astype(np.int32)
+    audio = torch.empty(n_doc * spf, dtype=torch.float32, device=dev)
+    t_doc = _time(lambda: codec_front.decode_document(front, wave, doc, out=audio), reps=3, warm=1)
+    if not torch.isfinite(audio).all():
+        raise SystemExit("bench: non-finite document audio")
+    fl = geo.flops_per_frame() * lanes * frames
+    windows = -(-n_doc // codec_front.CHUNK_FRAMES)
+    doc_fl = windows * frames * (geo.flops_per_frame() + geo.upsample * codec.CONFIG5.flops_per_frame())
+    res = {"front": {"lanes": lanes, "frames": frames, "ms": round(t_front, 4),
+                     "code_frames_per_s": round(lanes * frames / (t_front / 1e3), 1),
+                     "tflops": round(fl / (t_front / 1e3) / 1e12, 2)},
+           "document": {"frames": n_doc, "windows": windows, "ms": round(t_doc, 3),
+                        "audio_s": n_doc * spf / SAMPLE_RATE,
+                        "audio_s_per_s": round(n_doc * spf / SAMPLE_RATE / (t_doc / 1e3), 1),
+                        "tflops": round(doc_fl / (t_doc / 1e3) / 1e12, 2),
+                        "note": "timed from host codes to device audio; includes the host-side "
+                                "window assembly and the codes' upload"}}
+    del front, wave
+    torch.cuda.empty_cache()
+    return _line("row f-3: codec front half, 48 lanes x 325 code frames (codes -> latent), and Codec::decode "
+                 "of a 3000-frame document (chunk 300, left context 25; codes -> f32 audio)",
+                 "front-half code frames/s at 48 lanes", res["front"]["code_frames_per_s"], "frames/s", res,
+                 {"dtype": "f16 storage / f32 accumulation",
+                  "frac_mfma_peak": round(res["front"]["tflops"] / PEAK_TFLOPS_F16, 4)})
+
+
 # ---------------------------------------------------------------- rocprofv3 counter digest
 
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: a mul kernel reading and writing 1 GiB
@@ -369,7 +418,7 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
 
 
 WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
-             "stack": workload_stack}
+             "stack": workload_stack, "front": workload_front}
 
 
 def main():
@@ -386,9 +435,9 @@ def main():
                     help="digest rocprofv3 FETCH_SIZE / WRITE_SIZE runs into per-kernel traffic (no GPU)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "codec_config5_pmc.json"),
                     help="per-kernel traffic from --pmc-summary, reported in roofline.traffic")
-    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "cfg5", "all"],
+    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5", "all"],
                     help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops; stack "
-                         "times the decoder-stack decode step")
+                         "times the decoder-stack decode step; front the codec front half and document decode")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -409,7 +458,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.workload != "cfg5":
-        for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack"] if args.workload == "all" else [args.workload]):
+        for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front"] if args.workload == "all" else [args.workload]):
             print(json.dumps(WORKLOADS[w](dev, args)), flush=True)
         if args.workload != "all":
             return

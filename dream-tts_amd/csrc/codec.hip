@@ -310,7 +310,7 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
         }
     }
     dtts_conv_desc d = desc(lanes, len, g.channels[g.n_blocks], 1, g.out_kernel, 1, x, w.out_w, w.out_b, audio);
-    d.act = 1;
+    d.act = g.out_clamp ? 3 : 1;
     push(d, "out%.0lld%.0lld", 0, 0);
     return DTTS_OK;
 }

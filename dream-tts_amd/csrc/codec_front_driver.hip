@@ -9,6 +9,7 @@
 // norms, SwiGLU, windowed attention and depthwise+LayerNorm have kernels of their own
 // (codec_front.hip). Activations are f16 in HBM, f32 inside every kernel.
 #include <cmath>
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -18,6 +19,12 @@ struct dtts_codec_front {
     dtts_codec_front_geometry geo;
     dtts_codec_front_weights w;
     float *cos_t = nullptr, *sin_t = nullptr;  // [max_frames, tf_head_dim / 2]
+    // Pinned staging for the host's codes: the host fills it, an async copy on the caller's stream
+    // reads it, and `staged` marks that copy's end, so the next call waits for it before refilling
+    // (calls on one front half from several host threads at once race on it).
+    mutable int32_t *pinned = nullptr;
+    mutable size_t pinned_n = 0;
+    mutable hipEvent_t staged = nullptr;
 };
 
 namespace dtts {
@@ -135,6 +142,7 @@ extern "C" int dtts_codec_front_create(const dtts_codec_front_geometry *geo, con
         if (e == hipSuccess) e = hipMalloc(&f->sin_t, sizeof(float) * c.size());
         if (e == hipSuccess) e = hipMemcpy(f->cos_t, c.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(f->sin_t, s.data(), sizeof(float) * c.size(), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&f->staged, hipEventDisableTiming);
     }
     if (rc != DTTS_OK || e != hipSuccess) {
         dtts_codec_front_destroy(f);
@@ -149,6 +157,11 @@ extern "C" void dtts_codec_front_destroy(dtts_codec_front *f) {
     if (!f) return;
     if (f->cos_t) (void)hipFree(f->cos_t);
     if (f->sin_t) (void)hipFree(f->sin_t);
+    if (f->staged) {
+        (void)hipEventSynchronize(f->staged);
+        (void)hipEventDestroy(f->staged);
+    }
+    if (f->pinned) (void)hipHostFree(f->pinned);
     delete f;
 }
 
@@ -157,24 +170,37 @@ extern "C" size_t dtts_codec_front_workspace_bytes(const dtts_codec_front *f, in
     return dtts::front_plan(f->geo, lanes, frames).total;
 }
 
-extern "C" int dtts_codec_front_decode(const dtts_codec_front *f, const int32_t *codes, dtts_f16 *latent,
-                                       int64_t lanes, int64_t frames, void *workspace, size_t ws_bytes,
-                                       hipStream_t stream) {
-    using dtts::pointwise;
-    const char *name = "dtts_codec_front_decode";
-    DTTS_REQUIRE(f, "%s: null front half", name);
-    DTTS_REQUIRE(lanes >= 0 && frames >= 0, "%s: bad shape", name);
-    if (lanes == 0 || frames == 0) return DTTS_OK;
+namespace dtts {
+namespace {
+
+// The pinned staging buffer, holding at least n codes, once the previous call's copy out of it
+// has ended; nullptr (error set) on failure.
+int32_t *stage_codes(const dtts_codec_front *f, size_t n, const char *name) {
+    hipError_t e = hipEventSynchronize(f->staged);
+    if (e == hipSuccess && f->pinned_n < n) {
+        if (f->pinned) e = hipHostFree(f->pinned);
+        f->pinned = nullptr;
+        f->pinned_n = 0;
+        if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&f->pinned), sizeof(int32_t) * n, 0);
+        if (e == hipSuccess) f->pinned_n = n;
+    }
+    if (e != hipSuccess) {
+        set_error("%s: staging codes: %s", name, hipGetErrorString(e));
+        return nullptr;
+    }
+    return f->pinned;
+}
+
+// The front half over codes already in the pinned staging buffer ([lanes, frames, n_books]).
+int front_decode_staged(const dtts_codec_front *f, dtts_f16 *latent, int64_t lanes, int64_t frames,
+                        void *workspace, size_t ws_bytes, hipStream_t stream, const char *name) {
     const dtts_codec_front_geometry &g = f->geo;
     const dtts_codec_front_weights &W = f->w;
-    DTTS_REQUIRE(codes && latent && workspace, "%s: null pointer", name);
-    DTTS_REQUIRE(frames <= g.max_frames, "%s: %lld frames exceed max_frames %lld", name, (long long)frames,
-                 (long long)g.max_frames);
-    DTTS_REQUIRE(lanes * frames < (int64_t(1) << 30), "%s: too many frames", name);
-    const dtts::FrontPlan pl = dtts::front_plan(g, lanes, frames);
+    const FrontPlan pl = front_plan(g, lanes, frames);
     DTTS_REQUIRE(ws_bytes >= pl.total, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, pl.total);
-    DTTS_REQUIRE(dtts::aligned(workspace, 256) && dtts::aligned(latent, 16), "%s: misaligned workspace or latent", name);
+    DTTS_REQUIRE(aligned(workspace, 256) && aligned(latent, 16), "%s: misaligned workspace or latent", name);
     const int64_t rows = lanes * frames;
+    const int32_t *codes = f->pinned;
     // Rvq::decode's index_select refuses codes outside the book (codec.rs:303-305)
     for (int64_t i = 0; i < rows * g.n_books; ++i)
         DTTS_REQUIRE(codes[i] >= 0 && codes[i] < g.book_size, "%s: code %d at %lld outside [0, %lld)", name, codes[i],
@@ -183,6 +209,7 @@ extern "C" int dtts_codec_front_decode(const dtts_codec_front *f, const int32_t 
     auto at = [&](size_t off) { return static_cast<void *>(ws + off); };
     DTTS_HIP_CHECK(hipMemcpyAsync(at(pl.codes), codes, sizeof(int32_t) * rows * g.n_books, hipMemcpyHostToDevice, stream),
                    name);
+    DTTS_HIP_CHECK(hipEventRecord(f->staged, stream), name);
     // split RVQ: both stacks' lookups side by side, then one projection over the joined width
     FRONT_STEP(dtts_rvq_lookup_sum_f16(static_cast<const int32_t *>(at(pl.codes)), W.codebooks, g.n_books, g.n_first,
                                        g.book_size, g.book_dim, static_cast<dtts_f16 *>(at(pl.s)), rows, stream));
@@ -247,5 +274,124 @@ extern "C" int dtts_codec_front_decode(const dtts_codec_front *f, const int32_t 
         FRONT_STEP(dtts::conv1d_nlc_f16(&d, stream));
         x = y;
     }
+    return DTTS_OK;
+}
+
+}  // namespace
+}  // namespace dtts
+
+extern "C" int dtts_codec_front_decode(const dtts_codec_front *f, const int32_t *codes, dtts_f16 *latent,
+                                       int64_t lanes, int64_t frames, void *workspace, size_t ws_bytes,
+                                       hipStream_t stream) {
+    const char *name = "dtts_codec_front_decode";
+    DTTS_REQUIRE(f, "%s: null front half", name);
+    DTTS_REQUIRE(lanes >= 0 && frames >= 0, "%s: bad shape", name);
+    if (lanes == 0 || frames == 0) return DTTS_OK;
+    DTTS_REQUIRE(codes && latent && workspace, "%s: null pointer", name);
+    DTTS_REQUIRE(frames <= f->geo.max_frames, "%s: %lld frames exceed max_frames %lld", name, (long long)frames,
+                 (long long)f->geo.max_frames);
+    DTTS_REQUIRE(lanes * frames < (int64_t(1) << 30), "%s: too many frames", name);
+    const size_t n = static_cast<size_t>(lanes * frames * f->geo.n_books);
+    int32_t *pin = dtts::stage_codes(f, n, name);
+    if (!pin) return DTTS_ERR_HIP;
+    std::memcpy(pin, codes, sizeof(int32_t) * n);
+    return dtts::front_decode_staged(f, latent, lanes, frames, workspace, ws_bytes, stream, name);
+}
+
+// ------------------------------------------------------------------ Codec::decode, chunked
+
+namespace dtts {
+namespace {
+
+struct DocPlan {
+    int64_t lanes, frames, spf;  // windows run as lanes, each `frames` long; samples per frame
+    size_t front, latent, codec, audio, total;
+};
+
+bool doc_plan(const dtts_codec_front *f, const dtts_codec *c, int64_t n, int64_t chunk, int64_t context, DocPlan &p) {
+    if (!f || !c || n <= 0 || chunk <= 0 || context < 0) return false;
+    // Every window is one lane of one length: the span when n >= span (the reference pads to it);
+    // otherwise n, the first window's length, with the later, shorter windows padded on the right
+    // by their last frame too -- the decoder is causal, so frames after the kept ones change nothing.
+    const int64_t span = chunk + context;
+    p.lanes = (n + chunk - 1) / chunk;
+    p.frames = n >= span ? span : n;
+    int64_t up = 1;
+    for (int64_t i = 0; i < f->geo.n_up; ++i) up *= f->geo.up_ratios[i];
+    p.spf = up * dtts_codec_hop(c);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += round256(bytes);
+        return at;
+    };
+    p.front = take(dtts_codec_front_workspace_bytes(f, p.lanes, p.frames));
+    p.latent = take(2 * static_cast<size_t>(p.lanes * p.frames * up * f->geo.latent_dim));
+    p.codec = take(dtts_codec_workspace_bytes(c, p.lanes, p.frames * up));
+    p.audio = take(2 * static_cast<size_t>(p.lanes * p.frames * p.spf));
+    p.total = off;
+    return true;
+}
+
+// out[o] = window w's sample at o - w's chunk start + its context's length, w = (o / spf) / chunk
+__global__ __launch_bounds__(256) void doc_gather_kernel(const half_t *audio, float *out, int64_t total, int64_t spf,
+                                                         int64_t chunk, int64_t context, int64_t win_len) {
+    for (int64_t o = blockIdx.x * int64_t(256) + threadIdx.x; o < total; o += int64_t(gridDim.x) * 256) {
+        const int64_t w = (o / spf) / chunk;
+        const int64_t start = w * chunk;
+        const int64_t from = start > context ? start - context : 0;
+        out[o] = static_cast<float>(audio[w * win_len + (start - from) * spf + (o - start * spf)]);
+    }
+}
+
+}  // namespace
+}  // namespace dtts
+
+extern "C" size_t dtts_codec_document_workspace_bytes(const dtts_codec_front *f, const dtts_codec *c, int64_t n,
+                                                      int64_t chunk, int64_t context) {
+    dtts::DocPlan p{};
+    return dtts::doc_plan(f, c, n, chunk, context, p) ? p.total : 0;
+}
+
+extern "C" int dtts_codec_decode_document(const dtts_codec_front *f, const dtts_codec *c, const int32_t *codes,
+                                          int64_t n, int64_t chunk, int64_t context, float *audio, void *workspace,
+                                          size_t ws_bytes, hipStream_t stream) {
+    const char *name = "dtts_codec_decode_document";
+    DTTS_REQUIRE(f && c, "%s: null front half or codec", name);
+    DTTS_REQUIRE(n >= 0 && chunk > 0 && context >= 0, "%s: bad sizes (n %lld, chunk %lld, context %lld)", name,
+                 (long long)n, (long long)chunk, (long long)context);
+    if (n == 0) return DTTS_OK;
+    DTTS_REQUIRE(codes && audio && workspace, "%s: null pointer", name);
+    dtts::DocPlan p{};
+    DTTS_REQUIRE(dtts::doc_plan(f, c, n, chunk, context, p), "%s: bad plan", name);
+    DTTS_REQUIRE(ws_bytes >= p.total, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, p.total);
+    DTTS_REQUIRE(dtts::aligned(workspace, 256), "%s: misaligned workspace", name);
+    const int64_t nb = f->geo.n_books;
+    DTTS_REQUIRE(p.frames <= f->geo.max_frames, "%s: %lld-frame windows exceed max_frames %lld", name,
+                 (long long)p.frames, (long long)f->geo.max_frames);
+    DTTS_REQUIRE(p.lanes * p.frames < (int64_t(1) << 30), "%s: too many frames", name);
+    // the windows' codes, each right-padded with its last frame (codec.rs:585-593)
+    int32_t *win = dtts::stage_codes(f, static_cast<size_t>(p.lanes * p.frames * nb), name);
+    if (!win) return DTTS_ERR_HIP;
+    for (int64_t w = 0; w < p.lanes; ++w) {
+        const int64_t start = w * chunk;
+        const int64_t from = start > context ? start - context : 0;
+        const int64_t to = from + p.frames < n ? from + p.frames : n;
+        for (int64_t t = 0; t < p.frames; ++t) {
+            const int64_t src = from + t < to ? from + t : to - 1;
+            for (int64_t b = 0; b < nb; ++b) win[(w * p.frames + t) * nb + b] = codes[src * nb + b];
+        }
+    }
+    char *ws = static_cast<char *>(workspace);
+    dtts_f16 *latent = reinterpret_cast<dtts_f16 *>(ws + p.latent);
+    dtts_f16 *wav = reinterpret_cast<dtts_f16 *>(ws + p.audio);
+    FRONT_STEP(dtts::front_decode_staged(f, latent, p.lanes, p.frames, ws + p.front, p.latent - p.front, stream, name));
+    int64_t up = 1;
+    for (int64_t i = 0; i < f->geo.n_up; ++i) up *= f->geo.up_ratios[i];
+    FRONT_STEP(dtts_codec_decode(c, latent, wav, p.lanes, p.frames * up, ws + p.codec, p.audio - p.codec, stream));
+    const int64_t total = n * p.spf;
+    dtts::doc_gather_kernel<<<dtts::grid_for(total, 256), 256, 0, stream>>>(
+        reinterpret_cast<const dtts::half_t *>(wav), audio, total, p.spf, chunk, context, p.frames * p.spf);
+    DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

@@ -149,7 +149,7 @@ struct Choice {
 
 Choice choose(const dtts_conv_desc *d) {
     Choice c{"direct", 0, 0, d->in_alpha != nullptr, direct_offsets_fit(d->len, d->cin, d->cout, d->k)};
-    if (conv_narrow_eligible(d) && d->act <= 1 && !d->out_scale) {
+    if (conv_narrow_eligible(d) && d->act != 2 && !d->out_scale) {
         c.path = "narrow";
         return c;
     }
@@ -205,7 +205,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     DTTS_REQUIRE(d->pad_left <= (d->k - 1) * d->dilation,
                  "%s: pad_left %lld exceeds the receptive field (k-1)*dil = %lld", name,
                  (long long)d->pad_left, (long long)((d->k - 1) * d->dilation));
-    DTTS_REQUIRE(d->act >= 0 && d->act <= 2, "%s: act %d unknown", name, d->act);
+    DTTS_REQUIRE(d->act >= 0 && d->act <= 3, "%s: act %d unknown", name, d->act);
     if (d->lanes == 0 || d->len == 0) return DTTS_OK;
     DTTS_REQUIRE(d->x && d->w && d->y, "%s: null x, w or y", name);
     DTTS_REQUIRE((d->in_alpha == nullptr) == (d->in_brecip == nullptr), "%s: in_alpha and in_brecip go together", name);

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
     if (p.bias) v += static_cast<float>(p.bias[0]);
     if (p.res) v += static_cast<float>(p.res[off]);
     if (p.act == 1) v = tanhf(v);
+    if (p.act == 3) v = fminf(fmaxf(v, -1.0f), 1.0f);
     half_t h = static_cast<half_t>(v);
     if (p.y_pre) p.y_pre[off] = h;
     if (p.a_out) h = static_cast<half_t>(snake_f16out(static_cast<float>(h), p.a_out[0], p.r_out[0]));

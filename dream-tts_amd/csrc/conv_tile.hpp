@@ -102,10 +102,11 @@ inline bool direct_offsets_fit(int64_t len, int64_t cin, int64_t cout, int64_t k
     return len * cin * 2 < (int64_t(1) << 31) && cout * k * cin * 2 < (int64_t(1) << 31);
 }
 
-// act 1: tanh; act 2: GELU, erf form (0.5 v (1 + erf(v / sqrt 2))).
+// act 1: tanh; act 2: GELU, erf form (0.5 v (1 + erf(v / sqrt 2))); act 3: clamp to [-1, 1].
 __device__ __forceinline__ float conv_act(float v, int act) {
     if (act == 1) return tanhf(v);
     if (act == 2) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == 3) return fminf(fmaxf(v, -1.0f), 1.0f);
     return v;
 }
 

@@ -67,6 +67,8 @@ SIGNATURES = {
     "dtts_codec_front_destroy": [_P],
     "dtts_codec_front_workspace_bytes": [_P, _I64, _I64],
     "dtts_codec_front_decode": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
+    "dtts_codec_document_workspace_bytes": [_P, _P, _I64, _I64, _I64],
+    "dtts_codec_decode_document": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _SZ, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
@@ -91,7 +93,8 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_decode_attention_workspace_bytes": ctypes.c_size_t,
              "dtts_gemm_f16_workspace_bytes": ctypes.c_size_t, "dtts_stack_destroy": None,
              "dtts_stack_workspace_bytes": ctypes.c_size_t, "dtts_codec_front_destroy": None,
-             "dtts_codec_front_workspace_bytes": ctypes.c_size_t}
+             "dtts_codec_front_workspace_bytes": ctypes.c_size_t,
+             "dtts_codec_document_workspace_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

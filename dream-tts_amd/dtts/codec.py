@@ -28,6 +28,7 @@ class Geometry:
     ru_kernel: int = 7
     ru_dilations: tuple = (1, 3, 9)
     out_kernel: int = 7
+    out_clamp: bool = False  # True: Codec::forward's clamp to [-1, 1]; False: tanh (config 5's form)
 
     @property
     def n_blocks(self):
@@ -106,7 +107,8 @@ class _Geometry(ctypes.Structure):
     _fields_ = [("latent_dim", ctypes.c_int64), ("head_kernel", ctypes.c_int64),
                 ("n_blocks", ctypes.c_int64), ("channels", ctypes.c_int64 * (MAX_BLOCKS + 1)),
                 ("rates", ctypes.c_int64 * MAX_BLOCKS), ("ru_kernel", ctypes.c_int64),
-                ("ru_dilations", ctypes.c_int64 * 3), ("out_kernel", ctypes.c_int64)]
+                ("ru_dilations", ctypes.c_int64 * 3), ("out_kernel", ctypes.c_int64),
+                ("out_clamp", ctypes.c_int64)]
 
 
 class _Unit(ctypes.Structure):
@@ -165,6 +167,7 @@ class Codec:
         for i, r in enumerate(geo.rates):
             g.rates[i] = r
         g.ru_kernel, g.out_kernel = geo.ru_kernel, geo.out_kernel
+        g.out_clamp = int(geo.out_clamp)
         for j, d in enumerate(geo.ru_dilations):
             g.ru_dilations[j] = d
         ws = _Weights()

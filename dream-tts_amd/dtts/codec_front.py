@@ -261,3 +261,24 @@ class CodecFront:
              ctypes.c_void_p(y.data_ptr()), lanes, frames, ctypes.c_void_p(ws.data_ptr()), ws.numel(),
              stream_handle(self.dev))
         return y
+
+
+CHUNK_FRAMES = 300  # crates/qwen3tts/src/cfg.rs:281
+CHUNK_LEFT_CONTEXT = 25  # cfg.rs:282
+
+
+def decode_document(front: CodecFront, wave, codes, chunk=CHUNK_FRAMES, context=CHUNK_LEFT_CONTEXT, out=None):
+    """Codec::decode (crates/qwen3tts/src/codec.rs:562-604) through dtts_codec_decode_document:
+    codes host int32 [n, n_books] -> audio [n * upsample * hop] f32 on the device. `wave` is a
+    dtts.codec.Codec (the waveform stack); its workspace is not used."""
+    codes = np.ascontiguousarray(codes, np.int32)
+    n, nb = codes.shape
+    assert nb == front.geo.n_books
+    spf = front.geo.upsample * wave.geo.hop
+    y = out if out is not None else torch.empty(n * spf, dtype=torch.float32, device=front.dev)
+    need = int(lib().dtts_codec_document_workspace_bytes(front.handle, wave.handle, n, chunk, context))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=front.dev)
+    call("dtts_codec_decode_document", front.handle, wave.handle, codes.ctypes.data_as(ctypes.c_void_p), n, chunk,
+         context, ctypes.c_void_p(y.data_ptr()), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+         stream_handle(front.dev))
+    return y

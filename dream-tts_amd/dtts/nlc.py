@@ -69,7 +69,7 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
                  _p(snake_in[0]) if snake_in else None, _p(snake_in[1]) if snake_in else None,
                  _p(residual), _p(y_pre),
                  _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
-                 _p(y), {None: 0, "tanh": 1, "gelu": 2}[act], _p(scale))
+                 _p(y), {None: 0, "tanh": 1, "gelu": 2, "clamp": 3}[act], _p(scale))
     call("dtts_conv1d_nlc_f16_ex", ctypes.byref(d), stream_handle())
     return (y_pre, y) if want_pre else y
 

@@ -84,7 +84,8 @@ int dtts_snake_nlc_f16(const dtts_f16 *x, const float *alpha, const float *breci
  * what the matrix cores consume. dtts_tap_weight_to_tap_major converts. x, w_tm, y, bias,
  * residual and y_pre must be 16-byte aligned for the matrix-core kernel; other shapes or
  * alignments take a direct (slow, exact-semantics) kernel. act: 0 none, 1 tanh, 2 GELU
- * (erf form, gelu_exact, crates/tts-nn/src/lib.rs:1129-1131). With out_scale the sum is
+ * (erf form, gelu_exact, crates/tts-nn/src/lib.rs:1129-1131), 3 clamp to [-1, 1] (Codec::forward's
+ * clamp, crates/qwen3tts/src/codec.rs:433-436). With out_scale the sum is
  *   s[l, n] = residual[l, n] + out_scale[n] * (bias[n] + sum ...), the scaled term rounded in
  * f32 before the add. */
 typedef struct dtts_conv_desc {
@@ -525,6 +526,8 @@ typedef struct dtts_codec_geometry {
     int64_t channels[DTTS_CODEC_MAX_BLOCKS + 1];
     int64_t rates[DTTS_CODEC_MAX_BLOCKS];
     int64_t ru_kernel, ru_dilations[3], out_kernel;
+    int64_t out_clamp; /* 0: tanh after the output conv (the benchmark's form); 1: clamp to [-1, 1]
+                          (Codec::forward, crates/qwen3tts/src/codec.rs:433-436) */
 } dtts_codec_geometry;
 
 /* Device pointers. Conv weights are f16 in the layouts dtts_tap_major_weight /
@@ -591,6 +594,21 @@ int dtts_codec_profile(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16
                        int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
                        hipStream_t stream, dtts_codec_stage *stages, int max_stages,
                        int *n_stages);
+
+/* Codec::decode (crates/qwen3tts/src/codec.rs:562-604) for one document of n code frames: windows
+ * of chunk + context frames starting every `chunk` frames (the first without context), each padded
+ * on the right to the full span by repeating its last frame when n >= span; every window through
+ * the front half and the waveform stack, then the audio of each window's own chunk, without its
+ * context, concatenated. The windows are independent forwards, so all of them run at once as
+ * lanes of one length (for n < span: n, the later windows padded like the rest, which leaves the
+ * kept audio of a causal decoder unchanged). codes [n, n_books] int32 on the HOST;
+ * audio [n * samples_per_frame] f32 on the device, samples_per_frame = prod(up_ratios) *
+ * dtts_codec_hop(codec). */
+size_t dtts_codec_document_workspace_bytes(const dtts_codec_front *front, const dtts_codec *codec, int64_t n,
+                                           int64_t chunk, int64_t context);
+int dtts_codec_decode_document(const dtts_codec_front *front, const dtts_codec *codec, const int32_t *codes,
+                               int64_t n, int64_t chunk, int64_t context, float *audio, void *workspace,
+                               size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -199,7 +199,7 @@ def conv1d_nlc_f16(x_bits, w_tap_bits, bias_bits, dil, pad_left=None, snake=None
         pad_left = (k - 1) * dil
     a, r = (None, None) if snake is None else (_f32(snake[0]), _f32(snake[1]))
     b, rs, sc = _u16(bias_bits), _u16(res_bits), _f32(scale)
-    code = {None: 0, "tanh": 1, "gelu": 2}["tanh" if act_tanh else act]
+    code = {None: 0, "tanh": 1, "gelu": 2, "clamp": 3}["tanh" if act_tanh else act]
     y = np.empty((lanes, length, cout), np.uint16)
     lib().or_conv1d_nlc_f16_ex(_ptr(x), _ptr(w), _ptr(b), _ptr(a), _ptr(r), _ptr(rs), _ptr(y),
                                _I64(lanes), _I64(length), _I64(cin), _I64(cout), _I64(k), _I64(dil),

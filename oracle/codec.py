@@ -61,7 +61,9 @@ def decode_f16(geo, prep, latent_bits):
             u = conv1d_nlc_f16(h2, un["c2"]["w16"], un["c2"]["b16"], 1, res_bits=u)
         x = u
     s = snake_nlc_f16(x, *prep["out_act"])
-    y = conv1d_nlc_f16(s, prep["out"]["w16"], prep["out"]["b16"], 1, act_tanh=True)
+    # tanh (the benchmark's form) or Codec::forward's clamp to [-1, 1] (codec.rs:433-436)
+    act = "clamp" if getattr(geo, "out_clamp", False) else "tanh"
+    y = conv1d_nlc_f16(s, prep["out"]["w16"], prep["out"]["b16"], 1, act=act)
     return y.reshape(lanes, length)
 
 

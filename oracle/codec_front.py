@@ -68,3 +68,34 @@ def decode_f16(geo, hw, codes):
         p = conv1d_nlc_f16(dn, _lin(U["pw1_w"]), _f16(U["pw1_b"]), 1, act="gelu")
         x = conv1d_nlc_f16(p, _lin(U["pw2_w"]), _f16(U["pw2_b"]), 1, res_bits=u, scale=U["gamma"])
     return x
+
+
+def document_windows(n, chunk, context):
+    """Codec::decode's windows (codec.rs:582-603): (from, to, length, drop, keep) per window, in
+    frames -- frames[from:to] right-padded with frame to-1 up to `length` (the full span when
+    n >= span), of whose forward the audio of frames drop .. drop + keep is kept."""
+    out, span, start = [], chunk + context, 0
+    while start < n:
+        end = min(start + chunk, n)
+        frm = max(start - context, 0)
+        to = min(frm + span, n)
+        length = span if n >= span else to - frm
+        out.append((frm, to, length, start - frm, end - start))
+        start = end
+    return out
+
+
+def decode_document_f32(front_geo, front_hw, codec_geo, codec_prep, codes, chunk, context):
+    """codes [n, n_books] -> audio [n * samples_per_frame] f32: every window through this module's
+    decode_f16 and the waveform oracle's (oracle.codec.decode_f16), one at a time, the kept audio
+    concatenated."""
+    from .codec import decode_f16 as wave_f16
+    codes = np.ascontiguousarray(codes, np.int32)
+    spf = front_geo.upsample * codec_geo.hop
+    parts = []
+    for frm, to, length, drop, keep in document_windows(codes.shape[0], chunk, context):
+        idx = np.minimum(np.arange(frm, frm + length), to - 1)
+        lat = decode_f16(front_geo, front_hw, codes[idx][None])
+        wav = wave_f16(codec_geo, codec_prep, lat)[0]
+        parts.append(wav[drop * spf:(drop + keep) * spf].view(np.float16).astype(np.float32))
+    return np.concatenate(parts) if parts else np.zeros(0, np.float32)

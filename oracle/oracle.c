@@ -314,6 +314,7 @@ void or_conv1d_nlc_f16_ex(const uint16_t *x, const uint16_t *w_tap, const uint16
                     if (rr) v += or_f16_to_f32(rr[co]);
                     if (act == 1) v = tanhf(v);
                     if (act == 2) v = or_gelu_erf(v);
+                    if (act == 3) v = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v);
                     yr[co] = or_f32_to_f16(v);
                 }
             }

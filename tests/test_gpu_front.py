@@ -162,3 +162,60 @@ def test_front_decode_rejects_bad_codes(dev):
     codes[0, 2, 1] = TINY.book_size
     with pytest.raises(DttsError, match="outside"):
         front.decode(codes)
+
+
+@pytest.mark.parametrize("n,chunk,context", [(14, 4, 2), (5, 4, 2), (3, 4, 2)])
+def test_document_decode_matches_oracle(dev, n, chunk, context):
+    """Codec::decode's chunked document (codec.rs:562-604) at a tiny front half and clamped waveform
+    stack, against the oracle's window-by-window decode: all windows run as lanes of one length
+    here, so for n < span the later windows are right-padded where the reference does not pad."""
+    from dtts import codec, codec_front
+    from oracle import codec as ocodec
+    from oracle import codec_front as ofront
+    from _doc_ref import TINY, TINY_WAVE, wave_weights
+    from _util import rel
+    hw, w = codec_front.random_weights(TINY, 62), wave_weights(62)
+    codes = synth.randint(62, "codes", (n, TINY.n_books), 0, TINY.book_size - 1)
+    front = codec_front.CodecFront(TINY, hw, dev)
+    wave = codec.Codec(TINY_WAVE, w, dev)
+    got = codec_front.decode_document(front, wave, codes, chunk, context).cpu().numpy()
+    want = ofront.decode_document_f32(TINY, hw, TINY_WAVE, ocodec.prepare(TINY_WAVE, w), codes, chunk, context)
+    assert got.shape == want.shape == (n * TINY.upsample * TINY_WAVE.hop,)
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel(got, want)[1] < 1e-2, (np.max(np.abs(got - want)),
+                                                                            rel(got, want))
+
+
+def test_document_decode_equals_its_windows(dev):
+    """The batched document decode keeps, bit for bit, what each padded window decoded on its own
+    (one lane through dtts_codec_front_decode and dtts_codec_decode) gives for its chunk."""
+    from dtts import codec, codec_front
+    from oracle import codec_front as ofront
+    from _doc_ref import TINY, TINY_WAVE, wave_weights
+    n, chunk, context = 23, 6, 3
+    front = codec_front.CodecFront(TINY, codec_front.random_weights(TINY, 63), dev)
+    wave = codec.Codec(TINY_WAVE, wave_weights(63), dev)
+    codes = synth.randint(63, "codes", (n, TINY.n_books), 0, TINY.book_size - 1)
+    got = codec_front.decode_document(front, wave, codes, chunk, context).cpu().numpy()
+    spf = TINY.upsample * TINY_WAVE.hop
+    for frm, to, length, drop, keep in ofront.document_windows(n, chunk, context):
+        idx = np.minimum(np.arange(frm, frm + length), to - 1)
+        lat = front.decode(codes[idx][None])
+        wav = wave.decode(lat).float().cpu().numpy()[0]
+        start = frm + drop
+        assert np.array_equal(got[start * spf:(start + keep) * spf], wav[drop * spf:(drop + keep) * spf])
+
+
+def test_document_decode_rejects_bad_arguments(dev):
+    from dtts import DttsError, codec, codec_front
+    from _doc_ref import TINY, TINY_WAVE, wave_weights
+    front = codec_front.CodecFront(TINY, codec_front.random_weights(TINY, 64), dev)
+    wave = codec.Codec(TINY_WAVE, wave_weights(64), dev)
+    codes = np.zeros((9, TINY.n_books), np.int32)
+    with pytest.raises(DttsError, match="bad sizes"):
+        codec_front.decode_document(front, wave, codes, chunk=0, context=2)
+    with pytest.raises(DttsError, match="max_frames"):
+        codec_front.decode_document(front, wave, np.zeros((TINY.max_frames + 10, TINY.n_books), np.int32),
+                                    chunk=TINY.max_frames, context=5)
+    codes[7, 3] = -1
+    with pytest.raises(DttsError, match="outside"):
+        codec_front.decode_document(front, wave, codes, chunk=4, context=2)
