@@ -16,9 +16,10 @@
 //                   arithmetic, one rounding out (the reference runs it in f32).
 //   SwiGLU rows    silu(gate) * up from a [rows, 2 * ffn] gate|up projection, f16 out.
 //   window attn    Stack::forward's prefill branch (crates/qwen3tts/src/qwen3.rs:420-443) for a
-//                   sliding window: RoPE on q and k as they are loaded, scores = q.k * scale,
-//                   the causal window mask of causal_window_mask (lib.rs:1210-1224: key j is
-//                   visible to query i when i - window < j <= i), softmax, weighted v.
+//                   sliding window: RoPE on q and k as they are loaded (the roped values are the
+//                   MFMA's f16 operands), scores = q.k * scale, the causal window mask of
+//                   causal_window_mask (lib.rs:1210-1224: key j is visible to query i when
+//                   i - window < j <= i), softmax, weighted v.
 //
 // The lookup, depthwise+LN, the norm and SwiGLU are HBM-bound passes: the lookup reads n_books
 // rows of `dim` f32 per frame and writes 2 * dim f16; depthwise+LN reads its k input rows (the
@@ -161,116 +162,150 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const half_t *gu, half
     }
 }
 
-// Windowed causal attention over a sequence, D = 64. Workgroup = (64-query block, query head,
-// lane); 4 threads per query, each taking every 4th key of the query's window with an online
-// softmax (running max, sum and weighted v), combined over the 4 at the end. The block's keys
-// ([first query - window + 1, last query]) are staged in LDS once: k roped in f32 (the
-// reference keeps roped k in f32), v as stored. q is roped in registers; scores are scaled
-// after the dot product, as the prefill branch scales the scores.
+// Windowed causal attention over a sequence, D = 64, on v_mfma_f32_16x16x32_f16. Workgroup =
+// (64-query block, query head, lane), one wave per 16 queries. The block's keys, from the first
+// query - window + 1 on, 16 (NT + 3) rows, are staged in LDS once: k roped in f32 and stored in
+// f16 (row-major, the scores' A operand), v transposed to [dim][key] (the weighted sum's A
+// operand); keys before 0 or past the sequence are zero rows. A wave's queries see NT 16-key
+// tiles starting at its first query - window + 1 (16 NT >= window + 15).
+//   scores^T = K . Q^T      two MFMAs per tile; a lane ends with one query (lane % 16) and four
+//                           keys per tile, so a query's max and sum are a lane's own values
+//                           plus two shuffles (xor 16, 32). Scaled after the dot product, as the
+//                           prefill branch scales the scores; keys outside (q - window, q]
+//                           masked to -inf.
+//   p = exp(s - max)        rounded to f16 (the MFMA operand); sum over the rounded p in f32.
+//   out^T = V^T . P^T       two tiles of p per MFMA: a lane's own p values are the B operand as
+//                           they stand, with V^T's k slots permuted to the same keys (exact: the
+//                           sum over keys is order-free). out = acc / sum, one f16 rounding.
 constexpr int kWinMax = 192;
 constexpr int kQBlock = 64;
 
+template <int NT>
 __global__ __launch_bounds__(256) void window_attn_kernel(const half_t *qkv, const float *cos_t, const float *sin_t,
                                                           half_t *out, int T, int heads, int n_kv, int window,
                                                           float scale) {
 #pragma clang fp contract(off)
-    constexpr int D = 64, HALF = 32;
-    constexpr int RMAX = kQBlock + kWinMax - 1;
-    __shared__ __attribute__((aligned(16))) float Ks[RMAX][D];
-    __shared__ __attribute__((aligned(16))) half_t Vs[RMAX][D];
+    constexpr int D = 64, HALF = 32, ROWS = 16 * (NT + 3);
+    constexpr int KP = D + 8;     // K row pitch, halves (144 bytes: 16-byte aligned rows)
+    constexpr int VP = ROWS + 8;  // V^T row pitch, halves
+    __shared__ __attribute__((aligned(16))) half_t Ks[ROWS * KP];
+    __shared__ __attribute__((aligned(16))) half_t Vt[D * VP];
     const int l0 = blockIdx.x * kQBlock;
     const int h = blockIdx.y;
     const int lane_idx = blockIdx.z;
     const int kh = h / (heads / n_kv);
     const int width = (heads + 2 * n_kv) * D;
     const half_t *base = qkv + static_cast<int64_t>(lane_idx) * T * width;
-    const int kbase = l0 - window + 1 > 0 ? l0 - window + 1 : 0;
-    const int kend = l0 + kQBlock < T ? l0 + kQBlock : T;  // exclusive
-    const int nrows = kend - kbase;
-    // stage k (roped, f32) and v: one thread per (row, rotation pair)
-    for (int e = threadIdx.x; e < nrows * HALF; e += 256) {
-        const int r = e / HALF, i = e - (e / HALF) * HALF;
-        const int j = kbase + r;
-        const half_t *kr = base + static_cast<int64_t>(j) * width + (heads + kh) * D;
-        float o1, o2;
-        rope_pair(static_cast<float>(kr[i]), static_cast<float>(kr[i + HALF]), cos_t[j * HALF + i], sin_t[j * HALF + i],
-                  o1, o2);
-        Ks[r][i] = o1;
-        Ks[r][i + HALF] = o2;
-        const half_t *vr = base + static_cast<int64_t>(j) * width + (heads + n_kv + kh) * D;
-        Vs[r][i] = vr[i];
-        Vs[r][i + HALF] = vr[i + HALF];
-    }
-    const int qi = threadIdx.x >> 2, sub = threadIdx.x & 3;
-    const int p = l0 + qi;
-    float q[D];
-    if (p < T) {
-        const half_t *qr = base + static_cast<int64_t>(p) * width + h * D;
+    const int j0 = l0 - window + 1;  // key of staged row 0
+    // stage: 4 threads per row; thread g takes dims [8g, 8g + 8) and their RoPE partners + 32
+    for (int e = threadIdx.x; e < ROWS * 4; e += 256) {
+        const int r = e >> 2, g = e & 3;
+        const int j = j0 + r;
+        half8_t k1 = {}, k2 = {}, v1 = {}, v2 = {};
+        if (j >= 0 && j < T) {
+            const half_t *kr = base + static_cast<int64_t>(j) * width + (heads + kh) * D + 8 * g;
+            const half8_t a = *reinterpret_cast<const half8_t *>(kr);
+            const half8_t b = *reinterpret_cast<const half8_t *>(kr + HALF);
+            const float *cr = cos_t + static_cast<int64_t>(j) * HALF + 8 * g;
+            const float *sr = sin_t + static_cast<int64_t>(j) * HALF + 8 * g;
 #pragma unroll
-        for (int i = 0; i < HALF; ++i)
-            rope_pair(static_cast<float>(qr[i]), static_cast<float>(qr[i + HALF]), cos_t[p * HALF + i],
-                      sin_t[p * HALF + i], q[i], q[i + HALF]);
-    }
-    __syncthreads();
-    if (p >= T) return;  // (no barrier follows)
-    const int jlo = p - window + 1 > 0 ? p - window + 1 : 0;
-    float m = -INFINITY, l = 0.0f, acc[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-    for (int j = jlo + sub; j <= p; j += 4) {
-        const float *kr = Ks[j - kbase];
-        float s = 0.0f;
-#pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const float4_t kv = *reinterpret_cast<const float4_t *>(kr + d);
-            s += q[d] * kv[0];
-            s += q[d + 1] * kv[1];
-            s += q[d + 2] * kv[2];
-            s += q[d + 3] * kv[3];
+            for (int u = 0; u < 8; ++u) {
+                float o1, o2;
+                rope_pair(static_cast<float>(a[u]), static_cast<float>(b[u]), cr[u], sr[u], o1, o2);
+                k1[u] = static_cast<half_t>(o1);
+                k2[u] = static_cast<half_t>(o2);
+            }
+            const half_t *vr = base + static_cast<int64_t>(j) * width + (heads + n_kv + kh) * D + 8 * g;
+            v1 = *reinterpret_cast<const half8_t *>(vr);
+            v2 = *reinterpret_cast<const half8_t *>(vr + HALF);
         }
-        s = s * scale;
-        const float mn = fmaxf(m, s);
-        const float c = __builtin_expf(m - mn);
-        const float w = __builtin_expf(s - mn);
-        l = l * c + w;
-        const half_t *vr = Vs[j - kbase];
-#pragma unroll
-        for (int d = 0; d < D; d += 8) {
-            const half8_t vv = *reinterpret_cast<const half8_t *>(vr + d);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc[d + u] = acc[d + u] * c + w * static_cast<float>(vv[u]);
-        }
-        m = mn;
-    }
-    // combine the 4 threads of the query (adjacent lanes)
-    float mx = m;
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    const float f = m == -INFINITY ? 0.0f : __builtin_expf(m - mx);
-    float ls = l * f;
-    ls += __shfl_xor(ls, 1, 64);
-    ls += __shfl_xor(ls, 2, 64);
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        float a = acc[d] * f;
-        a += __shfl_xor(a, 1, 64);
-        a += __shfl_xor(a, 2, 64);
-        acc[d] = a;
-    }
-    // thread `sub` stores dims [16 sub, 16 sub + 16); the branches keep acc's indices constant
-    // (a register array indexed at run time would be moved to LDS)
-    half_t *o = out + (static_cast<int64_t>(lane_idx) * T + p) * heads * D + h * D + sub * 16;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-        if (sub != s4) continue;
-        half8_t o0, o1;
+        *reinterpret_cast<half8_t *>(Ks + r * KP + 8 * g) = k1;
+        *reinterpret_cast<half8_t *>(Ks + r * KP + HALF + 8 * g) = k2;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            o0[u] = static_cast<half_t>(acc[s4 * 16 + u] / ls);
-            o1[u] = static_cast<half_t>(acc[s4 * 16 + 8 + u] / ls);
+            Vt[(8 * g + u) * VP + r] = v1[u];
+            Vt[(HALF + 8 * g + u) * VP + r] = v2[u];
         }
-        *reinterpret_cast<half8_t *>(o) = o0;
-        *reinterpret_cast<half8_t *>(o + 8) = o1;
+    }
+    // this lane's query (lane % 16 of the wave's 16) and its k slots [8g, 8g + 8) of each half
+    const int w = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    const int col = ln & 15, g = ln >> 4;
+    const int q = l0 + 16 * w + col;
+    half8_t qa = {}, qb = {};
+    if (q < T) {
+        const half_t *qr = base + static_cast<int64_t>(q) * width + h * D + 8 * g;
+        const half8_t a = *reinterpret_cast<const half8_t *>(qr);
+        const half8_t b = *reinterpret_cast<const half8_t *>(qr + HALF);
+        const float *cr = cos_t + static_cast<int64_t>(q) * HALF + 8 * g;
+        const float *sr = sin_t + static_cast<int64_t>(q) * HALF + 8 * g;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            float o1, o2;
+            rope_pair(static_cast<float>(a[u]), static_cast<float>(b[u]), cr[u], sr[u], o1, o2);
+            qa[u] = static_cast<half_t>(o1);
+            qb[u] = static_cast<half_t>(o2);
+        }
+    }
+    __syncthreads();
+    if (l0 + 16 * w >= T) return;  // the whole wave is past the sequence (no barrier follows)
+    // scores^T per tile: rows = keys 16 (w + t) + 4g + r of the staging, column = this query
+    float s[NT][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const half_t *kr = Ks + (16 * (w + t) + col) * KP + 8 * g;
+        const half8_t ka = *reinterpret_cast<const half8_t *>(kr);
+        const half8_t kb = *reinterpret_cast<const half8_t *>(kr + HALF);
+        float4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qa, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, qb, c, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = j0 + 16 * (w + t) + 4 * g + r;
+            const bool seen = j >= 0 && j <= q && j > q - window;
+            s[t][r] = seen ? c[r] * scale : -INFINITY;
+            mx = fmaxf(mx, s[t][r]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (mx == -INFINITY) mx = 0.0f;  // a query past the sequence (not stored)
+    half_t p[NT][4];
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[t][r] = static_cast<half_t>(__builtin_expf(s[t][r] - mx));
+            sum += static_cast<float>(p[t][r]);
+        }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    float4_t o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NT / 2; ++c) {
+        const half8_t pb = {p[2 * c][0], p[2 * c][1], p[2 * c][2], p[2 * c][3],
+                            p[2 * c + 1][0], p[2 * c + 1][1], p[2 * c + 1][2], p[2 * c + 1][3]};
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const half_t *vr = Vt + (16 * dt + col) * VP + 16 * (w + 2 * c) + 4 * g;
+            const half4_t a0 = *reinterpret_cast<const half4_t *>(vr);
+            const half4_t a1 = *reinterpret_cast<const half4_t *>(vr + 16);
+            const half8_t va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[dt], 0, 0, 0);
+        }
+    }
+    if (q >= T) return;
+    // out^T tile dt: this lane holds dims 16 dt + 4g + r of its query
+    half_t *dst = out + (static_cast<int64_t>(lane_idx) * T + q) * heads * D + h * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        half4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = static_cast<half_t>(o[dt][r] / sum);
+        *reinterpret_cast<half4_t *>(dst + 16 * dt) = v;
     }
 }
 
@@ -379,10 +414,26 @@ extern "C" int dtts_window_attention_prefill_f16(const dtts_f16 *qkv, const floa
                  "%s: shape too large", name);
     const dim3 grid(static_cast<unsigned>((len + dtts::kQBlock - 1) / dtts::kQBlock), static_cast<unsigned>(heads),
                     static_cast<unsigned>(lanes));
-    dtts::window_attn_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const half_t *>(qkv), cos_t, sin_t,
-                                                       reinterpret_cast<half_t *>(out), static_cast<int>(len),
-                                                       static_cast<int>(heads), static_cast<int>(n_kv),
-                                                       static_cast<int>(window), scale);
+    const half_t *x = reinterpret_cast<const half_t *>(qkv);
+    half_t *y = reinterpret_cast<half_t *>(out);
+    const int T = static_cast<int>(len), H = static_cast<int>(heads), KV = static_cast<int>(n_kv);
+    const int W = static_cast<int>(window);
+    switch (2 * ((W + 15 + 31) / 32)) {  // key tiles per wave: 16 NT >= window + 15
+#define WIN_CASE(NT)                                                                                   \
+    case NT:                                                                                           \
+        dtts::window_attn_kernel<NT><<<grid, 256, 0, stream>>>(x, cos_t, sin_t, y, T, H, KV, W, scale); \
+        break;
+        WIN_CASE(2)
+        WIN_CASE(4)
+        WIN_CASE(6)
+        WIN_CASE(8)
+        WIN_CASE(10)
+        WIN_CASE(12)
+        WIN_CASE(14)
+#undef WIN_CASE
+        default:
+            DTTS_REQUIRE(false, "%s: window %d has no tile count", name, W);
+    }
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

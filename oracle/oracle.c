@@ -936,7 +936,10 @@ void or_depthwise_layernorm_f16(const uint16_t *x, const float *taps, const floa
  * q and k half-split-roped in f32 at their positions (candle_nn::rotary_emb::rope as called at
  * qwen3.rs:384-387), scores = (q . k) * scale (qwen3.rs:433-436), the mask of causal_window_mask
  * (lib.rs:1210-1224), softmax_last_dim (max, exp(s - max), in-order sum, divide), then probs . v.
- * qkv [lanes, T, (heads + 2 n_kv) D] f16 (q heads, k heads, v heads); out [lanes, T, heads D] f16. */
+ * Two f16 storage points the GPU adds (its matrix-core operands): the roped q and k, and
+ * exp(s - max); the division by the sum of those rounded weights comes after the weighted sum,
+ * which is softmax-then-product reassociated. qkv [lanes, T, (heads + 2 n_kv) D] f16 (q heads,
+ * k heads, v heads); out [lanes, T, heads D] f16. */
 void or_window_attention_prefill_f16(const uint16_t *qkv, const float *cos_t, const float *sin_t,
                                      uint16_t *out, int64_t lanes, int64_t T, int64_t heads, int64_t n_kv,
                                      int64_t D, int64_t window, float scale) {
@@ -948,15 +951,18 @@ void or_window_attention_prefill_f16(const uint16_t *qkv, const float *cos_t, co
     for (int64_t b = 0; b < lanes; ++b)
         for (int64_t h = 0; h < heads; ++h) {
             const int64_t kh = h / gqa;
+            /* roped k, stored in f16 (the GPU's matrix-core operand) */
             for (int64_t j = 0; j < T; ++j) {
                 const uint16_t *kr = qkv + (b * T + j) * width + (heads + kh) * D;
                 for (int64_t d = 0; d < D; ++d) xin[d] = or_f16_to_f32(kr[d]);
                 rope_row(xin, cos_t + j * half, sin_t + j * half, k + j * D, half);
+                for (int64_t d = 0; d < D; ++d) k[j * D + d] = or_f16_to_f32(or_f32_to_f16(k[j * D + d]));
             }
             for (int64_t i = 0; i < T; ++i) {
                 const uint16_t *qr = qkv + (b * T + i) * width + h * D;
                 for (int64_t d = 0; d < D; ++d) xin[d] = or_f16_to_f32(qr[d]);
                 rope_row(xin, cos_t + i * half, sin_t + i * half, q, half);
+                for (int64_t d = 0; d < D; ++d) q[d] = or_f16_to_f32(or_f32_to_f16(q[d]));
                 const int64_t lo = i + 1 > window ? i + 1 - window : 0;
                 float mx = -INFINITY;
                 for (int64_t j = lo; j <= i; ++j) {
@@ -965,17 +971,17 @@ void or_window_attention_prefill_f16(const uint16_t *qkv, const float *cos_t, co
                     p[j] = s * scale;
                     mx = p[j] > mx ? p[j] : mx;
                 }
+                /* softmax's exp(s - max) in f16 (the weighted sum's operand), normalised after */
                 float sum = 0.0f;
                 for (int64_t j = lo; j <= i; ++j) {
-                    p[j] = expf(p[j] - mx);
+                    p[j] = or_f16_to_f32(or_f32_to_f16(expf(p[j] - mx)));
                     sum += p[j];
                 }
-                for (int64_t j = lo; j <= i; ++j) p[j] = p[j] / sum;
                 for (int64_t d = 0; d < D; ++d) {
                     float o = 0.0f;
                     for (int64_t j = lo; j <= i; ++j)
                         o += p[j] * or_f16_to_f32(qkv[(b * T + j) * width + (heads + n_kv + kh) * D + d]);
-                    out[(b * T + i) * heads * D + h * D + d] = or_f32_to_f16(o);
+                    out[(b * T + i) * heads * D + h * D + d] = or_f32_to_f16(o / sum);
                 }
             }
         }
