@@ -105,7 +105,7 @@ struct Tile {
 // fit the direct-staging buffer loads. Every tile needs cin % KC == 0 (the caller guarantees
 // cin % 32 == 0) and cout % BN == 0.
 template <int KMAX, int HMAX, typename F>
-auto with_tile(int len, int cin, int cout, bool direct, F &&f) {
+auto with_tile(int64_t lanes, int len, int cin, int cout, bool direct, F &&f) {
     if (direct) {
         // k <= 7 (dilated) at 96-multiples: eight waves of 64 x 96; short sequences take 256-row
         // tiles (two workgroups per CU) so the last tile of a lane is not mostly padding
@@ -113,15 +113,30 @@ auto with_tile(int len, int cin, int cout, bool direct, F &&f) {
             if (cout % 96 == 0 && len >= 1024) return f(Tile<ConvTile<512, 96, 8, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
             if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 16, KMAX, HMAX, 2, kStageDirect>>{});
         }
-        // k = 2 (the transposed convs): 256 x 96 over four waves, two workgroups per CU (their
-        // epilogues and prologues overlap the other's main loop). k = 1 at 192-multiples: 256 x 192
-        // over eight waves with 64-channel chunks (a chunk holds little matrix work at one tap;
-        // this halves the barriers per output)
-        if constexpr (KMAX == 2)
-            if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
-        if constexpr (KMAX == 1)
+        // k = 2 (the transposed convs) at 128-multiples: 2 x 2 waves of 128 x 64 when the input is
+        // wide (cin >= 768: more matrix work per staged chunk), else 2 x 2 waves of 64 x 64 with
+        // three 32-channel stages in flight (three workgroups per CU); at 96-multiples four waves of
+        // 32 x 96, three stages. Measured on the codec's four upsampling shapes: 10-20% over one
+        // 256 x 96 tile for all.
+        if constexpr (KMAX == 2) {
+            if (cout % 128 == 0 && cin >= 768) return f(Tile<ConvTile<256, 128, 2, 2, 32, KMAX, HMAX, 2, kStageDirect>>{});
+            if (cout % 128 == 0) return f(Tile<ConvTile<128, 128, 2, 2, 32, KMAX, HMAX, 3, kStageDirect>>{});
+            if (cout % 96 == 0) return f(Tile<ConvTile<128, 96, 4, 1, 32, KMAX, HMAX, 3, kStageDirect>>{});
+        }
+        // k = 1 at 128-multiples: 2 x 2 waves of 64 x 64. Three 32-channel stages in flight (three
+        // workgroups per CU) up to cin 2048; beyond, two 64-channel stages (fewer barriers per
+        // output). When that leaves fewer than 1024 tiles, 64-channel-wide tiles instead, to fill
+        // the 256 CUs. k = 1 at 192-multiples otherwise: 256 x 192 over eight waves.
+        if constexpr (KMAX == 1) {
+            const int64_t tiles128 = lanes * ((len + 127) / 128) * (cout / 128);
+            if (cout % 64 == 0 && cin % 64 == 0 && (cout % 128 != 0 || tiles128 < 1024))
+                return f(Tile<ConvTile<128, 64, 2, 2, 64, KMAX, HMAX, 2, kStageDirect>>{});
+            if (cout % 128 == 0 && cin % 64 == 0 && cin > 2048)
+                return f(Tile<ConvTile<128, 128, 2, 2, 64, KMAX, HMAX, 2, kStageDirect>>{});
+            if (cout % 128 == 0) return f(Tile<ConvTile<128, 128, 2, 2, 32, KMAX, HMAX, 3, kStageDirect>>{});
             if (cout % 192 == 0 && cin % 64 == 0)
                 return f(Tile<ConvTile<256, 192, 4, 2, 64, KMAX, HMAX, 2, kStageDirect>>{});
+        }
     }
     if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 32, KMAX, HMAX>>{});
     if (cout % 64 == 0) return f(Tile<ConvTile<256, 64, 4, 1, 32, KMAX, HMAX>>{});
@@ -129,10 +144,10 @@ auto with_tile(int len, int cin, int cout, bool direct, F &&f) {
 }
 
 template <typename F>
-auto with_tile_k(int kmax, int len, int cin, int cout, bool direct, F &&f) {
-    if (kmax == 1) return with_tile<1, 0>(len, cin, cout, direct, f);
-    if (kmax == 2) return with_tile<2, 8>(len, cin, cout, direct, f);
-    return with_tile<7, 64>(len, cin, cout, direct, f);
+auto with_tile_k(int kmax, int64_t lanes, int len, int cin, int cout, bool direct, F &&f) {
+    if (kmax == 1) return with_tile<1, 0>(lanes, len, cin, cout, direct, f);
+    if (kmax == 2) return with_tile<2, 8>(lanes, len, cin, cout, direct, f);
+    return with_tile<7, 64>(lanes, len, cin, cout, direct, f);
 }
 
 }  // namespace
@@ -182,7 +197,7 @@ const char *conv_kernel_name(const dtts_conv_desc *d) {
     static thread_local char buf[128];
     const Choice c = choose(d);
     if (std::strcmp(c.path, "mfma") == 0)
-        with_tile_k(c.kmax, static_cast<int>(d->len), static_cast<int>(d->cin), static_cast<int>(d->cout), c.direct_ok,
+        with_tile_k(c.kmax, d->lanes, static_cast<int>(d->len), static_cast<int>(d->cin), static_cast<int>(d->cout), c.direct_ok,
                     [&](auto t) {
             typedef typename decltype(t)::type Cfg;
             char tail[32];
@@ -241,7 +256,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
-        e = with_tile_k(ch.kmax, p.L, p.cin, p.cout, ch.direct_ok, [&](auto t) {
+        e = with_tile_k(ch.kmax, d->lanes, p.L, p.cin, p.cout, ch.direct_ok, [&](auto t) {
             return launch_tiled<typename decltype(t)::type>(p, d->lanes, stream);
         });
     } else {
