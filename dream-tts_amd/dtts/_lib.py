@@ -69,6 +69,26 @@ SIGNATURES = {
     "dtts_codec_front_decode": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
     "dtts_codec_document_workspace_bytes": [_P, _P, _I64, _I64, _I64],
     "dtts_codec_decode_document": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _SZ, _P],
+    "dtts_checkpoint_open": [ctypes.c_char_p, _P],
+    "dtts_checkpoint_close": [_P],
+    "dtts_checkpoint_count": [_P],
+    "dtts_checkpoint_at": [_P, _I64, _P],
+    "dtts_checkpoint_get": [_P, ctypes.c_char_p, _P],
+    "dtts_convert_f16": [_P, _I32, _P, _I64, _P],
+    "dtts_convert_f32": [_P, _I32, _P, _I64, _P],
+    "dtts_convert_f16_cols": [_P, _I32, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_convert_transpose_f16": [_P, _I32, _P, _I64, _I64, _P],
+    "dtts_convert_tap_major_f16": [_P, _I32, _P, _I64, _I64, _I64, _P],
+    "dtts_convert_transpose_tap_major_f16": [_P, _I32, _P, _I64, _I64, _I64, _I64, _P],
+    "dtts_convert_repeat_f16": [_P, _I32, _P, _I64, _I64, _P],
+    "dtts_convert_snake_fold": [_P, _P, _I32, _P, _P, _I64, _P],
+    "dtts_convert_codebook_fold": [_P, _P, _I32, _F32, _P, _I64, _I64, _P],
+    "dtts_convert_q8_0": [_P, _I32, _P, _I64, _I64, _P],
+    "dtts_codec_model_load": [_P, _P, _P, _P, _P],
+    "dtts_codec_model_destroy": [_P],
+    "dtts_codec_model_front": [_P],
+    "dtts_codec_model_wave": [_P],
+    "dtts_codec_model_bytes": [_P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
@@ -94,7 +114,10 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_gemm_f16_workspace_bytes": ctypes.c_size_t, "dtts_stack_destroy": None,
              "dtts_stack_workspace_bytes": ctypes.c_size_t, "dtts_codec_front_destroy": None,
              "dtts_codec_front_workspace_bytes": ctypes.c_size_t,
-             "dtts_codec_document_workspace_bytes": ctypes.c_size_t}
+             "dtts_codec_document_workspace_bytes": ctypes.c_size_t, "dtts_checkpoint_close": None,
+             "dtts_checkpoint_count": ctypes.c_int64, "dtts_codec_model_destroy": None,
+             "dtts_codec_model_front": ctypes.c_void_p, "dtts_codec_model_wave": ctypes.c_void_p,
+             "dtts_codec_model_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

@@ -143,6 +143,20 @@ def _f32_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
 
 
+def c_geometry(geo: Geometry) -> _Geometry:
+    g = _Geometry()
+    g.latent_dim, g.head_kernel, g.n_blocks = geo.latent_dim, geo.head_kernel, geo.n_blocks
+    for i, c in enumerate(geo.channels):
+        g.channels[i] = c
+    for i, r in enumerate(geo.rates):
+        g.rates[i] = r
+    g.ru_kernel, g.out_kernel = geo.ru_kernel, geo.out_kernel
+    g.out_clamp = int(geo.out_clamp)
+    for j, d in enumerate(geo.ru_dilations):
+        g.ru_dilations[j] = d
+    return g
+
+
 class Codec:
     """Device weights + a dtts_codec handle. Keeps every device tensor alive."""
 
@@ -160,16 +174,7 @@ class Codec:
             self._keep.append(t)
             return ctypes.c_void_p(t.data_ptr())
 
-        g = _Geometry()
-        g.latent_dim, g.head_kernel, g.n_blocks = geo.latent_dim, geo.head_kernel, geo.n_blocks
-        for i, c in enumerate(geo.channels):
-            g.channels[i] = c
-        for i, r in enumerate(geo.rates):
-            g.rates[i] = r
-        g.ru_kernel, g.out_kernel = geo.ru_kernel, geo.out_kernel
-        g.out_clamp = int(geo.out_clamp)
-        for j, d in enumerate(geo.ru_dilations):
-            g.ru_dilations[j] = d
+        g = c_geometry(geo)
         ws = _Weights()
         ws.head_w = f16(nlc.tap_major_weight(w.head_w))
         ws.head_b = f16(w.head_b)

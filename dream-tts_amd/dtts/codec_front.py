@@ -195,6 +195,16 @@ class _Weights(ctypes.Structure):
         ("out_b", ctypes.c_void_p), ("up", _Up * MAX_UP)]
 
 
+def c_geometry(geo: Geometry) -> _Geometry:
+    g = _Geometry(geo.n_books, geo.n_first, geo.book_size, geo.book_dim, geo.codebook_dim, geo.latent_dim,
+                  geo.pre_kernel, geo.tf_dim, geo.tf_layers, geo.tf_heads, geo.tf_n_kv, geo.tf_head_dim,
+                  geo.tf_ffn, geo.tf_window, geo.tf_eps, geo.tf_rope_base, len(geo.up_ratios))
+    for i, r in enumerate(geo.up_ratios):
+        g.up_ratios[i] = r
+    g.dw_kernel, g.ln_eps, g.max_frames = geo.dw_kernel, geo.ln_eps, geo.max_frames
+    return g
+
+
 class CodecFront:
     """Device weights + a dtts_codec_front handle (keeps every device tensor alive)."""
 
@@ -211,12 +221,7 @@ class CodecFront:
             self._keep.append(t)
             return t.data_ptr()
 
-        g = _Geometry(geo.n_books, geo.n_first, geo.book_size, geo.book_dim, geo.codebook_dim, geo.latent_dim,
-                      geo.pre_kernel, geo.tf_dim, geo.tf_layers, geo.tf_heads, geo.tf_n_kv, geo.tf_head_dim,
-                      geo.tf_ffn, geo.tf_window, geo.tf_eps, geo.tf_rope_base, len(geo.up_ratios))
-        for i, r in enumerate(geo.up_ratios):
-            g.up_ratios[i] = r
-        g.dw_kernel, g.ln_eps, g.max_frames = geo.dw_kernel, geo.ln_eps, geo.max_frames
+        g = c_geometry(geo)
         ws = _Weights()
         for n in ("codebooks", "out_proj", "pre_w", "pre_b", "in_w", "in_b", "tf_norm", "out_w", "out_b"):
             setattr(ws, n, put(kl[n]))

@@ -610,6 +610,96 @@ int dtts_codec_decode_document(const dtts_codec_front *front, const dtts_codec *
                                int64_t n, int64_t chunk, int64_t context, float *audio, void *workspace,
                                size_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------ f-4 checkpoints and weight formats
+ *
+ * What a loader must produce for the kernels (crates/tts-nn/src/lib.rs:143-360 Weights,
+ * 1252-1298 host_layout; crates/tts-nn/src/nlc.rs:30-183 the conv layouts). A safetensors file
+ * is memory-mapped and indexed by its header; tensors are read from the mapping in their
+ * on-disk dtype. The rearrangements run on the GPU from the raw tensor uploaded once: casts to
+ * f16/f32, the tap-major and polyphase conv layouts, the [out, in] -> [in, out] transpose,
+ * SnakeBeta's and the codebooks' folds and Q8_0 quantisation. */
+#define DTTS_DT_F32 0
+#define DTTS_DT_F16 1
+#define DTTS_DT_BF16 2
+#define DTTS_DT_F64 3
+#define DTTS_DT_I64 4
+#define DTTS_DT_I32 5
+#define DTTS_DT_I16 6
+#define DTTS_DT_I8 7
+#define DTTS_DT_U8 8
+#define DTTS_DT_BOOL 9
+#define DTTS_DT_OTHER 10 /* any other safetensors dtype (U16/U32/U64/F8_*): listed, not converted */
+#define DTTS_TENSOR_MAX_DIMS 8
+
+typedef struct dtts_checkpoint dtts_checkpoint;
+
+typedef struct dtts_tensor_info {
+    const char *name;   /* owned by the checkpoint */
+    int32_t dtype;      /* DTTS_DT_* */
+    int32_t ndim;
+    int64_t shape[DTTS_TENSOR_MAX_DIMS];
+    const void *data;   /* host pointer into the mapping */
+    size_t bytes;
+} dtts_tensor_info;
+
+/* Weights::load (lib.rs:161-173): maps the file and parses its header; the header's offsets and
+ * sizes are checked against the file and the dtypes' widths. */
+int dtts_checkpoint_open(const char *path, dtts_checkpoint **out);
+void dtts_checkpoint_close(dtts_checkpoint *ck);
+/* Weights::len (lib.rs:339-341); tensors in the header's order. */
+int64_t dtts_checkpoint_count(const dtts_checkpoint *ck);
+int dtts_checkpoint_at(const dtts_checkpoint *ck, int64_t index, dtts_tensor_info *out);
+/* Weights::cpu / file_shape (lib.rs:257-264, 349-351): "missing tensor <name>" when absent. */
+int dtts_checkpoint_get(const dtts_checkpoint *ck, const char *name, dtts_tensor_info *out);
+
+/* Device conversions: src is a raw tensor of dtype F32, F16, BF16 or F64 on the device; f16
+ * results are rounded to nearest even once from the exact value. */
+/* to_dtype (f16 / f32), n elements. */
+int dtts_convert_f16(const void *src, int32_t dtype, dtts_f16 *dst, int64_t n, hipStream_t stream);
+int dtts_convert_f32(const void *src, int32_t dtype, float *dst, int64_t n, hipStream_t stream);
+/* A [rows, cols] source into columns [col0, col0 + cols) of a [rows, ld] f16 destination: how
+ * tensors are concatenated along the last dimension (the codec's two RVQ output projections). */
+int dtts_convert_f16_cols(const void *src, int32_t dtype, dtts_f16 *dst, int64_t rows, int64_t cols, int64_t ld,
+                          int64_t col0, hipStream_t stream);
+/* host_layout (lib.rs:1252-1269): [rows, cols] -> [cols, rows] f16. */
+int dtts_convert_transpose_f16(const void *src, int32_t dtype, dtts_f16 *dst, int64_t rows, int64_t cols,
+                               hipStream_t stream);
+/* dtts_tap_major_weight's layout: torch Conv1d [cout, cin, k] -> [cout, k*cin] f16. */
+int dtts_convert_tap_major_f16(const void *w_oik, int32_t dtype, dtts_f16 *dst, int64_t cout, int64_t cin,
+                               int64_t k, hipStream_t stream);
+/* dtts_transpose_tap_major_weight's layout: ConvTranspose1d [cin, cout, kernel] ->
+ * [stride*cout, (kernel/stride)*cin] f16, taps reversed per phase. */
+int dtts_convert_transpose_tap_major_f16(const void *w_iok, int32_t dtype, dtts_f16 *dst, int64_t cin, int64_t cout,
+                                         int64_t kernel, int64_t stride, hipStream_t stream);
+/* nlc::transpose_bias (nlc.rs:177-183): [n] repeated `times` times, f16. */
+int dtts_convert_repeat_f16(const void *src, int32_t dtype, dtts_f16 *dst, int64_t n, int64_t times,
+                            hipStream_t stream);
+/* SnakeBeta::load (crates/qwen3tts/src/codec.rs:60-68): alpha = exp(alpha_log),
+ * brecip = 1 / (exp(beta_log) + 1e-9), in f32 (exp correctly rounded to f32). */
+int dtts_convert_snake_fold(const void *alpha_log, const void *beta_log, int32_t dtype, float *alpha, float *brecip,
+                            int64_t n, hipStream_t stream);
+/* Rvq::load (codec.rs:275-282): embedding_sum [size, dim] / clamp(cluster_usage [size], eps). */
+int dtts_convert_codebook_fold(const void *embedding_sum, const void *cluster_usage, int32_t dtype, float eps,
+                               float *dst, int64_t size, int64_t dim, hipStream_t stream);
+/* QTensor::quantize_onto for an [rows, k] weight into GGML block_q8_0 (the same rule as the host
+ * dtts_q8_0_quantize, bit for bit): blocks holds rows*k/32*34 bytes, 2-byte aligned. */
+int dtts_convert_q8_0(const void *w, int32_t dtype, void *blocks, int64_t rows, int64_t k, hipStream_t stream);
+
+/* Codec::load (crates/qwen3tts/src/codec.rs:347-399) from a checkpoint in the reference's naming
+ * ("decoder.quantizer.rvq_first.*", "decoder.pre_transformer.layers.<i>.*",
+ * "decoder.upsample.<i>.*", "decoder.decoder.<i>.*"): every tensor's presence and shape is
+ * checked against the two geometries before anything is allocated; then one device arena is
+ * allocated and filled by the conversions above (the raw tensors pass through a device staging
+ * buffer freed before return), and the front half and waveform stack are created on it. The
+ * call synchronises `stream`. */
+typedef struct dtts_codec_model dtts_codec_model;
+int dtts_codec_model_load(const dtts_checkpoint *ck, const dtts_codec_front_geometry *front,
+                          const dtts_codec_geometry *wave, hipStream_t stream, dtts_codec_model **out);
+void dtts_codec_model_destroy(dtts_codec_model *model);
+const dtts_codec_front *dtts_codec_model_front(const dtts_codec_model *model);
+const dtts_codec *dtts_codec_model_wave(const dtts_codec_model *model);
+size_t dtts_codec_model_bytes(const dtts_codec_model *model); /* the arena's size */
+
 #ifdef __cplusplus
 }
 #endif
