@@ -294,6 +294,12 @@ __global__ __launch_bounds__(256) void cvt_f32_kernel(const void *src, int dtype
         dst[i] = load_f32(src, dtype, i);
 }
 
+__global__ __launch_bounds__(256) void cvt_f32_scaled_kernel(const void *src, int dtype, float *dst, int64_t n,
+                                                              float scale) {
+    for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+        dst[i] = load_f32(src, dtype, i) * scale;
+}
+
 __global__ __launch_bounds__(256) void cvt_cols_kernel(const void *src, int dtype, half_t *dst, int64_t rows,
                                                         int64_t cols, int64_t ld, int64_t col0) {
     const int64_t n = rows * cols;
@@ -517,6 +523,17 @@ extern "C" int dtts_convert_f32(const void *src, int32_t dtype, float *dst, int6
     if (n == 0) return DTTS_OK;
     CVT_CHECK(name, src, dtype, dst);
     dtts::cvt_f32_kernel<<<grid_for(n, 256), 256, 0, stream>>>(src, dtype, dst, n);
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
+extern "C" int dtts_convert_f32_scaled(const void *src, int32_t dtype, float *dst, int64_t n, float scale,
+                                       hipStream_t stream) {
+    const char *name = "dtts_convert_f32_scaled";
+    DTTS_REQUIRE(n >= 0, "%s: negative size", name);
+    if (n == 0) return DTTS_OK;
+    CVT_CHECK(name, src, dtype, dst);
+    dtts::cvt_f32_scaled_kernel<<<grid_for(n, 256), 256, 0, stream>>>(src, dtype, dst, n, scale);
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

@@ -89,6 +89,11 @@ SIGNATURES = {
     "dtts_codec_model_front": [_P],
     "dtts_codec_model_wave": [_P],
     "dtts_codec_model_bytes": [_P],
+    "dtts_convert_f32_scaled": [_P, _I32, _P, _I64, _F32, _P],
+    "dtts_stack_model_load": [_P, ctypes.c_char_p, _P, _P, _P],
+    "dtts_stack_model_destroy": [_P],
+    "dtts_stack_model_stack": [_P],
+    "dtts_stack_model_bytes": [_P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
@@ -117,7 +122,8 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_codec_document_workspace_bytes": ctypes.c_size_t, "dtts_checkpoint_close": None,
              "dtts_checkpoint_count": ctypes.c_int64, "dtts_codec_model_destroy": None,
              "dtts_codec_model_front": ctypes.c_void_p, "dtts_codec_model_wave": ctypes.c_void_p,
-             "dtts_codec_model_bytes": ctypes.c_size_t}
+             "dtts_codec_model_bytes": ctypes.c_size_t, "dtts_stack_model_destroy": None,
+             "dtts_stack_model_stack": ctypes.c_void_p, "dtts_stack_model_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

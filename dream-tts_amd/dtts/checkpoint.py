@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import torch
 
-from . import codec, codec_front
+from . import codec, codec_front, stack
 from ._lib import call, lib, stream_handle
 
 DT_F32, DT_F16, DT_BF16, DT_F64, DT_I64, DT_I32, DT_I16, DT_I8, DT_U8, DT_BOOL, DT_OTHER = range(11)
@@ -141,6 +141,39 @@ class CodecModel:
     def decode(self, codes, chunk=codec_front.CHUNK_FRAMES, context=codec_front.CHUNK_LEFT_CONTEXT):
         """Codec::decode: codes [n, n_books] -> f32 audio on the device."""
         return codec_front.decode_document(self.front, self.wave, codes, chunk, context)
+
+
+class StackModel:
+    """Stack::load: a decoder stack's weights converted from a checkpoint into one device arena;
+    `.stack` decodes like a dtts.stack.Stack."""
+
+    def __init__(self, ck: Checkpoint, prefix: str, geo: stack.Geometry, dev):
+        self._g = stack.c_geometry(geo)
+        h = ctypes.c_void_p()
+        args = (ck.handle, prefix.encode(), ctypes.byref(self._g))
+        if dev is None:
+            call("dtts_stack_model_load", *args, ctypes.c_void_p(), ctypes.byref(h))
+        else:
+            with torch.cuda.device(dev):
+                call("dtts_stack_model_load", *args, stream_handle(dev), ctypes.byref(h))
+        self.handle, self.dev = h, dev
+        self.stack = stack.Stack.from_handle(geo, ctypes.c_void_p(lib().dtts_stack_model_stack(h)), dev, self)
+
+    @property
+    def nbytes(self):
+        return int(lib().dtts_stack_model_bytes(self.handle))
+
+    def close(self):
+        if self.handle:
+            self.stack.handle = None
+            lib().dtts_stack_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def convert(fn: str, *args, dev=None):

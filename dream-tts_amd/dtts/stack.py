@@ -190,6 +190,11 @@ def random_device_weights(geo: Geometry, dev, seed: int = 0):
     return out, u(geo.dim)
 
 
+def c_geometry(geo: Geometry) -> _Geometry:
+    return _Geometry(geo.dim, geo.layers, geo.heads, geo.n_kv, geo.head_dim, geo.ffn, geo.eps, geo.rope_base,
+                     int(geo.qk_norm), int(geo.layer_scale), geo.window, geo.capacity)
+
+
 class Stack:
     """Device weights + a dtts_stack handle (keeps every device tensor alive)."""
 
@@ -209,8 +214,7 @@ class Stack:
             self._keep.append(t)
             return t.data_ptr()
 
-        g = _Geometry(geo.dim, geo.layers, geo.heads, geo.n_kv, geo.head_dim, geo.ffn, geo.eps,
-                      geo.rope_base, int(geo.qk_norm), int(geo.layer_scale), geo.window, geo.capacity)
+        g = c_geometry(geo)
         ls = (_Layer * geo.layers)()
         for i, L in enumerate(layers):
             for name, _ in _Layer._fields_:
@@ -222,10 +226,17 @@ class Stack:
         self.handle = handle
         self._ws = None
 
+    @classmethod
+    def from_handle(cls, geo: Geometry, handle, dev, owner):
+        """A stack created elsewhere (dtts_stack_model_load); `owner` keeps it alive and destroys it."""
+        s = cls.__new__(cls)
+        s.geo, s.dev, s.handle, s._keep, s._ws, s._owner = geo, dev, handle, [], None, owner
+        return s
+
     def close(self):
-        if self.handle:
+        if self.handle and getattr(self, "_owner", None) is None:
             lib().dtts_stack_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:

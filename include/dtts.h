@@ -657,6 +657,8 @@ int dtts_checkpoint_get(const dtts_checkpoint *ck, const char *name, dtts_tensor
 /* to_dtype (f16 / f32), n elements. */
 int dtts_convert_f16(const void *src, int32_t dtype, dtts_f16 *dst, int64_t n, hipStream_t stream);
 int dtts_convert_f32(const void *src, int32_t dtype, float *dst, int64_t n, hipStream_t stream);
+/* f32 times a scale, one rounding: Layer::load's q_norm * 1/sqrt(head_dim) (qwen3.rs:78-84). */
+int dtts_convert_f32_scaled(const void *src, int32_t dtype, float *dst, int64_t n, float scale, hipStream_t stream);
 /* A [rows, cols] source into columns [col0, col0 + cols) of a [rows, ld] f16 destination: how
  * tensors are concatenated along the last dimension (the codec's two RVQ output projections). */
 int dtts_convert_f16_cols(const void *src, int32_t dtype, dtts_f16 *dst, int64_t rows, int64_t cols, int64_t ld,
@@ -699,6 +701,20 @@ void dtts_codec_model_destroy(dtts_codec_model *model);
 const dtts_codec_front *dtts_codec_model_front(const dtts_codec_model *model);
 const dtts_codec *dtts_codec_model_wave(const dtts_codec_model *model);
 size_t dtts_codec_model_bytes(const dtts_codec_model *model); /* the arena's size */
+
+/* Stack::load (crates/qwen3tts/src/qwen3.rs:61-119, 226-250) from a checkpoint: "<prefix>layers.<i>."
+ * input_layernorm / post_attention_layernorm, self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj,
+ * with QK-norm self_attn.{q,k}_norm (q's folded with 1/sqrt(head_dim)), with LayerScale
+ * self_attn_layer_scale.scale / mlp_layer_scale.scale, and "<prefix>norm.weight"; prefix e.g.
+ * "talker.model." (talker.rs:597) or "talker.code_predictor.model." (talker.rs:292). Checked,
+ * then converted into one arena (projections f16 [out, in], q|k|v and gate|up rows joined) on
+ * which the stack is created. The call synchronises `stream`. */
+typedef struct dtts_stack_model dtts_stack_model;
+int dtts_stack_model_load(const dtts_checkpoint *ck, const char *prefix, const dtts_stack_geometry *geo,
+                          hipStream_t stream, dtts_stack_model **out);
+void dtts_stack_model_destroy(dtts_stack_model *model);
+dtts_stack *dtts_stack_model_stack(const dtts_stack_model *model);
+size_t dtts_stack_model_bytes(const dtts_stack_model *model);
 
 #ifdef __cplusplus
 }

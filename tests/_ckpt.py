@@ -157,3 +157,25 @@ def write(path, tensors, dtype="F32"):
 
 
 TINY_CKPT_FRONT = replace(TINY, max_frames=64)
+
+
+def stack_tensors(geo, layers, final_norm, prefix):
+    """A decoder stack's checkpoint-layout weights (stack.random_weights' form) under Layer::load's
+    names (crates/qwen3tts/src/qwen3.rs:61-119) and Stack::load's final norm."""
+    T = {}
+    for i, L in enumerate(layers):
+        p = f"{prefix}layers.{i}."
+        T[p + "input_layernorm.weight"] = L["attn_norm"]
+        T[p + "post_attention_layernorm.weight"] = L["ffn_norm"]
+        for n, k in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo")):
+            T[p + f"self_attn.{n}_proj.weight"] = L[k]
+        for n in ("gate", "up", "down"):
+            T[p + f"mlp.{n}_proj.weight"] = L[n]
+        if geo.qk_norm:
+            T[p + "self_attn.q_norm.weight"] = L["q_norm"]
+            T[p + "self_attn.k_norm.weight"] = L["k_norm"]
+        if geo.layer_scale:
+            T[p + "self_attn_layer_scale.scale"] = L["attn_scale"]
+            T[p + "mlp_layer_scale.scale"] = L["mlp_scale"]
+    T[prefix + "norm.weight"] = final_norm
+    return T

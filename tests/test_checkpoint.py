@@ -134,3 +134,20 @@ def test_model_loader_refuses_missing_and_misshapen_tensors(tmp_path):
         with pytest.raises(DttsError, match="latent"):
             checkpoint.CodecModel(ck, _ckpt.TINY_CKPT_FRONT, bad, None)
     assert isinstance(codec_front.CODEC, codec_front.Geometry)
+
+
+def test_stack_loader_refuses_missing_qk_norm(tmp_path):
+    import _ckpt
+    from _stack_ref import SMALL
+    from dtts import stack
+
+    layers, fn = stack.random_weights(SMALL, 5)
+    T = _ckpt.stack_tensors(SMALL, layers, fn, "talker.model.")
+    del T["talker.model.layers.1.self_attn.k_norm.weight"]
+    p = tmp_path / "s.safetensors"
+    _ckpt.write(p, T)
+    with checkpoint.Checkpoint(p) as ck:
+        with pytest.raises(DttsError, match=r"missing tensor talker\.model\.layers\.1\.self_attn\.k_norm\.weight"):
+            checkpoint.StackModel(ck, "talker.model.", SMALL, None)
+        with pytest.raises(DttsError, match=r"missing tensor talker\.code_predictor\.model\.layers\.0"):
+            checkpoint.StackModel(ck, "talker.code_predictor.model.", SMALL, None)

@@ -151,3 +151,30 @@ def test_f64_source_rounds_through_f32(dev):
     torch.cuda.synchronize()
     want = np.float32([0.745849579666197, -0.745849579666197]).astype(np.float16)
     assert np.array_equal(out.cpu().numpy(), want) and want[0] != np.float16(0.745849579666197)
+
+
+@pytest.mark.parametrize("which", ["SMALL", "WINDOWED"])
+def test_stack_model_load_decodes_like_host_upload(dev, tmp_path, which):
+    """Stack::load from a checkpoint (QK-norm with D = 128; LayerScale with a window at D = 64)
+    steps bit for bit like the same weights uploaded by the host path, over two steps."""
+    import _stack_ref
+    from dtts import stack
+
+    geo = getattr(_stack_ref, which)
+    layers, fn = stack.random_weights(geo, 12)
+    prefix = "talker.model." if geo.qk_norm else "decoder.pre_transformer."
+    path = tmp_path / "stack.safetensors"
+    _ckpt.write(path, _ckpt.stack_tensors(geo, layers, fn, prefix))
+    with checkpoint.Checkpoint(path) as ck:
+        model = checkpoint.StackModel(ck, prefix, geo, dev)
+    host = stack.Stack(geo, layers, fn, dev)
+    lanes, cap = 3, geo.capacity
+    sa, sb = model.stack.new_state(lanes, cap), host.new_state(lanes, cap)
+    pos = np.array([0, 7, cap - 3], np.int32)
+    for s in range(2):
+        x = torch.from_numpy(synth.normal(12 + s, "ck.x", (lanes, geo.dim))).to(dev)
+        a = model.stack.decode(x, sa, pos + s).cpu().numpy()
+        b = host.decode(x, sb, pos + s).cpu().numpy()
+        assert np.array_equal(a, b) and np.isfinite(a).all()
+    assert model.nbytes > 0
+    model.close()
