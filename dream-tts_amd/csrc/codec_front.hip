@@ -119,6 +119,106 @@ __global__ __launch_bounds__(256) void depthwise_ln_kernel(const half_t *x, cons
     }
 }
 
+// The same op with the taps fixed at compile time, a workgroup per strip of P positions of one
+// lane: thread g owns channels [8g, 8g + 8) for the whole strip (taps, bias and LayerNorm
+// parameters loaded once into registers), loads the strip's P + K - 1 input rows once (16 bytes
+// per thread per row, a row coalesced across the workgroup), computes the P depthwise outputs in
+// registers and reduces the P row sums, then the P centred sums of squares, across the workgroup
+// in two LDS rounds (one barrier each). Threads = C/8 rounded up to a wave (C <= 2048).
+template <int K, int P>
+__global__ __launch_bounds__(256) void depthwise_ln_strip_kernel(const half_t *x, const float *taps, const float *bias,
+                                                                 const float *ln_w, const float *ln_b, half_t *y,
+                                                                 int len, int C, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float red[4][P];
+    const int g = threadIdx.x, wave = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    const bool on = g < C / 8;
+    const int l0 = blockIdx.x * P;
+    const half_t *xl = x + static_cast<int64_t>(blockIdx.y) * len * C + g * 8;
+    half_t *yl = y + static_cast<int64_t>(blockIdx.y) * len * C + g * 8;
+    float h[P][8];
+    if (on) {
+        float w[K][8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int t = 0; t < K; ++t) w[t][q] = taps[(g * 8 + q) * K + t];
+        half8_t win[P + K - 1];
+#pragma unroll
+        for (int r = 0; r < P + K - 1; ++r) {
+            const int src = l0 - (K - 1) + r;
+            win[r] = (src >= 0 && src < len) ? *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(src) * C)
+                                             : half8_t{};
+        }
+        const float4_t b0 = *reinterpret_cast<const float4_t *>(bias + g * 8);
+        const float4_t b1 = *reinterpret_cast<const float4_t *>(bias + g * 8 + 4);
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                float acc = static_cast<float>(win[p][q]) * w[0][q];
+#pragma unroll
+                for (int t = 1; t < K; ++t) acc = acc + static_cast<float>(win[p + t][q]) * w[t][q];
+                h[p][q] = acc + (q < 4 ? b0[q] : b1[q - 4]);
+            }
+    } else {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) h[p][q] = 0.0f;
+    }
+    // mean per position
+    float mean[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s += h[p][q];
+        s = wave_sum64(s);
+        if ((threadIdx.x & 63) == 0) red[wave][p] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float s = red[0][p];
+        for (int i = 1; i < nw; ++i) s += red[i][p];
+        mean[p] = s / static_cast<float>(C);
+    }
+    __syncthreads();  // red is reused
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float v2 = 0.0f;
+        if (on) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                h[p][q] = h[p][q] - mean[p];
+                v2 += h[p][q] * h[p][q];
+            }
+        }
+        v2 = wave_sum64(v2);
+        if ((threadIdx.x & 63) == 0) red[wave][p] = v2;
+    }
+    __syncthreads();
+    if (!on) return;
+    const float4_t w0 = *reinterpret_cast<const float4_t *>(ln_w + g * 8);
+    const float4_t w1 = *reinterpret_cast<const float4_t *>(ln_w + g * 8 + 4);
+    const float4_t c0 = *reinterpret_cast<const float4_t *>(ln_b + g * 8);
+    const float4_t c1 = *reinterpret_cast<const float4_t *>(ln_b + g * 8 + 4);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        if (l0 + p >= len) break;
+        float v2 = red[0][p];
+        for (int i = 1; i < nw; ++i) v2 += red[i][p];
+        const float den = sqrtf(v2 / static_cast<float>(C) + eps);
+        half8_t o;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            o[q] = static_cast<half_t>((h[p][q] / den) * (q < 4 ? w0[q] : w1[q - 4]) + (q < 4 ? c0[q] : c1[q - 4]));
+        *reinterpret_cast<half8_t *>(yl + static_cast<int64_t>(l0 + p) * C) = o;
+    }
+}
+
 // One wave per row: x f16 [rows, C] -> y f16, y = (x / sqrt(mean(x^2) + eps)) * gamma in f32.
 __global__ __launch_bounds__(256) void rms_rows_kernel(const half_t *x, const float *gamma, half_t *y, int64_t rows,
                                                        int C, float eps) {
@@ -355,6 +455,16 @@ extern "C" int dtts_depthwise_layernorm_nlc_f16(const dtts_f16 *x, const float *
     const half_t *xh = reinterpret_cast<const half_t *>(x);
     half_t *yh = reinterpret_cast<half_t *>(y);
     const int L = static_cast<int>(len), C = static_cast<int>(channels), K = static_cast<int>(k);
+    if (K == 7 && lanes < 65536 && dtts::aligned(taps, 16) && dtts::aligned(bias, 16) && dtts::aligned(ln_weight, 16) &&
+        dtts::aligned(ln_bias, 16)) {
+        constexpr int P = 8;
+        const dim3 sgrid(static_cast<unsigned>((len + P - 1) / P), static_cast<unsigned>(lanes));
+        const int threads = (C / 8 + 63) / 64 * 64;
+        dtts::depthwise_ln_strip_kernel<7, P><<<sgrid, threads, 0, stream>>>(xh, taps, bias, ln_weight, ln_bias, yh, L, C,
+                                                                            eps);
+        DTTS_LAUNCH_CHECK(name);
+        return DTTS_OK;
+    }
     if (ng <= 1)
         dtts::depthwise_ln_kernel<1><<<grid, 256, 0, stream>>>(xh, taps, bias, ln_weight, ln_bias, yh, rows, L, C, K, eps);
     else if (ng <= 2)
