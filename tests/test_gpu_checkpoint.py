@@ -178,3 +178,30 @@ def test_stack_model_load_decodes_like_host_upload(dev, tmp_path, which):
         assert np.array_equal(a, b) and np.isfinite(a).all()
     assert model.nbytes > 0
     model.close()
+
+
+def test_codec_model_load_full_geometry(dev, tmp_path):
+    """The Qwen3-TTS codec's own geometry end to end: a 457 MB f32 checkpoint in the reference's
+    naming (16 books of 2048 x 256, the 8-layer windowed transformer at 512, two ConvNeXt stages at
+    1024, the 1536 -> 96 waveform stack, clamped output) loaded by dtts_codec_model_load, then a
+    two-window document (40 frames, chunk 30, context 5) decoded bit for bit like the host-upload
+    models."""
+    import time
+    from dataclasses import replace
+
+    wave_geo = replace(codec.CONFIG5, out_clamp=True)
+    T, fw, ww = _ckpt.build(codec_front.CODEC, wave_geo, seed=4)
+    path = tmp_path / "full.safetensors"
+    _ckpt.write(path, T)
+    del T
+    t0 = time.perf_counter()
+    with checkpoint.Checkpoint(path) as ck:
+        model = checkpoint.CodecModel(ck, codec_front.CODEC, wave_geo, dev)
+    print(f"load: {time.perf_counter() - t0:.2f} s, arena {model.nbytes / 1e6:.1f} MB")
+    doc = synth.randint(4, "ck.fulldoc", (40, codec_front.CODEC.n_books), 0, codec_front.CODEC.book_size - 1)
+    a = model.decode(doc, chunk=30, context=5).cpu().numpy()
+    front, wave = codec_front.CodecFront(codec_front.CODEC, fw, dev), codec.Codec(wave_geo, ww, dev)
+    b = codec_front.decode_document(front, wave, doc, 30, 5).cpu().numpy()
+    assert a.shape == (40 * 1920,) and np.array_equal(a, b)
+    assert np.isfinite(a).all() and np.max(np.abs(a)) <= 1.0
+    model.close()
