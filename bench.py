@@ -58,18 +58,22 @@ def cpu_baseline(geo, weights, latent_np, budget_s=12.0, max_lanes=48):
     frames = latent_np.shape[1]
     ocodec.decode_f32_reference(geo, prep, latent_np[0, : max(2, frames // 50)])  # warm-up, untimed
     t0 = time.perf_counter()
-    done = 0
-    while done < max_lanes:
-        ocodec.decode_f32_reference(geo, prep, latent_np[done])
-        done += 1
+    lane_s = []
+    while len(lane_s) < max_lanes:
+        t1 = time.perf_counter()
+        ocodec.decode_f32_reference(geo, prep, latent_np[len(lane_s)])
+        lane_s.append(time.perf_counter() - t1)
         if time.perf_counter() - t0 >= budget_s:
             break
     wall = time.perf_counter() - t0
+    done = len(lane_s)
     audio_s = done * frames * geo.hop / SAMPLE_RATE
+    med = sorted(lane_s)[done // 2]
     return dict(value=round(audio_s / wall, 3), unit="audio-s/s", cores=threads, kind="port",
                 sample=f"{done} lane(s) x {frames} frames of the same workload through the oracle's "
                        f"f32 restatement of the reference CPU route (SnakeBeta passes; pad+cat+GEMM+bias "
-                       f"per conv; polyphase transposed convs), {wall:.1f} s on {threads} threads")
+                       f"per conv; polyphase transposed convs), {wall:.1f} s on {threads} threads; per lane "
+                       f"median {med:.2f} s, range {min(lane_s):.2f}-{max(lane_s):.2f} s")
 
 
 # ---------------------------------------------------------------- configs 1-4 (per-op lines)
