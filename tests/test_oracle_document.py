@@ -65,3 +65,20 @@ def test_kept_audio_equals_unpadded_causal_forward(n, chunk, context):
         plain = _forward(hw, prep, codes[frm:start + keep])
         assert np.array_equal(got[start * spf:(start + keep) * spf], plain[drop * spf:])
     assert 0.01 < np.std(got) < 0.99 and np.max(np.abs(got)) <= 1.0
+
+
+def test_reference_fixture_shapes():
+    """The reference's codec fixture manifest (fixtures/qwen3tts/oracle.json: codes [147, 16] ->
+    quantized [1, 512, 147] -> pre_tf [1, 147, 1024] -> wav [1, 1, 282240]; the long case
+    [400, 16] -> [1, 1, 768000], chunked and not) restated as this build's geometry: 16 books, the
+    512-wide quantizer sum, the 1024-wide latent, 1920 samples per frame, and Codec::decode's
+    windows covering both documents exactly once."""
+    from dtts import codec
+
+    g, w = codec_front.CODEC, codec.CONFIG5
+    assert g.n_books == 16 and g.codebook_dim == 512 and g.latent_dim == 1024
+    assert g.upsample * w.hop == 1920
+    for n, samples in ((147, 282240), (400, 768000)):
+        wins = ofront.document_windows(n, codec_front.CHUNK_FRAMES, codec_front.CHUNK_LEFT_CONTEXT)
+        assert sum(k for *_, k in wins) * g.upsample * w.hop == samples
+    assert ofront.document_windows(400, 300, 25) == [(0, 325, 325, 0, 300), (275, 400, 325, 25, 100)]
