@@ -102,7 +102,7 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
-constexpr int kChunk = 256;  // positions per workgroup when a span is split
+constexpr int kChunk = 512;  // positions per workgroup when a span is split
 
 // Chunks of a lane's window [lo, hi) when split.
 __device__ __host__ inline int chunks_of(int lo, int hi) { return (hi - lo + kChunk - 1) / kChunk; }

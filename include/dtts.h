@@ -266,7 +266,7 @@ int dtts_kv_append_f16(const dtts_f16 *k, const dtts_f16 *v, const int32_t *pos,
  * dtts_decode_attention_workspace_bytes(b, n_kv, gqa, D, max_b(span - window_start)) bytes, long
  * spans are split over several workgroups and merged by a second launch (the reference has no
  * such argument: its op allocates; a shim passes a cached buffer). Bytes needed are 0 when no
- * window exceeds 256 positions. */
+ * window exceeds 512 positions. */
 size_t dtts_decode_attention_workspace_bytes(int64_t b, int64_t n_kv, int64_t gqa,
                                              int64_t head_dim, int64_t max_window);
 int dtts_decode_attention_f16(const float *q, const dtts_f16 *kcache, const dtts_f16 *vcache,

@@ -77,14 +77,15 @@ def test_decode_attention_config2_geometry(dev):
 
 
 def test_decode_attention_split_and_single_pass_agree(dev):
-    """Windows past 256 positions split over workgroups when a workspace is given (merged by a
-    second launch); without room for every chunk's state, one workgroup takes the whole span."""
+    """Windows past 512 positions split over workgroups when a workspace is given (merged by a
+    second launch); without room for every chunk's state, one workgroup takes the whole span.
+    Windows of 1500 (three chunks), 513 (a last chunk of one position), 700, 556 and 1."""
     b, n_kv, gqa, cap = 5, 4, 2, 1500
     q, k, v = _inputs(74, b, n_kv, gqa, cap)
-    span = np.array([1500, 257, 1000, 300, 1], np.int32)
-    ws = np.array([0, 0, 700, 44, 0], np.int32)
+    span = np.array([1500, 513, 1000, 600, 1], np.int32)
+    ws = np.array([0, 0, 300, 44, 0], np.int32)
     need = ops.decode_attention_workspace_bytes(b, n_kv, gqa, 128, int(np.max(span - ws)))
-    assert need == b * n_kv * 6 * gqa * 130 * 4  # six chunks of 256 for the 1500-position window
+    assert need == b * n_kv * 3 * gqa * 130 * 4  # three chunks of 512 for the 1500-position window
     want = oracle.decode_attention_f32(q, k, v, span, ws)
     split = _run(dev, q, k, v, span, ws)
     single = _run(dev, q, k, v, span, ws, workspace=torch.empty(need - 16, dtype=torch.uint8, device=dev))

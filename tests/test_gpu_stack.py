@@ -90,7 +90,7 @@ def test_stack_windowed_layer_scale_no_qk_norm(dev):
 
 
 def test_stack_long_cache_splits_attention(dev):
-    """cap 700: windows past 256 positions run as chunks merged by a second launch."""
+    """cap 700: windows past 512 positions run as chunks merged by a second launch."""
     geo = replace(SMALL, capacity=700)
     p = Pair(dev, geo, 93, 4, 700)
     p.step(np.array([699, 256, 0, 513], np.int32))
