@@ -5,10 +5,11 @@
 //
 // xs is x or SnakeBeta(x) (full-precision sinf; f32 outputs are held to 1e-5). GEMM view per
 // lane: M = output channels, N = positions, K = (tap, channel). A workgroup owns 64 channels x
-// 128 positions; per 16-channel chunk it stages the dilated window of x (16 rows x
-// 128 + (k-1)*dil positions) and the 64 x k x 16 weight slice in LDS, then four waves (2 x 2)
-// run v_mfma_f32_32x32x2_f32, each tap reading the window at offset t*dil. The epilogue writes
-// straight from the accumulators: the 32 lanes of a C column are 32 consecutive positions.
+// 64 positions; per 16-channel chunk it stages the dilated window of x (16 rows x
+// 64 + (k-1)*dil positions) and the 64 x k x 16 weight slice in LDS (two buffers, the next
+// chunk prefetched through registers), then four waves (2 x 2) run v_mfma_f32_32x32x2_f32, each
+// tap reading the window at offset t*dil. The epilogue writes straight from the accumulators:
+// the 32 lanes of a C column are 32 consecutive positions.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -23,14 +24,21 @@ struct NclParams {
     int tiles_m, tiles_n, total, per_xcd;
 };
 
-constexpr int kBM = 64, kBN = 128, kKC = 16;
+constexpr int kBM = 64, kBN = 64, kKC = 16;
 
+// One workgroup = 64 output channels x 64 positions of one lane; four waves (2 x 2), each one
+// 32 x 32 accumulator block. Per 16-channel chunk the window (16 rows x 64 + (k-1)*dil
+// positions, SnakeBeta applied as it is staged) and the 64 x k x 16 weight slice sit in one of
+// two LDS buffers: chunk c+1 is stored from registers into the other buffer while chunk c+2 is
+// loaded into registers and chunk c is multiplied, one barrier per chunk.
 template <int KMAX, int HMAX, bool SNAKE>
 __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
-    constexpr int XW = kBN + HMAX;           // window positions per channel row
-    constexpr int WP = KMAX * kKC + 1;       // weight row pitch (floats); +1 spreads the banks
-    __shared__ float xs[kKC * XW];
-    __shared__ float ws[kBM * WP];
+    constexpr int XW = kBN + HMAX;                           // window positions per channel row
+    constexpr int WP = KMAX * kKC + 1;                       // weight row pitch (floats); +1 spreads the banks
+    constexpr int XN = (kKC * XW + 255) / 256;               // window elements per thread
+    constexpr int WN = (kBM * KMAX * kKC / 4 + 255) / 256;   // weight float4s per thread
+    __shared__ float xs[2][kKC * XW];
+    __shared__ float ws[2][kBM * WP];
     const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (tile >= p.total) return;
     const int m_tile = tile % p.tiles_m;  // output channels fastest: neighbours share the window
@@ -45,61 +53,96 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int kh = lane >> 5, lr = lane & 31;
+    const int nx = kKC * rows, nw = kBM * p.k * kKC / 4;
 
-    float16_t acc[2] = {float16_t{}, float16_t{}};
-    for (int c0 = 0; c0 < p.cin; c0 += kKC) {
-        for (int e = tid; e < kKC * rows; e += 256) {
-            const int ci = e / rows;
-            const int j = e - ci * rows;
+    float xr[XN];
+    float4_t wr[WN];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            const int e = tid + i * 256;
+            const int ci = e / rows, j = e - (e / rows) * rows;
             const int s = l0 - p.pad_left + j;
             float v = 0.0f;
-            if (s >= 0 && s < p.L) {
-                v = xl[static_cast<int64_t>(c0 + ci) * p.L + s];
-                if constexpr (SNAKE) v = snake_f32(v, p.a_in[c0 + ci], p.r_in[c0 + ci]);
-            }
-            xs[ci * XW + j] = v;
+            if (e < nx && s >= 0 && s < p.L) v = xl[static_cast<int64_t>(c0 + ci) * p.L + s];
+            xr[i] = v;
         }
-        for (int e = tid; e < kBM * p.k * kKC; e += 256) {
-            const int m = e / (p.k * kKC);
-            const int q = e - m * (p.k * kKC);
-            const int t = q / kKC;
-            const int ci = q - t * kKC;
-            ws[m * WP + t * kKC + ci] = p.w[static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 + ci];
-        }
-        __syncthreads();
-        for (int t = 0; t < p.k; ++t) {
-            const float *wa = ws + (wm * 32 + lr) * WP + t * kKC + kh;
-            const float *xb = xs + kh * XW + wn * 64 + lr + t * p.dil;
+        // weights: 16 consecutive input channels of one (output channel, tap) are 4 float4s
 #pragma unroll
-            for (int ci = 0; ci < kKC; ci += 2) {
-                const float a = wa[ci];
-                const float b0 = xb[ci * XW];
-                const float b1 = xb[ci * XW + 32];
-                acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b0, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b1, acc[1], 0, 0, 0);
+        for (int i = 0; i < WN; ++i) {
+            const int e = tid + i * 256;
+            const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
+            const int t = q >> 2, c4 = q & 3;
+            wr[i] = e < nw ? *reinterpret_cast<const float4_t *>(p.w + static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 +
+                                                               c4 * 4)
+                           : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    auto store = [&](int c0, int b) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            const int e = tid + i * 256;
+            if (e < nx) {
+                const int ci = e / rows, j = e - (e / rows) * rows;
+                const int s = l0 - p.pad_left + j;
+                float v = xr[i];
+                if constexpr (SNAKE)
+                    if (s >= 0 && s < p.L) v = snake_f32(v, p.a_in[c0 + ci], p.r_in[c0 + ci]);
+                xs[b][ci * XW + j] = v;
             }
+        }
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int e = tid + i * 256;
+            if (e < nw) {
+                const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
+                float *dst = &ws[b][m * WP + q * 4];  // rows are WP floats apart (odd): scalar stores
+                dst[0] = wr[i][0];
+                dst[1] = wr[i][1];
+                dst[2] = wr[i][2];
+                dst[3] = wr[i][3];
+            }
+        }
+    };
+
+    float16_t acc = float16_t{};
+    const int nchunks = p.cin / kKC;
+    load(0);
+    store(0, 0);
+    if (nchunks > 1) load(kKC);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int b = c & 1;
+        if (c + 1 < nchunks) {
+            store((c + 1) * kKC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
+            if (c + 2 < nchunks) load((c + 2) * kKC);
+        }
+        for (int t = 0; t < p.k; ++t) {
+            const float *wa = ws[b] + (wm * 32 + lr) * WP + t * kKC + kh;
+            const float *xb = xs[b] + kh * XW + wn * 32 + lr + t * p.dil;
+#pragma unroll
+            for (int ci = 0; ci < kKC; ci += 2)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[ci], xb[ci * XW], acc, 0, 0, 0);
         }
         __syncthreads();
     }
     const int64_t ybase = static_cast<int64_t>(lane_idx) * p.cout * p.L;
+    const int pos = l0 + wn * 32 + lr;
+    if (pos >= p.L) return;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int pos = l0 + wn * 64 + j * 32 + lr;
-        if (pos >= p.L) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
-            const int64_t off = ybase + static_cast<int64_t>(co) * p.L + pos;
-            float v = acc[j][r];
-            if (p.bias) v += p.bias[co];
-            if (p.res) v += p.res[off];
-            if (p.act == 1) v = tanhf(v);
-            if (p.y_pre) p.y_pre[off] = v;
-            if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
-            p.y[off] = v;
-        }
+    for (int r = 0; r < 16; ++r) {
+        const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+        const int64_t off = ybase + static_cast<int64_t>(co) * p.L + pos;
+        float v = acc[r];
+        if (p.bias) v += p.bias[co];
+        if (p.res) v += p.res[off];
+        if (p.act == 1) v = tanhf(v);
+        if (p.y_pre) p.y_pre[off] = v;
+        if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
+        p.y[off] = v;
     }
 }
+
 
 __global__ __launch_bounds__(256) void conv_ncl_f32_direct(NclParams p, int64_t total) {
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
@@ -195,7 +238,7 @@ extern "C" int dtts_conv1d_ncl_f32_ex(const dtts_conv_desc *d, hipStream_t strea
     p.act = d->act;
     const int64_t halo = (d->k - 1) * d->dilation;
     hipError_t e;
-    if (d->cin % dtts::kKC == 0 && d->cout % dtts::kBM == 0 && d->k <= 7 && halo <= 64) {
+    if (d->cin % dtts::kKC == 0 && d->cout % dtts::kBM == 0 && d->k <= 7 && halo <= 64 && dtts::aligned(d->w, 16)) {
         DTTS_REQUIRE(d->lanes * (d->cout / dtts::kBM) * ((d->len + dtts::kBN - 1) / dtts::kBN) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
         if (d->k == 1)
