@@ -264,14 +264,23 @@ def workload_cfg4(dev, args):
         blocks = torch.from_numpy(ops.q8_0_quantize(w)).to(dev)
         copies = max(1, int(300e6 // blocks.numel()))  # rotate > the 256 MB MALL
         sets = [blocks.clone() for _ in range(copies)]
+        packed = [ops.q8_0_repack(b, k) for b in sets[:copies]]
         for m in (1, 8, 48):
             x = torch.from_numpy(synth.f16_bits(synth.normal(0, f"cfg4.x{m}", (m, k))).view(np.int16)).view(torch.float16).to(dev)
+            ws = torch.empty(max(ops.q8_0_workspace_bytes(m, k, n), 16), dtype=torch.uint8, device=dev)
             for mode in ("w8a16", "w8a8"):
-                t = _graph_time(lambda: [ops.q8_0_matmul(x, b, mode) for b in sets], reps=5) / copies
-                wb = 34.0 * n * k / 32
-                res[f"k{k}_n{n}_m{m}_{mode}"] = {"us": t * 1e3, "gbs": (wb + 2.0 * m * k + 4.0 * m * n) / t / 1e6,
-                                                 "tops": 2.0 * m * n * k / t / 1e9}
-        del sets
+                # the workspace-free kernel, the A-sharing one with k ranges (dtts_gemm_q8_0_ws) and
+                # the same on the load-time repacked layout (dtts_gemm_q8_0_packed)
+                variants = (("", lambda: [ops.q8_0_matmul(x, b, mode) for b in sets]),
+                            ("_ws", lambda: [ops.q8_0_matmul(x, b, mode, workspace=ws) for b in sets]),
+                            ("_packed", lambda: [ops.q8_0_matmul_packed(x, pb, n, mode, workspace=ws) for pb in packed]))
+                for tag, fn in variants:
+                    t = _graph_time(fn, reps=5) / copies
+                    wb = 34.0 * n * k / 32
+                    res[f"k{k}_n{n}_m{m}_{mode}{tag}"] = {"us": t * 1e3,
+                                                          "gbs": (wb + 2.0 * m * k + 4.0 * m * n) / t / 1e6,
+                                                          "tops": 2.0 * m * n * k / t / 1e9}
+        del sets, packed
     best = max(r["gbs"] for r in res.values())
     return _line("config4: Q8_0 projections (GGML blocks), weights rotated past the MALL, graph-replayed",
                  "best weight-streaming GB/s", best, "GB/s", res, {"dtype": "int8/f16"})

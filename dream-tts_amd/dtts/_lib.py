@@ -94,6 +94,11 @@ SIGNATURES = {
     "dtts_stack_model_destroy": [_P],
     "dtts_stack_model_stack": [_P],
     "dtts_stack_model_bytes": [_P],
+    "dtts_gemm_q8_0_workspace_bytes": [_I64, _I64, _I64],
+    "dtts_gemm_q8_0_ws": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
+    "dtts_q8_0_packed_bytes": [_I64, _I64],
+    "dtts_q8_0_repack": [_P, _P, _I64, _I64, _P],
+    "dtts_gemm_q8_0_packed": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
@@ -123,7 +128,8 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_checkpoint_count": ctypes.c_int64, "dtts_codec_model_destroy": None,
              "dtts_codec_model_front": ctypes.c_void_p, "dtts_codec_model_wave": ctypes.c_void_p,
              "dtts_codec_model_bytes": ctypes.c_size_t, "dtts_stack_model_destroy": None,
-             "dtts_stack_model_stack": ctypes.c_void_p, "dtts_stack_model_bytes": ctypes.c_size_t}
+             "dtts_stack_model_stack": ctypes.c_void_p, "dtts_stack_model_bytes": ctypes.c_size_t,
+             "dtts_gemm_q8_0_workspace_bytes": ctypes.c_size_t, "dtts_q8_0_packed_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

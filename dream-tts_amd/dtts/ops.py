@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import DttsError, call, ptr, stream_handle
+from ._lib import DttsError, call, lib, ptr, stream_handle
 
 _F16 = torch.float16
 _F32 = torch.float32
@@ -281,15 +281,48 @@ def q8_0_dequantize(blocks, k):
     return w
 
 
-def q8_0_matmul(x, blocks, mode="w8a16"):
-    """QMatMul::forward on a Q8_0 weight [n, k]: x [m, k] f16 -> y [m, n] f32."""
+def q8_0_workspace_bytes(m, k, n):
+    return int(lib().dtts_gemm_q8_0_workspace_bytes(m, k, n))
+
+
+def q8_0_repack(blocks, k):
+    """GGML blocks (device uint8 [n, k/32, 34]) -> the packed layout (dtts_q8_0_repack)."""
+    n = blocks.shape[0]
+    out = torch.empty(int(lib().dtts_q8_0_packed_bytes(n, k)), dtype=torch.uint8, device=blocks.device)
+    call("dtts_q8_0_repack", ptr(blocks), ptr(out), n, k, stream_handle())
+    return out
+
+
+def q8_0_matmul_packed(x, packed, n, mode="w8a16", workspace=None):
+    """dtts_gemm_q8_0_packed: x [m, k] f16 times a repacked Q8_0 weight [n, k] -> y [m, n] f32."""
+    _mat(x, "q8_0_matmul_packed", "x", _F16)
+    m, k = x.shape
+    y = torch.empty((m, n), dtype=_F32, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(max(q8_0_workspace_bytes(m, k, n), 16), dtype=torch.uint8, device=x.device)
+    call("dtts_gemm_q8_0_packed", ptr(x), ptr(packed), ptr(y), m, k, n, {"w8a16": 0, "w8a8": 1}[mode], ptr(workspace),
+         workspace.numel(), stream_handle())
+    return y
+
+
+def q8_0_matmul(x, blocks, mode="w8a16", workspace=None):
+    """QMatMul::forward on a Q8_0 weight [n, k]: x [m, k] f16 -> y [m, n] f32. With a workspace
+    (a device uint8 tensor, or "auto" to allocate one) the A-sharing kernel runs
+    (dtts_gemm_q8_0_ws)."""
     _mat(x, "q8_0_matmul", "x", _F16)
     m, k = x.shape
     n = blocks.shape[0]
     if blocks.dtype != torch.uint8 or not blocks.is_cuda or blocks.numel() != n * (k // 32) * 34:
         raise DttsError("q8_0_matmul: blocks must be device uint8 [n, k/32, 34]")
     y = torch.empty((m, n), dtype=_F32, device=x.device)
-    call("dtts_gemm_q8_0", ptr(x), ptr(blocks), ptr(y), m, k, n, {"w8a16": 0, "w8a8": 1}[mode], stream_handle())
+    md = {"w8a16": 0, "w8a8": 1}[mode]
+    if workspace is None:
+        call("dtts_gemm_q8_0", ptr(x), ptr(blocks), ptr(y), m, k, n, md, stream_handle())
+        return y
+    if isinstance(workspace, str):
+        workspace = torch.empty(max(q8_0_workspace_bytes(m, k, n), 16), dtype=torch.uint8, device=x.device)
+    call("dtts_gemm_q8_0_ws", ptr(x), ptr(blocks), ptr(y), m, k, n, md, ptr(workspace), workspace.numel(),
+         stream_handle())
     return y
 
 

@@ -505,6 +505,27 @@ int dtts_q8_0_dequantize_f32(const void *blocks, float *w, int64_t rows, int64_t
 int dtts_gemm_q8_0(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k,
                    int64_t n, int32_t mode, hipStream_t stream);
 
+/* The same product (QMatMul::forward, lib.rs:531) with an optional device workspace (16-byte
+ * aligned, at least dtts_gemm_q8_0_workspace_bytes(m, k, n) bytes; 0 means none is needed): when
+ * m > 16, n % 64 == 0 and k % 256 == 0, workgroups of 64 columns share the activation slab in LDS
+ * (W8A8: quantised once per workgroup) and k is split into ranges merged in order by a second
+ * launch. Without room (or for other shapes) it is dtts_gemm_q8_0. */
+size_t dtts_gemm_q8_0_workspace_bytes(int64_t m, int64_t k, int64_t n);
+int dtts_gemm_q8_0_ws(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                      int32_t mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Load-time repack of GGML blocks [rows, k/32] into a layout the matrix cores read with 16-byte
+ * loads (same bytes, dtts_q8_0_packed_bytes of them, 16-byte aligned): per row, the quantised
+ * weights lane-group major (weights 8g .. 8g + 7 of block b at g * (k/32) * 8 + b * 8), then the
+ * k/32 f16 scales. k % 256 == 0. */
+size_t dtts_q8_0_packed_bytes(int64_t rows, int64_t k);
+int dtts_q8_0_repack(const void *blocks, void *packed, int64_t rows, int64_t k, hipStream_t stream);
+/* QMatMul::forward (lib.rs:531) on the packed layout, by the A-sharing kernel at every m (bit for
+ * bit dtts_gemm_q8_0_ws's result where that kernel runs there). n % 64 == 0, k % 256 == 0,
+ * m <= 64; the workspace (dtts_gemm_q8_0_workspace_bytes) is required when nonzero. */
+int dtts_gemm_q8_0_packed(const dtts_f16 *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
+                          int32_t mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------ codec decoder stack */
 
 /* The qwen3tts codec's waveform stack on f16 channels-last activations, all lanes at once:

@@ -104,3 +104,55 @@ def test_q8_0_matmul(dev, m, k, n):
     got16 = to_host(ops.q8_0_matmul(xd, bd, "w8a16"))
     ab, rl = rel(got16, oracle.q8_0_matmul_f64(x, blocks))
     assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
+
+
+@pytest.mark.parametrize("m,k,n", Q8_SHAPES + [(33, 512, 128)])
+def test_q8_0_matmul_workspace_path(dev, m, k, n):
+    """dtts_gemm_q8_0_ws: for m > 16, workgroups of 64 columns share the activation slab in LDS and
+    k splits into ranges merged in order -- the same bars against the oracle as the workspace-free
+    kernel, and without room for the ranges (or at m <= 16) it is that kernel bit for bit."""
+    w = synth.normal(84, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    xb = synth.f16_bits(synth.normal(84, "x", (m, k)))
+    x = synth.from_f16_bits(xb)
+    xd, bd = to_dev(xb, dev), torch.from_numpy(blocks).to(dev)
+    got8 = to_host(ops.q8_0_matmul(xd, bd, "w8a8", workspace="auto"))
+    assert rel(got8, oracle.q8_0_matmul_w8a8(x, blocks))[1] <= 1e-5
+    got16 = to_host(ops.q8_0_matmul(xd, bd, "w8a16", workspace="auto"))
+    ab, rl = rel(got16, oracle.q8_0_matmul_f64(x, blocks))
+    assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
+    tiny = torch.empty(16, dtype=torch.uint8, device=dev)
+    if ops.q8_0_workspace_bytes(m, k, n) > 16:
+        assert np.array_equal(to_host(ops.q8_0_matmul(xd, bd, "w8a16", workspace=tiny)),
+                              to_host(ops.q8_0_matmul(xd, bd, "w8a16")))
+
+
+def _repack_host(blocks, k):
+    """The packed layout restated on the host: per row, weights 8g .. 8g+7 of block b at
+    g * nb * 8 + b * 8, then the nb f16 scales."""
+    n, nb = blocks.shape[0], k // 32
+    b = blocks.reshape(n, nb, 34)
+    qs = b[:, :, 2:].reshape(n, nb, 4, 8).transpose(0, 2, 1, 3).reshape(n, k)
+    return np.concatenate([qs, b[:, :, :2].reshape(n, 2 * nb)], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("m,k,n", Q8_SHAPES + [(33, 512, 128)])
+def test_q8_0_packed_layout(dev, m, k, n):
+    """dtts_q8_0_repack writes the documented layout byte for byte; dtts_gemm_q8_0_packed on it meets
+    the oracle bars of the other Q8_0 paths and, where dtts_gemm_q8_0_ws runs the same A-sharing
+    kernel on the GGML blocks (m > 16), equals it bit for bit."""
+    w = synth.normal(85, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    bd = torch.from_numpy(blocks).to(dev)
+    packed = ops.q8_0_repack(bd, k)
+    assert np.array_equal(to_host(packed), _repack_host(blocks, k))
+    xb = synth.f16_bits(synth.normal(85, "x", (m, k)))
+    x, xd = synth.from_f16_bits(xb), to_dev(xb, dev)
+    got8 = to_host(ops.q8_0_matmul_packed(xd, packed, n, "w8a8"))
+    assert rel(got8, oracle.q8_0_matmul_w8a8(x, blocks))[1] <= 1e-5
+    got16 = to_host(ops.q8_0_matmul_packed(xd, packed, n, "w8a16"))
+    ab, rl = rel(got16, oracle.q8_0_matmul_f64(x, blocks))
+    assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
+    if m > 16:
+        for mode, got in (("w8a8", got8), ("w8a16", got16)):
+            assert np.array_equal(got, to_host(ops.q8_0_matmul(xd, bd, mode, workspace="auto"))), mode
