@@ -22,6 +22,8 @@
 //                 one barrier per chunk.
 #pragma once
 
+#include <type_traits>
+
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -485,6 +487,81 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
     __syncthreads();
     int st = 0;          // stage holding chunk c
     int st_new = S - 1;  // stage receiving chunk c + S - 1
+    if constexpr (!SNAKE_IN && KT >= 3) {
+        // The taps of all chunks as one stream: tap t+1's fragment reads go out between tap t's
+        // MFMAs, across chunk boundaries too. The barrier sits before the last tap's MFMAs, once
+        // that tap's reads are back in registers: every wave has then finished reading the chunk
+        // (its stage may be refilled) and the next chunk has landed (its first tap can be read in
+        // the shadow of this tap's MFMAs) -- instead of every wave starting each chunk with its
+        // first reads exposed behind the barrier. Measured A/B: the k=7 convs 3-5% faster; with
+        // one or two taps per chunk (k=1, the transposed convs) the chunk-end barrier is better.
+        constexpr int KS = Cfg::KC / 16;
+        half8_t fa[2][KS][Cfg::TM], fb[2][KS][Cfg::TN];
+        auto load = [&](int s, int t, half8_t (&a)[KS][Cfg::TM], half8_t (&b)[KS][Cfg::TN]) {
+            const char *A = smem + s * Cfg::STAGE_BYTES;
+            const char *B = A + Cfg::A_BYTES;
+            const int ra = arow0 + t * p.dil, rb = t * Cfg::BN + bcol0;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+#pragma unroll
+                for (int i = 0; i < Cfg::TM; ++i)
+                    a[kk][i] = *reinterpret_cast<const half8_t *>(
+                        A + (ra + i * 32) * RB + (((kk * 2 + qh) ^ seg_swizzle<Cfg::KC>(ra)) << 4));
+#pragma unroll
+                for (int j = 0; j < Cfg::TN; ++j)
+                    b[kk][j] = *reinterpret_cast<const half8_t *>(
+                        B + (rb + j * 32) * RB + (((kk * 2 + qh) ^ seg_swizzle<Cfg::KC>(rb)) << 4));
+            }
+        };
+        auto mma = [&](const half8_t (&a)[KS][Cfg::TM], const half8_t (&b)[KS][Cfg::TN]) {
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+                for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[kk][j], a[kk][i], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < KS * Cfg::TM * Cfg::TN; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        int c = 0;
+        // PAR: the fragment set of the chunk's tap 0 (tap t uses set (t + PAR) & 1); it flips
+        // from chunk to chunk when KT is odd, so chunks run in pairs with PAR fixed at compile time
+        auto chunk = [&](auto par) {
+            constexpr int PAR = decltype(par)::value;
+            if (c + S - 1 < nchunks) issue((c + S - 1) * Cfg::KC, st_new);
+            const bool more = c + 1 < nchunks;
+            const int st_next = st + 1 == S ? 0 : st + 1;
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+                const int cur = (t + PAR) & 1;
+                if (t + 1 < KT) {
+                    load(st, t + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                } else if (more) {
+                    wait_for_next(nchunks - 2 - c);
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    __syncthreads();
+                    load(st_next, 0, fa[cur ^ 1], fb[cur ^ 1]);
+                }
+                mma(fa[cur], fb[cur]);
+            }
+            st = st_next;
+            st_new = st_new + 1 == S ? 0 : st_new + 1;
+            ++c;
+        };
+        load(st, 0, fa[0], fb[0]);
+        while (c + 1 < nchunks) {
+            chunk(std::integral_constant<int, 0>{});
+            chunk(std::integral_constant<int, KT & 1>{});
+        }
+        if (c < nchunks) chunk(std::integral_constant<int, 0>{});
+        __syncthreads();
+        return;
+    }
     for (int c = 0; c < nchunks; ++c) {
         if (c + S - 1 < nchunks) issue((c + S - 1) * Cfg::KC, st_new);
         compute(st);
