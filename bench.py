@@ -322,9 +322,21 @@ def workload_stack(dev, args):
                      "tokens_per_s": round(lanes / (t_graph / 1e3), 1), "weight_bytes": wbytes, "kv_bytes": kv,
                      "gbs": round((wbytes + kv) / t_graph / 1e6, 1),
                      "us_per_layer": round(t_graph * 1e3 / geo.layers, 2)}
+        # the prefill branch: the predictor's per-frame [hidden, code0] (48 lanes x 2), the
+        # talker's prompt (8 lanes x 256 positions, as prefill_batch groups lanes)
+        pl, pt = (48, 2) if name == "predictor" else (8, 256)
+        pstate = st.new_state(pl, cap)
+        px = torch.randn((pl, pt, geo.dim), generator=gen, device=dev)
+        pout = torch.empty_like(px)
+        pws = torch.empty(st.prefill_workspace_bytes(pl, pt), dtype=torch.uint8, device=dev)
+        t_pre = _time(lambda: st.prefill(px, pstate, 0, out=pout, workspace=pws), reps=10)
+        if not torch.isfinite(pout).all():
+            raise SystemExit(f"bench: non-finite {name} prefill output")
+        res[name]["prefill"] = {"lanes": pl, "t": pt, "ms": round(t_pre, 4),
+                                "positions_per_s": round(pl * pt / (t_pre / 1e3), 1)}
         if best is None:
             best = res[name]
-        del st, state, layers
+        del st, state, layers, pstate
         torch.cuda.empty_cache()
     return _line("row f-2: decoder-stack decode step, 48 lanes at per-lane positions (talker 28 layers, cap 2048; "
                  "code predictor 5 layers), f16 weights and KV cache, one HIP graph per step",

@@ -84,8 +84,8 @@ __device__ __forceinline__ float4_t sum_parts(const float *p, int ys, int64_t st
 // row in flight at once); the sum of squares is reduced over the wave, then over the four waves
 // through LDS.
 template <typename TO, int NV>
-__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const float *scale, float *h,
-                                                  const float *gamma, TO *y, int dim, float eps) {
+__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const half_t *add16, const float *scale,
+                                                  float *h, const float *gamma, TO *y, int dim, float eps) {
 #pragma clang fp contract(off)
     __shared__ float part[4];
     const int row = blockIdx.x;
@@ -99,8 +99,15 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
         const float4_t z = float4_t{0.f, 0.f, 0.f, 0.f};
         v[i] = e < dim ? *reinterpret_cast<const float4_t *>(x + ro + e) : z;
         gm[i] = e < dim ? *reinterpret_cast<const float4_t *>(gamma + e) : z;
-        if (add.p && e < dim) {
-            float4_t u = sum_parts<12>(add.p + ro + e, add.ys, add.stride);
+        if ((add.p || add16) && e < dim) {
+            float4_t u;
+            if (add16) {  // a projection whose output the reference rounds to f16 (candle's f16 matmul)
+                const half4_t a4 = *reinterpret_cast<const half4_t *>(add16 + ro + e);
+                u = float4_t{static_cast<float>(a4[0]), static_cast<float>(a4[1]), static_cast<float>(a4[2]),
+                             static_cast<float>(a4[3])};
+            } else {
+                u = sum_parts<12>(add.p + ro + e, add.ys, add.stride);
+            }
             if (scale) {
                 const float4_t sc = *reinterpret_cast<const float4_t *>(scale + e);
                 u = u * sc;
@@ -129,16 +136,16 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
 // dim % 4 == 0 and dim <= 8192 (checked at create)
 template <typename TO>
 hipError_t launch_norm(const float *x, Partials add, const float *scale, float *h, const float *gamma, TO *y, int rows,
-                       int dim, float eps, hipStream_t stream) {
+                       int dim, float eps, hipStream_t stream, const half_t *add16 = nullptr) {
     const int nv = (dim + 1023) / 1024;
     if (nv <= 1)
-        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
     else if (nv <= 2)
-        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
     else if (nv <= 4)
-        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
     else
-        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
     return hipGetLastError();
 }
 
@@ -280,6 +287,368 @@ hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const d
     // h + the last MLP output, then the final norm
     return launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, lanes, dim, g.eps,
                        stream);
+}
+
+// ---------------------------------------------------------------- prefill (t >= 2)
+//
+// Stack::forward's prefill branch (qwen3.rs:329-336, 415-444) for lanes sharing `start`: rows are
+// (lane, t) pairs, lane-major. Proj::Half sends a projection of at most 48 rows (a multiple of 8)
+// to the skinny GEMM (f32 output, skinny.rs:123-131) and every other one to candle's f16 matmul,
+// whose output is f16 (lib.rs:516-529); the prefill keeps that routing: the A-sharing kernel for
+// the former, the channels-last tile kernel (k = 1, f32 accumulation, one f16 rounding) for the
+// latter. The new positions attend over their own f32 k and v and the cache's f16 prefix.
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+bool skinny_eligible(int64_t m, int64_t k, int64_t n) { return m <= 48 && m % 8 == 0 && k % 32 == 0 && n % 64 == 0; }
+
+// t = f16(silu(g) * u) from f16 gate|up outputs [rows, 2 * ffn] (swiglu_mul over the widened
+// values, fused.rs:289-385); four columns per thread.
+__global__ __launch_bounds__(256) void prefill_gateup_merge16(const half_t *gu, half_t *t, int rows, int ffn) {
+    const int c4n = ffn / 4;
+    const int64_t total = static_cast<int64_t>(rows) * c4n;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t row = e / c4n;
+        const int col = static_cast<int>(e - row * c4n) * 4;
+        const half4_t g = *reinterpret_cast<const half4_t *>(gu + row * 2 * ffn + col);
+        const half4_t u = *reinterpret_cast<const half4_t *>(gu + row * 2 * ffn + ffn + col);
+        half4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = static_cast<half_t>(silu_mul(static_cast<float>(g[j]), static_cast<float>(u[j])));
+        *reinterpret_cast<half4_t *>(t + row * ffn + col) = o;
+    }
+}
+
+// QK-norm (when norms is set), RoPE at start + ti and the cache write of every new position, with
+// the reference's f32 side outputs (qkrope.rs:26-69 with f32_kv): one wave per (row, head), the
+// lane holding pair (lane, lane + D/2) as the decode kernel does. qkv [rows, (heads + 2 n_kv) D]
+// of T (f32: the sum of ys partials ystride apart; f16: the f16 matmul's output). Out: q
+// [b, heads, t, D], kf and vf [b, n_kv, t, D] f32; kc, vc [b, n_kv, cap, D] at start .. start+t-1.
+template <typename T>
+__global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float *norms, const float *cos_t,
+                                                       const float *sin_t, float *q_out, float *kf, float *vf, half_t *kc,
+                                                       half_t *vc, int rows, int t, int start, int heads, int n_kv,
+                                                       int hd, int cap, float eps, int ys, int64_t ystride) {
+#pragma clang fp contract(off)
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int per = heads + n_kv;
+    if (wid >= rows * per) return;
+    const int row = wid / per;
+    const int h = wid - row * per;
+    const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
+    const int half = hd / 2;
+    const T *src_row = qkv + static_cast<int64_t>(row) * (heads + 2 * n_kv) * hd;
+    const bool is_q = h < heads;
+    const bool act = lane < half;
+    auto ld = [&](const T *q) {
+        float v = static_cast<float>(q[0]);
+        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
+        return v;
+    };
+    float x1 = 0.0f, x2 = 0.0f;
+    if (act) {
+        x1 = ld(src_row + h * hd + lane);
+        x2 = ld(src_row + h * hd + lane + half);
+    }
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float m = sqrtf(ss / static_cast<float>(hd) + eps);
+    if (!act) return;
+    float y1 = x1, y2 = x2;
+    if (norms) {
+        const float *w = norms + (is_q ? 0 : hd);
+        y1 = (x1 / m) * w[lane];
+        y2 = (x2 / m) * w[lane + half];
+    }
+    const float c = cos_t[static_cast<int64_t>(p) * half + lane];
+    const float s = sin_t[static_cast<int64_t>(p) * half + lane];
+    float o1, o2;
+    rope_pair(y1, y2, c, s, o1, o2);
+    if (is_q) {
+        float *dq = q_out + ((static_cast<int64_t>(bi) * heads + h) * t + ti) * hd;
+        dq[lane] = o1;
+        dq[lane + half] = o2;
+        return;
+    }
+    const int kh = h - heads;
+    const int64_t dst = ((static_cast<int64_t>(bi) * n_kv + kh) * cap + p) * hd;
+    const int64_t fdst = ((static_cast<int64_t>(bi) * n_kv + kh) * t + ti) * hd;
+    const T *vs = src_row + (heads + n_kv + kh) * hd;
+    const float v1 = ld(vs + lane), v2 = ld(vs + lane + half);
+    kc[dst + lane] = static_cast<half_t>(o1);
+    kc[dst + lane + half] = static_cast<half_t>(o2);
+    vc[dst + lane] = static_cast<half_t>(v1);
+    vc[dst + lane + half] = static_cast<half_t>(v2);
+    kf[fdst + lane] = o1;
+    kf[fdst + lane + half] = o2;
+    vf[fdst + lane] = v1;
+    vf[fdst + lane + half] = v2;
+}
+
+constexpr int kPrefillMaxKeys = 16384;  // a wave's scores in LDS: at most 64 KB per workgroup
+
+// The prefill branch's attention for one query per wave (row = (lane, ti), head h): keys
+// lo .. start + ti, lo = start + ti + 1 - window (or 0), from the f16 cache below start and the
+// f32 kf / vf from start on. scores = q . k (times `scale` when the layer has no QK-norm), then
+// softmax_last_dim as candle computes it (max, exp(s - max), sum, probs = e / sum), then
+// probs . v; the result is stored f16, as wo's Proj::Half casts it. WPB waves per workgroup,
+// each with `keys` floats of LDS.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_attention(const float *q, const half_t *kc, const half_t *vc,
+                                                         const float *kf, const float *vf, half_t *out, int rows, int t,
+                                                         int start, int heads, int n_kv, int cap, int window, float scale,
+                                                         int keys, int wpb) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sc_all[];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wid = blockIdx.x * wpb + w;
+    if (w >= wpb || wid >= rows * heads) return;
+    float *sc = sc_all + static_cast<int64_t>(w) * keys;
+    const int row = wid / heads, h = wid - (wid / heads) * heads;
+    const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
+    const int kh = h / (heads / n_kv);
+    const int lo = window > 0 && p + 1 > window ? p + 1 - window : 0;
+    const int n = p - lo + 1;
+    const float *qr = q + ((static_cast<int64_t>(bi) * heads + h) * t + ti) * D;
+    const half_t *kcr = kc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
+    const half_t *vcr = vc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
+    const float *kfr = kf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
+    const float *vfr = vf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
+    float qv[D];
+#pragma unroll
+    for (int d = 0; d < D; d += 4) {
+        const float4_t v4 = *reinterpret_cast<const float4_t *>(qr + d);
+        qv[d] = v4[0];
+        qv[d + 1] = v4[1];
+        qv[d + 2] = v4[2];
+        qv[d + 3] = v4[3];
+    }
+    // scores: a key per lane, the dot product in dimension order
+    float mx = -INFINITY;
+    for (int i = lane; i < n; i += 64) {
+        const int j = lo + i;
+        float acc = 0.0f;
+        if (j < start) {
+            const half_t *kr = kcr + static_cast<int64_t>(j) * D;
+#pragma unroll
+            for (int d = 0; d < D; d += 8) {
+                const half8_t k8 = *reinterpret_cast<const half8_t *>(kr + d);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += qv[d + e] * static_cast<float>(k8[e]);
+            }
+        } else {
+            const float *kr = kfr + static_cast<int64_t>(j - start) * D;
+#pragma unroll
+            for (int d = 0; d < D; d += 4) {
+                const float4_t k4 = *reinterpret_cast<const float4_t *>(kr + d);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc += qv[d + e] * k4[e];
+            }
+        }
+        if (scale != 1.0f) acc = acc * scale;
+        sc[i] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int i = lane; i < n; i += 64) {
+        const float e = expf(sc[i] - mx);
+        sc[i] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    for (int i = lane; i < n; i += 64) sc[i] = sc[i] / sum;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's probabilities, read by every lane below
+    // probs . v: the lane owns D / 64 dimensions, keys in order
+    constexpr int PER = D / 64;
+    float o[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) o[r] = 0.0f;
+    int i = 0;
+    const int n_prior = start > lo ? start - lo : 0;
+    for (; i < n_prior; ++i) {
+        const float pj = sc[i];
+        const half_t *vr = vcr + static_cast<int64_t>(lo + i) * D;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) o[r] += pj * static_cast<float>(vr[lane + 64 * r]);
+    }
+    for (; i < n; ++i) {
+        const float pj = sc[i];
+        const float *vr = vfr + static_cast<int64_t>(lo + i - start) * D;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) o[r] += pj * vr[lane + 64 * r];
+    }
+    half_t *dst = out + static_cast<int64_t>(row) * heads * D + h * D;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) dst[lane + 64 * r] = static_cast<half_t>(o[r]);
+}
+
+struct PrefillPlan {
+    size_t h, a16, t16, qkv, q, kf, vf, p16, part, total;
+    size_t part_bytes;
+    int rows;
+};
+
+PrefillPlan prefill_plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t t) {
+    PrefillPlan p{};
+    const int64_t rows = lanes * t;
+    const int64_t qw = g.heads * g.head_dim, kvw = g.n_kv * g.head_dim, qkvw = qw + 2 * kvw;
+    const int64_t aw = g.dim > qw ? g.dim : qw;
+    const int64_t pw = g.dim > 2 * g.ffn ? g.dim : 2 * g.ffn;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    p.rows = static_cast<int>(rows);
+    p.h = take(sizeof(float) * rows * g.dim);
+    p.a16 = take(2 * rows * aw);
+    p.t16 = take(2 * rows * g.ffn);
+    p.qkv = take(sizeof(float) * rows * qkvw);
+    p.q = take(sizeof(float) * rows * qw);
+    p.kf = take(sizeof(float) * rows * kvw);
+    p.vf = take(sizeof(float) * rows * kvw);
+    p.p16 = take(2 * rows * pw);
+    size_t gb = 0;
+    if (rows <= kStackMaxLanes) {
+        const int64_t shapes[4][3] = {{g.dim, qkvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}};
+        for (const auto &sh : shapes) {
+            const size_t v =
+                lds_partial_bytes(pick_lds(static_cast<int>(rows), sh[0], sh[1], static_cast<int>(sh[2])), rows, sh[1]);
+            gb = v > gb ? v : gb;
+        }
+    }
+    p.part_bytes = gb;
+    p.part = take(gb);
+    p.total = off;
+    return p;
+}
+
+// One projection of the prefill on the tile kernel: y16 [rows, n] = f16(a16 [rows, k] . w^T).
+int prefill_gemm16(const half_t *a16, const half_t *w, half_t *y16, int rows, int k, int n, hipStream_t stream) {
+    dtts_conv_desc d{};
+    d.lanes = 1;
+    d.len = rows;
+    d.cin = k;
+    d.cout = n;
+    d.k = 1;
+    d.dilation = 1;
+    d.pad_left = 0;
+    d.x = a16;
+    d.w = w;
+    d.y = y16;
+    return dtts_conv1d_nlc_f16_ex(&d, stream);
+}
+
+#define PREFILL_STEP(expr)                                         \
+    do {                                                           \
+        const hipError_t e_ = (expr);                              \
+        if (e_ != hipSuccess) {                                    \
+            set_error("dtts_stack_prefill: %s", hipGetErrorString(e_)); \
+            return DTTS_ERR_HIP;                                   \
+        }                                                          \
+    } while (0)
+#define PREFILL_CALL(expr)               \
+    do {                                 \
+        const int rc_ = (expr);          \
+        if (rc_ != DTTS_OK) return rc_;  \
+    } while (0)
+
+int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_stack_cache *caches, int lanes, int t,
+                    int start, int cap, char *ws, const PrefillPlan &pl, hipStream_t stream) {
+    const dtts_stack_geometry &g = s.geo;
+    const int dim = static_cast<int>(g.dim), hd = static_cast<int>(g.head_dim);
+    const int heads = static_cast<int>(g.heads), n_kv = static_cast<int>(g.n_kv), ffn = static_cast<int>(g.ffn);
+    const int qw = heads * hd, kvw = n_kv * hd, qkvw = qw + 2 * kvw;
+    const int rows = lanes * t;
+    float *h = reinterpret_cast<float *>(ws + pl.h);
+    half_t *a16 = reinterpret_cast<half_t *>(ws + pl.a16);
+    half_t *t16 = reinterpret_cast<half_t *>(ws + pl.t16);
+    float *qkv = reinterpret_cast<float *>(ws + pl.qkv);
+    float *q = reinterpret_cast<float *>(ws + pl.q);
+    float *kf = reinterpret_cast<float *>(ws + pl.kf);
+    float *vf = reinterpret_cast<float *>(ws + pl.vf);
+    half_t *p16 = reinterpret_cast<half_t *>(ws + pl.p16);
+    float *gpart = pl.part_bytes ? reinterpret_cast<float *>(ws + pl.part) : nullptr;
+    // the layers without QK-norm scale the scores (qwen3.rs:311-316, 433-436)
+    const float scale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
+    const bool sk_qkv = skinny_eligible(rows, dim, qkvw), sk_o = skinny_eligible(rows, qw, dim);
+    const bool sk_gu = skinny_eligible(rows, dim, ffn), sk_d = skinny_eligible(rows, ffn, dim);
+    const int keys = start + t;
+    const int wpb = keys * 4 * 4 <= 65536 ? 4 : (keys * 4 * 2 <= 65536 ? 2 : 1);
+    Partials pending{};
+    const half_t *pending16 = nullptr;
+    const float *pending_scale = nullptr;
+    for (int64_t li = 0; li < g.layers; ++li) {
+        const dtts_stack_layer &L = s.layers[li];
+        half_t *kc = reinterpret_cast<half_t *>(caches[li].k);
+        half_t *vc = reinterpret_cast<half_t *>(caches[li].v);
+        PREFILL_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a16, rows, dim, g.eps, stream,
+                                 pending16));
+        const unsigned qk_blocks = static_cast<unsigned>((rows * (heads + n_kv) + 3) / 4);
+        const float *norms = g.qk_norm ? L.qk_norms : nullptr;
+        if (sk_qkv) {
+            Partials r{};
+            PREFILL_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, rows, dim,
+                                       qkvw, gpart, qkv, r, stream));
+            prefill_qk_rope<float><<<qk_blocks, 256, 0, stream>>>(r.p, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc, rows,
+                                                                  t, start, heads, n_kv, hd, cap, g.eps, r.ys, r.stride);
+        } else {
+            half_t *qkv16 = reinterpret_cast<half_t *>(qkv);
+            PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv16, rows, dim, qkvw, stream));
+            prefill_qk_rope<half_t><<<qk_blocks, 256, 0, stream>>>(qkv16, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc,
+                                                                   rows, t, start, heads, n_kv, hd, cap, g.eps, 1, 0);
+        }
+        PREFILL_STEP(hipGetLastError());
+        const unsigned at_blocks = static_cast<unsigned>((rows * heads + wpb - 1) / wpb);
+        const size_t lds = sizeof(float) * keys * wpb;
+        if (hd == 128)
+            prefill_attention<128><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, rows, t, start, heads, n_kv,
+                                                                    cap, static_cast<int>(g.window), scale, keys, wpb);
+        else
+            prefill_attention<64><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, rows, t, start, heads, n_kv,
+                                                                   cap, static_cast<int>(g.window), scale, keys, wpb);
+        PREFILL_STEP(hipGetLastError());
+        const float *attn_scale = g.layer_scale ? L.attn_scale : nullptr;
+        Partials r{};
+        const half_t *r16 = nullptr;
+        if (sk_o) {
+            PREFILL_STEP(stack_gemm<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr, attn_scale, rows, qw, dim,
+                                       gpart, nullptr, r, stream));
+        } else {
+            PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.wo), p16, rows, qw, dim, stream));
+            r16 = p16;
+        }
+        PREFILL_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, rows, dim, g.eps, stream, r16));
+        if (sk_gu) {
+            PREFILL_STEP(stack_gemm<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, rows,
+                                       dim, 2 * ffn, gpart, nullptr, r, stream));
+            if (r.p) stack_gateup_merge<<<grid_for(int64_t(rows) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, rows, ffn);
+        } else {
+            PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.w_gateup), p16, rows, dim, 2 * ffn, stream));
+            prefill_gateup_merge16<<<grid_for(int64_t(rows) * ffn / 4, 256, 4), 256, 0, stream>>>(p16, t16, rows, ffn);
+        }
+        PREFILL_STEP(hipGetLastError());
+        const float *mlp_scale = g.layer_scale ? L.mlp_scale : nullptr;
+        pending = Partials{};
+        pending16 = nullptr;
+        if (sk_d) {
+            PREFILL_STEP(stack_gemm<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr, mlp_scale, rows, ffn,
+                                       dim, gpart, nullptr, pending, stream));
+        } else {
+            PREFILL_CALL(prefill_gemm16(t16, reinterpret_cast<const half_t *>(L.wdown), p16, rows, ffn, dim, stream));
+            pending16 = p16;
+        }
+        pending_scale = mlp_scale;
+    }
+    PREFILL_STEP(launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, rows, dim,
+                             g.eps, stream, pending16));
+    return DTTS_OK;
 }
 
 bool tiles_ok(int64_t k, int64_t n, int mode) { return pick_lds(kStackMaxLanes, k, n, mode).nc > 0; }
@@ -434,4 +803,40 @@ extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, cons
     }
     DTTS_HIP_CHECK(hipGraphLaunch(s->exec, stream), name);
     return DTTS_OK;
+}
+
+extern "C" size_t dtts_stack_prefill_workspace_bytes(const dtts_stack *s, int64_t lanes, int64_t t) {
+    if (!s || lanes <= 0 || t < 2 || lanes * t > (int64_t(1) << 20)) return 0;
+    return dtts::prefill_plan_of(s->geo, lanes, t).total;
+}
+
+extern "C" int dtts_stack_prefill(dtts_stack *s, const float *x, float *out, const dtts_stack_cache *caches,
+                                  int64_t lanes, int64_t t, int64_t start, int64_t cap, void *workspace,
+                                  size_t ws_bytes, hipStream_t stream) {
+    const char *name = "dtts_stack_prefill";
+    DTTS_REQUIRE(s, "%s: null stack", name);
+    DTTS_REQUIRE(lanes >= 0 && t >= 2, "%s: %lld lanes, t = %lld (t >= 2; one position is dtts_stack_decode)", name,
+                 (long long)lanes, (long long)t);
+    if (lanes == 0) return DTTS_OK;
+    const dtts_stack_geometry &g = s->geo;
+    DTTS_REQUIRE(lanes * t <= (int64_t(1) << 20), "%s: %lld rows (at most 2^20)", name, (long long)(lanes * t));
+    DTTS_REQUIRE(cap > 0 && cap <= g.capacity, "%s: cache capacity %lld outside (0, %lld] (the RoPE table)", name,
+                 (long long)cap, (long long)g.capacity);
+    // Stack::forward refuses start + t > capacity (crates/qwen3tts/src/qwen3.rs:303-309)
+    DTTS_REQUIRE(start >= 0 && start + t <= cap, "%s: %lld positions exceeds cache capacity %lld", name,
+                 (long long)(start + t), (long long)cap);
+    DTTS_REQUIRE(start + t <= dtts::kPrefillMaxKeys, "%s: %lld positions (at most %d attended at once)", name,
+                 (long long)(start + t), dtts::kPrefillMaxKeys);
+    DTTS_REQUIRE(lanes * g.n_kv * cap * g.head_dim < (int64_t(1) << 40), "%s: caches too large", name);
+    DTTS_REQUIRE(x && out && caches && workspace, "%s: null pointer", name);
+    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(out, 16) && dtts::aligned(workspace, 256),
+                 "%s: x and out must be 16-byte aligned, the workspace 256-byte aligned", name);
+    for (int64_t i = 0; i < g.layers; ++i)
+        DTTS_REQUIRE(caches[i].k && caches[i].v && dtts::aligned(caches[i].k, 16) && dtts::aligned(caches[i].v, 16),
+                     "%s: layer %lld cache missing or misaligned", name, (long long)i);
+    const dtts::PrefillPlan pl = dtts::prefill_plan_of(g, lanes, t);
+    DTTS_REQUIRE(ws_bytes >= pl.total, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, pl.total);
+    return dtts::enqueue_prefill(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(t),
+                                 static_cast<int>(start), static_cast<int>(cap), static_cast<char *>(workspace), pl,
+                                 stream);
 }

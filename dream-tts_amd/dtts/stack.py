@@ -273,3 +273,23 @@ class Stack:
              ctypes.cast(state._c, ctypes.c_void_p), lanes, state.cap, p.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ws.data_ptr()),
              ws.numel(), GRAPH if graph else 0, stream_handle(self.dev))
         return out
+
+    def prefill_workspace_bytes(self, lanes: int, t: int) -> int:
+        return int(lib().dtts_stack_prefill_workspace_bytes(self.handle, lanes, t))
+
+    def prefill(self, x: torch.Tensor, state: State, start: int, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+        """Stack::forward at t >= 2 (the prefill branch) for lanes sharing `start`: x [lanes, t, dim]
+        f32 -> the normed hidden states [lanes, t, dim] f32; the new positions' k and v land in the
+        caches at start .. start + t - 1."""
+        lanes, t, dim = x.shape
+        assert x.dtype == torch.float32 and x.is_contiguous() and dim == self.geo.dim
+        if out is None:
+            out = torch.empty_like(x)
+        if workspace is None:
+            workspace = torch.empty(max(self.prefill_workspace_bytes(lanes, t), 256), dtype=torch.uint8,
+                                    device=self.dev)
+        call("dtts_stack_prefill", self.handle, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+             ctypes.cast(state._c, ctypes.c_void_p), lanes, t, start, state.cap, ctypes.c_void_p(workspace.data_ptr()),
+             workspace.numel(), stream_handle(self.dev))
+        return out

@@ -343,6 +343,19 @@ int dtts_stack_decode(dtts_stack *stack, const float *x, float *out, const dtts_
                       int64_t cap, const int32_t *pos, void *workspace, size_t ws_bytes, int32_t flags,
                       hipStream_t stream);
 
+/* Stack::forward at t >= 2, the prefill branch (crates/qwen3tts/src/qwen3.rs:294-467, :415-444)
+ * for lanes sharing one start (State::width): the code predictor's [talker_hidden, code0_embed]
+ * per frame (talker.rs:417-420) and the talker's prompt. x [lanes, t, dim] f32 -> out
+ * [lanes, t, dim] f32; caches written at start .. start + t - 1 (k roped, v as given, f16) and
+ * read below start; the new positions attend over their own f32 k and v. Projections follow
+ * Proj::Half's routing by row count (lanes * t): at most 48 rows and a multiple of 8, f32 outputs
+ * (skinny::eligible, crates/tts-nn/src/skinny.rs:123-131); otherwise f16 outputs, as candle's f16
+ * matmul gives (lib.rs:516-529). start + t <= cap <= capacity and <= 16384, lanes * t <= 2^20. */
+size_t dtts_stack_prefill_workspace_bytes(const dtts_stack *stack, int64_t lanes, int64_t t);
+int dtts_stack_prefill(dtts_stack *stack, const float *x, float *out, const dtts_stack_cache *caches, int64_t lanes,
+                       int64_t t, int64_t start, int64_t cap, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
 /* ------------------------------------------------------------------ f-3 codec front half */
 
 /* Rvq::decode's lookups (crates/qwen3tts/src/codec.rs:296-313) for both quantizer stacks at

@@ -499,6 +499,98 @@ def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
     return rms_norm_f32(h, final_norm, geo.eps)                                       # :466
 
 
+def _skinny_eligible(m, k, n):
+    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131, MAX_M = 48 at :152): the shapes
+    Proj::Half sends to the skinny GEMM (f32 output); every other shape goes through candle's f16
+    matmul, whose output is f16 (lib.rs:516-529)."""
+    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
+
+
+def _proj_half(x, w_out_in):
+    """Proj::Half's forward at any row count (crates/tts-nn/src/lib.rs:514-529): the skinny GEMM's
+    f32 result for eligible shapes, else the f16 matmul's output (f32 accumulation, rounded once
+    to f16) widened back to f32."""
+    y = _proj_f16(x, w_out_in)
+    m, k = x.shape
+    return y if _skinny_eligible(m, k, w_out_in.shape[0]) else f16_to_f32(f32_to_f16(y))
+
+
+def prefill_attention_f32(q, k_all, v_all, start, window, scale):
+    """The prefill branch's attention (crates/qwen3tts/src/qwen3.rs:415-444): q [b, heads, t, D]
+    f32, k_all / v_all [b, n_kv, start + t, D] f32 (the cache's prefix widened, then the new
+    positions' own f32 k and v); query heads sharing a kv head stacked along rows; scores scaled
+    by `scale` (None when folded into q_norm), plus causal_window_mask(start + t, window) rows
+    start .. start + t - 1 (lib.rs:1210-1224); softmax_last_dim; probs . v. Returns
+    [b, t, heads * D] f32."""
+    q, k_all, v_all = _f32(q), _f32(k_all), _f32(v_all)
+    b, heads, t, hd = q.shape
+    n_kv, n = k_all.shape[1], k_all.shape[2]
+    assert n == start + t
+    gqa = heads // n_kv
+    rows = np.arange(start, start + t)[:, None]
+    cols = np.arange(n)[None, :]
+    lo = np.maximum(rows + 1 - window, 0) if window else np.zeros_like(rows)
+    mask = np.where((cols > rows) | (cols < lo), np.float32(-np.inf), np.float32(0.0)).astype(np.float32)
+    mask = np.concatenate([mask] * gqa, axis=0)                                      # [gqa * t, n]
+    qg = q.reshape(b, n_kv, gqa * t, hd)
+    scores = np.matmul(qg, np.swapaxes(k_all, -1, -2)).astype(np.float32)
+    if scale is not None:
+        scores = (scores * np.float32(scale)).astype(np.float32)
+    scores = scores + mask
+    e = np.exp(scores - scores.max(-1, keepdims=True)).astype(np.float32)
+    probs = (e / e.sum(-1, keepdims=True)).astype(np.float32)
+    out = np.matmul(probs, v_all).astype(np.float32)                                 # [b, n_kv, gqa*t, D]
+    return out.reshape(b, heads, t, hd).transpose(0, 2, 1, 3).reshape(b, t, heads * hd)
+
+
+def stack_prefill_f32(geo, layers, final_norm, x, kcaches, vcaches, start):
+    """Stack::forward at t >= 2 (crates/qwen3tts/src/qwen3.rs:294-467, the prefill branch) for a
+    batch that shares `start`: x [b, t, dim] f32; kcaches / vcaches per layer uint16
+    [b, n_kv, cap, D], written at start .. start + t - 1 in place and read below start. The
+    projections follow Proj::Half's routing by row count (b * t rows); the new positions attend
+    over their own f32 k and v and the cache's f16 prefix. Returns [b, t, dim] f32."""
+    b, t, dim = x.shape
+    rows = b * t
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw = heads * hd, n_kv * hd
+    cos_t, sin_t = rope_table_f32(geo.capacity, hd, geo.rope_base)
+    scale = None if geo.qk_norm else float(1.0 / np.sqrt(np.float64(hd)))          # :311-316
+    h = _f32(x).reshape(rows, dim).copy()
+    for li, L in enumerate(layers):
+        normed = rms_norm_f32(h, L["attn_norm"], geo.eps)                             # :339
+        qkv = _proj_half(normed, np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0)).reshape(b, t, -1)
+        q = np.empty((b, heads, t, hd), np.float32)
+        kf = np.empty((b, n_kv, t, hd), np.float32)
+        vf = np.ascontiguousarray(qkv[:, :, qw + kvw:].reshape(b, t, n_kv, hd).transpose(0, 2, 1, 3))
+        for ti in range(t):                          # qkrope::apply with f32_kv (qkrope.rs:26-69)
+            pos = np.full(b, start + ti, np.int32)
+            row = np.ascontiguousarray(qkv[:, ti])
+            if geo.qk_norm:
+                s = np.float32(1.0 / np.sqrt(np.float64(hd)))
+                norms = np.stack([_f32(L["q_norm"]) * s, _f32(L["k_norm"])])
+                q[:, :, ti], kf[:, :, ti] = qk_norm_rope_append_f32(row, norms, cos_t, sin_t, pos, kcaches[li],
+                                                                    vcaches[li], heads, n_kv, geo.eps)
+            else:                                                                     # :358-394
+                q[:, :, ti] = rope_halfsplit_f32(row[:, :qw].reshape(b, heads, hd), cos_t, sin_t, pos)
+                kf[:, :, ti] = rope_halfsplit_f32(row[:, qw:qw + kvw].reshape(b, n_kv, hd), cos_t, sin_t, pos)
+                kv_append_f32(kf[:, :, ti], vf[:, :, ti], pos, kcaches[li], vcaches[li])
+        prior = lambda c: f16_to_f32(c[:, :, :start])                                 # :425-431
+        k_all = np.concatenate([prior(kcaches[li]), kf], axis=2)
+        v_all = np.concatenate([prior(vcaches[li]), vf], axis=2)
+        attn = prefill_attention_f32(q, k_all, v_all, start, geo.window, scale).reshape(rows, qw)
+        o = _proj_half(attn, L["wo"])                                                 # :446
+        if geo.layer_scale:
+            o = o * _f32(L["attn_scale"])
+        h = h + o
+        normed = rms_norm_f32(h, L["ffn_norm"], geo.eps)                              # :453
+        tail = swiglu_mul_f32(_proj_half(normed, L["gate"]), _proj_half(normed, L["up"]))
+        mlp = _proj_half(tail, L["down"])                                             # :458
+        if geo.layer_scale:
+            mlp = mlp * _f32(L["mlp_scale"])
+        h = h + mlp
+    return rms_norm_f32(h, final_norm, geo.eps).reshape(b, t, dim)                    # :466
+
+
 def q8_0_quantize(w):
     w = _f32(w)
     rows, k = w.shape

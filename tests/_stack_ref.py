@@ -100,3 +100,70 @@ def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
             m = m * L["mlp_scale"]
         h = h + m
     return _rms(h, final_norm, geo.eps), kc, vc
+
+
+def _eligible(m, k, n):
+    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131): f32 output; else candle's f16 matmul."""
+    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
+
+
+def stack_prefill_f64(geo, layers, final_norm, x, kc, vc, start):
+    """Stack::forward's prefill branch (t >= 2, qwen3.rs:294-467) in float64 with the reference's
+    f16 roundings: projection inputs and weights; projection outputs where Proj::Half takes the f16
+    matmul (more than 48 rows, or rows not a multiple of 8); cache entries. The new positions'
+    own k and v enter the attention unrounded. x [b, t, dim]; returns (out [b, t, dim], kc, vc)."""
+    b, t, dim = x.shape
+    rows = b * t
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw, gqa = heads * hd, n_kv * hd, heads // n_kv
+    kc = [k.copy() for k in kc]
+    vc = [v.copy() for v in vc]
+    pos = start + np.arange(t)
+
+    def proj(a, w):
+        y = _h(a) @ _h(w).T
+        return y if _eligible(rows, a.shape[1], w.shape[0]) else _h(y)
+
+    h = np.asarray(x, np.float64).reshape(rows, dim)
+    n = start + t
+    rr, cc = pos[:, None], np.arange(n)[None, :]
+    lo = np.maximum(rr + 1 - geo.window, 0) if geo.window else np.zeros_like(rr)
+    allowed = (cc <= rr) & (cc >= lo)                                                # [t, n]
+    for li, L in enumerate(layers):
+        qkv = proj(_rms(h, L["attn_norm"], geo.eps), np.concatenate([L["wq"], L["wk"], L["wv"]], 0))
+        qkv = qkv.reshape(b, t, -1)
+        q = qkv[..., :qw].reshape(b, t, heads, hd)
+        k = qkv[..., qw:qw + kvw].reshape(b, t, n_kv, hd)
+        v = qkv[..., qw + kvw:].reshape(b, t, n_kv, hd)
+        if geo.qk_norm:
+            q = _rms(q, np.float64(L["q_norm"]) / np.sqrt(hd), geo.eps)
+            k = _rms(k, L["k_norm"], geo.eps)
+        # rope over [b, t, heads, hd] at positions start + ti
+        q = np.stack([_rope(q[:, ti], np.full(b, pos[ti]), geo) for ti in range(t)], 1)
+        k = np.stack([_rope(k[:, ti], np.full(b, pos[ti]), geo) for ti in range(t)], 1)
+        kc[li][:, :, start:n] = synth.f16_bits(k.transpose(0, 2, 1, 3))
+        vc[li][:, :, start:n] = synth.f16_bits(v.transpose(0, 2, 1, 3))
+        kk = np.concatenate([synth.from_f16_bits(kc[li][:, :, :start]).astype(np.float64),
+                             k.transpose(0, 2, 1, 3)], 2)                              # [b, n_kv, n, hd]
+        vv = np.concatenate([synth.from_f16_bits(vc[li][:, :, :start]).astype(np.float64),
+                             v.transpose(0, 2, 1, 3)], 2)
+        att = np.empty((b, t, heads, hd))
+        for hh in range(heads):
+            kh = hh // gqa
+            s = np.einsum("btd,bnd->btn", q[:, :, hh], kk[:, kh])
+            if not geo.qk_norm:
+                s = s / np.sqrt(hd)
+            s = np.where(allowed[None], s, -np.inf)
+            e = np.exp(s - s.max(-1, keepdims=True))
+            att[:, :, hh] = np.einsum("btn,bnd->btd", e / e.sum(-1, keepdims=True), vv[:, kh])
+        o = proj(att.reshape(rows, qw), L["wo"])
+        if geo.layer_scale:
+            o = o * L["attn_scale"]
+        h = h + o
+        a = _rms(h, L["ffn_norm"], geo.eps)
+        g, u = proj(a, L["gate"]), proj(a, L["up"])
+        m = proj(g / (1.0 + np.exp(-g)) * u, L["down"])
+        if geo.layer_scale:
+            m = m * L["mlp_scale"]
+        h = h + m
+    return _rms(h, final_norm, geo.eps).reshape(b, t, dim), kc, vc

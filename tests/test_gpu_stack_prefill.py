@@ -1,0 +1,107 @@
+"""dtts_stack_prefill (Stack::forward at t >= 2, the prefill branch of crates/qwen3tts/src/
+qwen3.rs:294-467) against the oracle's restatement (oracle.stack_prefill_f32) on the same seeded
+weights, inputs and cache prefix: the normed outputs within max-rel 5e-4 (f32 sums in another
+order, and an f16-rounded projection output may land on the other side of a tie), every cache
+entry written at start .. start + t - 1 within max-rel 1e-3 and every other entry bit-identical.
+Cases cover both routes of Proj::Half (the skinny GEMM's f32 outputs at <= 48 rows that are a
+multiple of 8, the f16 matmul's outputs otherwise, including the code predictor's 48 lanes x 2),
+a cache prefix, windows reaching into it, spans longer than a wave, and a decode step after the
+prefill; plus the argument checks."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dtts import DttsError, stack, synth
+
+from _stack_ref import SMALL, WINDOWED, inputs
+from _util import rel, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+LONG = replace(SMALL, capacity=160)
+
+
+def _setup(dev, geo, seed, lanes, t, cap):
+    layers, fn = stack.random_weights(geo, seed)
+    _, kc, vc = inputs(geo, seed, lanes, cap)
+    x = synth.normal(seed, "prefill.x", (lanes, t, geo.dim))
+    st = stack.Stack(geo, layers, fn, dev)
+    state = st.new_state(lanes, cap)
+    for i in range(geo.layers):
+        state.k[i].copy_(to_dev(kc[i], dev))
+        state.v[i].copy_(to_dev(vc[i], dev))
+    return layers, fn, x, kc, vc, st, state
+
+
+def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
+    for li in range(geo.layers):
+        for dev_t, want, old in ((state.k[li], kc_want[li], kc_before[li]), (state.v[li], vc_want[li], vc_before[li])):
+            g = to_host(dev_t)
+            keep = np.ones(g.shape[2], bool)
+            keep[start:start + t] = False
+            assert np.array_equal(g[:, :, keep], old[:, :, keep]), "a cache slot outside the new positions changed"
+            assert rel(synth.from_f16_bits(g[:, :, ~keep]), synth.from_f16_bits(want[:, :, ~keep]))[1] < 1e-3
+
+
+@pytest.mark.parametrize("geo,lanes,t,start,cap", [
+    (SMALL, 3, 5, 0, 64),       # 15 rows: f16-output projections
+    (SMALL, 8, 2, 0, 64),       # 16 rows: the skinny GEMM's f32 outputs
+    (SMALL, 24, 2, 0, 32),      # 48 rows: skinny, the A-sharing kernel's k ranges
+    (SMALL, 48, 2, 0, 17),      # the code predictor's per-frame prefill: 96 rows, f16 outputs
+    (SMALL, 4, 3, 10, 64),      # a cache prefix
+    (LONG, 2, 20, 100, 160),    # spans of 101 .. 120 keys (more than a wave)
+    (WINDOWED, 2, 9, 6, 32),    # windows into the prefix, no QK-norm (scaled scores), D = 64
+    (WINDOWED, 1, 30, 0, 32),   # t longer than the window
+])
+def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
+    layers, fn, x, kc, vc, st, state = _setup(dev, geo, 95, lanes, t, cap)
+    kb, vb = [k.copy() for k in kc], [v.copy() for v in vc]
+    print(f"prefill lanes={lanes} t={t} start={start} cap={cap} dim={geo.dim}", flush=True)
+    want = oracle.stack_prefill_f32(geo, layers, fn, x, kc, vc, start)
+    got = st.prefill(to_dev(x, dev), state, start)
+    torch.cuda.synchronize()
+    got = to_host(got)
+    assert rel(got, want)[1] < 5e-4, rel(got, want)
+    _check(geo, state, kb, vb, kc, vc, start, t)
+
+
+def test_prefill_then_decode(dev):
+    """The per-frame pattern of the code predictor: a prefill of 2 positions, then decode steps
+    over the cache it wrote (each side continuing from the GPU's cache)."""
+    geo, lanes, cap = SMALL, 8, 17
+    layers, fn, x, kc, vc, st, state = _setup(dev, geo, 96, lanes, 2, cap)
+    for i in range(geo.layers):
+        state.k[i].zero_()
+        state.v[i].zero_()
+    st.prefill(to_dev(x, dev), state, 0)
+    torch.cuda.synchronize()
+    kc = [to_host(k) for k in state.k]
+    vc = [to_host(v) for v in state.v]
+    for step in range(3):
+        xs = synth.normal(96, f"prefill.step{step}", (lanes, geo.dim))
+        pos = np.full(lanes, 2 + step, np.int32)
+        want = oracle.stack_decode_f32(geo, layers, fn, xs, kc, vc, pos)
+        got = to_host(st.decode(to_dev(xs, dev), state, pos))
+        assert rel(got, want)[1] < 2e-4
+        kc = [to_host(k) for k in state.k]
+        vc = [to_host(v) for v in state.v]
+
+
+def test_prefill_rejects_bad_arguments(dev):
+    geo = SMALL
+    st = stack.Stack(geo, *stack.random_weights(geo, 97), dev)
+    state = st.new_state(2, 16)
+    x = torch.zeros((2, 4, geo.dim), dtype=torch.float32, device=dev)
+    with pytest.raises(DttsError, match="t >= 2"):
+        st.prefill(torch.zeros((2, 1, geo.dim), dtype=torch.float32, device=dev), state, 0)
+    with pytest.raises(DttsError, match="exceeds cache capacity 16"):
+        st.prefill(x, state, 13)
+    small = torch.empty(256, dtype=torch.uint8, device=dev)
+    with pytest.raises(DttsError, match="workspace"):
+        st.prefill(x, state, 0, workspace=small)
+    before = [to_host(k) for k in state.k]
+    torch.cuda.synchronize()
+    assert all(np.array_equal(a, to_host(b)) for a, b in zip(before, state.k))
