@@ -300,12 +300,15 @@ struct LdsPlan {
     int nc, ys, tiles;
 };
 
-inline LdsPlan pick_lds(int64_t m, int64_t k, int64_t n, int mode) {
+// max_m: callers other than the decode step (the stack's prefill) may pass up to 128 rows; past 64
+// the range is two chunks (the slab and the f32 tile then stay within 35 KB of LDS).
+inline LdsPlan pick_lds(int64_t m, int64_t k, int64_t n, int mode, int64_t max_m = 64) {
     const int64_t per = mode == 1 ? 32 : 64;
     const int64_t cols = mode == 1 ? n / 2 : n;
-    if (m <= 0 || m > 64 || k % 128 != 0 || cols % per != 0 || cols / per > kLdsMaxTiles) return LdsPlan{0, 0, 0};
+    if (m <= 0 || m > max_m || m > 128 || k % 128 != 0 || cols % per != 0 || cols / per > kLdsMaxTiles)
+        return LdsPlan{0, 0, 0};
     const int64_t tiles = cols / per;
-    const int nc = k % 256 != 0 ? 2 : (k % 512 == 0 && tiles * (k / 512) >= 192) ? 8 : 4;
+    const int nc = (k % 256 != 0 || m > 64) ? 2 : (k % 512 == 0 && tiles * (k / 512) >= 192) ? 8 : 4;
     return LdsPlan{nc, static_cast<int>(k / (nc * 64)), static_cast<int>(tiles)};
 }
 
@@ -335,7 +338,12 @@ hipError_t launch_lds_nt(const GemmParams &p0, const LdsPlan &pl, void *workspac
         case 1: DTTS_LDS_NT(1) break;
         case 2: DTTS_LDS_NT(2) break;
         case 3: DTTS_LDS_NT(3) break;
-        default: DTTS_LDS_NT(4) break;
+        case 4: DTTS_LDS_NT(4) break;
+        // more than 64 rows: two-chunk ranges only (pick_lds)
+        case 5: gemm_lds_nt<5, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
+        case 6: gemm_lds_nt<6, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
+        case 7: gemm_lds_nt<7, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
+        default: gemm_lds_nt<8, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
     }
 #undef DTTS_LDS_NT
     hipError_t e = hipGetLastError();

@@ -83,9 +83,16 @@ __device__ __forceinline__ float4_t sum_parts(const float *p, int ys, int64_t st
 // unset, h set). One workgroup per row; each thread holds NV float4 of the row (every load of the
 // row in flight at once); the sum of squares is reduced over the wave, then over the four waves
 // through LDS.
+__device__ __forceinline__ float4_t round_f16x4(float4_t u) {
+    return float4_t{static_cast<float>(static_cast<half_t>(u[0])), static_cast<float>(static_cast<half_t>(u[1])),
+                    static_cast<float>(static_cast<half_t>(u[2])), static_cast<float>(static_cast<half_t>(u[3]))};
+}
+
+// round16: the added projection output is the f16 matmul's (rounded once, after the sum)
 template <typename TO, int NV>
-__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const half_t *add16, const float *scale,
-                                                  float *h, const float *gamma, TO *y, int dim, float eps) {
+__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const half_t *add16, bool round16,
+                                                  const float *scale, float *h, const float *gamma, TO *y, int dim,
+                                                  float eps) {
 #pragma clang fp contract(off)
     __shared__ float part[4];
     const int row = blockIdx.x;
@@ -107,6 +114,7 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
                              static_cast<float>(a4[3])};
             } else {
                 u = sum_parts<12>(add.p + ro + e, add.ys, add.stride);
+                if (round16) u = round_f16x4(u);
             }
             if (scale) {
                 const float4_t sc = *reinterpret_cast<const float4_t *>(scale + e);
@@ -136,29 +144,34 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
 // dim % 4 == 0 and dim <= 8192 (checked at create)
 template <typename TO>
 hipError_t launch_norm(const float *x, Partials add, const float *scale, float *h, const float *gamma, TO *y, int rows,
-                       int dim, float eps, hipStream_t stream, const half_t *add16 = nullptr) {
+                       int dim, float eps, hipStream_t stream, const half_t *add16 = nullptr, bool round16 = false) {
     const int nv = (dim + 1023) / 1024;
     if (nv <= 1)
-        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     else if (nv <= 2)
-        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     else if (nv <= 4)
-        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     else
-        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, add16, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     return hipGetLastError();
 }
 
 // t = f16(silu(g) * u) from the gate|up projection's partials (gate columns, then up columns, ys
 // arrays of [rows, 2 * ffn]); four columns per thread.
-__global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t, int rows, int ffn) {
+__global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t, int rows, int ffn,
+                                                          bool round16 = false) {
     const int c4n = ffn / 4;
     const int64_t total = static_cast<int64_t>(rows) * c4n;
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t row = e / c4n;
         const int col = static_cast<int>(e - row * c4n) * 4;
         const float *pr = gu.p + row * 2 * ffn + col;
-        const float4_t g = sum_parts<8>(pr, gu.ys, gu.stride), u = sum_parts<8>(pr + ffn, gu.ys, gu.stride);
+        float4_t g = sum_parts<8>(pr, gu.ys, gu.stride), u = sum_parts<8>(pr + ffn, gu.ys, gu.stride);
+        if (round16) {  // gate and up as the f16 matmul gives them
+            g = round_f16x4(g);
+            u = round_f16x4(u);
+        }
         half4_t o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = static_cast<half_t>(silu_mul(g[j], u[j]));
@@ -211,7 +224,7 @@ Plan plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t cap) {
 // whose result is already in h).
 template <int MODE>
 hipError_t stack_gemm(const half_t *a, const half_t *w, float *c, half_t *c16, const float *scale, int m, int k, int n,
-                      float *part, const float *plain, Partials &out, hipStream_t stream) {
+                      float *part, const float *plain, Partials &out, hipStream_t stream, int max_m = 64) {
     GemmParams p{};
     p.a = a;
     p.w = w;
@@ -221,7 +234,7 @@ hipError_t stack_gemm(const half_t *a, const half_t *w, float *c, half_t *c16, c
     p.m = m;
     p.k = k;
     p.n = n;
-    const LdsPlan pl = pick_lds(m, k, n, MODE);
+    const LdsPlan pl = pick_lds(m, k, n, MODE, max_m);
     out = pl.ys > 1 ? Partials{part, pl.ys, static_cast<int64_t>(m) * n} : Partials{plain, 1, 0};
     return launch_lds_nt<MODE>(p, pl, part, stream, false);
 }
@@ -332,7 +345,8 @@ template <typename T>
 __global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float *norms, const float *cos_t,
                                                        const float *sin_t, float *q_out, float *kf, float *vf, half_t *kc,
                                                        half_t *vc, int rows, int t, int start, int heads, int n_kv,
-                                                       int hd, int cap, float eps, int ys, int64_t ystride) {
+                                                       int hd, int cap, float eps, int ys, int64_t ystride,
+                                                       bool round16) {
 #pragma clang fp contract(off)
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float
     auto ld = [&](const T *q) {
         float v = static_cast<float>(q[0]);
         for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
-        return v;
+        return round16 ? static_cast<float>(static_cast<half_t>(v)) : v;
     };
     float x1 = 0.0f, x2 = 0.0f;
     if (act) {
@@ -487,6 +501,10 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     for (int r = 0; r < PER; ++r) dst[lane + 64 * r] = static_cast<half_t>(o[r]);
 }
 
+// Up to this many rows the prefill's projections run on the A-sharing kernel (its k ranges keep
+// the weights streaming at decode's rate); past it, on the tile kernel.
+constexpr int kPrefillMaxLdsRows = 128;
+
 struct PrefillPlan {
     size_t h, a16, t16, qkv, q, kf, vf, p16, part, total;
     size_t part_bytes;
@@ -509,17 +527,20 @@ PrefillPlan prefill_plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t
     p.h = take(sizeof(float) * rows * g.dim);
     p.a16 = take(2 * rows * aw);
     p.t16 = take(2 * rows * g.ffn);
-    p.qkv = take(sizeof(float) * rows * qkvw);
+    // the QKV output, and at 49 .. 128 rows every projection's f32 output (one at a time)
+    const int64_t fw = qkvw > pw ? qkvw : pw;
+    p.qkv = take(sizeof(float) * rows * fw);
     p.q = take(sizeof(float) * rows * qw);
     p.kf = take(sizeof(float) * rows * kvw);
     p.vf = take(sizeof(float) * rows * kvw);
     p.p16 = take(2 * rows * pw);
     size_t gb = 0;
-    if (rows <= kStackMaxLanes) {
-        const int64_t shapes[4][3] = {{g.dim, qkvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}};
+    if (rows <= kPrefillMaxLdsRows) {
+        const int64_t shapes[5][3] = {
+            {g.dim, qkvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}, {g.dim, 2 * g.ffn, 0}};
         for (const auto &sh : shapes) {
-            const size_t v =
-                lds_partial_bytes(pick_lds(static_cast<int>(rows), sh[0], sh[1], static_cast<int>(sh[2])), rows, sh[1]);
+            const size_t v = lds_partial_bytes(
+                pick_lds(static_cast<int>(rows), sh[0], sh[1], static_cast<int>(sh[2]), kPrefillMaxLdsRows), rows, sh[1]);
             gb = v > gb ? v : gb;
         }
     }
@@ -579,30 +600,37 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     const float scale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
     const bool sk_qkv = skinny_eligible(rows, dim, qkvw), sk_o = skinny_eligible(rows, qw, dim);
     const bool sk_gu = skinny_eligible(rows, dim, ffn), sk_d = skinny_eligible(rows, ffn, dim);
+    // not skinny-eligible but few rows: the A-sharing kernel in f32, each consumer rounding the
+    // summed output to f16 as the f16 matmul would
+    const bool mid = rows <= kPrefillMaxLdsRows;
+    constexpr int MM = kPrefillMaxLdsRows;
     const int keys = start + t;
     const int wpb = keys * 4 * 4 <= 65536 ? 4 : (keys * 4 * 2 <= 65536 ? 2 : 1);
     Partials pending{};
     const half_t *pending16 = nullptr;
+    bool pending_round = false;
     const float *pending_scale = nullptr;
     for (int64_t li = 0; li < g.layers; ++li) {
         const dtts_stack_layer &L = s.layers[li];
         half_t *kc = reinterpret_cast<half_t *>(caches[li].k);
         half_t *vc = reinterpret_cast<half_t *>(caches[li].v);
         PREFILL_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a16, rows, dim, g.eps, stream,
-                                 pending16));
+                                 pending16, pending_round));
         const unsigned qk_blocks = static_cast<unsigned>((rows * (heads + n_kv) + 3) / 4);
         const float *norms = g.qk_norm ? L.qk_norms : nullptr;
-        if (sk_qkv) {
+        if (sk_qkv || mid) {
             Partials r{};
             PREFILL_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, rows, dim,
-                                       qkvw, gpart, qkv, r, stream));
+                                       qkvw, gpart, qkv, r, stream, MM));
             prefill_qk_rope<float><<<qk_blocks, 256, 0, stream>>>(r.p, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc, rows,
-                                                                  t, start, heads, n_kv, hd, cap, g.eps, r.ys, r.stride);
+                                                                  t, start, heads, n_kv, hd, cap, g.eps, r.ys, r.stride,
+                                                                  !sk_qkv);
         } else {
             half_t *qkv16 = reinterpret_cast<half_t *>(qkv);
             PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv16, rows, dim, qkvw, stream));
             prefill_qk_rope<half_t><<<qk_blocks, 256, 0, stream>>>(qkv16, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc,
-                                                                   rows, t, start, heads, n_kv, hd, cap, g.eps, 1, 0);
+                                                                   rows, t, start, heads, n_kv, hd, cap, g.eps, 1, 0,
+                                                                   false);
         }
         PREFILL_STEP(hipGetLastError());
         const unsigned at_blocks = static_cast<unsigned>((rows * heads + wpb - 1) / wpb);
@@ -620,15 +648,22 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
         if (sk_o) {
             PREFILL_STEP(stack_gemm<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr, attn_scale, rows, qw, dim,
                                        gpart, nullptr, r, stream));
+        } else if (mid) {
+            PREFILL_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wo), qkv, nullptr, nullptr, rows, qw, dim,
+                                       gpart, qkv, r, stream, MM));
         } else {
             PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.wo), p16, rows, qw, dim, stream));
             r16 = p16;
         }
-        PREFILL_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, rows, dim, g.eps, stream, r16));
+        PREFILL_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, rows, dim, g.eps, stream, r16, !sk_o && mid));
         if (sk_gu) {
             PREFILL_STEP(stack_gemm<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, rows,
                                        dim, 2 * ffn, gpart, nullptr, r, stream));
             if (r.p) stack_gateup_merge<<<grid_for(int64_t(rows) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, rows, ffn);
+        } else if (mid) {
+            PREFILL_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.w_gateup), qkv, nullptr, nullptr, rows,
+                                       dim, 2 * ffn, gpart, qkv, r, stream, MM));
+            stack_gateup_merge<<<grid_for(int64_t(rows) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, rows, ffn, true);
         } else {
             PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.w_gateup), p16, rows, dim, 2 * ffn, stream));
             prefill_gateup_merge16<<<grid_for(int64_t(rows) * ffn / 4, 256, 4), 256, 0, stream>>>(p16, t16, rows, ffn);
@@ -637,9 +672,14 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
         const float *mlp_scale = g.layer_scale ? L.mlp_scale : nullptr;
         pending = Partials{};
         pending16 = nullptr;
+        pending_round = false;
         if (sk_d) {
             PREFILL_STEP(stack_gemm<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr, mlp_scale, rows, ffn,
                                        dim, gpart, nullptr, pending, stream));
+        } else if (mid) {
+            PREFILL_STEP(stack_gemm<0>(t16, reinterpret_cast<const half_t *>(L.wdown), qkv, nullptr, nullptr, rows, ffn,
+                                       dim, gpart, qkv, pending, stream, MM));
+            pending_round = true;
         } else {
             PREFILL_CALL(prefill_gemm16(t16, reinterpret_cast<const half_t *>(L.wdown), p16, rows, ffn, dim, stream));
             pending16 = p16;
@@ -647,7 +687,7 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
         pending_scale = mlp_scale;
     }
     PREFILL_STEP(launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, rows, dim,
-                             g.eps, stream, pending16));
+                             g.eps, stream, pending16, pending_round));
     return DTTS_OK;
 }
 
