@@ -403,14 +403,14 @@ __global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float
     vf[fdst + lane + half] = v2;
 }
 
-constexpr int kPrefillMaxKeys = 16384;  // a wave's scores in LDS: at most 64 KB per workgroup
+constexpr int kPrefillMaxKeys = 16000;  // a wave's scores and query in LDS: at most 64 KB per workgroup
 
 // The prefill branch's attention for one query per wave (row = (lane, ti), head h): keys
 // lo .. start + ti, lo = start + ti + 1 - window (or 0), from the f16 cache below start and the
 // f32 kf / vf from start on. scores = q . k (times `scale` when the layer has no QK-norm), then
 // softmax_last_dim as candle computes it (max, exp(s - max), sum, probs = e / sum), then
 // probs . v; the result is stored f16, as wo's Proj::Half casts it. WPB waves per workgroup,
-// each with `keys` floats of LDS.
+// each with keys + D floats of LDS.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_attention(const float *q, const half_t *kc, const half_t *vc,
                                                          const float *kf, const float *vf, half_t *out, int rows, int t,
@@ -421,7 +421,8 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int wid = blockIdx.x * wpb + w;
     if (w >= wpb || wid >= rows * heads) return;
-    float *sc = sc_all + static_cast<int64_t>(w) * keys;
+    float *sc = sc_all + static_cast<int64_t>(w) * (keys + D);
+    float *qs = sc + keys;  // the query, read by every lane from LDS (registers would halve occupancy)
     const int row = wid / heads, h = wid - (wid / heads) * heads;
     const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
     const int kh = h / (heads / n_kv);
@@ -432,15 +433,9 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     const half_t *vcr = vc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
     const float *kfr = kf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
     const float *vfr = vf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
-    float qv[D];
 #pragma unroll
-    for (int d = 0; d < D; d += 4) {
-        const float4_t v4 = *reinterpret_cast<const float4_t *>(qr + d);
-        qv[d] = v4[0];
-        qv[d + 1] = v4[1];
-        qv[d + 2] = v4[2];
-        qv[d + 3] = v4[3];
-    }
+    for (int r = 0; r < D / 64; ++r) qs[lane + 64 * r] = qr[lane + 64 * r];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // scores: a key per lane, the dot product in dimension order
     float mx = -INFINITY;
     for (int i = lane; i < n; i += 64) {
@@ -451,16 +446,21 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
 #pragma unroll
             for (int d = 0; d < D; d += 8) {
                 const half8_t k8 = *reinterpret_cast<const half8_t *>(kr + d);
+                const float4_t q0 = *reinterpret_cast<const float4_t *>(qs + d);
+                const float4_t q1 = *reinterpret_cast<const float4_t *>(qs + d + 4);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc += qv[d + e] * static_cast<float>(k8[e]);
+                for (int e = 0; e < 4; ++e) acc += q0[e] * static_cast<float>(k8[e]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc += q1[e] * static_cast<float>(k8[e + 4]);
             }
         } else {
             const float *kr = kfr + static_cast<int64_t>(j - start) * D;
 #pragma unroll
             for (int d = 0; d < D; d += 4) {
                 const float4_t k4 = *reinterpret_cast<const float4_t *>(kr + d);
+                const float4_t q4 = *reinterpret_cast<const float4_t *>(qs + d);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc += qv[d + e] * k4[e];
+                for (int e = 0; e < 4; ++e) acc += q4[e] * k4[e];
             }
         }
         if (scale != 1.0f) acc = acc * scale;
@@ -482,13 +482,43 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     float o[PER];
 #pragma unroll
     for (int r = 0; r < PER; ++r) o[r] = 0.0f;
+    // U keys' loads are issued together, then summed in key order (the loop is latency-bound)
+    constexpr int U = 8;
     int i = 0;
     const int n_prior = start > lo ? start - lo : 0;
+    for (; i + U <= n_prior; i += U) {
+        float pj[U], vv[U][PER];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            pj[u] = sc[i + u];
+            const half_t *vr = vcr + static_cast<int64_t>(lo + i + u) * D;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) vv[u][r] = static_cast<float>(vr[lane + 64 * r]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < PER; ++r) o[r] += pj[u] * vv[u][r];
+    }
     for (; i < n_prior; ++i) {
         const float pj = sc[i];
         const half_t *vr = vcr + static_cast<int64_t>(lo + i) * D;
 #pragma unroll
         for (int r = 0; r < PER; ++r) o[r] += pj * static_cast<float>(vr[lane + 64 * r]);
+    }
+    for (; i + U <= n; i += U) {
+        float pj[U], vv[U][PER];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            pj[u] = sc[i + u];
+            const float *vr = vfr + static_cast<int64_t>(lo + i + u - start) * D;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) vv[u][r] = vr[lane + 64 * r];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < PER; ++r) o[r] += pj[u] * vv[u][r];
     }
     for (; i < n; ++i) {
         const float pj = sc[i];
@@ -605,7 +635,8 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     const bool mid = rows <= kPrefillMaxLdsRows;
     constexpr int MM = kPrefillMaxLdsRows;
     const int keys = start + t;
-    const int wpb = keys * 4 * 4 <= 65536 ? 4 : (keys * 4 * 2 <= 65536 ? 2 : 1);
+    const int per_wave = (keys + hd) * 4;  // LDS bytes: the scores and the query
+    const int wpb = per_wave * 4 <= 65536 ? 4 : (per_wave * 2 <= 65536 ? 2 : 1);
     Partials pending{};
     const half_t *pending16 = nullptr;
     bool pending_round = false;
@@ -634,7 +665,7 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
         }
         PREFILL_STEP(hipGetLastError());
         const unsigned at_blocks = static_cast<unsigned>((rows * heads + wpb - 1) / wpb);
-        const size_t lds = sizeof(float) * keys * wpb;
+        const size_t lds = static_cast<size_t>(per_wave) * wpb;
         if (hd == 128)
             prefill_attention<128><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, rows, t, start, heads, n_kv,
                                                                     cap, static_cast<int>(g.window), scale, keys, wpb);

@@ -350,7 +350,7 @@ int dtts_stack_decode(dtts_stack *stack, const float *x, float *out, const dtts_
  * read below start; the new positions attend over their own f32 k and v. Projections follow
  * Proj::Half's routing by row count (lanes * t): at most 48 rows and a multiple of 8, f32 outputs
  * (skinny::eligible, crates/tts-nn/src/skinny.rs:123-131); otherwise f16 outputs, as candle's f16
- * matmul gives (lib.rs:516-529). start + t <= cap <= capacity and <= 16384, lanes * t <= 2^20. */
+ * matmul gives (lib.rs:516-529). start + t <= cap <= capacity and <= 16000, lanes * t <= 2^20. */
 size_t dtts_stack_prefill_workspace_bytes(const dtts_stack *stack, int64_t lanes, int64_t t);
 int dtts_stack_prefill(dtts_stack *stack, const float *x, float *out, const dtts_stack_cache *caches, int64_t lanes,
                        int64_t t, int64_t start, int64_t cap, void *workspace, size_t workspace_bytes,

@@ -105,3 +105,35 @@ def test_prefill_rejects_bad_arguments(dev):
     before = [to_host(k) for k in state.k]
     torch.cuda.synchronize()
     assert all(np.array_equal(a, to_host(b)) for a, b in zip(before, state.k))
+
+
+def test_prefill_shared_prefix_split(dev):
+    """prefill_batch's shared voice prefix (crates/qwen3tts/src/talker.rs:1076-1113) as validate.rs
+    checks it (bin/validate.rs:210-245): one lane's prefix prefilled once and copied into every
+    lane's cache, then each lane's rest prefilled from `shared` on; each lane's last hidden state
+    within 1e-4 of one whole prefill, and the split run matches the oracle's split run."""
+    geo = SMALL
+    layers, fn = stack.random_weights(geo, 94)
+    lanes, n, shared, cap = 2, 12, 5, 16
+    x = synth.normal(94, "prefill.shared.x", (lanes, n, geo.dim))
+    x[1, :shared] = x[0, :shared]
+    st = stack.Stack(geo, layers, fn, dev)
+    whole_state = st.new_state(lanes, cap)
+    whole = to_host(st.prefill(to_dev(x, dev), whole_state, 0))
+    one = st.new_state(1, cap)
+    st.prefill(to_dev(np.ascontiguousarray(x[:1, :shared]), dev), one, 0)
+    split_state = st.new_state(lanes, cap)
+    for li in range(geo.layers):  # State::fill_prefix: the one lane's prefix into every lane
+        split_state.k[li][:, :, :shared].copy_(one.k[li][:, :, :shared].expand(lanes, -1, -1, -1))
+        split_state.v[li][:, :, :shared].copy_(one.v[li][:, :, :shared].expand(lanes, -1, -1, -1))
+    split = to_host(st.prefill(to_dev(np.ascontiguousarray(x[:, shared:]), dev), split_state, shared))
+    torch.cuda.synchronize()
+    assert rel(split[:, -1], whole[:, -1])[1] < 1e-4
+    _, k1, v1 = inputs(geo, 94, 1, cap, fill=False)
+    oracle.stack_prefill_f32(geo, layers, fn, np.ascontiguousarray(x[:1, :shared]), k1, v1, 0)
+    _, ks, vs = inputs(geo, 94, lanes, cap, fill=False)
+    for li in range(geo.layers):
+        ks[li][:, :, :shared] = k1[li][:, :, :shared]
+        vs[li][:, :, :shared] = v1[li][:, :, :shared]
+    want = oracle.stack_prefill_f32(geo, layers, fn, np.ascontiguousarray(x[:, shared:]), ks, vs, shared)
+    assert rel(split, want)[1] < 5e-4

@@ -84,3 +84,26 @@ def test_prefill_oracle_window_hides_old_positions():
     a = oracle.stack_prefill_f32(geo, layers, fn, x, kc, vc, 12)
     b = oracle.stack_prefill_f32(geo, layers, fn, x, k2, v2, 12)
     assert np.array_equal(a, b)
+
+
+def test_prefill_oracle_shared_prefix_split():
+    """validate.rs's "prefill.shared" claim (crates/qwen3tts/src/bin/validate.rs:210-245): the voice's
+    positions prefilled once for one lane and copied into every lane's cache, then the rest of each
+    prompt prefilled from there, give each lane's last hidden state within 1e-4 of one whole
+    prefill (the prefix enters as f16 cache entries instead of f32)."""
+    geo = SMALL
+    layers, fn = stack.random_weights(geo, 94)
+    lanes, n, shared, cap = 2, 12, 5, 16
+    x = synth.normal(94, "prefill.shared.x", (lanes, n, geo.dim))
+    x[1, :shared] = x[0, :shared]
+    _, kc, vc = inputs(geo, 94, lanes, cap, fill=False)
+    whole = oracle.stack_prefill_f32(geo, layers, fn, x, kc, vc, 0)
+    _, k1, v1 = inputs(geo, 94, 1, cap, fill=False)
+    oracle.stack_prefill_f32(geo, layers, fn, np.ascontiguousarray(x[:1, :shared]), k1, v1, 0)
+    _, ks, vs = inputs(geo, 94, lanes, cap, fill=False)
+    for li in range(geo.layers):
+        ks[li][:, :, :shared] = k1[li][:, :, :shared]
+        vs[li][:, :, :shared] = v1[li][:, :, :shared]
+    split = oracle.stack_prefill_f32(geo, layers, fn, np.ascontiguousarray(x[:, shared:]), ks, vs, shared)
+    assert rel(split[:, -1], whole[:, -1])[1] < 1e-4
+    assert not np.array_equal(split[:, -1], whole[:, -1])  # the prefix's f16 rounding is visible
