@@ -102,7 +102,7 @@ int qk_rope(const char *name, const T *qkv, const float *norms, const float *cos
     qk_rope_kernel<T, Positions><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
         qkv, norms, cos_t, sin_t, p, q_out, k_out, reinterpret_cast<half_t *>(kc), reinterpret_cast<half_t *>(vc),
         static_cast<int>(b), static_cast<int>(heads), static_cast<int>(n_kv), static_cast<int>(hd),
-        static_cast<int>(cap), eps, 1.0f, 1, 0);
+        static_cast<int>(cap), eps, 1.0f, 1, 0, false);
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

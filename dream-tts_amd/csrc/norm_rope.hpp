@@ -85,12 +85,14 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 // holds pair j < D/2). norms == nullptr skips the QK-norm (layers without it); q_scale then
 // multiplies the roped q (Stack::forward's q * 1/sqrt(D) for such layers, crates/qwen3tts/src/
 // qwen3.rs:404-408), and is 1 otherwise. P: Positions or DevPositions. ys > 1: qkv is the sum,
-// in order, of ys partial arrays ystride elements apart (a projection's k-split partials).
+// in order, of ys partial arrays ystride elements apart (a projection's k-split partials);
+// round16 rounds that sum to f16 first.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float *norms, const float *cos_t,
                                                       const float *sin_t, P pos, T *q_out, float *k_out,
                                                       half_t *kc, half_t *vc, int b, int heads, int n_kv, int hd,
-                                                      int cap, float eps, float q_scale, int ys, int64_t ystride) {
+                                                      int cap, float eps, float q_scale, int ys, int64_t ystride,
+                                                      bool round16) {
 #pragma clang fp contract(off)
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -114,7 +116,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
         for (int y = 1; y < 8; ++y)
             if (y < ys) v += w[y];
         for (int y = 8; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
-        return v;
+        // round16: the projection's output as candle's f16 matmul gives it (one rounding of the sum)
+        return round16 ? static_cast<float>(static_cast<half_t>(v)) : v;
     };
     float x1 = 0.0f, x2 = 0.0f;
     if (act) {

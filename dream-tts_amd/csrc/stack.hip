@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t
 }
 
 struct Plan {  // workspace carve-up for one (lanes, cap)
-    size_t h, a16, t16, qkv, q, gemm_part, attn_part, total;
+    size_t h, a16, t16, qkv, q, f32out, gemm_part, attn_part, total;
     size_t gemm_bytes, attn_bytes;
     int max_window;
 };
@@ -200,10 +200,13 @@ Plan plan_of(const dtts_stack_geometry &g, int64_t lanes, int64_t cap) {
     p.t16 = take(2 * lanes * g.ffn);
     p.qkv = take(sizeof(float) * lanes * (qw + 2 * kvw));
     p.q = take(sizeof(float) * lanes * qw);
+    // the plain f32 output of a projection whose consumer rounds it to f16 (wo, gate|up, down)
+    p.f32out = take(sizeof(float) * lanes * (g.dim > 2 * g.ffn ? g.dim : 2 * g.ffn));
     // one partial region serves every projection: each one's partials are summed by its consumer
     // before the next projection runs
     size_t gb = 0;
-    const int64_t shapes[4][3] = {{g.dim, qw + 2 * kvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}};
+    const int64_t shapes[5][3] = {
+        {g.dim, qw + 2 * kvw, 0}, {qw, g.dim, 2}, {g.dim, 2 * g.ffn, 1}, {g.ffn, g.dim, 2}, {g.dim, 2 * g.ffn, 0}};
     for (const auto &sh : shapes) {
         const size_t v = lds_partial_bytes(pick_lds(lanes, sh[0], sh[1], static_cast<int>(sh[2])), lanes, sh[1]);
         gb = v > gb ? v : gb;
@@ -239,6 +242,11 @@ hipError_t stack_gemm(const half_t *a, const half_t *w, float *c, half_t *c16, c
     return launch_lds_nt<MODE>(p, pl, part, stream, false);
 }
 
+// skinny::eligible (crates/tts-nn/src/skinny.rs:123-131, MAX_M = 48): the projections Proj::Half
+// sends to the skinny GEMM, whose output is f32; every other one goes through candle's f16 matmul,
+// whose output is f16 (lib.rs:516-529).
+bool skinny_eligible(int64_t m, int64_t k, int64_t n) { return m <= 48 && m % 8 == 0 && k % 32 == 0 && n % 64 == 0; }
+
 #define STACK_STEP(expr)                          \
     do {                                          \
         const hipError_t e_ = (expr);             \
@@ -263,12 +271,20 @@ hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const d
     const int max_chunks = apart ? (pl.max_window + kChunk - 1) / kChunk : 0;
     const float qscale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
     const DevSpans spans{s.pos, static_cast<int>(g.window)};
+    // Projections the reference runs through candle's f16 matmul (lanes not a multiple of 8, or
+    // more than 48: a single lane's decode among them) take the plain-output form here, and each
+    // consumer rounds the summed output to f16 as that matmul's output is.
+    const bool r_qkv = !skinny_eligible(lanes, dim, qkvw), r_o = !skinny_eligible(lanes, qw, dim);
+    const bool r_gu = !skinny_eligible(lanes, dim, ffn), r_d = !skinny_eligible(lanes, ffn, dim);
+    float *fbuf = reinterpret_cast<float *>(ws + pl.f32out);
     Partials pending{};             // the previous layer's down projection, not yet in h
     const float *pending_scale = nullptr;
+    bool pending_round = false;
     for (int64_t li = 0; li < g.layers; ++li) {
         const dtts_stack_layer &L = s.layers[li];
         // h = x (layer 0) or h + the previous layer's MLP output; a = f16(rms_norm(h))
-        STACK_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a16, lanes, dim, g.eps, stream));
+        STACK_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a16, lanes, dim, g.eps, stream,
+                               nullptr, pending_round));
         Partials r{};
         STACK_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, lanes, dim, qkvw,
                                  gpart, qkv, r, stream));
@@ -276,30 +292,46 @@ hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const d
         qk_rope_kernel<float, DevPositions><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
             r.p, g.qk_norm ? L.qk_norms : nullptr, s.cos_t, s.sin_t, DevPositions{s.pos}, q, nullptr,
             reinterpret_cast<half_t *>(caches[li].k), reinterpret_cast<half_t *>(caches[li].v), lanes, heads, n_kv,
-            hd, cap, g.eps, qscale, r.ys, r.stride);
+            hd, cap, g.eps, qscale, r.ys, r.stride, r_qkv);
         STACK_STEP(hipGetLastError());
         STACK_STEP(launch_attention(q, reinterpret_cast<const half_t *>(caches[li].k),
                                     reinterpret_cast<const half_t *>(caches[li].v), a16, apart, max_chunks, lanes,
                                     n_kv, gqa, hd, cap, spans, stream));
         const float *attn_scale = g.layer_scale ? L.attn_scale : nullptr;
-        STACK_STEP(stack_gemm<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr, attn_scale, lanes, qw, dim,
-                                 gpart, nullptr, r, stream));
+        if (r_o)
+            STACK_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wo), fbuf, nullptr, nullptr, lanes, qw, dim,
+                                     gpart, fbuf, r, stream));
+        else
+            STACK_STEP(stack_gemm<2>(a16, reinterpret_cast<const half_t *>(L.wo), h, nullptr, attn_scale, lanes, qw, dim,
+                                     gpart, nullptr, r, stream));
         // h += attn * attn_scale (when the projection left partials); a = f16(rms_norm(h))
-        STACK_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, lanes, dim, g.eps, stream));
-        STACK_STEP(stack_gemm<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, lanes, dim,
-                                 2 * ffn, gpart, nullptr, r, stream));
-        if (r.p) {
-            stack_gateup_merge<<<grid_for(int64_t(lanes) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, lanes, ffn);
+        STACK_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a16, lanes, dim, g.eps, stream, nullptr, r_o));
+        if (r_gu) {
+            STACK_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.w_gateup), fbuf, nullptr, nullptr, lanes,
+                                     dim, 2 * ffn, gpart, fbuf, r, stream));
+            stack_gateup_merge<<<grid_for(int64_t(lanes) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, lanes, ffn, true);
             STACK_STEP(hipGetLastError());
+        } else {
+            STACK_STEP(stack_gemm<1>(a16, reinterpret_cast<const half_t *>(L.w_gateup), nullptr, t16, nullptr, lanes,
+                                     dim, 2 * ffn, gpart, nullptr, r, stream));
+            if (r.p) {
+                stack_gateup_merge<<<grid_for(int64_t(lanes) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t16, lanes, ffn);
+                STACK_STEP(hipGetLastError());
+            }
         }
         const float *mlp_scale = g.layer_scale ? L.mlp_scale : nullptr;
-        STACK_STEP(stack_gemm<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr, mlp_scale, lanes, ffn, dim,
-                                 gpart, nullptr, pending, stream));
+        if (r_d)
+            STACK_STEP(stack_gemm<0>(t16, reinterpret_cast<const half_t *>(L.wdown), fbuf, nullptr, nullptr, lanes, ffn,
+                                     dim, gpart, fbuf, pending, stream));
+        else
+            STACK_STEP(stack_gemm<2>(t16, reinterpret_cast<const half_t *>(L.wdown), h, nullptr, mlp_scale, lanes, ffn,
+                                     dim, gpart, nullptr, pending, stream));
         pending_scale = mlp_scale;
+        pending_round = r_d;
     }
     // h + the last MLP output, then the final norm
     return launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, lanes, dim, g.eps,
-                       stream);
+                       stream, nullptr, pending_round);
 }
 
 // ---------------------------------------------------------------- prefill (t >= 2)
@@ -317,7 +349,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-bool skinny_eligible(int64_t m, int64_t k, int64_t n) { return m <= 48 && m % 8 == 0 && k % 32 == 0 && n % 64 == 0; }
 
 // t = f16(silu(g) * u) from f16 gate|up outputs [rows, 2 * ffn] (swiglu_mul over the widened
 // values, fused.rs:289-385); four columns per thread.

@@ -333,7 +333,9 @@ size_t dtts_stack_workspace_bytes(const dtts_stack *stack, int64_t lanes, int64_
 /* x [lanes, dim] f32 (the embedded tokens) -> out [lanes, dim] f32 (the normed hidden state);
  * caches[layers]: layer i's k and v, written at each lane's position and read over its window;
  * pos a HOST int32[lanes], each < cap (checked before anything is enqueued, as Stack::forward
- * refuses start + t > capacity). lanes <= 64. The reference advances one position for the whole
+ * refuses start + t > capacity). lanes <= 64. Projection outputs follow Proj::Half's routing by lane
+ * count: f32 for 8, 16, .. 48 lanes (skinny::eligible), f16-rounded otherwise (one lane included),
+ * as candle's f16 matmul gives them. The reference advances one position for the whole
  * batch; a position per lane is the batched-decode generalisation. With DTTS_STACK_GRAPH the
  * launches are captured on the first call and replayed while x, out, the caches, lanes, cap and
  * the workspace stay the same (any change captures again). Calls on one stack must be ordered

@@ -454,9 +454,26 @@ def _proj_f16(x, w_out_in):
     return gemm_f16_f32acc(f32_to_f16(x), np.ascontiguousarray(f32_to_f16(w_out_in).T))
 
 
+def _skinny_eligible(m, k, n):
+    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131, MAX_M = 48 at :152): the shapes
+    Proj::Half sends to the skinny GEMM (f32 output); every other shape goes through candle's f16
+    matmul, whose output is f16 (lib.rs:516-529)."""
+    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
+
+
+def _proj_half(x, w_out_in):
+    """Proj::Half's forward at any row count (crates/tts-nn/src/lib.rs:514-529): the skinny GEMM's
+    f32 result for eligible shapes, else the f16 matmul's output (f32 accumulation, rounded once
+    to f16) widened back to f32."""
+    y = _proj_f16(x, w_out_in)
+    m, k = x.shape
+    return y if _skinny_eligible(m, k, w_out_in.shape[0]) else f16_to_f32(f32_to_f16(y))
+
+
 def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
     """Stack::forward at t = 1 (crates/qwen3tts/src/qwen3.rs:294-467) with f16 weights and f16
-    caches, each lane at its own position. geo: an object with the Geometry fields (dim, layers,
+    caches, each lane at its own position; the projections follow Proj::Half's routing by lane
+    count (f32 outputs for 8, 16, .. 48 lanes, f16 outputs otherwise, one lane included). geo: an object with the Geometry fields (dim, layers,
     heads, n_kv, head_dim, ffn, eps, rope_base, qk_norm, layer_scale, window, capacity); layers:
     dicts of checkpoint-layout f32 weights (wq, wk, wv, wo, gate, up, down [out, in]; attn_norm,
     ffn_norm; q_norm, k_norm; attn_scale, mlp_scale); x [b, dim] f32; kcaches / vcaches: per
@@ -473,7 +490,7 @@ def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
     h = _f32(x).copy()
     for li, L in enumerate(layers):
         normed = rms_norm_f32(h, L["attn_norm"], geo.eps)                             # :339
-        qkv = _proj_f16(normed, np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0))  # :340, :69-77
+        qkv = _proj_half(normed, np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0))  # :340, :69-77
         if geo.qk_norm:                                                               # :343-357
             s = np.float32(1.0 / np.sqrt(np.float64(hd)))
             norms = np.stack([_f32(L["q_norm"]) * s, _f32(L["k_norm"])])              # :78-91
@@ -486,33 +503,17 @@ def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
             q = q * np.float32(1.0 / np.sqrt(np.float64(hd)))                         # :404-408
         attn = decode_attention_f32(q.reshape(b, n_kv, heads // n_kv, hd), kcaches[li], vcaches[li],
                                     span, wstart).reshape(b, qw)                      # :413-414
-        o = _proj_f16(attn, L["wo"])                                                  # :446
+        o = _proj_half(attn, L["wo"])                                                 # :446
         if geo.layer_scale:
             o = o * _f32(L["attn_scale"])                                             # :447-450
         h = h + o                                                                     # :451
         normed = rms_norm_f32(h, L["ffn_norm"], geo.eps)                              # :453
-        tail = swiglu_mul_f32(_proj_f16(normed, L["gate"]), _proj_f16(normed, L["up"]))  # :454-457
-        mlp = _proj_f16(tail, L["down"])                                              # :458
+        tail = swiglu_mul_f32(_proj_half(normed, L["gate"]), _proj_half(normed, L["up"]))  # :454-457
+        mlp = _proj_half(tail, L["down"])                                             # :458
         if geo.layer_scale:
             mlp = mlp * _f32(L["mlp_scale"])                                          # :459-462
         h = h + mlp                                                                   # :463
     return rms_norm_f32(h, final_norm, geo.eps)                                       # :466
-
-
-def _skinny_eligible(m, k, n):
-    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131, MAX_M = 48 at :152): the shapes
-    Proj::Half sends to the skinny GEMM (f32 output); every other shape goes through candle's f16
-    matmul, whose output is f16 (lib.rs:516-529)."""
-    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
-
-
-def _proj_half(x, w_out_in):
-    """Proj::Half's forward at any row count (crates/tts-nn/src/lib.rs:514-529): the skinny GEMM's
-    f32 result for eligible shapes, else the f16 matmul's output (f32 accumulation, rounded once
-    to f16) widened back to f32."""
-    y = _proj_f16(x, w_out_in)
-    m, k = x.shape
-    return y if _skinny_eligible(m, k, w_out_in.shape[0]) else f16_to_f32(f32_to_f16(y))
 
 
 def prefill_attention_f32(q, k_all, v_all, start, window, scale):

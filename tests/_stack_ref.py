@@ -1,7 +1,8 @@
 """Shared pieces of the decoder-stack tests: small geometries, seeded inputs, and an independent
 float64 restatement of Stack::forward's decode step (crates/qwen3tts/src/qwen3.rs:294-467) in
 numpy, with the reference's f16 roundings at the same points (projection inputs, weights, cache
-entries) and everything else in float64."""
+entries, and projection outputs where Proj::Half takes candle's f16 matmul) and everything else in
+float64."""
 from dataclasses import replace
 
 import numpy as np
@@ -34,6 +35,11 @@ def inputs(geo, seed, lanes, cap, fill=True):
     return x, kc, vc
 
 
+def _eligible(m, k, n):
+    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131): f32 output; else candle's f16 matmul."""
+    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
+
+
 def _h(a):
     """Round to f16 (numpy's conversion is round-to-nearest-even) and back, in float64."""
     return np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
@@ -62,10 +68,14 @@ def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
     kc = [k.copy() for k in kc]
     vc = [v.copy() for v in vc]
     h = np.asarray(x, np.float64)
+
+    def out(y, k, n):  # Proj::Half's routing by lane count (skinny.rs:123-131)
+        return y if _eligible(b, k, n) else _h(y)
+
     for li, L in enumerate(layers):
         a = _h(_rms(h, L["attn_norm"], geo.eps))
         wqkv = _h(np.concatenate([L["wq"], L["wk"], L["wv"]], 0))
-        qkv = a @ wqkv.T
+        qkv = out(a @ wqkv.T, geo.dim, wqkv.shape[0])
         q = qkv[:, :qw].reshape(b, heads, hd)
         k = qkv[:, qw:qw + kvw].reshape(b, n_kv, hd)
         v = qkv[:, qw + kvw:].reshape(b, n_kv, hd)
@@ -88,23 +98,18 @@ def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
             s = np.einsum("hgd,hnd->hgn", qg, kk)
             e = np.exp(s - s.max(-1, keepdims=True))
             att[i] = np.einsum("hgn,hnd->hgd", e / e.sum(-1, keepdims=True), vv).reshape(heads, hd)
-        o = _h(att.reshape(b, qw)) @ _h(L["wo"]).T
+        o = out(_h(att.reshape(b, qw)) @ _h(L["wo"]).T, qw, geo.dim)
         if geo.layer_scale:
             o = o * L["attn_scale"]
         h = h + o
         a = _h(_rms(h, L["ffn_norm"], geo.eps))
-        g, u = a @ _h(L["gate"]).T, a @ _h(L["up"]).T
+        g, u = out(a @ _h(L["gate"]).T, geo.dim, geo.ffn), out(a @ _h(L["up"]).T, geo.dim, geo.ffn)
         t = _h(g / (1.0 + np.exp(-g)) * u)
-        m = t @ _h(L["down"]).T
+        m = out(t @ _h(L["down"]).T, geo.ffn, geo.dim)
         if geo.layer_scale:
             m = m * L["mlp_scale"]
         h = h + m
     return _rms(h, final_norm, geo.eps), kc, vc
-
-
-def _eligible(m, k, n):
-    """skinny::eligible (crates/tts-nn/src/skinny.rs:123-131): f32 output; else candle's f16 matmul."""
-    return m <= 48 and m % 8 == 0 and k % 32 == 0 and n % 64 == 0
 
 
 def stack_prefill_f64(geo, layers, final_norm, x, kc, vc, start):

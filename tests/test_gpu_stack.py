@@ -67,6 +67,17 @@ def test_stack_step_matches_oracle(dev):
     p.step(np.array([0, 63, 17, 40, 1], np.int32))
 
 
+@pytest.mark.parametrize("lanes", [1, 8, 16, 9])
+def test_stack_routes_projections_by_lane_count(dev, lanes):
+    """Proj::Half's routing (crates/tts-nn/src/lib.rs:516-529, skinny.rs:123-131): 8 and 16 lanes
+    keep the skinny GEMM's f32 outputs; 1 lane (a single utterance's decode) and 9 take candle's
+    f16 matmul, whose outputs are f16 -- on the graph path too."""
+    p = Pair(dev, SMALL, 95, lanes, 64)
+    start = synth.randint(95, "stack.route.pos", (lanes,), 0, 60).astype(np.int32)
+    p.step(start)
+    p.step(start + 1, graph=True)
+
+
 def test_stack_steps_advance_eager_and_graph_agree(dev):
     """Three steps eager, then the same three steps again from the same history as a graph."""
     lanes, cap = 6, 64

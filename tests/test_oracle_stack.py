@@ -36,7 +36,8 @@ def _run_both(geo, seed, lanes, cap, steps):
     return worst_out, worst_cache
 
 
-@pytest.mark.parametrize("geo,lanes,cap,steps", [(SMALL, 3, 64, 3), (WINDOWED, 4, 32, 9)])
+@pytest.mark.parametrize("geo,lanes,cap,steps", [(SMALL, 3, 64, 3), (WINDOWED, 4, 32, 9), (SMALL, 1, 64, 3),
+                                                   (SMALL, 8, 64, 3)])
 def test_stack_oracle_matches_f64(geo, lanes, cap, steps):
     out, cache = _run_both(geo, 80, lanes, cap, steps)
     assert out < 2e-4, out  # an f16 activation rounding may land on the other side of a tie
@@ -79,3 +80,18 @@ def test_stack_oracle_window_hides_old_positions():
     a = oracle.stack_decode_f32(geo, layers, fn, x, kc, vc, pos)
     b = oracle.stack_decode_f32(geo, layers, fn, x, k2, v2, pos)
     assert np.array_equal(a, b)
+
+
+def test_stack_oracle_routes_by_lane_count():
+    """One lane takes candle's f16 matmul (its projection outputs rounded to f16); eight lanes the
+    skinny GEMM (f32 outputs): the same lane's result differs between the two batch sizes, and the
+    eight-lane batch equals eight one-lane-compatible rows only up to that rounding."""
+    geo = SMALL
+    layers, fn = stack.random_weights(geo, 83)
+    x, kc, vc = inputs(geo, 83, 8, 16)
+    pos = np.arange(8, dtype=np.int32)
+    k1, v1 = [k[:1].copy() for k in kc], [v[:1].copy() for v in vc]
+    eight = oracle.stack_decode_f32(geo, layers, fn, x, kc, vc, pos)
+    one = oracle.stack_decode_f32(geo, layers, fn, np.ascontiguousarray(x[:1]), k1, v1, pos[:1])
+    assert not np.array_equal(one[0], eight[0])
+    assert rel(one[0], eight[0])[1] < 2e-3
