@@ -4,7 +4,8 @@ weights, inputs and cache prefix: the normed outputs within max-rel 5e-4 (f32 su
 order, and an f16-rounded projection output may land on the other side of a tie), every cache
 entry written at start .. start + t - 1 within max-rel 1e-3 and every other entry bit-identical.
 Cases cover both routes of Proj::Half (the skinny GEMM's f32 outputs at <= 48 rows that are a
-multiple of 8, the f16 matmul's outputs otherwise, including the code predictor's 48 lanes x 2),
+multiple of 8, the f16 matmul's outputs otherwise: from the A-sharing kernel up to 128 rows,
+including the code predictor's 48 lanes x 2, and from the tile kernel past that),
 a cache prefix, windows reaching into it, spans longer than a wave, and a decode step after the
 prefill; plus the argument checks."""
 from dataclasses import replace
@@ -55,6 +56,8 @@ def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
     (LONG, 2, 20, 100, 160),    # spans of 101 .. 120 keys (more than a wave)
     (WINDOWED, 2, 9, 6, 32),    # windows into the prefix, no QK-norm (scaled scores), D = 64
     (WINDOWED, 1, 30, 0, 32),   # t longer than the window
+    (SMALL, 3, 50, 0, 64),      # 150 rows: the tile kernel's f16 outputs
+    (WINDOWED, 5, 30, 2, 32),   # 150 rows, windowed
 ])
 def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
     layers, fn, x, kc, vc, st, state = _setup(dev, geo, 95, lanes, t, cap)
