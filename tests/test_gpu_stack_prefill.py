@@ -56,6 +56,8 @@ def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
     (LONG, 2, 20, 100, 160),    # spans of 101 .. 120 keys (more than a wave)
     (WINDOWED, 2, 9, 6, 32),    # windows into the prefix, no QK-norm (scaled scores), D = 64
     (WINDOWED, 1, 30, 0, 32),   # t longer than the window
+    (SMALL, 64, 2, 0, 16),      # 128 rows: the A-sharing kernel's largest row block
+    (SMALL, 43, 3, 0, 16),      # 129 rows: the first count on the tile kernel
     (SMALL, 3, 50, 0, 64),      # 150 rows: the tile kernel's f16 outputs
     (WINDOWED, 5, 30, 2, 32),   # 150 rows, windowed
 ])
