@@ -436,130 +436,173 @@ __global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float
 
 constexpr int kPrefillMaxKeys = 16000;  // a wave's scores and query in LDS: at most 64 KB per workgroup
 
-// The prefill branch's attention for one query per wave (row = (lane, ti), head h): keys
-// lo .. start + ti, lo = start + ti + 1 - window (or 0), from the f16 cache below start and the
-// f32 kf / vf from start on. scores = q . k (times `scale` when the layer has no QK-norm), then
-// softmax_last_dim as candle computes it (max, exp(s - max), sum, probs = e / sum), then
-// probs . v; the result is stored f16, as wo's Proj::Half casts it. WPB waves per workgroup,
-// each with keys + D floats of LDS.
-template <int D>
+// The prefill branch's attention, QP consecutive queries of one (lane, head) per wave (rows
+// bi*t + ti0 .. ti0+QP-1): query ti attends over keys lo .. start + ti, lo = start + ti + 1 - window
+// (or 0), from the f16 cache below start and the f32 kf / vf from start on. scores = q . k (times
+// `scale` when the layer has no QK-norm), then softmax_last_dim as candle computes it (max,
+// exp(s - max), sum, probs = e / sum), then probs . v; the result is stored f16, as wo's
+// Proj::Half casts it. Each key and value row is read once for the wave's queries: a key outside
+// a query's range gets probability exactly 0, so its term adds nothing and the sums keep key
+// order. WPB waves per workgroup, each with QP * (keys + D) floats of LDS.
+template <int D, int QP>
 __global__ __launch_bounds__(256) void prefill_attention(const float *q, const half_t *kc, const half_t *vc,
-                                                         const float *kf, const float *vf, half_t *out, int rows, int t,
+                                                         const float *kf, const float *vf, half_t *out, int lanes, int t,
                                                          int start, int heads, int n_kv, int cap, int window, float scale,
                                                          int keys, int wpb) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sc_all[];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int groups = (t + QP - 1) / QP;
     const int wid = blockIdx.x * wpb + w;
-    if (w >= wpb || wid >= rows * heads) return;
-    float *sc = sc_all + static_cast<int64_t>(w) * (keys + D);
-    float *qs = sc + keys;  // the query, read by every lane from LDS (registers would halve occupancy)
-    const int row = wid / heads, h = wid - (wid / heads) * heads;
-    const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
+    if (w >= wpb || wid >= lanes * groups * heads) return;
+    float *sc = sc_all + static_cast<int64_t>(w) * QP * (keys + D);  // [QP][keys]
+    float *qs = sc + QP * keys;                                       // [QP][D]
+    const int h = wid % heads, grp = (wid / heads) % groups, bi = wid / (heads * groups);
+    const int ti0 = grp * QP;
+    const int nq = t - ti0 < QP ? t - ti0 : QP;  // valid queries of the wave
     const int kh = h / (heads / n_kv);
-    const int lo = window > 0 && p + 1 > window ? p + 1 - window : 0;
-    const int n = p - lo + 1;
-    const float *qr = q + ((static_cast<int64_t>(bi) * heads + h) * t + ti) * D;
+    auto lo_of = [&](int ti) { return window > 0 && start + ti + 1 > window ? start + ti + 1 - window : 0; };
+    const int lo = lo_of(ti0), hi = start + ti0 + nq - 1;  // the union of the queries' key ranges
+    const int n = hi - lo + 1;
     const half_t *kcr = kc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
     const half_t *vcr = vc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
     const float *kfr = kf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
     const float *vfr = vf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
 #pragma unroll
-    for (int r = 0; r < D / 64; ++r) qs[lane + 64 * r] = qr[lane + 64 * r];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // scores: a key per lane, the dot product in dimension order
-    float mx = -INFINITY;
+    for (int a = 0; a < QP; ++a) {
+        const float *qr = q + ((static_cast<int64_t>(bi) * heads + h) * t + (a < nq ? ti0 + a : ti0)) * D;
+#pragma unroll
+        for (int r = 0; r < D / 64; ++r) qs[a * D + lane + 64 * r] = qr[lane + 64 * r];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the queries, read by every lane below
+    // scores: a key per lane, each dot product in dimension order
+    float mx[QP];
+#pragma unroll
+    for (int a = 0; a < QP; ++a) mx[a] = -INFINITY;
     for (int i = lane; i < n; i += 64) {
         const int j = lo + i;
-        float acc = 0.0f;
+        float acc[QP];
+#pragma unroll
+        for (int a = 0; a < QP; ++a) acc[a] = 0.0f;
         if (j < start) {
             const half_t *kr = kcr + static_cast<int64_t>(j) * D;
-#pragma unroll
+#pragma unroll 4
             for (int d = 0; d < D; d += 8) {
                 const half8_t k8 = *reinterpret_cast<const half8_t *>(kr + d);
-                const float4_t q0 = *reinterpret_cast<const float4_t *>(qs + d);
-                const float4_t q1 = *reinterpret_cast<const float4_t *>(qs + d + 4);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc += q0[e] * static_cast<float>(k8[e]);
+                for (int a = 0; a < QP; ++a) {
+                    const float4_t q0 = *reinterpret_cast<const float4_t *>(qs + a * D + d);
+                    const float4_t q1 = *reinterpret_cast<const float4_t *>(qs + a * D + d + 4);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc += q1[e] * static_cast<float>(k8[e + 4]);
+                    for (int e = 0; e < 4; ++e) acc[a] += q0[e] * static_cast<float>(k8[e]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[a] += q1[e] * static_cast<float>(k8[e + 4]);
+                }
             }
         } else {
             const float *kr = kfr + static_cast<int64_t>(j - start) * D;
-#pragma unroll
+#pragma unroll 4
             for (int d = 0; d < D; d += 4) {
                 const float4_t k4 = *reinterpret_cast<const float4_t *>(kr + d);
-                const float4_t q4 = *reinterpret_cast<const float4_t *>(qs + d);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc += q4[e] * k4[e];
+                for (int a = 0; a < QP; ++a) {
+                    const float4_t q4 = *reinterpret_cast<const float4_t *>(qs + a * D + d);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[a] += q4[e] * k4[e];
+                }
             }
         }
-        if (scale != 1.0f) acc = acc * scale;
-        sc[i] = acc;
-        mx = fmaxf(mx, acc);
-    }
-    mx = wave_max(mx);
-    float sum = 0.0f;
-    for (int i = lane; i < n; i += 64) {
-        const float e = expf(sc[i] - mx);
-        sc[i] = e;
-        sum += e;
-    }
-    sum = wave_sum(sum);
-    for (int i = lane; i < n; i += 64) sc[i] = sc[i] / sum;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's probabilities, read by every lane below
-    // probs . v: the lane owns D / 64 dimensions, keys in order
-    constexpr int PER = D / 64;
-    float o[PER];
 #pragma unroll
-    for (int r = 0; r < PER; ++r) o[r] = 0.0f;
-    // U keys' loads are issued together, then summed in key order (the loop is latency-bound)
+        for (int a = 0; a < QP; ++a) {
+            const bool in = a < nq && j >= lo_of(ti0 + a) && j <= start + ti0 + a;
+            float v = acc[a];
+            if (scale != 1.0f) v = v * scale;
+            sc[a * keys + i] = in ? v : -INFINITY;
+            if (in) mx[a] = fmaxf(mx[a], v);
+        }
+    }
+    float sum[QP];
+#pragma unroll
+    for (int a = 0; a < QP; ++a) {
+        mx[a] = wave_max(mx[a]);
+        sum[a] = 0.0f;
+    }
+    for (int i = lane; i < n; i += 64) {
+#pragma unroll
+        for (int a = 0; a < QP; ++a) {
+            const float e = a < nq ? expf(sc[a * keys + i] - mx[a]) : 0.0f;  // exactly 0 outside the range
+            sc[a * keys + i] = e;
+            sum[a] += e;
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < QP; ++a) sum[a] = wave_sum(sum[a]);
+    for (int i = lane; i < n; i += 64) {
+#pragma unroll
+        for (int a = 0; a < QP; ++a) sc[a * keys + i] = a < nq ? sc[a * keys + i] / sum[a] : 0.0f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's probabilities, read by every lane below
+    // probs . v: the lane owns D / 64 dimensions; U keys' loads in flight, summed in key order
+    constexpr int PER = D / 64;
     constexpr int U = 8;
+    float o[QP][PER];
+#pragma unroll
+    for (int a = 0; a < QP; ++a)
+#pragma unroll
+        for (int r = 0; r < PER; ++r) o[a][r] = 0.0f;
+    auto add = [&](int i0, const float (&vv)[PER]) {
+#pragma unroll
+        for (int a = 0; a < QP; ++a) {
+            const float pj = sc[a * keys + i0];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) o[a][r] += pj * vv[r];
+        }
+    };
     int i = 0;
-    const int n_prior = start > lo ? start - lo : 0;
+    const int n_prior = start > lo ? (start - lo < n ? start - lo : n) : 0;
     for (; i + U <= n_prior; i += U) {
-        float pj[U], vv[U][PER];
+        float vv[U][PER];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            pj[u] = sc[i + u];
             const half_t *vr = vcr + static_cast<int64_t>(lo + i + u) * D;
 #pragma unroll
             for (int r = 0; r < PER; ++r) vv[u][r] = static_cast<float>(vr[lane + 64 * r]);
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int r = 0; r < PER; ++r) o[r] += pj[u] * vv[u][r];
+        for (int u = 0; u < U; ++u) add(i + u, vv[u]);
     }
     for (; i < n_prior; ++i) {
-        const float pj = sc[i];
+        float vv[PER];
         const half_t *vr = vcr + static_cast<int64_t>(lo + i) * D;
 #pragma unroll
-        for (int r = 0; r < PER; ++r) o[r] += pj * static_cast<float>(vr[lane + 64 * r]);
+        for (int r = 0; r < PER; ++r) vv[r] = static_cast<float>(vr[lane + 64 * r]);
+        add(i, vv);
     }
     for (; i + U <= n; i += U) {
-        float pj[U], vv[U][PER];
+        float vv[U][PER];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            pj[u] = sc[i + u];
             const float *vr = vfr + static_cast<int64_t>(lo + i + u - start) * D;
 #pragma unroll
             for (int r = 0; r < PER; ++r) vv[u][r] = vr[lane + 64 * r];
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int r = 0; r < PER; ++r) o[r] += pj[u] * vv[u][r];
+        for (int u = 0; u < U; ++u) add(i + u, vv[u]);
     }
     for (; i < n; ++i) {
-        const float pj = sc[i];
+        float vv[PER];
         const float *vr = vfr + static_cast<int64_t>(lo + i - start) * D;
 #pragma unroll
-        for (int r = 0; r < PER; ++r) o[r] += pj * vr[lane + 64 * r];
+        for (int r = 0; r < PER; ++r) vv[r] = vr[lane + 64 * r];
+        add(i, vv);
     }
-    half_t *dst = out + static_cast<int64_t>(row) * heads * D + h * D;
 #pragma unroll
-    for (int r = 0; r < PER; ++r) dst[lane + 64 * r] = static_cast<half_t>(o[r]);
+    for (int a = 0; a < QP; ++a) {
+        if (a >= nq) break;
+        half_t *dst = out + (static_cast<int64_t>(bi) * t + ti0 + a) * heads * D + h * D;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) dst[lane + 64 * r] = static_cast<half_t>(o[a][r]);
+    }
 }
 
 // Up to this many rows the prefill's projections run on the A-sharing kernel (its k ranges keep
@@ -666,8 +709,11 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     const bool mid = rows <= kPrefillMaxLdsRows;
     constexpr int MM = kPrefillMaxLdsRows;
     const int keys = start + t;
-    const int per_wave = (keys + hd) * 4;  // LDS bytes: the scores and the query
+    // queries per wave: 4 (2 at t = 2 or 3) while their scores fit, else 1
+    const int qp = t >= 4 && (keys + hd) * 4 * 4 <= 65536 ? 4 : (t >= 2 && (keys + hd) * 4 * 2 <= 65536 ? 2 : 1);
+    const int per_wave = (keys + hd) * 4 * qp;  // LDS bytes: the scores and the queries
     const int wpb = per_wave * 4 <= 65536 ? 4 : (per_wave * 2 <= 65536 ? 2 : 1);
+    const int att_waves = lanes * ((t + qp - 1) / qp) * heads;
     Partials pending{};
     const half_t *pending16 = nullptr;
     bool pending_round = false;
@@ -695,14 +741,27 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
                                                                    false);
         }
         PREFILL_STEP(hipGetLastError());
-        const unsigned at_blocks = static_cast<unsigned>((rows * heads + wpb - 1) / wpb);
+        const unsigned at_blocks = static_cast<unsigned>((att_waves + wpb - 1) / wpb);
         const size_t lds = static_cast<size_t>(per_wave) * wpb;
-        if (hd == 128)
-            prefill_attention<128><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, rows, t, start, heads, n_kv,
-                                                                    cap, static_cast<int>(g.window), scale, keys, wpb);
-        else
-            prefill_attention<64><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, rows, t, start, heads, n_kv,
-                                                                   cap, static_cast<int>(g.window), scale, keys, wpb);
+#define DTTS_PREFILL_ATTN(D_, QP_)                                                                                   \
+    prefill_attention<D_, QP_><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, lanes, t, start, heads, n_kv, \
+                                                                 cap, static_cast<int>(g.window), scale, keys, wpb)
+        if (hd == 128) {
+            if (qp == 4)
+                DTTS_PREFILL_ATTN(128, 4);
+            else if (qp == 2)
+                DTTS_PREFILL_ATTN(128, 2);
+            else
+                DTTS_PREFILL_ATTN(128, 1);
+        } else {
+            if (qp == 4)
+                DTTS_PREFILL_ATTN(64, 4);
+            else if (qp == 2)
+                DTTS_PREFILL_ATTN(64, 2);
+            else
+                DTTS_PREFILL_ATTN(64, 1);
+        }
+#undef DTTS_PREFILL_ATTN
         PREFILL_STEP(hipGetLastError());
         const float *attn_scale = g.layer_scale ? L.attn_scale : nullptr;
         Partials r{};
