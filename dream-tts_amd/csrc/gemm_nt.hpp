@@ -301,14 +301,15 @@ struct LdsPlan {
 };
 
 // max_m: callers other than the decode step (the stack's prefill) may pass up to 128 rows; past 64
-// the range is two chunks (the slab and the f32 tile then stay within 35 KB of LDS).
+// the range is four chunks up to 96 rows and two past that (the slab then stays within 51 KB of
+// LDS).
 inline LdsPlan pick_lds(int64_t m, int64_t k, int64_t n, int mode, int64_t max_m = 64) {
     const int64_t per = mode == 1 ? 32 : 64;
     const int64_t cols = mode == 1 ? n / 2 : n;
     if (m <= 0 || m > max_m || m > 128 || k % 128 != 0 || cols % per != 0 || cols / per > kLdsMaxTiles)
         return LdsPlan{0, 0, 0};
     const int64_t tiles = cols / per;
-    const int nc = (k % 256 != 0 || m > 64) ? 2 : (k % 512 == 0 && tiles * (k / 512) >= 192) ? 8 : 4;
+    const int nc = (k % 256 != 0 || m > 96) ? 2 : m > 64 ? 4 : (k % 512 == 0 && tiles * (k / 512) >= 192) ? 8 : 4;
     return LdsPlan{nc, static_cast<int>(k / (nc * 64)), static_cast<int>(tiles)};
 }
 
@@ -339,9 +340,19 @@ hipError_t launch_lds_nt(const GemmParams &p0, const LdsPlan &pl, void *workspac
         case 2: DTTS_LDS_NT(2) break;
         case 3: DTTS_LDS_NT(3) break;
         case 4: DTTS_LDS_NT(4) break;
-        // more than 64 rows: two-chunk ranges only (pick_lds)
-        case 5: gemm_lds_nt<5, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
-        case 6: gemm_lds_nt<6, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
+        // more than 64 rows: four-chunk ranges up to 96 rows, two-chunk past that (pick_lds)
+        case 5:
+            if (pl.nc == 4)
+                gemm_lds_nt<5, 4, MODE><<<grid, 256, lds, stream>>>(p);
+            else
+                gemm_lds_nt<5, 2, MODE><<<grid, 256, lds, stream>>>(p);
+            break;
+        case 6:
+            if (pl.nc == 4)
+                gemm_lds_nt<6, 4, MODE><<<grid, 256, lds, stream>>>(p);
+            else
+                gemm_lds_nt<6, 2, MODE><<<grid, 256, lds, stream>>>(p);
+            break;
         case 7: gemm_lds_nt<7, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
         default: gemm_lds_nt<8, 2, MODE><<<grid, 256, lds, stream>>>(p); break;
     }
