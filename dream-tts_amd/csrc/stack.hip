@@ -76,25 +76,27 @@ __device__ __forceinline__ float4_t sum_parts(const float *p, int ys, int64_t st
     return u;
 }
 
-// Row-wise RMSNorm of the stack, f32 in, the f16 input of the next projection out (or the final
-// f32 output). When `add` is set, the row first takes the residual update of the projection that
-// precedes it: x + (sum of add's partials) * scale (LayerScale, or 1), rounded as the reference
-// rounds h + attn; the updated row is written to h. Layer 0 copies x into h the same way (add
-// unset, h set). One workgroup per row; each thread holds NV float4 of the row (every load of the
-// row in flight at once); the sum of squares is reduced over the wave, then over the four waves
-// through LDS.
+// Each component rounded to f16 and widened back.
 __device__ __forceinline__ float4_t round_f16x4(float4_t u) {
     return float4_t{static_cast<float>(static_cast<half_t>(u[0])), static_cast<float>(static_cast<half_t>(u[1])),
                     static_cast<float>(static_cast<half_t>(u[2])), static_cast<float>(static_cast<half_t>(u[3]))};
 }
 
+// Row-wise RMSNorm of the stack, f32 in, the f16 input of the next projection out (or the final
+// f32 output). When `add` is set, the row first takes the residual update of the projection that
+// precedes it: x + (sum of add's partials) * scale (LayerScale, or 1), rounded as the reference
+// rounds h + attn; the updated row is written to h. Layer 0 copies x into h the same way (add
+// unset, h set). One workgroup per row; each thread holds NV float4 of the row (every load of the
+// row in flight at once); the sum of squares is reduced over the wave, then over the TH/64 waves
+// through LDS in wave order.
 // round16: the added projection output is the f16 matmul's (rounded once, after the sum)
-template <typename TO, int NV>
-__global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, const half_t *add16, bool round16,
-                                                  const float *scale, float *h, const float *gamma, TO *y, int dim,
-                                                  float eps) {
+template <typename TO, int NV, int TH>
+__global__ __launch_bounds__(TH) void stack_norm(const float *x, Partials add, const half_t *add16, bool round16,
+                                                 const float *scale, float *h, const float *gamma, TO *y, int dim,
+                                                 float eps) {
 #pragma clang fp contract(off)
-    __shared__ float part[4];
+    constexpr int NWAVE = TH / 64;
+    __shared__ float part[NWAVE];
     const int row = blockIdx.x;
     const int t = threadIdx.x;
     const int64_t ro = static_cast<int64_t>(row) * dim;
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int e = (i * 256 + t) * 4;
+        const int e = (i * TH + t) * 4;
         const float4_t z = float4_t{0.f, 0.f, 0.f, 0.f};
         v[i] = e < dim ? *reinterpret_cast<const float4_t *>(x + ro + e) : z;
         gm[i] = e < dim ? *reinterpret_cast<const float4_t *>(gamma + e) : z;
@@ -128,11 +130,13 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
-    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NWAVE; ++k) ss += part[k];
     const float m = sqrtf(ss / static_cast<float>(dim) + eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int e = (i * 256 + t) * 4;
+        const int e = (i * TH + t) * 4;
         if (e >= dim) continue;
         TO *yo = y + ro + e;
 #pragma unroll
@@ -145,15 +149,16 @@ __global__ __launch_bounds__(256) void stack_norm(const float *x, Partials add, 
 template <typename TO>
 hipError_t launch_norm(const float *x, Partials add, const float *scale, float *h, const float *gamma, TO *y, int rows,
                        int dim, float eps, hipStream_t stream, const half_t *add16 = nullptr, bool round16 = false) {
-    const int nv = (dim + 1023) / 1024;
-    if (nv <= 1)
-        stack_norm<TO, 1><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
-    else if (nv <= 2)
-        stack_norm<TO, 2><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
-    else if (nv <= 4)
-        stack_norm<TO, 4><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
+    // one float4 per thread up to 4096 columns (more threads per row keep more of its loads in
+    // flight: the step's rows are few, so each runs alone on a CU), two up to 8192
+    if (dim <= 1024)
+        stack_norm<TO, 1, 256><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
+    else if (dim <= 2048)
+        stack_norm<TO, 1, 512><<<rows, 512, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
+    else if (dim <= 4096)
+        stack_norm<TO, 1, 1024><<<rows, 1024, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     else
-        stack_norm<TO, 8><<<rows, 256, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
+        stack_norm<TO, 2, 1024><<<rows, 1024, 0, stream>>>(x, add, add16, round16, scale, h, gamma, y, dim, eps);
     return hipGetLastError();
 }
 
