@@ -473,7 +473,8 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(lanes are data-parallel; see DESIGN.md for how the path shards)", file=sys.stderr)
+              "(lanes are data-parallel: N GPUs would each take lanes / N with the weights replicated)",
+              file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
