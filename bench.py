@@ -134,8 +134,9 @@ def workload_cfg1(dev, args):
     a1 = synth.uniform(0, "cfg1.alpha1", (c,), 0.5, 1.5)
     a2 = synth.uniform(0, "cfg1.alpha2", (c,), 0.5, 1.5)
     f = lambda v: torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(dev)
-    w1 = f(oracle.tap_major_weight_f32(synth.kaiming_normal(0, "cfg1.w1", (c, c, 7), c * 7)))
-    w2 = f(oracle.tap_major_weight_f32(synth.kaiming_normal(0, "cfg1.w2", (c, c, 1), c)))
+    w1_oik = synth.kaiming_normal(0, "cfg1.w1", (c, c, 7), c * 7)
+    w2_oik = synth.kaiming_normal(0, "cfg1.w2", (c, c, 1), c)
+    w1, w2 = f(nlc.tap_major_weight(w1_oik)), f(nlc.tap_major_weight(w2_oik))  # the product's host layout
     b1, b2 = f(synth.normal(0, "cfg1.b1", (c,), 0, 0.01)), f(synth.normal(0, "cfg1.b2", (c,), 0, 0.01))
     s1, s2 = (f(a1), f(1.0 / a1)), (f(a2), f(1.0 / a2))
     h = torch.empty_like(x)
@@ -149,7 +150,7 @@ def workload_cfg1(dev, args):
             "conv1_residual": {"ms": t1, "tflops": f1 / t1 / 1e9, "gbs": 3 * by / t1 / 1e6}}
     # CPU: the reference route on the oracle (snake pass, im2col + GEMM + bias, snake, GEMM, + x)
     xn = synth.normal(0, "cfg1.x", (1, c, length))
-    w1n, w2n = w1.cpu().numpy(), w2.cpu().numpy()
+    w1n, w2n = oracle.tap_major_weight_f32(w1_oik), oracle.tap_major_weight_f32(w2_oik)
     t0 = time.perf_counter()
     sn = oracle.snake_ncl_f32(xn, a1, (1.0 / a1).astype(np.float32))
     hn = oracle.conv1d_ncl_gemm_f32(sn, w1n, b1.cpu().numpy(), 7, 3, 9)
@@ -442,6 +443,51 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
     return out
 
 
+SIMDS = 1024  # MI355X: 256 CUs x 4 SIMDs
+
+
+def pmc_counters(stages_json, csv_paths):
+    """Per-kernel SQ/GRBM counters of one decode from rocprofv3 --pmc runs (one CSV per pass; the
+    first dtts dispatches of each are the decode, in stage order, as for pmc_summary): the mean
+    per launch of every counter, plus VALU instructions per MFMA instruction, the share of LDS
+    instruction cycles lost to bank conflicts and the MFMA-busy fraction of the SIMDs."""
+    import csv
+
+    stages = json.load(open(stages_json))["stages"]
+    n = len(stages)
+    per_stage = [dict() for _ in range(n)]
+    for path in csv_paths:
+        disp = {}
+        for r in csv.DictReader(open(path)):
+            if "dtts::" not in r["Kernel_Name"]:
+                continue
+            disp.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        order = sorted(disp)
+        if len(order) < n:
+            raise SystemExit(f"pmc-counters: {len(order)} dtts dispatches in {path} < {n} stages")
+        for i, d in enumerate(order[:n]):
+            per_stage[i].update(disp[d])
+    out = {"source": [os.path.basename(p) for p in csv_paths], "kernels": {}}
+    for st, c in zip(stages, per_stage):
+        k = out["kernels"].setdefault(st["kernel"], {"launches": 0, "ms": 0.0, "flops": 0.0, "counters": {}})
+        k["launches"] += 1
+        k["ms"] += st["ms"]
+        k["flops"] += st["flops"]
+        for name, v in c.items():
+            k["counters"][name] = k["counters"].get(name, 0.0) + v
+    for k in out["kernels"].values():
+        c = {name: v / k["launches"] for name, v in k["counters"].items()}
+        k["counters"] = c
+        if c.get("SQ_INSTS_MFMA"):
+            k["valu_per_mfma"] = round(c.get("SQ_INSTS_VALU", 0.0) / c["SQ_INSTS_MFMA"], 3)
+        if c.get("SQ_ACTIVE_INST_LDS"):
+            k["lds_bank_conflict_per_lds_cycle"] = round(c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_ACTIVE_INST_LDS"], 4)
+        if c.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            k["mfma_busy_frac"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * SIMDS), 4)
+        k["tflops"] = round(k["flops"] / k["ms"] / 1e9, 1)
+    return out
+
+
 WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
              "stack": workload_stack, "front": workload_front}
 
@@ -458,6 +504,8 @@ def main():
     ap.add_argument("--stages-out", default=None, help="write the per-launch profile as JSON here")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "STAGES_JSON"),
                     help="digest rocprofv3 FETCH_SIZE / WRITE_SIZE runs into per-kernel traffic (no GPU)")
+    ap.add_argument("--pmc-counters", nargs="+", metavar="STAGES_JSON CSV",
+                    help="digest rocprofv3 --pmc runs of SQ/GRBM counters into per-kernel figures (no GPU)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "codec_config5_pmc.json"),
                     help="per-kernel traffic from --pmc-summary, reported in roofline.traffic")
     ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5", "all"],
@@ -469,6 +517,9 @@ def main():
 
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return
+    if args.pmc_counters:
+        print(json.dumps(pmc_counters(args.pmc_counters[0], args.pmc_counters[1:]), indent=1))
         return
 
     if args.gpus != 1:

@@ -240,10 +240,18 @@ int parse_header(dtts_checkpoint *ck, const char *hdr, size_t len, const char *p
             e.name = key;
             int esize = 0;
             if (!parse_entry(js, e, esize)) break;
-            uint64_t numel = 1;
+            // The element count is bounded so that numel * esize stays below 2^62 and cannot wrap
+            // (a [2^61 + 1] F64 entry would wrap to 8 bytes); the byte count is compared after.
+            bool empty = false;
             for (int i = 0; i < e.ndim; ++i) {
-                DTTS_REQUIRE(e.shape[i] >= 0 && (e.shape[i] == 0 || numel <= (uint64_t(1) << 62) / uint64_t(e.shape[i])),
-                             "%s: %s: tensor %s: shape too large", name, path, key.c_str());
+                DTTS_REQUIRE(e.shape[i] >= 0, "%s: %s: tensor %s: negative dimension", name, path, key.c_str());
+                empty = empty || e.shape[i] == 0;
+            }
+            uint64_t numel = empty ? 0 : 1;
+            const uint64_t most = (uint64_t(1) << 62) / uint64_t(esize);
+            for (int i = 0; i < e.ndim && !empty; ++i) {
+                DTTS_REQUIRE(numel <= most / uint64_t(e.shape[i]), "%s: %s: tensor %s: shape too large", name, path,
+                             key.c_str());
                 numel *= uint64_t(e.shape[i]);
             }
             DTTS_REQUIRE(e.begin <= e.end && e.end <= ck->data_size,

@@ -64,8 +64,20 @@ int rms_norm(const char *name, const T *x, const T *gamma, T *y, int64_t rows, i
     if (rows == 0) return DTTS_OK;
     DTTS_REQUIRE(x && gamma && y, "%s: null pointer", name);
     DTTS_REQUIRE(rows < (int64_t(1) << 31), "%s: too many rows", name);
-    rms_norm_kernel<T><<<static_cast<unsigned>((rows + 3) / 4), 256, 0, stream>>>(x, gamma, y, static_cast<int>(rows),
-                                                                                  static_cast<int>(dim), eps);
+    const unsigned blocks = static_cast<unsigned>((rows + 3) / 4);
+    constexpr int64_t row_vec = 64 * (16 / sizeof(T));  // one 16-byte vector per lane
+    const int64_t nv = dim / row_vec;
+    if (dim % row_vec == 0 && nv <= 8 && aligned(x, 16) && aligned(gamma, 16) && aligned(y, 16)) {
+        const int r = static_cast<int>(rows), d = static_cast<int>(dim);
+        if (nv <= 2)
+            rms_norm_vec_kernel<T, 2><<<blocks, 256, 0, stream>>>(x, gamma, y, r, d, eps);
+        else if (nv <= 4)
+            rms_norm_vec_kernel<T, 4><<<blocks, 256, 0, stream>>>(x, gamma, y, r, d, eps);
+        else
+            rms_norm_vec_kernel<T, 8><<<blocks, 256, 0, stream>>>(x, gamma, y, r, d, eps);
+    } else {
+        rms_norm_kernel<T><<<blocks, 256, 0, stream>>>(x, gamma, y, static_cast<int>(rows), static_cast<int>(dim), eps);
+    }
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }
@@ -103,6 +115,33 @@ int qk_rope(const char *name, const T *qkv, const float *norms, const float *cos
         qkv, norms, cos_t, sin_t, p, q_out, k_out, reinterpret_cast<half_t *>(kc), reinterpret_cast<half_t *>(vc),
         static_cast<int>(b), static_cast<int>(heads), static_cast<int>(n_kv), static_cast<int>(hd),
         static_cast<int>(cap), eps, 1.0f, 1, 0, false);
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
+// qkrope::apply: t positions per lane from one start, optional f32 k/v side outputs.
+int qkrope_apply(const char *name, const float *qkv, const float *norms, const float *cos_t, const float *sin_t,
+                 dtts_f16 *kc, dtts_f16 *vc, int64_t heads, int64_t start, float eps, float *q_out, float *k_f32,
+                 float *v_f32, int64_t b, int64_t t, int64_t n_kv, int64_t hd, int64_t cap, int64_t table_len,
+                 hipStream_t stream) {
+    DTTS_REQUIRE(b >= 0 && t >= 0 && start >= 0 && heads > 0 && n_kv > 0 && hd > 0 && hd % 2 == 0 && hd <= 128 &&
+                     cap > 0 && table_len > 0,
+                 "%s: bad shape (b %lld, t %lld, start %lld, heads %lld, n_kv %lld, head_dim %lld, cap %lld)", name,
+                 (long long)b, (long long)t, (long long)start, (long long)heads, (long long)n_kv, (long long)hd,
+                 (long long)cap);
+    // qkrope.rs:40-44: the new positions must fit the cache (and here the RoPE table too)
+    DTTS_REQUIRE(start + t <= cap, "%s: %lld positions exceed %lld", name, (long long)(start + t), (long long)cap);
+    DTTS_REQUIRE(start + t <= table_len, "%s: %lld positions exceed the RoPE table's %lld", name,
+                 (long long)(start + t), (long long)table_len);
+    if (b == 0 || t == 0) return DTTS_OK;
+    DTTS_REQUIRE(qkv && norms && cos_t && sin_t && q_out && kc && vc, "%s: null pointer", name);
+    DTTS_REQUIRE((k_f32 == nullptr) == (v_f32 == nullptr), "%s: f32 k and v come together (f32_kv)", name);
+    const int64_t waves = b * t * (heads + n_kv);
+    DTTS_REQUIRE(waves < (int64_t(1) << 31) && cap < (int64_t(1) << 31), "%s: too many rows", name);
+    qk_rope_span_kernel<float><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
+        qkv, norms, cos_t, sin_t, q_out, k_f32, v_f32, reinterpret_cast<half_t *>(kc), reinterpret_cast<half_t *>(vc),
+        static_cast<int>(b * t), static_cast<int>(t), static_cast<int>(start), static_cast<int>(heads),
+        static_cast<int>(n_kv), static_cast<int>(hd), static_cast<int>(cap), eps, 1, 0, false);
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }
@@ -187,6 +226,14 @@ extern "C" int dtts_qk_norm_rope_kv_append_f16(const dtts_f16 *qkv, const float 
     return dtts::qk_rope<half_t>("dtts_qk_norm_rope_kv_append_f16", reinterpret_cast<const half_t *>(qkv), norms, cos_t,
                                  sin_t, pos, reinterpret_cast<half_t *>(q_out), k_out, kcache, vcache, b, heads, n_kv,
                                  head_dim, cap, table_len, eps, stream);
+}
+
+extern "C" int dtts_qkrope_apply_f32(const float *qkv, const float *norms, const float *cos_t, const float *sin_t,
+                                     dtts_f16 *kcache, dtts_f16 *vcache, int64_t heads, int64_t start, float eps,
+                                     float *q_out, float *k_f32, float *v_f32, int64_t b, int64_t t, int64_t n_kv,
+                                     int64_t head_dim, int64_t cap, int64_t table_len, hipStream_t stream) {
+    return dtts::qkrope_apply("dtts_qkrope_apply_f32", qkv, norms, cos_t, sin_t, kcache, vcache, heads, start, eps,
+                              q_out, k_f32, v_f32, b, t, n_kv, head_dim, cap, table_len, stream);
 }
 
 extern "C" int dtts_kv_append_f32(const float *k, const float *v, const int32_t *pos, dtts_f16 *kcache,

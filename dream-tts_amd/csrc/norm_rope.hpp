@@ -69,6 +69,58 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const T *x, const T *gamm
     }
 }
 
+// The same arithmetic with 16-byte accesses, for rows of a multiple of 64 vectors: lane j owns
+// vectors j, j + 64, ... (each 8 f16 or 4 f32), at most NV of them, all loaded before the first
+// use, with gamma's loaded beside them. The row stays in registers between the two passes.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T *x, const T *gamma, T *y, int rows, int dim,
+                                                           float eps) {
+#pragma clang fp contract(off)
+    constexpr int E = 16 / sizeof(T);  // elements per vector
+    typedef T vec_t __attribute__((ext_vector_type(E)));
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int nv = dim / (64 * E);
+    const vec_t *xr = reinterpret_cast<const vec_t *>(x + static_cast<int64_t>(row) * dim);
+    const vec_t *gr = reinterpret_cast<const vec_t *>(gamma);
+    vec_t *yr = reinterpret_cast<vec_t *>(y + static_cast<int64_t>(row) * dim);
+    vec_t v[NV], g[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i < nv) {
+            v[i] = xr[i * 64 + lane];
+            g[i] = gr[i * 64 + lane];
+        }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i < nv)
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float f = static_cast<float>(v[i][e]);
+                ss += f * f;
+            }
+    ss = wave_sum(ss);
+    const float m = sqrtf(ss / static_cast<float>(dim) + eps);
+    const float mh = static_cast<float>(static_cast<half_t>(m));
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (i < nv) {
+            vec_t o;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (sizeof(T) == 2) {  // candle's f16 form, as rms_norm_kernel
+                    const float q = static_cast<float>(static_cast<half_t>(static_cast<float>(v[i][e]) / mh));
+                    o[e] = static_cast<half_t>(q * static_cast<float>(g[i][e]));
+                } else {
+                    o[e] = (v[i][e] / m) * g[i][e];
+                }
+            }
+            yr[i * 64 + lane] = o;
+        }
+}
+
 // ---------------------------------------------------------------- RoPE
 
 __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
@@ -159,6 +211,76 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
         float *fk = k_out + (static_cast<int64_t>(bi) * n_kv + kh) * hd;
         fk[lane] = o1;
         fk[lane + half] = o2;
+    }
+}
+
+// QK-norm (when norms is set), RoPE at start + ti and the cache write of t new positions per lane,
+// with the reference's optional f32 side outputs (qkrope::apply with f32_kv, qkrope.rs:26-69):
+// one wave per (row, head), row = bi * t + ti, the lane holding pair (lane, lane + D/2) as the
+// decode kernel does. qkv [rows, (heads + 2 n_kv) D] of T (f32: the sum of ys partials ystride
+// apart, a projection's k-split; f16: the f16 matmul's output). Out: q [b, heads, t, D]; kf and
+// vf [b, n_kv, t, D] f32 (both or neither); kc, vc [b, n_kv, cap, D] at start .. start + t - 1.
+template <typename T>
+__global__ __launch_bounds__(256) void qk_rope_span_kernel(const T *qkv, const float *norms, const float *cos_t,
+                                                           const float *sin_t, float *q_out, float *kf, float *vf,
+                                                           half_t *kc, half_t *vc, int rows, int t, int start, int heads,
+                                                           int n_kv, int hd, int cap, float eps, int ys, int64_t ystride,
+                                                           bool round16) {
+#pragma clang fp contract(off)
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int per = heads + n_kv;
+    if (wid >= rows * per) return;
+    const int row = wid / per;
+    const int h = wid - row * per;
+    const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
+    const int half = hd / 2;
+    const T *src_row = qkv + static_cast<int64_t>(row) * (heads + 2 * n_kv) * hd;
+    const bool is_q = h < heads;
+    const bool act = lane < half;
+    auto ld = [&](const T *q) {
+        float v = static_cast<float>(q[0]);
+        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
+        return round16 ? static_cast<float>(static_cast<half_t>(v)) : v;
+    };
+    float x1 = 0.0f, x2 = 0.0f;
+    if (act) {
+        x1 = ld(src_row + h * hd + lane);
+        x2 = ld(src_row + h * hd + lane + half);
+    }
+    const float ss = wave_sum(x1 * x1 + x2 * x2);
+    const float m = sqrtf(ss / static_cast<float>(hd) + eps);
+    if (!act) return;
+    float y1 = x1, y2 = x2;
+    if (norms) {
+        const float *w = norms + (is_q ? 0 : hd);
+        y1 = (x1 / m) * w[lane];
+        y2 = (x2 / m) * w[lane + half];
+    }
+    const float c = cos_t[static_cast<int64_t>(p) * half + lane];
+    const float s = sin_t[static_cast<int64_t>(p) * half + lane];
+    float o1, o2;
+    rope_pair(y1, y2, c, s, o1, o2);
+    if (is_q) {
+        float *dq = q_out + ((static_cast<int64_t>(bi) * heads + h) * t + ti) * hd;
+        dq[lane] = o1;
+        dq[lane + half] = o2;
+        return;
+    }
+    const int kh = h - heads;
+    const int64_t dst = ((static_cast<int64_t>(bi) * n_kv + kh) * cap + p) * hd;
+    const int64_t fdst = ((static_cast<int64_t>(bi) * n_kv + kh) * t + ti) * hd;
+    const T *vs = src_row + (heads + n_kv + kh) * hd;
+    const float v1 = ld(vs + lane), v2 = ld(vs + lane + half);
+    kc[dst + lane] = static_cast<half_t>(o1);
+    kc[dst + lane + half] = static_cast<half_t>(o2);
+    vc[dst + lane] = static_cast<half_t>(v1);
+    vc[dst + lane + half] = static_cast<half_t>(v2);
+    if (kf) {
+        kf[fdst + lane] = o1;
+        kf[fdst + lane + half] = o2;
+        vf[fdst + lane] = v1;
+        vf[fdst + lane + half] = v2;
     }
 }
 

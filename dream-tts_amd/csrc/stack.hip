@@ -372,73 +372,6 @@ __global__ __launch_bounds__(256) void prefill_gateup_merge16(const half_t *gu, 
     }
 }
 
-// QK-norm (when norms is set), RoPE at start + ti and the cache write of every new position, with
-// the reference's f32 side outputs (qkrope.rs:26-69 with f32_kv): one wave per (row, head), the
-// lane holding pair (lane, lane + D/2) as the decode kernel does. qkv [rows, (heads + 2 n_kv) D]
-// of T (f32: the sum of ys partials ystride apart; f16: the f16 matmul's output). Out: q
-// [b, heads, t, D], kf and vf [b, n_kv, t, D] f32; kc, vc [b, n_kv, cap, D] at start .. start+t-1.
-template <typename T>
-__global__ __launch_bounds__(256) void prefill_qk_rope(const T *qkv, const float *norms, const float *cos_t,
-                                                       const float *sin_t, float *q_out, float *kf, float *vf, half_t *kc,
-                                                       half_t *vc, int rows, int t, int start, int heads, int n_kv,
-                                                       int hd, int cap, float eps, int ys, int64_t ystride,
-                                                       bool round16) {
-#pragma clang fp contract(off)
-    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int per = heads + n_kv;
-    if (wid >= rows * per) return;
-    const int row = wid / per;
-    const int h = wid - row * per;
-    const int bi = row / t, ti = row - (row / t) * t, p = start + ti;
-    const int half = hd / 2;
-    const T *src_row = qkv + static_cast<int64_t>(row) * (heads + 2 * n_kv) * hd;
-    const bool is_q = h < heads;
-    const bool act = lane < half;
-    auto ld = [&](const T *q) {
-        float v = static_cast<float>(q[0]);
-        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
-        return round16 ? static_cast<float>(static_cast<half_t>(v)) : v;
-    };
-    float x1 = 0.0f, x2 = 0.0f;
-    if (act) {
-        x1 = ld(src_row + h * hd + lane);
-        x2 = ld(src_row + h * hd + lane + half);
-    }
-    const float ss = wave_sum(x1 * x1 + x2 * x2);
-    const float m = sqrtf(ss / static_cast<float>(hd) + eps);
-    if (!act) return;
-    float y1 = x1, y2 = x2;
-    if (norms) {
-        const float *w = norms + (is_q ? 0 : hd);
-        y1 = (x1 / m) * w[lane];
-        y2 = (x2 / m) * w[lane + half];
-    }
-    const float c = cos_t[static_cast<int64_t>(p) * half + lane];
-    const float s = sin_t[static_cast<int64_t>(p) * half + lane];
-    float o1, o2;
-    rope_pair(y1, y2, c, s, o1, o2);
-    if (is_q) {
-        float *dq = q_out + ((static_cast<int64_t>(bi) * heads + h) * t + ti) * hd;
-        dq[lane] = o1;
-        dq[lane + half] = o2;
-        return;
-    }
-    const int kh = h - heads;
-    const int64_t dst = ((static_cast<int64_t>(bi) * n_kv + kh) * cap + p) * hd;
-    const int64_t fdst = ((static_cast<int64_t>(bi) * n_kv + kh) * t + ti) * hd;
-    const T *vs = src_row + (heads + n_kv + kh) * hd;
-    const float v1 = ld(vs + lane), v2 = ld(vs + lane + half);
-    kc[dst + lane] = static_cast<half_t>(o1);
-    kc[dst + lane + half] = static_cast<half_t>(o2);
-    vc[dst + lane] = static_cast<half_t>(v1);
-    vc[dst + lane + half] = static_cast<half_t>(v2);
-    kf[fdst + lane] = o1;
-    kf[fdst + lane + half] = o2;
-    vf[fdst + lane] = v1;
-    vf[fdst + lane + half] = v2;
-}
-
 constexpr int kPrefillMaxKeys = 16000;  // a wave's scores and query in LDS: at most 64 KB per workgroup
 
 // The prefill branch's attention, QP consecutive queries of one (lane, head) per wave (rows
@@ -735,13 +668,13 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
             Partials r{};
             PREFILL_STEP(stack_gemm<0>(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv, nullptr, nullptr, rows, dim,
                                        qkvw, gpart, qkv, r, stream, MM));
-            prefill_qk_rope<float><<<qk_blocks, 256, 0, stream>>>(r.p, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc, rows,
+            qk_rope_span_kernel<float><<<qk_blocks, 256, 0, stream>>>(r.p, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc, rows,
                                                                   t, start, heads, n_kv, hd, cap, g.eps, r.ys, r.stride,
                                                                   !sk_qkv);
         } else {
             half_t *qkv16 = reinterpret_cast<half_t *>(qkv);
             PREFILL_CALL(prefill_gemm16(a16, reinterpret_cast<const half_t *>(L.wqkv), qkv16, rows, dim, qkvw, stream));
-            prefill_qk_rope<half_t><<<qk_blocks, 256, 0, stream>>>(qkv16, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc,
+            qk_rope_span_kernel<half_t><<<qk_blocks, 256, 0, stream>>>(qkv16, norms, s.cos_t, s.sin_t, q, kf, vf, kc, vc,
                                                                    rows, t, start, heads, n_kv, hd, cap, g.eps, 1, 0,
                                                                    false);
         }

@@ -53,6 +53,8 @@ SIGNATURES = {
                                         _I64, _I64, _F32, _P],
     "dtts_qk_norm_rope_kv_append_f16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                         _I64, _I64, _F32, _P],
+    "dtts_qkrope_apply_f32": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P, _P, _P, _I64, _I64, _I64, _I64,
+                              _I64, _I64, _P],
     "dtts_kv_append_f32": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_kv_append_f16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "dtts_decode_attention_workspace_bytes": [_I64, _I64, _I64, _I64, _I64],

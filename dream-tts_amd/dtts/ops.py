@@ -137,6 +137,38 @@ def qk_norm_rope_kv_append(qkv, norms, cos, sin, pos, k_cache, v_cache, heads, e
     return (q, k) if f32_k else q
 
 
+def qkrope_apply(qkv, norms, cos, sin, k_cache, v_cache, heads, start, eps, f32_kv=False):
+    """qkrope::apply (crates/tts-nn/src/qkrope.rs:19-69) with the reference's signature.
+
+    qkv [b, t, (heads + 2*n_kv) * D] f32; norms [2, D]; cos/sin [positions, D/2]; caches
+    [b, n_kv, cap, D] f16 (a lane window, e.g. ``cache.narrow(0, off, b)``, is fine), written in
+    place at start .. start + t - 1. Returns (q [b, heads, t, D], (k, v) [b, n_kv, t, D] f32 when
+    f32_kv else None)."""
+    name = "qkrope_apply"
+    _check(qkv, name, (_F32,), "qkv")
+    _check(norms, name, (_F32,), "norms")
+    for t_, w in ((cos, "cos"), (sin, "sin")):
+        _check(t_, name, (_F32,), w)
+    for t_, w in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _check(t_, name, (_F16,), w)
+    if qkv.dim() != 3:
+        raise DttsError(f"{name}: qkv must be [b, t, width]")
+    b, t, width = qkv.shape
+    if k_cache.shape != v_cache.shape or k_cache.shape[0] != b:
+        raise DttsError(f"{name}: caches {tuple(k_cache.shape)} / {tuple(v_cache.shape)} do not hold {b} lanes")
+    _, n_kv, cap, hd = k_cache.shape
+    if width != (heads + 2 * n_kv) * hd:
+        raise DttsError(f"{name}: qkv width {width} != (heads + 2*n_kv)*D")
+    q = torch.empty((b, heads, t, hd), dtype=_F32, device=qkv.device)
+    side = None
+    if f32_kv:
+        side = tuple(torch.empty((b, n_kv, t, hd), dtype=_F32, device=qkv.device) for _ in range(2))
+    call("dtts_qkrope_apply_f32", ptr(qkv), ptr(norms), ptr(cos), ptr(sin), ptr(k_cache), ptr(v_cache),
+         heads, start, float(eps), ptr(q), ptr(side[0]) if side else None, ptr(side[1]) if side else None,
+         b, t, n_kv, hd, cap, cos.shape[0], stream_handle())
+    return q, side
+
+
 def kv_append(k, v, pos, k_cache, v_cache):
     """cache.slice_set(k.to_dtype(F16), 2, pos) for k and v (crates/qwen3tts/src/qwen3.rs:389-392),
     a position per lane: k, v [b, n_kv, D]; caches [b, n_kv, cap, D] f16, in place."""

@@ -241,6 +241,19 @@ int dtts_qk_norm_rope_kv_append_f16(const dtts_f16 *qkv, const float *norms, con
                                     int64_t heads, int64_t n_kv, int64_t head_dim, int64_t cap,
                                     int64_t table_len, float eps, hipStream_t stream);
 
+/* qkrope::apply (crates/tts-nn/src/qkrope.rs:19-69; kernel qk_rope_f32, mtl.rs:773-838) with its
+ * own signature: qkv [b, t, (heads + 2*n_kv) * D] f32 (q heads, then k, then v); norms [2, D] f32
+ * (q's weight, then k's); cos/sin [table_len, D/2]; the caches [b, n_kv, cap, D] f16 (a lane window
+ * of a larger cache is a pointer into it) are written in place at positions start .. start + t - 1
+ * (k normed and roped, v as given, RNE) and nowhere else. Out: q_out [b, heads, t, D] f32 and, with
+ * f32_kv, k_f32 and v_f32 [b, n_kv, t, D] f32 (pass both or neither). start + t must not exceed cap
+ * ("positions exceed", qkrope.rs:40-44) nor table_len; checked before anything is enqueued.
+ * D even and <= 128. */
+int dtts_qkrope_apply_f32(const float *qkv, const float *norms, const float *cos_t, const float *sin_t,
+                          dtts_f16 *kcache, dtts_f16 *vcache, int64_t heads, int64_t start, float eps,
+                          float *q_out, float *k_f32, float *v_f32, int64_t b, int64_t t, int64_t n_kv,
+                          int64_t head_dim, int64_t cap, int64_t table_len, hipStream_t stream);
+
 /* The KV append alone: cache.k.slice_set(&k.to_dtype(F16), 2, start) and the same for v
  * (crates/qwen3tts/src/qwen3.rs:389-392), one position per lane. k, v [b, n_kv, D]; caches
  * [b, n_kv, cap, D] f16 written at pos[bi] (HOST int32[b], each < cap), RNE, bit-exact. */

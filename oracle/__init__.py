@@ -333,6 +333,33 @@ def qk_norm_rope_append_f32(qkv, norms, cos_t, sin_t, pos, kcache, vcache, heads
     return q, k
 
 
+def qkrope_apply_f32(qkv, norms, cos_t, sin_t, kcache, vcache, heads, start, eps, f32_kv=True):
+    """qkrope::apply's result as the composed CPU path computes it (crates/qwen3tts/src/qwen3.rs:
+    358-394; the op's contract, crates/tts-nn/src/qkrope.rs:19-69): split q|k|v, rms_norm each
+    head over D (candle: f32 sum of squares, (x / m) * w), heads first [b, h, t, D], half-split
+    rope at positions start .. start + t - 1, then slice_set of f16(k) and f16(v) into the caches
+    (uint16 [b, n_kv, cap, D], updated in place). Returns (q, (k, v) or None), all f32."""
+    qkv = _f32(qkv)
+    b, t, width = qkv.shape
+    hd = norms.shape[-1]
+    n_kv = (width // hd - heads) // 2
+    cap = kcache.shape[2]
+    assert start + t <= cap, f"{start + t} positions exceed {cap}"
+    assert kcache.dtype == np.uint16 and kcache.flags["C_CONTIGUOUS"]
+    x = qkv.reshape(b, t, heads + 2 * n_kv, hd)
+    norms = _f32(norms)
+    q = rms_norm_f32(x[:, :, :heads].reshape(-1, hd), norms[0], eps).reshape(b, t, heads, hd)
+    k = rms_norm_f32(x[:, :, heads:heads + n_kv].reshape(-1, hd), norms[1], eps).reshape(b, t, n_kv, hd)
+    v = np.ascontiguousarray(x[:, :, heads + n_kv:])
+    pos = np.tile(start + np.arange(t, dtype=np.int32), b)  # row bi * t + ti sits at start + ti
+    q = rope_halfsplit_f32(q.reshape(b * t, heads, hd), cos_t, sin_t, pos).reshape(b, t, heads, hd)
+    k = rope_halfsplit_f32(k.reshape(b * t, n_kv, hd), cos_t, sin_t, pos).reshape(b, t, n_kv, hd)
+    q, k, v = (np.ascontiguousarray(a.transpose(0, 2, 1, 3)) for a in (q, k, v))
+    kcache[:, :, start:start + t] = f32_to_f16(k)
+    vcache[:, :, start:start + t] = f32_to_f16(v)
+    return q, ((k, v) if f32_kv else None)
+
+
 def kv_append_f32(k, v, pos, kcache, vcache):
     k, v = _f32(k), _f32(v)
     b, n_kv, hd = k.shape

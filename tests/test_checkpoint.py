@@ -62,6 +62,8 @@ def test_reader_matches_safetensors(tmp_path):
     ("json", "header"),
     ("offsets", "outside the 8-byte buffer"),
     ("size", "8 bytes for 4 elements"),
+    ("wrap", "shape too large"),          # 2^61 + 1 doubles: numel * 8 wraps to 8 in 64 bits
+    ("wrap2", "shape too large"),         # the same count over two dimensions
     ("dtype", "unknown dtype"),
     ("dup", "header"),
     ("missing", "mapping"),
@@ -80,6 +82,11 @@ def test_reader_refuses_damaged_files(tmp_path, case, match):
         _write_raw(path, {"x": {"dtype": "F32", "shape": [2], "data_offsets": [0, 16]}}, bytes(8))
     elif case == "size":
         _write_raw(path, {"x": {"dtype": "F32", "shape": [4], "data_offsets": [0, 8]}}, bytes(8))
+    elif case == "wrap":
+        _write_raw(path, {"x": {"dtype": "F64", "shape": [(1 << 61) + 1], "data_offsets": [0, 8]}}, bytes(8))
+    elif case == "wrap2":
+        _write_raw(path, {"x": {"dtype": "F64", "shape": [(1 << 31), (1 << 30) + 1], "data_offsets": [0, 8]}},
+                   bytes(8))
     elif case == "dtype":
         _write_raw(path, {"x": {"dtype": "F33", "shape": [2], "data_offsets": [0, 8]}}, bytes(8))
     elif case == "dup":

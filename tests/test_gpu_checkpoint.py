@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import _ckpt
+import oracle
 from dtts import checkpoint, codec, codec_front, nlc, synth
 from dtts._lib import call, ptr
 
@@ -114,6 +115,24 @@ def test_q8_0_device_matches_host(dev, dtype):
     src = np.ascontiguousarray(w32, np.float32)
     call("dtts_q8_0_quantize", src.ctypes.data_as(ctypes.c_void_p), host.ctypes.data_as(ctypes.c_void_p), rows, k)
     assert np.array_equal(blocks.cpu().numpy(), host)
+
+
+def test_q8_0_device_ties_round_half_away(dev):
+    """dtts_convert_q8_0 on exact ties (amax 127, so d = id = 1): away from zero, as the oracle's
+    closed form and ggml's roundf / candle's f32::round give."""
+    from test_oracle_gemm_q8 import TIE_CODES, tie_block_weights
+
+    w32 = tie_block_weights()
+    rows, k = w32.shape
+    w = torch.from_numpy(w32).to(dev)
+    blocks = torch.zeros(rows * k // 32 * 34, dtype=torch.uint8, device=dev)
+    checkpoint.convert("q8_0", ptr(w), CODE["F32"], ptr(blocks), rows, k)
+    torch.cuda.synchronize()
+    got = blocks.cpu().numpy().reshape(rows, k // 32, 34)
+    q = got[..., 2:].view(np.int8).astype(np.int32)
+    assert np.array_equal(q[0, 0, :12], TIE_CODES)
+    assert np.array_equal(q[1, 1, :12], TIE_CODES)
+    assert np.array_equal(got, oracle.q8_0_quantize(w32))
 
 
 def _python_models(fw, ww, dev):

@@ -38,7 +38,7 @@ def test_centered_conv_matches_oracle_and_torch(dev, cout, cin, length, k, dil):
     w = synth.normal(91, "w", (cout, cin, k), 0, 0.1)
     b = synth.normal(91, "b", (cout,))
     w_tm = oracle.tap_major_weight_f32(w)
-    got = to_host(nlc.conv1d_ncl_f32(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil,
+    got = to_host(nlc.conv1d_ncl_f32(to_dev(x, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(b, dev), k=k, dilation=dil,
                                      pad_left=pad))
     assert rel(got, oracle.conv1d_ncl_gemm_f32(x, w_tm, b, k, dil, pad))[1] < 1e-5
     want = F.conv1d(torch.from_numpy(x).double(), torch.from_numpy(w).double(), torch.from_numpy(b).double(),
@@ -56,7 +56,7 @@ def test_causal_conv_with_snake_and_residual(dev):
     a1, r1 = synth.uniform(92, "a1", (cin,), 0.5, 1.5), synth.uniform(92, "r1", (cin,), 0.5, 1.5)
     a2, r2 = synth.uniform(92, "a2", (cout,), 0.5, 1.5), synth.uniform(92, "r2", (cout,), 0.5, 1.5)
     w_tm = oracle.tap_major_weight_f32(w)
-    y_pre, y = nlc.conv1d_ncl_f32(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil,
+    y_pre, y = nlc.conv1d_ncl_f32(to_dev(x, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(b, dev), k=k, dilation=dil,
                                   snake_in=(to_dev(a1, dev), to_dev(r1, dev)), residual=to_dev(res, dev),
                                   snake_out=(to_dev(a2, dev), to_dev(r2, dev)), want_pre=True)
     s = oracle.snake_ncl_f32(x, a1, r1)
@@ -82,10 +82,10 @@ def test_config1_residual_unit(dev):
     r1, r2 = (1.0 / a1).astype(np.float32), (1.0 / a2).astype(np.float32)
     w1t, w2t = oracle.tap_major_weight_f32(w1), oracle.tap_major_weight_f32(w2)
     xd = to_dev(x, dev)
-    h = nlc.conv1d_ncl_f32(xd, to_dev(w1t, dev), to_dev(b1, dev), k=7, dilation=3, pad_left=9,
+    h = nlc.conv1d_ncl_f32(xd, to_dev(nlc.tap_major_weight(w1), dev), to_dev(b1, dev), k=7, dilation=3, pad_left=9,
                            snake_in=(to_dev(a1, dev), to_dev(r1, dev)),
                            snake_out=(to_dev(a2, dev), to_dev(r2, dev)))
-    y = to_host(nlc.conv1d_ncl_f32(h, to_dev(w2t, dev), to_dev(b2, dev), k=1, residual=xd))
+    y = to_host(nlc.conv1d_ncl_f32(h, to_dev(nlc.tap_major_weight(w2), dev), to_dev(b2, dev), k=1, residual=xd))
     s1 = oracle.snake_ncl_f32(x, a1, r1)
     h_ref = oracle.conv1d_ncl_gemm_f32(s1, w1t, b1, 7, 3, 9)
     s2 = oracle.snake_ncl_f32(h_ref, a2, r2)

@@ -4,7 +4,9 @@ Bars: RoPE and both appends bit-exact against the oracle (the append must be, an
 products are rounded exactly as the oracle's); RMSNorm max-rel <= 1e-5 in f32 and within one
 f16 ulp in f16 (the sum of squares is reduced in a different order); the fused QK kernel's q and
 f32 k max-rel <= 1e-5, its cached k the RNE cast of its own f32 k and its cached v bit-exact;
-every cache element outside the appended positions keeps its sentinel (qkrope.rs:245-257).
+every cache element outside the appended positions keeps its sentinel (qkrope.rs:245-257), and
+the cached k is within one f16 ulp of the oracle's own cache bits. qkrope::apply's t-position form
+is held to the reference test's three (b, t, start, lane offset) cases.
 Shapes: config 2 (48 lanes, 16 q / 8 kv heads, D 128, cache [48, 8, 2048, 128], theta 1e6,
 positions U[0, 2047]) and the reference test's (b, heads, n_kv, cap) = (8, 16, 8, 64).
 """
@@ -85,6 +87,8 @@ def test_qk_norm_rope_kv_append_f32(dev, b, heads, n_kv, cap):
     for bi in range(b):
         assert np.array_equal(hk[bi, :, pos[bi]], synth.f16_bits(gk[bi]))  # RNE of its own f32 k
         assert np.array_equal(hv[bi, :, pos[bi]], ovc[bi, :, pos[bi]])      # v: bit-exact
+        # against the oracle's own cache bits: within one f16 ulp (its f32 k is within 1e-5)
+        assert f16_ulp_diff(hk[bi, :, pos[bi]], okc[bi, :, pos[bi]]) <= 1
     assert _untouched(hk, pos) and _untouched(hv, pos)
 
 
@@ -108,7 +112,52 @@ def test_qk_norm_rope_kv_append_f16(dev):
     for bi in range(b):
         assert np.array_equal(hk[bi, :, pos[bi]], synth.f16_bits(gk[bi]))
         assert np.array_equal(hv[bi, :, pos[bi]], ovc[bi, :, pos[bi]])
+        assert f16_ulp_diff(hk[bi, :, pos[bi]], okc[bi, :, pos[bi]]) <= 1
     assert _untouched(hk, pos) and _untouched(hv, pos)
+
+
+@pytest.mark.parametrize("b,t,start,off", [(8, 1, 37, 2), (4, 5, 0, 1), (4, 7, 10, 0)])
+def test_qkrope_apply_reference_cases_on_a_lane_window(dev, b, t, start, off):
+    """qkrope::apply's own test (crates/tts-nn/src/qkrope.rs:191-260): t positions from start on a
+    lane window of a (b + 3)-lane cache; q and f32 k within rel 1e-5, f32 v within 1e-6 (here
+    exact), the cached values within 1e-3 (here: v bit-exact, k within an ulp of the oracle's
+    bits and the RNE of the kernel's own f32 k), nothing outside the window touched."""
+    heads, n_kv, hd, cap, eps = 16, 8, 128, 64, 1e-6
+    c, s = oracle.rope_table_f32(cap, hd, 1e6)
+    norms = synth.uniform(65, "norms", (2, hd), 0.5, 1.5)
+    qkv = synth.normal(65, f"qkv{b}.{t}", (b, t, (heads + 2 * n_kv) * hd))
+    kc, vc = _fill((b + 3, n_kv, cap, hd), dev), _fill((b + 3, n_kv, cap, hd), dev)
+    q, (k, v) = ops.qkrope_apply(to_dev(qkv, dev), to_dev(norms, dev), to_dev(c, dev), to_dev(s, dev),
+                                 kc.narrow(0, off, b), vc.narrow(0, off, b), heads, start, eps, f32_kv=True)
+    okc = np.full((b + 3, n_kv, cap, hd), SENTINEL, np.uint16)
+    ovc = okc.copy()
+    wq, (wk, wv) = oracle.qkrope_apply_f32(qkv, norms, c, s, okc[off:off + b], ovc[off:off + b], heads, start, eps)
+    gq, gk, gv = to_host(q), to_host(k), to_host(v)
+    assert gq.shape == (b, heads, t, hd) and gk.shape == gv.shape == (b, n_kv, t, hd)
+    assert rel(gq, wq)[1] < 1e-5
+    assert rel(gk, wk)[1] < 1e-5
+    assert np.array_equal(gv, wv)
+    hk, hv = to_host(kc), to_host(vc)
+    win = (slice(off, off + b), slice(None), slice(start, start + t))
+    assert np.array_equal(hk[win], synth.f16_bits(gk))
+    assert f16_ulp_diff(hk[win], okc[win]) <= 1
+    assert rel(synth.from_f16_bits(hk[win]), synth.from_f16_bits(okc[win]))[1] < 1e-3
+    assert np.array_equal(hv[win], ovc[win])
+    mask = np.ones(hk.shape, bool)
+    mask[win] = False
+    assert np.all(hk[mask] == SENTINEL) and np.all(hv[mask] == SENTINEL), "writes escaped the lane window"
+
+
+def test_qkrope_apply_refuses_positions_past_the_cache(dev):
+    heads, n_kv, hd, cap = 4, 2, 128, 16
+    c, s = oracle.rope_table_f32(cap, hd, 1e6)
+    qkv = to_dev(synth.normal(66, "qkv", (2, 5, (heads + 2 * n_kv) * hd)), dev)
+    norms = to_dev(synth.uniform(66, "n", (2, hd), 0.5, 1.5), dev)
+    kc, vc = _fill((2, n_kv, cap, hd), dev), _fill((2, n_kv, cap, hd), dev)
+    with pytest.raises(DttsError, match="17 positions exceed 16"):
+        ops.qkrope_apply(qkv, norms, to_dev(c, dev), to_dev(s, dev), kc, vc, heads, 12, 1e-6)
+    torch.cuda.synchronize()
+    assert np.all(to_host(kc) == SENTINEL) and np.all(to_host(vc) == SENTINEL)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])

@@ -54,6 +54,34 @@ def test_q8_0_oracle_closed_form_and_library_quantizer_agree():
     assert np.array_equal(ops.q8_0_quantize(w), blocks)
 
 
+# A block whose amax is exactly 127 has d = 127/127 = 1 and id = 1, so x * id is x itself and
+# every x.5 below is an exact tie. ggml's quantize_row_q8_0 (roundf) and candle's
+# BlockQ8_0::from_float (f32::round) round ties away from zero; round-half-even would give
+# 2, -2, 0, 0, 4, -6, 126, -126 for the first eight, so this pins the rule.
+TIE_VALUES = np.array([2.5, -2.5, 0.5, -0.5, 4.5, -6.5, 126.5, -126.5, 1.5, -1.5, 3.5, 127.0], np.float32)
+TIE_CODES = np.array([3, -3, 1, -1, 5, -7, 127, -127, 2, -2, 4, 127], np.int32)
+
+
+def tie_block_weights():
+    w = np.zeros((2, 64), np.float32)
+    w[0, :12] = TIE_VALUES
+    w[1, 32:44] = TIE_VALUES * 0.5  # amax 63.5: d = 0.5 exactly in f16, id = 2, the same ties
+    return w
+
+
+def test_q8_0_ties_round_half_away_from_zero():
+    # the block discriminates: round-half-even (numpy's rint) disagrees on 8 of the 12 codes
+    assert int(np.sum(np.rint(TIE_VALUES).astype(np.int32) != TIE_CODES)) == 8
+    w = tie_block_weights()
+    blocks = oracle.q8_0_quantize(w)
+    d = synth.from_f16_bits(blocks[..., :2].copy().view(np.uint16)[..., 0])
+    q = blocks[..., 2:].view(np.int8).astype(np.int32)
+    assert d[0, 0] == 1.0 and d[1, 1] == 0.5
+    assert np.array_equal(q[0, 0, :12], TIE_CODES) and np.all(q[0, 0, 12:] == 0)
+    assert np.array_equal(q[1, 1, :12], TIE_CODES) and np.all(q[1, 1, 12:] == 0)
+    assert np.array_equal(ops.q8_0_quantize(w), blocks)  # the library's host quantizer
+
+
 def test_q8_0_w8a8_is_exact_on_prequantized_activations():
     # activations that are already Q8_0 values quantize to themselves, so the w8a8 result is the
     # exact block dot up to the f32 scale products

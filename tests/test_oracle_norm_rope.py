@@ -94,3 +94,59 @@ def test_kv_append_places_exactly():
     for bi in range(b):
         want[bi, :, pos[bi]] = k[bi].astype(np.float16).view(np.uint16)
     assert np.array_equal(kc, want)
+
+
+# qkrope.rs:191-260's cases: (b, t, start, lane offset) on a lane window of a (b + 3)-lane cache
+QKROPE_CASES = [(8, 1, 37, 2), (4, 5, 0, 1), (4, 7, 10, 0)]
+
+
+def _qkrope_f64(qkv, norms, c, s, heads, n_kv, start, eps):
+    """An independent float64 evaluation of the composed path: norm, heads first, rope."""
+    b, t, _ = qkv.shape
+    hd = norms.shape[-1]
+    x = qkv.reshape(b, t, heads + 2 * n_kv, hd).astype(np.float64).transpose(0, 2, 1, 3)  # [b, h, t, D]
+    cc = c[start:start + t].astype(np.float64)[None, None]
+    ss = s[start:start + t].astype(np.float64)[None, None]
+    half = hd // 2
+
+    def norm_rope(v, w):
+        v = v / np.sqrt(np.mean(v ** 2, -1, keepdims=True) + eps) * w.astype(np.float64)
+        return np.concatenate([v[..., :half] * cc - v[..., half:] * ss, v[..., half:] * cc + v[..., :half] * ss], -1)
+
+    return norm_rope(x[:, :heads], norms[0]), norm_rope(x[:, heads:heads + n_kv], norms[1]), x[:, heads + n_kv:]
+
+
+def test_qkrope_apply_oracle_matches_f64_at_the_reference_cases():
+    heads, n_kv, hd, cap, eps = 16, 8, 128, 64, 1e-6
+    c, s = oracle.rope_table_f32(cap, hd, 1e6)
+    norms = synth.uniform(54, "norms", (2, hd), 0.5, 1.5)
+    for b, t, start, off in QKROPE_CASES:
+        qkv = synth.normal(54, f"qkv{b}.{t}", (b, t, (heads + 2 * n_kv) * hd))
+        kc = np.full((b + 3, n_kv, cap, hd), 0x5555, np.uint16)
+        vc = kc.copy()
+        q, (k, v) = oracle.qkrope_apply_f32(qkv, norms, c, s, kc[off:off + b], vc[off:off + b], heads, start, eps)
+        wq, wk, wv = _qkrope_f64(qkv, norms, c, s, heads, n_kv, start, eps)
+        assert q.shape == (b, heads, t, hd) and k.shape == v.shape == (b, n_kv, t, hd)
+        assert oracle.abs_and_rel(q.ravel(), wq.astype(np.float32).ravel())[1] < 1e-6
+        assert oracle.abs_and_rel(k.ravel(), wk.astype(np.float32).ravel())[1] < 1e-6
+        assert np.array_equal(v, wv.astype(np.float32))  # v passes through untouched
+        win_k, win_v = kc[off:off + b, :, start:start + t], vc[off:off + b, :, start:start + t]
+        assert np.array_equal(win_k, synth.f16_bits(k)) and np.array_equal(win_v, synth.f16_bits(v))
+        mask = np.ones(kc.shape, bool)
+        mask[off:off + b, :, start:start + t] = False
+        assert np.all(kc[mask] == 0x5555) and np.all(vc[mask] == 0x5555), "writes escaped the window"
+
+
+def test_qkrope_apply_oracle_at_one_position_is_the_decode_form():
+    """t = 1 with every lane at `start` is the per-lane decode restatement bit for bit."""
+    b, heads, n_kv, hd, cap, start = 6, 4, 2, 128, 32, 19
+    c, s = oracle.rope_table_f32(cap, hd, 1e6)
+    qkv = synth.normal(55, "qkv", (b, 1, (heads + 2 * n_kv) * hd))
+    norms = synth.uniform(55, "n", (2, hd), 0.5, 1.5)
+    kc1 = np.zeros((b, n_kv, cap, hd), np.uint16)
+    vc1, kc2, vc2 = kc1.copy(), kc1.copy(), kc1.copy()
+    q1, (k1, _) = oracle.qkrope_apply_f32(qkv, norms, c, s, kc1, vc1, heads, start, 1e-6)
+    q2, k2 = oracle.qk_norm_rope_append_f32(qkv[:, 0], norms, c, s, np.full(b, start, np.int32), kc2, vc2,
+                                            heads, n_kv, 1e-6)
+    assert np.array_equal(q1[:, :, 0], q2) and np.array_equal(k1[:, :, 0], k2)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
