@@ -49,6 +49,36 @@ def dominant(stages_runs):
     return name, by[name], by
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def kernel_rooflines(by):
+    """Every kernel of one decode at its own roofline: MFMA-bound when its algorithmic intensity
+    (FLOP per byte, each input, output and weight once) is above the ridge, HBM-bound below."""
+    ridge = PEAK_TFLOPS_F16 * 1e12 / (PEAK_HBM_GBS * 1e9)
+    out = []
+    for name, e in sorted(by.items(), key=lambda kv: -kv[1]["ms"]):
+        per = e["ms"] / e["launches"]
+        if e["flops"] / max(e["bytes"], 1.0) > ridge:
+            ach, peak, unit, bound = e["flops"] / e["launches"] / (per / 1e3) / 1e12, PEAK_TFLOPS_F16, "TFLOP/s", "mfma"
+        else:
+            ach, peak, unit, bound = e["bytes"] / e["launches"] / (per / 1e3) / 1e9, PEAK_HBM_GBS, "GB/s", "hbm"
+        out.append({"kernel": name, "launches": e["launches"], "ms_per_launch": round(per, 4),
+                    "share": None, "bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": unit,
+                    "frac": round(ach / peak, 4)})
+    total = sum(e["ms"] for e in by.values())
+    for o, (name, e) in zip(out, sorted(by.items(), key=lambda kv: -kv[1]["ms"])):
+        o["share"] = round(e["ms"] / total, 4)
+    return out
+
+
 def cpu_baseline(geo, weights, latent_np, budget_s=12.0, max_lanes=48):
     import oracle  # noqa: F401  (the oracle is the timed CPU baseline, never the product)
     from oracle import codec as ocodec
@@ -69,7 +99,7 @@ def cpu_baseline(geo, weights, latent_np, budget_s=12.0, max_lanes=48):
     done = len(lane_s)
     audio_s = done * frames * geo.hop / SAMPLE_RATE
     med = sorted(lane_s)[done // 2]
-    return dict(value=round(audio_s / wall, 3), unit="audio-s/s", cores=threads, kind="port",
+    return dict(value=round(audio_s / wall, 3), unit="audio-s/s", cores=threads, kind="port", cpu_model=cpu_model(),
                 sample=f"{done} lane(s) x {frames} frames of the same workload through the oracle's "
                        f"f32 restatement of the reference CPU route (SnakeBeta passes; pad+cat+GEMM+bias "
                        f"per conv; polyphase transposed convs), {wall:.1f} s on {threads} threads; per lane "
@@ -395,6 +425,54 @@ def workload_front(dev, args):
                   "frac_mfma_peak": round(res["front"]["tflops"] / PEAK_TFLOPS_F16, 4)})
 
 
+def workload_cfg5f32(dev, args):
+    """Config 5's geometry at the reference's own precision (f32 storage and arithmetic,
+    WAV_DTYPE = F32): 48 lanes x 250 frames through dtts_codec_decode_f32. An extra line; the f16
+    decode stays the headline."""
+    import numpy as np
+    import torch
+
+    from dtts import codec, synth
+
+    geo = codec.CONFIG5
+    lanes, frames = args.lanes, args.frames
+    model = codec.Codec(geo, codec.random_weights(geo, seed=0), dev, dtype="f32")
+    latent = torch.from_numpy(synth.normal(0, "latent", (lanes, frames, geo.latent_dim))).to(dev)
+    audio = torch.empty((lanes, frames * geo.hop), dtype=torch.float32, device=dev)
+    model.workspace(lanes, frames)
+    t = _time(lambda: model.decode(latent, out=audio), reps=5, warm=1)
+    if not torch.isfinite(audio).all():
+        raise SystemExit("bench: non-finite f32 audio")
+    stages = model.profile(latent, out=audio)
+    by = {}
+    for st in stages:
+        e = by.setdefault(st["kernel"], dict(flops=0.0, bytes=0.0, ms=0.0, launches=0))
+        e["flops"] += st["flops"]
+        e["bytes"] += st["bytes"]
+        e["ms"] += st["ms"]
+        e["launches"] += 1
+    ridge = PEAK_TFLOPS_F32 * 1e12 / (PEAK_HBM_GBS * 1e9)
+    kern = []
+    for name, e in sorted(by.items(), key=lambda kv: -kv[1]["ms"]):
+        per = e["ms"] / e["launches"]
+        mfma = e["flops"] / max(e["bytes"], 1.0) > ridge
+        ach = (e["flops"] if mfma else e["bytes"]) / e["launches"] / (per / 1e3) / (1e12 if mfma else 1e9)
+        peak = PEAK_TFLOPS_F32 if mfma else PEAK_HBM_GBS
+        kern.append({"kernel": name, "launches": e["launches"], "ms_per_launch": round(per, 4),
+                     "bound": "mfma" if mfma else "hbm", "achieved": round(ach, 1), "peak": peak,
+                     "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(ach / peak, 4)})
+    audio_s = lanes * frames * geo.hop / SAMPLE_RATE
+    flops = lanes * frames * geo.flops_per_frame()
+    del model
+    torch.cuda.empty_cache()
+    return _line("config5 geometry at f32 (the reference's WAV_DTYPE): codec decoder stack, 48 lanes x 250 frames, "
+                 "f32 storage and arithmetic on the f32 matrix cores",
+                 "codec audio-sec/sec at 48 lanes (f32)", audio_s / (t / 1e3), "audio-s/s",
+                 {"ms_per_step": round(t, 3), "tflops": round(flops / (t / 1e3) / 1e12, 2),
+                  "frac_f32_matrix_peak": round(flops / (t / 1e3) / 1e12 / PEAK_TFLOPS_F32, 4), "kernels": kern},
+                 {"dtype": "f32"})
+
+
 # ---------------------------------------------------------------- rocprofv3 counter digest
 
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: a mul kernel reading and writing 1 GiB
@@ -443,9 +521,6 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
     return out
 
 
-SIMDS = 1024  # MI355X: 256 CUs x 4 SIMDs
-
-
 def pmc_counters(stages_json, csv_paths):
     """Per-kernel SQ/GRBM counters of one decode from rocprofv3 --pmc runs (one CSV per pass; the
     first dtts dispatches of each are the decode, in stage order, as for pmc_summary): the mean
@@ -482,14 +557,21 @@ def pmc_counters(stages_json, csv_paths):
             k["valu_per_mfma"] = round(c.get("SQ_INSTS_VALU", 0.0) / c["SQ_INSTS_MFMA"], 3)
         if c.get("SQ_ACTIVE_INST_LDS"):
             k["lds_bank_conflict_per_lds_cycle"] = round(c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_ACTIVE_INST_LDS"], 4)
-        if c.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
-            k["mfma_busy_frac"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * SIMDS), 4)
+        if c.get("SQ_BUSY_CU_CYCLES") and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            # per-SIMD MFMA-busy cycles over the CUs' busy cycles (both summed over the chip; four
+            # SIMDs per CU). GRBM_GUI_ACTIVE reads as the sum over the 8 XCDs, so it is not used.
+            k["mfma_busy_frac"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * c["SQ_BUSY_CU_CYCLES"]), 4)
+        if c.get("SQ_BUSY_CU_CYCLES") and "SQ_INSTS_VALU" in c:
+            # wave64 VALU instructions take 4 issue cycles on a SIMD
+            k["valu_issue_frac"] = round(4.0 * c["SQ_INSTS_VALU"] / (4.0 * c["SQ_BUSY_CU_CYCLES"]), 4)
+        if c.get("SQ_BUSY_CU_CYCLES") and "SQ_LDS_IDX_ACTIVE" in c:
+            k["lds_active_frac"] = round(c["SQ_LDS_IDX_ACTIVE"] / c["SQ_BUSY_CU_CYCLES"], 4)
         k["tflops"] = round(k["flops"] / k["ms"] / 1e9, 1)
     return out
 
 
 WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
-             "stack": workload_stack, "front": workload_front}
+             "stack": workload_stack, "front": workload_front, "cfg5f32": workload_cfg5f32}
 
 
 def main():
@@ -508,7 +590,8 @@ def main():
                     help="digest rocprofv3 --pmc runs of SQ/GRBM counters into per-kernel figures (no GPU)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "codec_config5_pmc.json"),
                     help="per-kernel traffic from --pmc-summary, reported in roofline.traffic")
-    ap.add_argument("--workload", default="cfg5", choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5", "all"],
+    ap.add_argument("--workload", default="cfg5",
+                    choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5f32", "cfg5", "all"],
                     help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops; stack "
                          "times the decoder-stack decode step; front the codec front half and document decode")
     ap.add_argument("--copy-probe", action="store_true",
@@ -535,7 +618,8 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.workload != "cfg5":
-        for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front"] if args.workload == "all" else [args.workload]):
+        for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5f32"] if args.workload == "all"
+                  else [args.workload]):
             print(json.dumps(WORKLOADS[w](dev, args)), flush=True)
         if args.workload != "all":
             return
@@ -553,12 +637,20 @@ def main():
     for _ in range(args.warmup):
         model.decode(latent, out=audio)
     torch.cuda.synchronize()
+    # per-step HIP events on the decode's stream, recorded between steps (no host wait inside)
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    events[0].record()
+    for i in range(args.steps):
         model.decode(latent, out=audio)
+        events[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = wall * 1e3 / args.steps
+    step_ms = sorted(events[i].elapsed_time(events[i + 1]) for i in range(args.steps))
+    steps_stat = {"median_ms": round(step_ms[len(step_ms) // 2], 4), "min_ms": round(step_ms[0], 4),
+                  "max_ms": round(step_ms[-1], 4), "first_ms": round(events[0].elapsed_time(events[1]), 4),
+                  "last_ms": round(events[-2].elapsed_time(events[-1]), 4)}
     audio_s = args.lanes * args.frames * geo.hop / SAMPLE_RATE
     value = audio_s / (ms / 1e3)
     if not torch.isfinite(audio.float()).all():
@@ -621,7 +713,9 @@ def main():
                    "lanes": args.lanes, "frames": args.frames, "latent_dim": geo.latent_dim,
                    "channels": list(geo.channels), "rates": list(geo.rates),
                    "audio_s_per_step": audio_s, "parallelism": "single GPU"},
+        "step_ms": steps_stat,
         "roofline": roof,
+        "kernels": kernel_rooflines(by),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

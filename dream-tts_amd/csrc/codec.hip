@@ -22,6 +22,7 @@
 struct dtts_codec {
     dtts_codec_geometry geo;
     dtts_codec_weights w;
+    bool f32;  // made by dtts_codec_create_f32: every tensor f32, every conv the f32 kernel
     // act1 of unit 0 of each block, repeated over the TransConv's `rate` output phases (the
     // TransConv's output channel p*C + c is channel c of phase p).
     std::vector<float *> phase_alpha, phase_brecip;
@@ -75,7 +76,9 @@ dtts_conv_desc desc(int64_t lanes, int64_t len, int64_t cin, int64_t cout, int64
 
 using dtts::set_error;
 
-extern "C" int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, dtts_codec **out) {
+namespace dtts {
+namespace {
+int codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, bool f32, dtts_codec **out) {
     DTTS_REQUIRE(geo && w && out, "dtts_codec_create: null argument");
     *out = nullptr;
     const dtts_codec_geometry &g = *geo;
@@ -104,6 +107,7 @@ extern "C" int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_code
     DTTS_REQUIRE(c, "dtts_codec_create: out of host memory");
     c->geo = g;
     c->w = *w;
+    c->f32 = f32;
     for (int64_t i = 0; i < g.n_blocks; ++i) {
         const int64_t cout = g.channels[i + 1];
         const int64_t rate = g.rates[i];
@@ -131,6 +135,16 @@ extern "C" int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_code
     *out = c;
     return DTTS_OK;
 }
+}  // namespace
+}  // namespace dtts
+
+extern "C" int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, dtts_codec **out) {
+    return dtts::codec_create(geo, w, false, out);
+}
+
+extern "C" int dtts_codec_create_f32(const dtts_codec_geometry *geo, const dtts_codec_weights *w, dtts_codec **out) {
+    return dtts::codec_create(geo, w, true, out);
+}
 
 extern "C" void dtts_codec_destroy(dtts_codec *c) {
     if (!c) return;
@@ -145,7 +159,8 @@ extern "C" int64_t dtts_codec_hop(const dtts_codec *c) { return c ? dtts::hop_of
 
 extern "C" size_t dtts_codec_workspace_bytes(const dtts_codec *c, int64_t lanes, int64_t frames) {
     if (!c || lanes <= 0 || frames <= 0) return 0;
-    const size_t one = dtts::round_up(static_cast<size_t>(lanes * dtts::stage_elems(c->geo, frames)) * 2, 256);
+    const size_t esize = c->f32 ? 4 : 2;
+    const size_t one = dtts::round_up(static_cast<size_t>(lanes * dtts::stage_elems(c->geo, frames)) * esize, 256);
     return 4 * one;
 }
 
@@ -159,12 +174,13 @@ struct Stage {
     char name[32];
 };
 
-int run_stage(const Stage &st, hipStream_t stream) {
-    return st.ru ? residual_unit_nlc_f16(&st.r, stream) : conv1d_nlc_f16(&st.d, stream);
+int run_stage(const Stage &st, bool f32, hipStream_t stream) {
+    if (st.ru) return residual_unit_nlc_f16(&st.r, stream);
+    return f32 ? conv1d_nlc_f32(&st.d, stream) : conv1d_nlc_f16(&st.d, stream);
 }
 
 // The decode as a list of conv launches over the workspace's four buffers.
-int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes, int64_t frames,
+int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lanes, int64_t frames,
                void *workspace, size_t ws_bytes, std::vector<Stage> &plan) {
     DTTS_REQUIRE(c, "dtts_codec_decode: null codec");
     DTTS_REQUIRE(lanes > 0 && frames > 0, "dtts_codec_decode: empty shape");
@@ -215,7 +231,7 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
         probe.channels = cout;
         probe.k = g.ru_kernel;
         probe.x = probe.w1 = probe.w2 = probe.b1 = probe.b2 = probe.y = buf[0];
-        const bool fused = [&] {
+        const bool fused = !c->f32 && [&] {
             for (int j = 0; j < 3; ++j) {
                 probe.dilation = g.ru_dilations[j];
                 const dtts_codec_unit &un = blk.units[j];
@@ -318,19 +334,38 @@ int build_plan(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int
 }  // namespace
 }  // namespace dtts
 
-extern "C" int dtts_codec_decode(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes,
-                                 int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
-    DTTS_REQUIRE(lanes >= 0 && frames >= 0, "dtts_codec_decode: negative shape");
+namespace dtts {
+namespace {
+int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *latent, void *audio, int64_t lanes,
+                 int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    DTTS_REQUIRE(lanes >= 0 && frames >= 0, "%s: negative shape", name);
     if (lanes == 0 || frames == 0) return DTTS_OK;
-    std::vector<dtts::Stage> plan;
-    int rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
+    DTTS_REQUIRE(c, "%s: null codec", name);
+    DTTS_REQUIRE(c->f32 == f32, "%s: the codec was made by %s", name,
+                 c->f32 ? "dtts_codec_create_f32 (decode it with dtts_codec_decode_f32)"
+                        : "dtts_codec_create (decode it with dtts_codec_decode)");
+    std::vector<Stage> plan;
+    int rc = build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
     if (rc != DTTS_OK) return rc;
-    for (const dtts::Stage &st : plan)
-        if ((rc = dtts::run_stage(st, stream)) != DTTS_OK) return rc;
+    for (const Stage &st : plan)
+        if ((rc = run_stage(st, c->f32, stream)) != DTTS_OK) return rc;
     return DTTS_OK;
 }
+}  // namespace
+}  // namespace dtts
 
-extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes,
+extern "C" int dtts_codec_decode(const dtts_codec *c, const dtts_f16 *latent, dtts_f16 *audio, int64_t lanes,
+                                 int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    return dtts::codec_decode("dtts_codec_decode", c, false, latent, audio, lanes, frames, workspace, ws_bytes, stream);
+}
+
+extern "C" int dtts_codec_decode_f32(const dtts_codec *c, const float *latent, float *audio, int64_t lanes,
+                                     int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    return dtts::codec_decode("dtts_codec_decode_f32", c, true, latent, audio, lanes, frames, workspace, ws_bytes,
+                              stream);
+}
+
+extern "C" int dtts_codec_profile(const dtts_codec *c, const void *latent, void *audio, int64_t lanes,
                                   int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream,
                                   dtts_codec_stage *stages, int max_stages, int *n_stages) {
     DTTS_REQUIRE(stages && n_stages && max_stages > 0, "dtts_codec_profile: no stage table");
@@ -344,7 +379,7 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, d
     int status = DTTS_OK;
     hipError_t he = hipEventRecord(ev[0], stream);
     for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
-        status = dtts::run_stage(plan[i], stream);
+        status = dtts::run_stage(plan[i], c->f32, stream);
         if (status == DTTS_OK) he = hipEventRecord(ev[i + 1], stream);
     }
     if (he == hipSuccess && status == DTTS_OK) he = hipEventSynchronize(ev.back());
@@ -365,7 +400,7 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, d
             s.bytes = 2.0 * r.lanes * r.len * c * (r.y_pre ? 3.0 : 2.0) + 2.0 * c * c * (r.k + 1);
         } else {
             const dtts_conv_desc &d = plan[i].d;
-            snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::conv_kernel_name(&d));
+            snprintf(s.kernel, sizeof(s.kernel), "%s", c->f32 ? dtts::conv_f32_kernel_name(&d) : dtts::conv_kernel_name(&d));
             s.lanes = d.lanes;
             s.len = d.len;
             s.cin = d.cin;
@@ -374,7 +409,8 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const dtts_f16 *latent, d
             s.dilation = d.dilation;
             s.flops = 2.0 * d.lanes * d.len * d.cin * d.cout * d.k;
             const double outs = (d.y_pre ? 2.0 : 1.0) + (d.residual ? 1.0 : 0.0);
-            s.bytes = 2.0 * d.lanes * d.len * (d.cin + d.cout * outs) + 2.0 * d.cout * d.k * d.cin;
+            const double es = c->f32 ? 4.0 : 2.0;
+            s.bytes = es * d.lanes * d.len * (d.cin + d.cout * outs) + es * d.cout * d.k * d.cin;
         }
         he = hipEventElapsedTime(&s.ms, ev[i], ev[i + 1]);
     }

@@ -13,6 +13,10 @@ const char *conv_path_name(const dtts_conv_desc *d);
 const char *conv_kernel_name(const dtts_conv_desc *d);
 int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream);
 
+// The f32 form (conv_nlc_f32.hip): same descriptor, f32 operands.
+const char *conv_f32_kernel_name(const dtts_conv_desc *d);
+int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream);
+
 // The fused residual unit (ru.hip).
 bool residual_unit_supported(const dtts_ru_desc *d);
 const char *residual_unit_kernel_name(const dtts_ru_desc *d);

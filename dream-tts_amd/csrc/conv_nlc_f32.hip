@@ -1,0 +1,274 @@
+// Channels-last f32 conv1d at NlcConv's own precision (crates/tts-nn/src/nlcconv.rs:15-198, its
+// CPU form nlcconv.rs:33-73; kernel nlc_conv_f32, mtl.rs:937-1065), as an implicit GEMM on the f32
+// matrix cores:
+//
+//   s[b, l, n] = bias[n] + sum_t sum_c xs[b, l + t*dil - pad_left, c] * w[n, t*cin + c]
+//   y[b, l, n] = act(res[b, l, n] + scale[n] * s)         (scale 1 and res 0 when absent)
+//
+// xs is x, or SnakeBeta(x) applied as the window is staged (full-precision sinf; a padded tap
+// stays 0, as snake(0) = 0 gives). GEMM view per lane: M = positions, N = output channels,
+// K = (tap, channel). A workgroup owns 64 positions x 64 output channels of one lane; per
+// 16-channel chunk it stages the dilated window (64 + (k-1)*dil rows x 16 channels) and the
+// 64 x k x 16 weight slice in LDS (two buffers: chunk c+1 goes from registers into one while chunk
+// c+2's loads are in flight and chunk c is multiplied, one barrier per chunk). Four waves (2 x 2)
+// each own a 32 x 32 block and run v_mfma_f32_32x32x2_f32, tap t reading the window at row offset
+// t*dil. The 32 lanes of an accumulator row are 32 consecutive output channels of one position,
+// so the epilogue's loads and stores are 128-byte runs straight from the accumulators.
+// Fewer than 32 output channels (the codec's 96 -> 1 output conv) run a direct kernel.
+#include "conv.hpp"
+#include "snake.hpp"
+
+namespace dtts {
+namespace {
+
+struct NlcF32Params {
+    const float *x, *w, *bias, *a_in, *r_in, *res, *scale;
+    float *y_pre, *y;
+    const float *a_out, *r_out;
+    int L, cin, cout, k, dil, pad_left, act;
+    int tiles_m, tiles_n, total, per_xcd;
+};
+
+constexpr int kF32BM = 64, kF32BN = 64, kF32KC = 16;
+
+__device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off, const NlcF32Params &p) {
+    float v = s;
+    if (p.bias) v += p.bias[co];
+    if (p.scale) v = p.scale[co] * v;
+    if (p.res) v += p.res[off];
+    if (p.act == 1) v = tanhf(v);
+    if (p.act == 3) v = fminf(fmaxf(v, -1.0f), 1.0f);
+    return v;
+}
+
+template <int KMAX, int HMAX, bool SNAKE>
+__global__ __launch_bounds__(256, 2) void conv_nlc_f32_mfma(NlcF32Params p) {
+    constexpr int XR = kF32BM + HMAX;                          // window rows
+    constexpr int XP = kF32KC + 1;                             // window row pitch (floats, odd: no bank conflicts)
+    constexpr int WP = KMAX * kF32KC + 1;                      // weight row pitch
+    constexpr int XN = (XR * kF32KC / 4 + 255) / 256;          // window float4s per thread
+    constexpr int WN = (kF32BN * KMAX * kF32KC / 4 + 255) / 256;  // weight float4s per thread
+    __shared__ float xs[2][XR * XP];
+    __shared__ float ws[2][kF32BN * WP];
+    const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+    if (tile >= p.total) return;
+    const int n_tile = tile % p.tiles_n;  // output channels fastest: neighbours share the window
+    const int rest = tile / p.tiles_n;
+    const int m_tile = rest % p.tiles_m;
+    const int lane_idx = rest / p.tiles_m;
+    const int co0 = n_tile * kF32BN;
+    const int l0 = m_tile * kF32BM;
+    const int rows = kF32BM + (p.k - 1) * p.dil;
+    const int K = p.k * p.cin;
+    const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int kh = lane >> 5, lr = lane & 31;
+    const int nx = rows * (kF32KC / 4), nw = kF32BN * p.k * (kF32KC / 4);
+
+    float4_t xr[XN], wr[WN];
+    auto load = [&](int c0) {
+        // window: row j holds positions l0 - pad_left + j, channels c0 .. c0+15 (four float4s)
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            const int e = tid + i * 256;
+            const int j = e >> 2, c4 = e & 3;
+            const int s = l0 - p.pad_left + j;
+            float4_t v = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (e < nx && s >= 0 && s < p.L)
+                v = *reinterpret_cast<const float4_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + c4 * 4);
+            xr[i] = v;
+        }
+        // weights: 16 consecutive input channels of one (output channel, tap) are four float4s
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int e = tid + i * 256;
+            const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
+            const int t = q >> 2, c4 = q & 3;
+            float4_t v = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (e < nw && co0 + m < p.cout)
+                v = *reinterpret_cast<const float4_t *>(p.w + static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 + c4 * 4);
+            wr[i] = v;
+        }
+    };
+    auto store = [&](int c0, int b) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            const int e = tid + i * 256;
+            if (e < nx) {
+                const int j = e >> 2, c4 = e & 3;
+                const int s = l0 - p.pad_left + j;
+                float *dst = &xs[b][j * XP + c4 * 4];  // rows are XP floats apart (odd): scalar stores
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v = xr[i][q];
+                    if constexpr (SNAKE)
+                        if (s >= 0 && s < p.L) v = snake_f32(v, p.a_in[c0 + c4 * 4 + q], p.r_in[c0 + c4 * 4 + q]);
+                    dst[q] = v;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WN; ++i) {
+            const int e = tid + i * 256;
+            if (e < nw) {
+                const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
+                float *dst = &ws[b][m * WP + q * 4];
+                dst[0] = wr[i][0];
+                dst[1] = wr[i][1];
+                dst[2] = wr[i][2];
+                dst[3] = wr[i][3];
+            }
+        }
+    };
+
+    float16_t acc = float16_t{};
+    const int nchunks = p.cin / kF32KC;
+    load(0);
+    store(0, 0);
+    if (nchunks > 1) load(kF32KC);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int b = c & 1;
+        if (c + 1 < nchunks) {
+            store((c + 1) * kF32KC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
+            if (c + 2 < nchunks) load((c + 2) * kF32KC);
+        }
+        for (int t = 0; t < p.k; ++t) {
+            // A[m][kk] = window[row m (+ tap offset)][channel kk]; B[kk][n] = w[n][tap t, channel kk]
+            const float *xa = xs[b] + (wm * 32 + lr + t * p.dil) * XP + kh;
+            const float *wb = ws[b] + (wn * 32 + lr) * WP + t * kF32KC + kh;
+#pragma unroll
+            for (int ci = 0; ci < kF32KC; ci += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[ci], wb[ci], acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int co = co0 + wn * 32 + lr;
+    if (co >= p.cout) return;
+    const int64_t lbase = static_cast<int64_t>(lane_idx) * p.L;
+    const float a_o = p.a_out ? p.a_out[co] : 0.0f, r_o = p.a_out ? p.r_out[co] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int pos = l0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+        if (pos >= p.L) continue;
+        const int64_t off = (lbase + pos) * p.cout + co;
+        float v = conv_f32_epilogue(acc[r], co, off, p);
+        if (p.y_pre) p.y_pre[off] = v;
+        if (p.a_out) v = snake_f32(v, a_o, r_o);
+        p.y[off] = v;
+    }
+}
+
+// Any shape: one thread per output, f32 accumulation in (tap, channel) order.
+__global__ __launch_bounds__(256) void conv_nlc_f32_direct(NlcF32Params p, int64_t total) {
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int co = static_cast<int>(e % p.cout);
+        const int64_t row = e / p.cout;  // lane * L + position
+        const int l = static_cast<int>(row % p.L);
+        const float *xl = p.x + (row - l) * p.cin;
+        const float *wr = p.w + static_cast<int64_t>(co) * p.k * p.cin;
+        float acc = 0.0f;
+        for (int t = 0; t < p.k; ++t) {
+            const int s = l + t * p.dil - p.pad_left;
+            if (s < 0 || s >= p.L) continue;
+            const float *xs = xl + static_cast<int64_t>(s) * p.cin;
+            for (int c = 0; c < p.cin; ++c) {
+                float v = xs[c];
+                if (p.a_in) v = snake_f32(v, p.a_in[c], p.r_in[c]);
+                acc += v * wr[t * p.cin + c];
+            }
+        }
+        float v = conv_f32_epilogue(acc, co, e, p);
+        if (p.y_pre) p.y_pre[e] = v;
+        if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
+        p.y[e] = v;
+    }
+}
+
+template <int KMAX, int HMAX>
+hipError_t launch_nlc_f32(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
+    p.tiles_n = (p.cout + kF32BN - 1) / kF32BN;
+    p.tiles_m = (p.L + kF32BM - 1) / kF32BM;
+    const int64_t total = lanes * p.tiles_m * p.tiles_n;
+    p.total = static_cast<int>(total);
+    p.per_xcd = static_cast<int>((total + 7) / 8);
+    const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
+    if (snake)
+        conv_nlc_f32_mfma<KMAX, HMAX, true><<<grid, 256, 0, stream>>>(p);
+    else
+        conv_nlc_f32_mfma<KMAX, HMAX, false><<<grid, 256, 0, stream>>>(p);
+    return hipGetLastError();
+}
+
+bool nlc_f32_tiled(const dtts_conv_desc *d) {
+    return d->cin % kF32KC == 0 && d->cout % 32 == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= 64 &&
+           aligned(d->x, 16) && aligned(d->w, 16);
+}
+
+}  // namespace
+
+const char *conv_f32_kernel_name(const dtts_conv_desc *d) {
+    if (!nlc_f32_tiled(d)) return "conv_nlc_f32_direct";
+    if (d->k == 1) return "conv_nlc_f32_mfma<1, 0";
+    return d->k == 2 && d->dilation == 1 ? "conv_nlc_f32_mfma<2, 1" : "conv_nlc_f32_mfma<7, 64";
+}
+
+int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
+    const char *name = "dtts_conv1d_nlc_f32";
+    DTTS_REQUIRE(d, "%s: null descriptor", name);
+    DTTS_REQUIRE(d->lanes >= 0 && d->len >= 0 && d->cin > 0 && d->cout > 0 && d->k > 0 && d->dilation > 0 &&
+                     d->pad_left >= 0 && d->pad_left <= (d->k - 1) * d->dilation,
+                 "%s: bad shape or pad_left", name);
+    DTTS_REQUIRE(d->act == 0 || d->act == 1 || d->act == 3, "%s: act %d unknown (0, 1 tanh, 3 clamp)", name, d->act);
+    if (d->lanes == 0 || d->len == 0) return DTTS_OK;
+    DTTS_REQUIRE(d->x && d->w && d->y, "%s: null x, w or y", name);
+    DTTS_REQUIRE((d->in_alpha == nullptr) == (d->in_brecip == nullptr) &&
+                     (d->out_alpha == nullptr) == (d->out_brecip == nullptr),
+                 "%s: snake alpha and brecip go together", name);
+    DTTS_REQUIRE(d->lanes * d->len * d->cout < (int64_t(1) << 40) && d->lanes * d->len * d->cin < (int64_t(1) << 40) &&
+                     d->len < (int64_t(1) << 30) && d->cin * d->k < (int64_t(1) << 30),
+                 "%s: shape too large", name);
+    NlcF32Params p{};
+    p.x = static_cast<const float *>(d->x);
+    p.w = static_cast<const float *>(d->w);
+    p.bias = static_cast<const float *>(d->bias);
+    p.a_in = d->in_alpha;
+    p.r_in = d->in_brecip;
+    p.res = static_cast<const float *>(d->residual);
+    p.scale = d->out_scale;
+    p.y_pre = static_cast<float *>(d->y_pre);
+    p.y = static_cast<float *>(d->y);
+    p.a_out = d->out_alpha;
+    p.r_out = d->out_brecip;
+    p.L = static_cast<int>(d->len);
+    p.cin = static_cast<int>(d->cin);
+    p.cout = static_cast<int>(d->cout);
+    p.k = static_cast<int>(d->k);
+    p.dil = static_cast<int>(d->dilation);
+    p.pad_left = static_cast<int>(d->pad_left);
+    p.act = d->act;
+    hipError_t e;
+    if (nlc_f32_tiled(d)) {
+        DTTS_REQUIRE(d->lanes * ((d->cout + kF32BN - 1) / kF32BN) * ((d->len + kF32BM - 1) / kF32BM) < (int64_t(1) << 31),
+                     "%s: too many tiles", name);
+        const bool snake = d->in_alpha != nullptr;
+        if (d->k == 1)
+            e = launch_nlc_f32<1, 0>(p, d->lanes, snake, stream);
+        else if (d->k == 2 && d->dilation == 1)
+            e = launch_nlc_f32<2, 1>(p, d->lanes, snake, stream);
+        else
+            e = launch_nlc_f32<7, 64>(p, d->lanes, snake, stream);
+    } else {
+        const int64_t total = d->lanes * d->len * d->cout;
+        conv_nlc_f32_direct<<<grid_for(total, 256, 16), 256, 0, stream>>>(p, total);
+        e = hipGetLastError();
+    }
+    DTTS_HIP_CHECK(e, name);
+    return DTTS_OK;
+}
+
+}  // namespace dtts
+
+extern "C" int dtts_conv1d_nlc_f32_ex(const dtts_conv_desc *desc, hipStream_t stream) {
+    return dtts::conv1d_nlc_f32(desc, stream);
+}

@@ -33,6 +33,7 @@ SIGNATURES = {
     "dtts_snake_nlc_f32": [_P, _P, _P, _P, _I64, _I64, _P],
     "dtts_snake_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _P],
     "dtts_conv1d_nlc_f16_ex": [_P, _P],
+    "dtts_conv1d_nlc_f32_ex": [_P, _P],
     "dtts_causal_conv1d_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "dtts_snake_conv_residual_nlc_f16": [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _I64, _P],
@@ -116,10 +117,12 @@ SIGNATURES = {
     "dtts_q8_0_dequantize_f32": [_P, _P, _I64, _I64, _P],
     "dtts_gemm_q8_0": [_P, _P, _P, _I64, _I64, _I64, _I32, _P],
     "dtts_codec_create": [_P, _P, _P],
+    "dtts_codec_create_f32": [_P, _P, _P],
     "dtts_codec_destroy": [_P],
     "dtts_codec_hop": [_P],
     "dtts_codec_workspace_bytes": [_P, _I64, _I64],
     "dtts_codec_decode": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
+    "dtts_codec_decode_f32": [_P, _P, _P, _I64, _I64, _P, _SZ, _P],
     "dtts_codec_profile": [_P, _P, _P, _I64, _I64, _P, _SZ, _P, _P, _I32, _P],
 }
 _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,

@@ -158,14 +158,22 @@ def c_geometry(geo: Geometry) -> _Geometry:
 
 
 class Codec:
-    """Device weights + a dtts_codec handle. Keeps every device tensor alive."""
+    """Device weights + a dtts_codec handle. Keeps every device tensor alive.
 
-    def __init__(self, geo: Geometry, w: HostWeights, dev):
+    dtype "f16" (the default): f16 storage with f32 arithmetic, the benchmark's form. "f32": every
+    tensor f32, the reference's own precision for its waveform stack (WAV_DTYPE = F32,
+    crates/qwen3tts/src/codec.rs:33-43), through dtts_codec_create_f32 / dtts_codec_decode_f32."""
+
+    def __init__(self, geo: Geometry, w: HostWeights, dev, dtype: str = "f16"):
+        if dtype not in ("f16", "f32"):
+            raise DttsError(f"codec: dtype {dtype!r} is not f16 or f32")
         self.geo = geo
+        self.dtype = dtype
+        self.torch_dtype = torch.float16 if dtype == "f16" else torch.float32
         self._keep = []
 
-        def f16(a):
-            t = _f16_dev(a, dev)
+        def cw(a):  # conv weights and biases, in the codec's element type
+            t = _f16_dev(a, dev) if dtype == "f16" else _f32_dev(a, dev)
             self._keep.append(t)
             return ctypes.c_void_p(t.data_ptr())
 
@@ -176,25 +184,26 @@ class Codec:
 
         g = c_geometry(geo)
         ws = _Weights()
-        ws.head_w = f16(nlc.tap_major_weight(w.head_w))
-        ws.head_b = f16(w.head_b)
+        ws.head_w = cw(nlc.tap_major_weight(w.head_w))
+        ws.head_b = cw(w.head_b)
         for i, blk in enumerate(w.blocks):
             b = ws.blocks[i]
             b.act_alpha, b.act_brecip = f32(blk["act"][0]), f32(blk["act"][1])
             r = geo.rates[i]
-            b.up_w = f16(nlc.transpose_tap_major_weight(blk["up_w"], r))
-            b.up_b = f16(nlc.transpose_bias(blk["up_b"], r))
+            b.up_w = cw(nlc.transpose_tap_major_weight(blk["up_w"], r))
+            b.up_b = cw(nlc.transpose_bias(blk["up_b"], r))
             for j, un in enumerate(blk["units"]):
                 u = b.units[j]
                 u.act1_alpha, u.act1_brecip = f32(un["act1"][0]), f32(un["act1"][1])
-                u.conv1_w, u.conv1_b = f16(nlc.tap_major_weight(un["w1"])), f16(un["b1"])
+                u.conv1_w, u.conv1_b = cw(nlc.tap_major_weight(un["w1"])), cw(un["b1"])
                 u.act2_alpha, u.act2_brecip = f32(un["act2"][0]), f32(un["act2"][1])
-                u.conv2_w, u.conv2_b = f16(nlc.tap_major_weight(un["w2"])), f16(un["b2"])
+                u.conv2_w, u.conv2_b = cw(nlc.tap_major_weight(un["w2"])), cw(un["b2"])
         ws.out_alpha, ws.out_brecip = f32(w.out_act[0]), f32(w.out_act[1])
-        ws.out_w, ws.out_b = f16(nlc.tap_major_weight(w.out_w)), f16(w.out_b)
+        ws.out_w, ws.out_b = cw(nlc.tap_major_weight(w.out_w)), cw(w.out_b)
         self._geo_c, self._w_c = g, ws
         handle = ctypes.c_void_p()
-        call("dtts_codec_create", ctypes.byref(g), ctypes.byref(ws), ctypes.byref(handle))
+        call("dtts_codec_create" if dtype == "f16" else "dtts_codec_create_f32", ctypes.byref(g), ctypes.byref(ws),
+             ctypes.byref(handle))
         self.handle = handle
         self.dev = dev
         self._ws = None
@@ -209,14 +218,15 @@ class Codec:
         return self._ws, need
 
     def decode(self, latent, out=None):
-        """latent [lanes, frames, latent_dim] f16 (device) -> audio [lanes, frames*hop] f16."""
-        if latent.dtype != torch.float16 or not latent.is_contiguous() or latent.dim() != 3:
-            raise DttsError("codec.decode: latent must be a contiguous f16 [lanes, frames, dim]")
+        """latent [lanes, frames, latent_dim] (device, the codec's dtype) -> audio [lanes, frames*hop]."""
+        if latent.dtype != self.torch_dtype or not latent.is_contiguous() or latent.dim() != 3:
+            raise DttsError(f"codec.decode: latent must be a contiguous {self.dtype} [lanes, frames, dim]")
         lanes, frames, _ = latent.shape
         audio = out if out is not None else torch.empty((lanes, frames * self.geo.hop),
-                                                        dtype=torch.float16, device=latent.device)
+                                                        dtype=self.torch_dtype, device=latent.device)
         ws, need = self.workspace(lanes, frames)
-        call("dtts_codec_decode", self.handle, ctypes.c_void_p(latent.data_ptr()),
+        call("dtts_codec_decode" if self.dtype == "f16" else "dtts_codec_decode_f32", self.handle,
+             ctypes.c_void_p(latent.data_ptr()),
              ctypes.c_void_p(audio.data_ptr()), lanes, frames, ctypes.c_void_p(ws.data_ptr()),
              ctypes.c_size_t(need), stream_handle())
         return audio
@@ -226,7 +236,7 @@ class Codec:
         kernel, shape, algorithmic flops/bytes, ms). Synchronises the stream."""
         lanes, frames, _ = latent.shape
         audio = out if out is not None else torch.empty((lanes, frames * self.geo.hop),
-                                                        dtype=torch.float16, device=latent.device)
+                                                        dtype=self.torch_dtype, device=latent.device)
         ws, need = self.workspace(lanes, frames)
         table = (_Stage * 128)()
         n = ctypes.c_int(0)

@@ -41,27 +41,31 @@ def _need(t, name, what, dtype, shape=None):
 
 def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, residual=None,
            snake_out=None, want_pre=False, act=None, scale=None, out=None):
-    """The general fused channels-last conv (dtts_conv1d_nlc_f16_ex).
+    """The general fused channels-last conv (dtts_conv1d_nlc_f16_ex, or dtts_conv1d_nlc_f32_ex
+    when x is f32: NlcConv's own precision).
 
-    x [lanes, L, cin] f16, w_tm [cout, k*cin] f16, bias [cout] f16. snake_in / snake_out are
-    (alpha, brecip) f32 pairs applied to the input as loaded / to the rounded output. act: None,
-    "tanh" or "gelu"; scale: f32 [cout] on (sum + bias) before the residual. Returns y, or
-    (y_pre, y) when want_pre."""
+    x [lanes, L, cin], w_tm [cout, k*cin], bias [cout], residual: all f16, or all f32. snake_in /
+    snake_out are (alpha, brecip) f32 pairs applied to the input as loaded / to the (rounded)
+    output. act: None, "tanh", "gelu" (f16 only) or "clamp"; scale: f32 [cout] on (sum + bias)
+    before the residual. Returns y, or (y_pre, y) when want_pre."""
     name = "nlc.conv1d"
     if x.dim() != 3:
         raise DttsError(f"{name}: x must be [lanes, L, cin]")
     lanes, length, cin = x.shape
     cout = w_tm.shape[0]
-    _need(x, name, "x", torch.float16)
-    _need(w_tm, name, "w_tm", torch.float16, (cout, k * cin))
-    _need(bias, name, "bias", torch.float16, (cout,))
-    _need(residual, name, "residual", torch.float16, (lanes, length, cout))
+    dt = x.dtype
+    if dt not in (torch.float16, torch.float32):
+        raise DttsError(f"{name}: x must be f16 or f32, not {dt}")
+    _need(x, name, "x", dt)
+    _need(w_tm, name, "w_tm", dt, (cout, k * cin))
+    _need(bias, name, "bias", dt, (cout,))
+    _need(residual, name, "residual", dt, (lanes, length, cout))
     _need(scale, name, "scale", torch.float32, (cout,))
     for pair, what, c in ((snake_in, "snake_in", cin), (snake_out, "snake_out", cout)):
         if pair is not None:
             for t in pair:
                 _need(t, name, what, torch.float32, (c,))
-    y = torch.empty((lanes, length, cout), dtype=torch.float16, device=x.device) if out is None else out
+    y = torch.empty((lanes, length, cout), dtype=dt, device=x.device) if out is None else out
     y_pre = torch.empty_like(y) if want_pre else None
     d = ConvDesc(lanes, length, cin, cout, k, dilation,
                  (k - 1) * dilation if pad_left is None else pad_left,
@@ -70,7 +74,8 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
                  _p(residual), _p(y_pre),
                  _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
                  _p(y), {None: 0, "tanh": 1, "gelu": 2, "clamp": 3}[act], _p(scale))
-    call("dtts_conv1d_nlc_f16_ex", ctypes.byref(d), stream_handle())
+    call("dtts_conv1d_nlc_f16_ex" if dt == torch.float16 else "dtts_conv1d_nlc_f32_ex", ctypes.byref(d),
+         stream_handle())
     return (y_pre, y) if want_pre else y
 
 

@@ -107,6 +107,13 @@ typedef struct dtts_conv_desc {
 
 int dtts_conv1d_nlc_f16_ex(const dtts_conv_desc *desc, hipStream_t stream);
 
+/* The same conv at NlcConv's own precision: every operand f32 (x, w, bias, residual, y_pre, y),
+ * f32 accumulation -- NlcConv::cpu_fwd / nlc_conv_f32 (crates/tts-nn/src/nlcconv.rs:33-73,
+ * mtl.rs:937-1065; the reference's op is f32-only, nlcconv.rs:185-198) with any lane count.
+ * act: 0, 1 (tanh) or 3 (clamp). Matrix cores when cin % 16 == 0, cout % 32 == 0, k <= 7,
+ * (k-1)*dilation <= 64 and x, w are 16-byte aligned; a direct kernel otherwise. */
+int dtts_conv1d_nlc_f32_ex(const dtts_conv_desc *desc, hipStream_t stream);
+
 /* nlc::causal_conv1d (crates/tts-nn/src/nlc.rs:70-132): causal, pad (k-1)*dilation. Any lane
  * count (the reference requires one, crates/tts-nn/src/nlcconv.rs:192). */
 int dtts_causal_conv1d_nlc_f16(const dtts_f16 *x, const dtts_f16 *w_tm, const dtts_f16 *bias,
@@ -610,13 +617,20 @@ typedef struct dtts_codec dtts_codec;
  * freed by dtts_codec_destroy). Uses the current HIP device. */
 int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *weights,
                       dtts_codec **out);
+/* The same stack at the reference's own precision: every conv weight and bias is f32 in the same
+ * layouts, and the codec decodes f32 activations with dtts_codec_decode_f32 only. The reference
+ * keeps its waveform stack f32 because f16 storage "missed the fixtures by 6x"
+ * (crates/qwen3tts/src/codec.rs:33-43, WAV_DTYPE = F32); every conv runs the f32 channels-last
+ * kernel (dtts_conv1d_nlc_f32_ex) and every residual unit is its two convs. */
+int dtts_codec_create_f32(const dtts_codec_geometry *geo, const dtts_codec_weights *weights,
+                          dtts_codec **out);
 void dtts_codec_destroy(dtts_codec *codec);
 
 /* Audio samples per latent frame (the product of the rates). */
 int64_t dtts_codec_hop(const dtts_codec *codec);
 
-/* Scratch bytes dtts_codec_decode needs for `lanes` x `frames` (four ping-pong activation
- * buffers at the widest stage). */
+/* Scratch bytes dtts_codec_decode (or _f32) needs for `lanes` x `frames` (four ping-pong
+ * activation buffers at the widest stage, in the codec's element type). */
 size_t dtts_codec_workspace_bytes(const dtts_codec *codec, int64_t lanes, int64_t frames);
 
 /* latent [lanes, frames, latent_dim] f16 -> audio [lanes, frames * hop] f16 in [-1, 1].
@@ -624,6 +638,11 @@ size_t dtts_codec_workspace_bytes(const dtts_codec *codec, int64_t lanes, int64_
 int dtts_codec_decode(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
                       int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);
+/* latent [lanes, frames, latent_dim] f32 -> audio [lanes, frames * hop] f32, for a codec made by
+ * dtts_codec_create_f32 (the other kind is refused, and vice versa). */
+int dtts_codec_decode_f32(const dtts_codec *codec, const float *latent, float *audio,
+                          int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
+                          hipStream_t stream);
 
 /* One launch of the decode, as dtts_codec_profile reports it. flops and bytes are algorithmic
  * (2*MACs; each input, output and weight moved once); ms is the launch's own duration between
@@ -636,10 +655,11 @@ typedef struct dtts_codec_stage {
     float ms;
 } dtts_codec_stage;
 
-/* dtts_codec_decode with a HIP event around every launch; synchronises the stream and fills
- * stages[0 .. *n_stages). The per-stage timing Codec::profile does (crates/qwen3tts/src/
- * codec.rs:465-542), at kernel granularity. */
-int dtts_codec_profile(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
+/* dtts_codec_decode (or _f32, by the codec's kind; latent and audio in its element type) with a
+ * HIP event around every launch; synchronises the stream and fills stages[0 .. *n_stages). The
+ * per-stage timing Codec::profile does (crates/qwen3tts/src/codec.rs:465-542), at kernel
+ * granularity. */
+int dtts_codec_profile(const dtts_codec *codec, const void *latent, void *audio,
                        int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
                        hipStream_t stream, dtts_codec_stage *stages, int max_stages,
                        int *n_stages);

@@ -193,7 +193,7 @@ def test_full_length_stages_match_oracle(dev, full):
         print(name, flush=True)
         _check_stage(name, geo, prep, inp, outs)
         names.append(name)
-    assert len(names) == 2 + 2 * 4 + 3 * 2 + 3 * 2  # head, 4 ups, 6 two-conv units, 6 fused, out
+    assert len(names) == 1 + 4 + 2 * 3 * 2 + 2 * 3 + 1  # head, 4 ups, 2 blocks of two-conv units, 2 fused, out
     # the codec runs exactly these launches: identical bits on every lane
     assert np.array_equal(to_host(chain.audio), full["audio"])
 

@@ -1,0 +1,115 @@
+"""The channels-last conv at NlcConv's own precision (dtts_conv1d_nlc_f32_ex) through the C ABI.
+
+NlcConv is f32-only (crates/tts-nn/src/nlcconv.rs:185-198). Bars are the reference's own:
+abs_and_rel max-rel < 1e-5 (nlc.rs:294-405) against the oracle's NlcConv::cpu_fwd restatement
+(oracle.conv1d_nlc_f32, itself pinned to torch's float64 conv1d) and against torch's float64
+conv1d directly. Shapes: nlc.rs:294-328's direct cases (odd channel counts: the direct kernel),
+nlc.rs:362-398's fused-conv shapes, the codec's own stages (several lanes, per-lane zero
+boundaries), the transposed conv's polyphase form, and the fused prologue/epilogue operands.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from dtts import nlc, synth
+
+from _util import rel, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, lanes, length, cin, cout, k):
+    x = synth.normal(seed, "x", (lanes, length, cin))
+    w = synth.normal(seed, "w", (cout, cin, k), 0, np.sqrt(2.0 / (cin * k)))
+    b = synth.normal(seed, "b", (cout,), 0, 0.01)
+    return x, w, b
+
+
+def _torch_f64(x, w, b, dil, pad_left, snake=None):
+    xt = torch.from_numpy(x).double().transpose(1, 2)  # [lanes, cin, L]
+    if snake is not None:
+        a = torch.from_numpy(np.asarray(snake[0], np.float64))[None, :, None]
+        r = torch.from_numpy(np.asarray(snake[1], np.float64))[None, :, None]
+        xt = xt + r * torch.sin(a * xt) ** 2
+    k = w.shape[2]
+    pad_right = (k - 1) * dil - pad_left
+    y = F.conv1d(F.pad(xt, (pad_left, pad_right)), torch.from_numpy(w).double(), torch.from_numpy(b).double(),
+                 dilation=dil)
+    return y.transpose(1, 2).numpy()
+
+
+@pytest.mark.parametrize("lanes,cin,cout,length,k,dil", [
+    (1, 8, 12, 40, 7, 1), (1, 16, 16, 33, 7, 3), (1, 6, 9, 20, 1, 1),             # nlc.rs:294-328
+    (1, 96, 96, 4200, 7, 9), (1, 32, 96, 4096, 7, 1), (1, 128, 192, 5000, 7, 3),  # nlc.rs:362-398
+    (1, 64, 96, 4097, 1, 1),
+    (3, 96, 96, 700, 7, 9), (2, 192, 192, 513, 7, 3), (2, 384, 384, 300, 7, 1),   # codec stages
+    (2, 768, 768, 250, 1, 1), (2, 1024, 1536, 60, 7, 1), (2, 96, 1, 900, 7, 1),
+])
+def test_causal_conv_f32_matches_oracle_and_torch(dev, lanes, cin, cout, length, k, dil):
+    x, w, b = _case(100, lanes, length, cin, cout, k)
+    got = to_host(nlc.conv1d(to_dev(x, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(b, dev), k=k,
+                             dilation=dil))
+    want = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil)
+    assert rel(got, want)[1] < 1e-5
+    assert rel(got, _torch_f64(x, w, b, dil, (k - 1) * dil))[1] < 1e-5
+
+
+def test_centered_pad_f32(dev):
+    """pad_left below (k-1)*dil: the centred form (config 1's k=7, d=3, pad 9) channels-last."""
+    x, w, b = _case(101, 2, 600, 64, 64, 7)
+    got = to_host(nlc.conv1d(to_dev(x, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(b, dev), k=7,
+                             dilation=3, pad_left=9))
+    assert rel(got, oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, 3, pad_left=9))[1] < 1e-5
+    assert rel(got, _torch_f64(x, w, b, 3, 9))[1] < 1e-5
+
+
+@pytest.mark.parametrize("lanes,c,length,k,dil", [(2, 96, 3000, 7, 9), (1, 192, 1100, 1, 1), (2, 384, 300, 7, 3)])
+def test_fused_snake_residual_f32(dev, lanes, c, length, k, dil):
+    """NlcConv's has_snake / has_res (nlc::snake_conv_residual, nlc.rs:40-68) plus the epilogue
+    SnakeBeta and y_pre the codec uses."""
+    x, w, b = _case(102, lanes, length, c, c, k)
+    res = synth.normal(102, "res", (lanes, length, c))
+    a1 = synth.uniform(102, "a1", (c,), 0.5, 1.5)
+    a2 = synth.uniform(102, "a2", (c,), 0.5, 1.5)
+    r1, r2 = (1.0 / a1).astype(np.float32), (1.0 / a2).astype(np.float32)
+    y_pre, y = nlc.conv1d(to_dev(x, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(b, dev), k=k, dilation=dil,
+                          snake_in=(to_dev(a1, dev), to_dev(r1, dev)), residual=to_dev(res, dev),
+                          snake_out=(to_dev(a2, dev), to_dev(r2, dev)), want_pre=True)
+    want_pre = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil, snake=(a1, r1), res=res)
+    assert rel(to_host(y_pre), want_pre)[1] < 1e-5
+    assert rel(to_host(y_pre), _torch_f64(x, w, b, dil, (k - 1) * dil, snake=(a1, r1)) + res)[1] < 1e-5
+    assert rel(to_host(y), oracle.snake_nlc_f32(want_pre, a2, r2))[1] < 1e-5
+
+
+def test_activations_and_scale_f32(dev):
+    x, w, b = _case(103, 2, 700, 96, 96, 7)
+    scale = synth.uniform(103, "s", (96,), 0.1, 2.0)
+    res = synth.normal(103, "res", (2, 700, 96))
+    w_tm = to_dev(nlc.tap_major_weight(w), dev)
+    plain = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, 1)
+    got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), k=7, act="tanh"))
+    assert rel(got, np.tanh(plain))[1] < 1e-5
+    got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), k=7, act="clamp"))
+    assert rel(got, np.clip(plain, -1, 1))[1] < 1e-5
+    got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), k=7, residual=to_dev(res, dev),
+                             scale=to_dev(scale, dev)))
+    assert rel(got, res + scale * plain)[1] < 1e-5
+
+
+@pytest.mark.parametrize("cin,cout,length,stride", [(1536, 768, 20, 8), (768, 384, 40, 5), (384, 192, 64, 4),
+                                                    (192, 96, 128, 3), (8, 6, 12, 2), (12, 8, 9, 5)])
+def test_transposed_conv_f32_matches_definition(dev, cin, cout, length, stride):
+    """The polyphase transposed conv at f32 against the scatter definition (nlc.rs:329-360 shapes
+    and the codec's four)."""
+    lanes, k = 2, 2 * stride
+    x = synth.normal(104, "x", (lanes, length, cin))
+    w = synth.normal(104, "w", (cin, cout, k), 0, np.sqrt(2.0 / (cout * k)))
+    b = synth.normal(104, "b", (cout,), 0, 0.01)
+    w_tm = nlc.transpose_tap_major_weight(w, stride)
+    got = to_host(nlc.causal_conv_transpose1d(to_dev(x, dev), to_dev(w_tm, dev),
+                                              to_dev(nlc.transpose_bias(b, stride), dev), stride))
+    for li in range(lanes):
+        want = oracle.conv_transpose1d_causal_f64(x[li], w, b, stride)
+        assert rel(got[li], want)[1] < 1e-5
