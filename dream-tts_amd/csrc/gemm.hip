@@ -1,8 +1,42 @@
 // Decode-shape projection GEMMs: the entry points, the [k, n] operand kernel and the direct
 // kernel for shapes the matrix-core kernels do not tile. The NT kernel is in gemm_nt.hpp.
+#include <mutex>
+
 #include "gemm_nt.hpp"
 
+// Scratch of dtts_gemm_f16_nt_noalloc: the k-range partial tiles [ranges][m][n] f32 that
+// dtts_gemm_f16_nt keeps in a caller's workspace. Each GPU the library runs on holds its own copy
+// until the process ends. Host code never passes this name to a kernel (on the host it is a
+// stand-in, not a device address): it passes the address hipGetSymbolAddress gave for the device.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace dtts {
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices];  // per device: scratch's device address there
+}  // namespace
+
+// Resolves scratch's address on the current device once (dtts_init calls this; the entry point
+// calls it again on a device it has not seen).
+int noalloc_scratch_address(const char *name, void **out) {
+    int dev = 0;
+    DTTS_HIP_CHECK(hipGetDevice(&dev), name);
+    DTTS_REQUIRE(dev >= 0 && dev < kScratchDevices, "%s: device %d beyond the %d this library tracks", name, dev,
+                 kScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        DTTS_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), name);
+        DTTS_REQUIRE(p && aligned(p, 256), "%s: scratch address %p", name, p);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DTTS_OK;
+}
+
 namespace {
 
 // The reference's own operand layout W[k, n] (skinny::matmul's b, crates/tts-nn/src/skinny.rs:
@@ -167,6 +201,24 @@ extern "C" size_t dtts_gemm_f16_workspace_bytes(int64_t m, int64_t k, int64_t n,
 extern "C" int dtts_gemm_f16_nt(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k, int64_t n,
                                 void *workspace, size_t ws_bytes, hipStream_t stream) {
     return dtts::gemm("dtts_gemm_f16_nt", a, w_nk, c, m, k, n, 0, 0, workspace, ws_bytes, stream);
+}
+
+extern "C" int dtts_gemm_f16_nt_noalloc(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k,
+                                        int64_t n, hipStream_t stream) {
+    const char *name = "dtts_gemm_f16_nt_noalloc";
+    DTTS_REQUIRE(m >= 0 && k > 0 && n > 0, "%s: bad shape (%lld, %lld, %lld)", name, (long long)m, (long long)k,
+                 (long long)n);
+    if (m == 0) return DTTS_OK;
+    const size_t need = dtts::nt_workspace_bytes(m, k, n, 0);
+    DTTS_REQUIRE(need <= kNoAllocScratchBytes,
+                 "%s: (%lld, %lld, %lld) needs %zu bytes of scratch, more than the %zu this library holds", name,
+                 (long long)m, (long long)k, (long long)n, need, kNoAllocScratchBytes);
+    void *ws = nullptr;
+    if (need > 0) {
+        const int rc = dtts::noalloc_scratch_address(name, &ws);
+        if (rc != DTTS_OK) return rc;
+    }
+    return dtts::gemm(name, a, w_nk, c, m, k, n, 0, 0, ws, need, stream);
 }
 
 extern "C" int dtts_gemm_f16_gateup_silu(const dtts_f16 *a, const dtts_f16 *w_gu, float *y, int64_t m, int64_t k,

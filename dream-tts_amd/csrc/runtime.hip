@@ -6,6 +6,8 @@
 
 namespace dtts {
 
+int noalloc_scratch_address(const char *name, void **out);  // gemm.hip
+
 static thread_local char g_error[1024] = "";
 
 void set_error(const char *fmt, ...) {
@@ -33,5 +35,6 @@ extern "C" int dtts_init(void) {
                         prop.gcnArchName);
         return DTTS_ERR_UNSUPPORTED;
     }
-    return DTTS_OK;
+    void *scratch = nullptr;  // the allocation-free projection's scratch on this device
+    return dtts::noalloc_scratch_address("dtts_init", &scratch);
 }

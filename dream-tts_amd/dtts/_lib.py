@@ -111,6 +111,7 @@ SIGNATURES = {
     "dtts_gemm_f16_skinny": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_gemm_f16_workspace_bytes": [_I64, _I64, _I64, _I32],
     "dtts_gemm_f16_nt": [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P],
+    "dtts_gemm_f16_nt_noalloc": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_gemm_f16_gateup_silu": [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "dtts_swiglu_mul_f32": [_P, _P, _P, _I64, _P],
     "dtts_q8_0_quantize": [_P, _P, _I64, _I64],

@@ -505,6 +505,17 @@ size_t dtts_gemm_f16_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t ga
 int dtts_gemm_f16_nt(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k,
                      int64_t n, void *workspace, size_t ws_bytes, hipStream_t stream);
 
+/* dtts_gemm_f16_nt without a workspace argument and without allocating: no counterpart in the
+ * reference. It is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The k-range partials live in a
+ * library-owned device array of 16 MiB per GPU, held until the process ends; shapes whose
+ * dtts_gemm_f16_workspace_bytes(m, k, n, 0) exceeds it are refused (DTTS_ERR_INVALID) before
+ * anything is enqueued. Results are bit-identical to dtts_gemm_f16_nt given that workspace. Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other streams, other threads)
+ * race, so order them. */
+int dtts_gemm_f16_nt_noalloc(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, int64_t m, int64_t k,
+                             int64_t n, hipStream_t stream);
+
 /* gate|up projection with SwiGLU fused: y[m, j] = silu(g) * u, g = A . Wg^T, u = A . Wu^T, where
  * w_gu [2*ffn, k] holds gate's rows then up's (f16, [out, in]). Replaces
  * swiglu_mul(gate.forward(x), up.forward(x)) at crates/qwen3tts/src/qwen3.rs:454-457. y f32.
