@@ -23,6 +23,11 @@ struct dtts_codec {
     dtts_codec_geometry geo;
     dtts_codec_weights w;
     bool f32;  // made by dtts_codec_create_f32: every tensor f32, every conv the f32 kernel
+    // A decode runs its lanes as two halves, one on the caller's stream and one on `side`, forked
+    // and joined with the two events: each launch of one half fills the ramp and tail of the
+    // other's (measured: 19.58 -> 19.06 ms for config 5).
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     // act1 of unit 0 of each block, repeated over the TransConv's `rate` output phases (the
     // TransConv's output channel p*C + c is channel c of phase p).
     std::vector<float *> phase_alpha, phase_brecip;
@@ -108,6 +113,16 @@ int codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, bo
     c->geo = g;
     c->w = *w;
     c->f32 = f32;
+    {
+        hipError_t e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&c->fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&c->join, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            dtts_codec_destroy(c);
+            set_error("dtts_codec_create: %s", hipGetErrorString(e));
+            return DTTS_ERR_HIP;
+        }
+    }
     for (int64_t i = 0; i < g.n_blocks; ++i) {
         const int64_t cout = g.channels[i + 1];
         const int64_t rate = g.rates[i];
@@ -148,6 +163,9 @@ extern "C" int dtts_codec_create_f32(const dtts_codec_geometry *geo, const dtts_
 
 extern "C" void dtts_codec_destroy(dtts_codec *c) {
     if (!c) return;
+    if (c->side) (void)hipStreamDestroy(c->side);
+    if (c->fork) (void)hipEventDestroy(c->fork);
+    if (c->join) (void)hipEventDestroy(c->join);
     for (float *p : c->phase_alpha)
         if (p) (void)hipFree(p);
     for (float *p : c->phase_brecip)
@@ -157,11 +175,24 @@ extern "C" void dtts_codec_destroy(dtts_codec *c) {
 
 extern "C" int64_t dtts_codec_hop(const dtts_codec *c) { return c ? dtts::hop_of(c->geo) : 0; }
 
+namespace dtts {
+namespace {
+// One plan's workspace: four ping-pong buffers of `lanes` x the widest stage.
+size_t plan_bytes(const dtts_codec *c, int64_t lanes, int64_t frames) {
+    if (lanes <= 0) return 0;
+    const size_t esize = c->f32 ? 4 : 2;
+    return 4 * round_up(static_cast<size_t>(lanes * stage_elems(c->geo, frames)) * esize, 256);
+}
+// The decode's two halves: lanes [0, first) and [first, lanes).
+int64_t first_half(int64_t lanes) { return (lanes + 1) / 2; }
+}  // namespace
+}  // namespace dtts
+
 extern "C" size_t dtts_codec_workspace_bytes(const dtts_codec *c, int64_t lanes, int64_t frames) {
     if (!c || lanes <= 0 || frames <= 0) return 0;
-    const size_t esize = c->f32 ? 4 : 2;
-    const size_t one = dtts::round_up(static_cast<size_t>(lanes * dtts::stage_elems(c->geo, frames)) * esize, 256);
-    return 4 * one;
+    // room for both halves' plans side by side; a plan over all lanes (the profile) fits too
+    const int64_t h0 = dtts::first_half(lanes);
+    return dtts::plan_bytes(c, h0, frames) + dtts::plan_bytes(c, lanes - h0, frames);
 }
 
 namespace dtts {
@@ -179,19 +210,13 @@ int run_stage(const Stage &st, bool f32, hipStream_t stream) {
     return f32 ? conv1d_nlc_f32(&st.d, stream) : conv1d_nlc_f16(&st.d, stream);
 }
 
-// The decode as a list of conv launches over the workspace's four buffers.
+// The decode of `lanes` lanes as a list of conv launches over four buffers of one plan's
+// workspace (plan_bytes). The caller has checked the pointers, the workspace's size and alignment.
 int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lanes, int64_t frames,
-               void *workspace, size_t ws_bytes, std::vector<Stage> &plan) {
-    DTTS_REQUIRE(c, "dtts_codec_decode: null codec");
-    DTTS_REQUIRE(lanes > 0 && frames > 0, "dtts_codec_decode: empty shape");
-    DTTS_REQUIRE(latent && audio && workspace, "dtts_codec_decode: null pointer");
-    const size_t need = dtts_codec_workspace_bytes(c, lanes, frames);
-    DTTS_REQUIRE(ws_bytes >= need, "dtts_codec_decode: workspace %zu bytes < %zu needed", ws_bytes, need);
-    DTTS_REQUIRE(aligned(workspace, 256), "dtts_codec_decode: workspace must be 256-byte aligned");
-
+               void *workspace, std::vector<Stage> &plan) {
     const dtts_codec_geometry &g = c->geo;
     const dtts_codec_weights &w = c->w;
-    const size_t one = need / 4;
+    const size_t one = plan_bytes(c, lanes, frames) / 4;
     char *buf[4];
     for (int i = 0; i < 4; ++i) buf[i] = static_cast<char *>(workspace) + i * one;
     auto pick = [&](const void *a, const void *b, const void *d) -> char * {
@@ -336,6 +361,16 @@ int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lan
 
 namespace dtts {
 namespace {
+int check_call(const char *name, const dtts_codec *c, const void *latent, void *audio, int64_t lanes, int64_t frames,
+               void *workspace, size_t ws_bytes) {
+    DTTS_REQUIRE(c, "%s: null codec", name);
+    DTTS_REQUIRE(latent && audio && workspace, "%s: null pointer", name);
+    const size_t need = dtts_codec_workspace_bytes(c, lanes, frames);
+    DTTS_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, need);
+    DTTS_REQUIRE(aligned(workspace, 256), "%s: workspace must be 256-byte aligned", name);
+    return DTTS_OK;
+}
+
 int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *latent, void *audio, int64_t lanes,
                  int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream) {
     DTTS_REQUIRE(lanes >= 0 && frames >= 0, "%s: negative shape", name);
@@ -344,11 +379,34 @@ int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *la
     DTTS_REQUIRE(c->f32 == f32, "%s: the codec was made by %s", name,
                  c->f32 ? "dtts_codec_create_f32 (decode it with dtts_codec_decode_f32)"
                         : "dtts_codec_create (decode it with dtts_codec_decode)");
-    std::vector<Stage> plan;
-    int rc = build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
+    int rc = check_call(name, c, latent, audio, lanes, frames, workspace, ws_bytes);
     if (rc != DTTS_OK) return rc;
-    for (const Stage &st : plan)
-        if ((rc = run_stage(st, c->f32, stream)) != DTTS_OK) return rc;
+    const size_t es = c->f32 ? 4 : 2;
+    const int64_t h0 = first_half(lanes), h1 = lanes - h0;
+    std::vector<Stage> a, b;
+    rc = build_plan(c, latent, audio, h0, frames, workspace, a);
+    if (rc == DTTS_OK && h1 > 0)
+        rc = build_plan(c, static_cast<const char *>(latent) + h0 * frames * c->geo.latent_dim * es,
+                        static_cast<char *>(audio) + h0 * frames * hop_of(c->geo) * es, h1, frames,
+                        static_cast<char *>(workspace) + plan_bytes(c, h0, frames), b);
+    if (rc != DTTS_OK) return rc;
+    if (b.empty()) {
+        for (const Stage &st : a)
+            if ((rc = run_stage(st, c->f32, stream)) != DTTS_OK) return rc;
+        return DTTS_OK;
+    }
+    // fork: the side stream starts after everything the caller enqueued before this decode
+    DTTS_HIP_CHECK(hipEventRecord(c->fork, stream), name);
+    DTTS_HIP_CHECK(hipStreamWaitEvent(c->side, c->fork, 0), name);
+    for (size_t i = 0; i < a.size() && rc == DTTS_OK; ++i) {
+        rc = run_stage(a[i], c->f32, stream);
+        if (rc == DTTS_OK) rc = run_stage(b[i], c->f32, c->side);
+    }
+    // join, whatever was enqueued: the caller's stream then orders after all of the side's work
+    const hipError_t e1 = hipEventRecord(c->join, c->side);
+    const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(stream, c->join, 0) : e1;
+    if (rc != DTTS_OK) return rc;
+    DTTS_HIP_CHECK(e2, name);
     return DTTS_OK;
 }
 }  // namespace
@@ -369,8 +427,11 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const void *latent, void 
                                   int64_t frames, void *workspace, size_t ws_bytes, hipStream_t stream,
                                   dtts_codec_stage *stages, int max_stages, int *n_stages) {
     DTTS_REQUIRE(stages && n_stages && max_stages > 0, "dtts_codec_profile: no stage table");
-    std::vector<dtts::Stage> plan;
-    int rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, ws_bytes, plan);
+    DTTS_REQUIRE(lanes > 0 && frames > 0, "dtts_codec_profile: empty shape");
+    int rc = dtts::check_call("dtts_codec_profile", c, latent, audio, lanes, frames, workspace, ws_bytes);
+    if (rc != DTTS_OK) return rc;
+    std::vector<dtts::Stage> plan;  // all lanes in one plan on one stream: each launch timed alone
+    rc = dtts::build_plan(c, latent, audio, lanes, frames, workspace, plan);
     if (rc != DTTS_OK) return rc;
     DTTS_REQUIRE(static_cast<int>(plan.size()) <= max_stages, "dtts_codec_profile: %zu stages > table of %d",
                  plan.size(), max_stages);

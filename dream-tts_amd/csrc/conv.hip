@@ -76,6 +76,7 @@ hipError_t launch_tiled(const ConvParams &p0, int64_t lanes, hipStream_t stream)
     ConvParams p = p0;
     p.tiles_m = (p.L + Cfg::BM - 1) / Cfg::BM;
     p.tiles_n = p.cout / Cfg::BN;
+    if (p.tiles_ng <= 0) p.tiles_ng = pick_tiles_ng(p.tiles_n, int64_t(Cfg::BN) * p.k * p.cin * 2);
     const int64_t total = lanes * p.tiles_m * p.tiles_n;
     p.total_tiles = static_cast<int>(total);
     p.tiles_per_xcd = static_cast<int>((total + 7) / 8);

@@ -96,7 +96,20 @@ struct ConvArgs {
     const float *scale;  // [cout] factor on (sum + bias) before the residual, or null
     int L, cin, cout, k, dil, pad_left, act;
     int tiles_m, tiles_n, total_tiles, tiles_per_xcd;
+    int tiles_ng;  // N tiles per group of the tile order (a divisor of tiles_n; tiles_n: N fastest)
 };
+
+// N tiles per group of the tile order: the largest divisor of tiles_n whose weight slices (each
+// BN x k x cin f16) fit `budget` bytes, so a group's weights stay in an XCD's 4 MB L2 while every
+// lane's M tiles pass over them. All of tiles_n when the whole weight fits (the plain N-fastest
+// order, where an M tile's window is what L2 reuses).
+inline int pick_tiles_ng(int tiles_n, int64_t slice_bytes, int64_t budget = int64_t(4) << 20) {
+    if (int64_t(tiles_n) * slice_bytes <= budget) return tiles_n;
+    int best = 1;
+    for (int g = 1; g <= tiles_n; ++g)
+        if (tiles_n % g == 0 && int64_t(g) * slice_bytes <= budget) best = g;
+    return best;
+}
 
 // Host check for direct staging: every byte offset a buffer load forms stays below 2^31, where
 // the out-of-range marker sits.
@@ -122,15 +135,21 @@ __device__ __forceinline__ float conv_sum(float acc, float bias, const float *sc
 }
 
 // XCD-aware tile order: dispatch slot b runs on XCD b % 8; each XCD takes a contiguous range of
-// (lane, m, n) tiles, N fastest, so an M tile's window is fetched into one L2 and reused by its
-// N tiles there. Returns false for the padding slots past the last tile.
+// tiles ordered (N group, lane, m, n within the group), N fastest within a group. An M tile's
+// window is fetched into one L2 and reused by the group's N tiles there, and a group's weight
+// slices stay in that L2 while the lanes' M tiles pass (pick_tiles_ng sizes the group to fit;
+// with one group this is the plain (lane, m, n) order). Returns false for the padding slots past
+// the last tile.
 __device__ __forceinline__ bool conv_tile_coords(const ConvArgs &p, int &lane_idx, int &m_tile, int &n_tile) {
     const int tile = (blockIdx.x & 7) * p.tiles_per_xcd + (blockIdx.x >> 3);
     if (tile >= p.total_tiles) return false;
-    n_tile = tile % p.tiles_n;
-    const int rest = tile / p.tiles_n;
-    m_tile = rest % p.tiles_m;
-    lane_idx = rest / p.tiles_m;
+    const int per_group = p.total_tiles / p.tiles_n * p.tiles_ng;  // lanes * tiles_m * tiles_ng
+    const int group = tile / per_group;
+    const int rest = tile - group * per_group;
+    n_tile = group * p.tiles_ng + rest % p.tiles_ng;
+    const int mm = rest / p.tiles_ng;  // lane * tiles_m + m
+    m_tile = mm % p.tiles_m;
+    lane_idx = mm / p.tiles_m;
     return true;
 }
 

@@ -40,8 +40,9 @@ struct RuArgs {
     int tiles_m, total_tiles, tiles_per_xcd;
 };
 
-// C channels; a wave owns WP positions x all C channels; NW waves; KC channels per chunk.
-template <int C_, int WP_, int NW_, int KC_>
+// C channels; a wave owns WP positions x all C channels; NW waves; KC channels per chunk; WPE_:
+// waves per SIMD the registers are budgeted for (0: as many as the LDS lets workgroups share a CU).
+template <int C_, int WP_, int NW_, int KC_, int WPE_ = 0>
 struct RuCfg {
     static constexpr int C = C_, WP = WP_, NW = NW_, KC = KC_;
     static constexpr int BM = WP * NW;  // positions per workgroup
@@ -67,6 +68,9 @@ struct RuCfg {
     static constexpr int TAB_BYTES = 8 * C * 4;
     static constexpr int LDS = 2 * STAGE + TAB_BYTES;
     static constexpr int MIN_WG = 2 * LDS <= 160 * 1024 ? 2 : 1;
+    // __launch_bounds__'s second argument is waves per SIMD: workgroups per CU x NW / 4
+    static constexpr int WPE = WPE_ > 0 ? WPE_ : (MIN_WG * NW + 3) / 4;
+    static constexpr int WPE_ARG = WPE_;
     // W2 in LDS for conv2, written once the main loop is done (both stages are free then):
     // rows padded to C + 8 halves (16 consecutive rows at one 16-byte column hit distinct banks)
     static constexpr int W2_PITCH = C + 8;
@@ -98,7 +102,7 @@ __device__ __forceinline__ half_t snake_h(half_t x, float ka, float r) {
 }
 
 template <typename Cfg, int KT>
-__global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void ru_nlc_f16(RuArgs q) {
+__global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
     constexpr int C = Cfg::C, KC = Cfg::KC, SEGS = Cfg::SEGS, TM = Cfg::TM, TN = Cfg::TN, NW = Cfg::NW;
     constexpr int APITCH = Cfg::APITCH;
     __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
@@ -486,8 +490,8 @@ bool ru_shape_ok(const dtts_ru_desc *d) {
 
 template <typename Cfg>
 const char *ru_name(char *buf, size_t n, int k) {
-    snprintf(buf, n, "ru_nlc_f16<dtts::(anonymous namespace)::RuCfg<%d, %d, %d, %d>, %d>", Cfg::C, Cfg::WP, Cfg::NW,
-             Cfg::KC, k == Cfg::KMAX ? Cfg::KMAX : 0);
+    snprintf(buf, n, "ru_nlc_f16<dtts::(anonymous namespace)::RuCfg<%d, %d, %d, %d, %d>, %d>", Cfg::C, Cfg::WP, Cfg::NW,
+             Cfg::KC, Cfg::WPE_ARG, k == Cfg::KMAX ? Cfg::KMAX : 0);
     return buf;
 }
 

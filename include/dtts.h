@@ -645,7 +645,11 @@ int64_t dtts_codec_hop(const dtts_codec *codec);
 size_t dtts_codec_workspace_bytes(const dtts_codec *codec, int64_t lanes, int64_t frames);
 
 /* latent [lanes, frames, latent_dim] f16 -> audio [lanes, frames * hop] f16 in [-1, 1].
- * Enqueues ~35 kernels on `stream`; workspace must hold dtts_codec_workspace_bytes bytes. */
+ * Enqueues ~35 kernels per half of the lanes: the first half on `stream`, the second on a stream
+ * the codec owns, forked from and joined back into `stream` with events, so the call is ordered
+ * on `stream` like any other work (the two halves overlap each other's ramps and tails). The
+ * workspace must hold dtts_codec_workspace_bytes bytes. Calls on one codec share its side stream
+ * and events: order them (one host thread at a time). */
 int dtts_codec_decode(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
                       int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);
