@@ -502,9 +502,10 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
     n = len(stages)
     if len(fd) < n or len(wd) < n:
         raise SystemExit("pmc-summary: fewer dtts dispatches than stages")
-    # the first n dispatches are the timed decode (steps=1, warmup=0), in stage order
+    # the last n dispatches are the profile run's: one plan over all lanes on one stream, in stage
+    # order (the timed decode before it interleaves its two half-batch plans)
     out = {"fetch_scale": cf, "write_scale": cw, "kernels": {}, "stages": []}
-    for st, f, w in zip(stages, fd[:n], wd[:n]):
+    for st, f, w in zip(stages, fd[-n:], wd[-n:]):
         rd, wb = float(f["Counter_Value"]) * 1024 * cf, float(w["Counter_Value"]) * 1024 * cw
         out["stages"].append({"name": st["name"], "kernel": st["kernel"], "fetch_bytes": rd, "write_bytes": wb,
                               "alg_bytes": st["bytes"]})
@@ -523,7 +524,7 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
 
 def pmc_counters(stages_json, csv_paths):
     """Per-kernel SQ/GRBM counters of one decode from rocprofv3 --pmc runs (one CSV per pass; the
-    first dtts dispatches of each are the decode, in stage order, as for pmc_summary): the mean
+    last dtts dispatches of each are the profile run's, in stage order, as for pmc_summary): the mean
     per launch of every counter, plus VALU instructions per MFMA instruction, the share of LDS
     instruction cycles lost to bank conflicts and the MFMA-busy fraction of the SIMDs."""
     import csv
@@ -540,7 +541,7 @@ def pmc_counters(stages_json, csv_paths):
         order = sorted(disp)
         if len(order) < n:
             raise SystemExit(f"pmc-counters: {len(order)} dtts dispatches in {path} < {n} stages")
-        for i, d in enumerate(order[:n]):
+        for i, d in enumerate(order[-n:]):
             per_stage[i].update(disp[d])
     out = {"source": [os.path.basename(p) for p in csv_paths], "kernels": {}}
     for st, c in zip(stages, per_stage):

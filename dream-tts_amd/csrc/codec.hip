@@ -175,6 +175,8 @@ extern "C" void dtts_codec_destroy(dtts_codec *c) {
 
 extern "C" int64_t dtts_codec_hop(const dtts_codec *c) { return c ? dtts::hop_of(c->geo) : 0; }
 
+bool dtts::codec_is_f32(const dtts_codec *c) { return c && c->f32; }
+
 namespace dtts {
 namespace {
 // One plan's workspace: four ping-pong buffers of `lanes` x the widest stage.

@@ -305,7 +305,8 @@ namespace {
 
 struct DocPlan {
     int64_t lanes, frames, spf;  // windows run as lanes, each `frames` long; samples per frame
-    size_t front, latent, codec, audio, total;
+    bool f32;                    // an f32 waveform stack: its latent widened from the front half's f16
+    size_t front, latent, latent32, codec, audio, total;
 };
 
 bool doc_plan(const dtts_codec_front *f, const dtts_codec *c, int64_t n, int64_t chunk, int64_t context, DocPlan &p) {
@@ -319,6 +320,8 @@ bool doc_plan(const dtts_codec_front *f, const dtts_codec *c, int64_t n, int64_t
     int64_t up = 1;
     for (int64_t i = 0; i < f->geo.n_up; ++i) up *= f->geo.up_ratios[i];
     p.spf = up * dtts_codec_hop(c);
+    p.f32 = codec_is_f32(c);
+    const size_t es = p.f32 ? 4 : 2;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t at = off;
@@ -327,14 +330,16 @@ bool doc_plan(const dtts_codec_front *f, const dtts_codec *c, int64_t n, int64_t
     };
     p.front = take(dtts_codec_front_workspace_bytes(f, p.lanes, p.frames));
     p.latent = take(2 * static_cast<size_t>(p.lanes * p.frames * up * f->geo.latent_dim));
+    p.latent32 = take(p.f32 ? 4 * static_cast<size_t>(p.lanes * p.frames * up * f->geo.latent_dim) : 0);
     p.codec = take(dtts_codec_workspace_bytes(c, p.lanes, p.frames * up));
-    p.audio = take(2 * static_cast<size_t>(p.lanes * p.frames * p.spf));
+    p.audio = take(es * static_cast<size_t>(p.lanes * p.frames * p.spf));
     p.total = off;
     return true;
 }
 
 // out[o] = window w's sample at o - w's chunk start + its context's length, w = (o / spf) / chunk
-__global__ __launch_bounds__(256) void doc_gather_kernel(const half_t *audio, float *out, int64_t total, int64_t spf,
+template <typename T>
+__global__ __launch_bounds__(256) void doc_gather_kernel(const T *audio, float *out, int64_t total, int64_t spf,
                                                          int64_t chunk, int64_t context, int64_t win_len) {
     for (int64_t o = blockIdx.x * int64_t(256) + threadIdx.x; o < total; o += int64_t(gridDim.x) * 256) {
         const int64_t w = (o / spf) / chunk;
@@ -342,6 +347,11 @@ __global__ __launch_bounds__(256) void doc_gather_kernel(const half_t *audio, fl
         const int64_t from = start > context ? start - context : 0;
         out[o] = static_cast<float>(audio[w * win_len + (start - from) * spf + (o - start * spf)]);
     }
+}
+
+__global__ __launch_bounds__(256) void widen_f16_kernel(const half_t *x, float *y, int64_t n) {
+    for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+        y[i] = static_cast<float>(x[i]);
 }
 
 }  // namespace
@@ -384,14 +394,28 @@ extern "C" int dtts_codec_decode_document(const dtts_codec_front *f, const dtts_
     }
     char *ws = static_cast<char *>(workspace);
     dtts_f16 *latent = reinterpret_cast<dtts_f16 *>(ws + p.latent);
-    dtts_f16 *wav = reinterpret_cast<dtts_f16 *>(ws + p.audio);
     FRONT_STEP(dtts::front_decode_staged(f, latent, p.lanes, p.frames, ws + p.front, p.latent - p.front, stream, name));
     int64_t up = 1;
     for (int64_t i = 0; i < f->geo.n_up; ++i) up *= f->geo.up_ratios[i];
-    FRONT_STEP(dtts_codec_decode(c, latent, wav, p.lanes, p.frames * up, ws + p.codec, p.audio - p.codec, stream));
     const int64_t total = n * p.spf;
-    dtts::doc_gather_kernel<<<dtts::grid_for(total, 256), 256, 0, stream>>>(
-        reinterpret_cast<const dtts::half_t *>(wav), audio, total, p.spf, chunk, context, p.frames * p.spf);
+    if (p.f32) {
+        // the reference's own precision for the waveform stack: the latent widened exactly
+        float *latent32 = reinterpret_cast<float *>(ws + p.latent32);
+        float *wav = reinterpret_cast<float *>(ws + p.audio);
+        const int64_t ne = p.lanes * p.frames * up * f->geo.latent_dim;
+        dtts::widen_f16_kernel<<<dtts::grid_for(ne, 256), 256, 0, stream>>>(
+            reinterpret_cast<const dtts::half_t *>(latent), latent32, ne);
+        DTTS_LAUNCH_CHECK(name);
+        FRONT_STEP(dtts_codec_decode_f32(c, latent32, wav, p.lanes, p.frames * up, ws + p.codec, p.audio - p.codec,
+                                         stream));
+        dtts::doc_gather_kernel<float><<<dtts::grid_for(total, 256), 256, 0, stream>>>(wav, audio, total, p.spf, chunk,
+                                                                                      context, p.frames * p.spf);
+    } else {
+        dtts_f16 *wav = reinterpret_cast<dtts_f16 *>(ws + p.audio);
+        FRONT_STEP(dtts_codec_decode(c, latent, wav, p.lanes, p.frames * up, ws + p.codec, p.audio - p.codec, stream));
+        dtts::doc_gather_kernel<dtts::half_t><<<dtts::grid_for(total, 256), 256, 0, stream>>>(
+            reinterpret_cast<const dtts::half_t *>(wav), audio, total, p.spf, chunk, context, p.frames * p.spf);
+    }
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }

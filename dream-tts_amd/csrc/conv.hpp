@@ -17,6 +17,9 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream);
 const char *conv_f32_kernel_name(const dtts_conv_desc *d);
 int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream);
 
+// True for a codec made by dtts_codec_create_f32 (codec.hip).
+bool codec_is_f32(const dtts_codec *c);
+
 // The fused residual unit (ru.hip).
 bool residual_unit_supported(const dtts_ru_desc *d);
 const char *residual_unit_kernel_name(const dtts_ru_desc *d);

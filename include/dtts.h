@@ -687,7 +687,8 @@ int dtts_codec_profile(const dtts_codec *codec, const void *latent, void *audio,
  * lanes of one length (for n < span: n, the later windows padded like the rest, which leaves the
  * kept audio of a causal decoder unchanged). codes [n, n_books] int32 on the HOST;
  * audio [n * samples_per_frame] f32 on the device, samples_per_frame = prod(up_ratios) *
- * dtts_codec_hop(codec). */
+ * dtts_codec_hop(codec). A codec made by dtts_codec_create_f32 runs the waveform stack at f32 (the
+ * reference's WAV_DTYPE) on the front half's latent widened exactly from f16. */
 size_t dtts_codec_document_workspace_bytes(const dtts_codec_front *front, const dtts_codec *codec, int64_t n,
                                            int64_t chunk, int64_t context);
 int dtts_codec_decode_document(const dtts_codec_front *front, const dtts_codec *codec, const int32_t *codes,

@@ -85,4 +85,7 @@ def decode_f32_reference(geo, prep, latent):
         x = u
     s = snake_nlc_f32(x, *prep["out_act"])
     y = conv1d_nlc_cat_gemm_f32(s, prep["out"]["w32"], prep["out"]["b32"], 1)
+    # tanh (the benchmark's form) or Codec::forward's clamp to [-1, 1] (codec.rs:433-436)
+    if getattr(geo, "out_clamp", False):
+        return np.clip(y.reshape(length), -1.0, 1.0)
     return np.tanh(y.reshape(length))

@@ -85,17 +85,23 @@ def document_windows(n, chunk, context):
     return out
 
 
-def decode_document_f32(front_geo, front_hw, codec_geo, codec_prep, codes, chunk, context):
+def decode_document_f32(front_geo, front_hw, codec_geo, codec_prep, codes, chunk, context, wave="f16"):
     """codes [n, n_books] -> audio [n * samples_per_frame] f32: every window through this module's
-    decode_f16 and the waveform oracle's (oracle.codec.decode_f16), one at a time, the kept audio
-    concatenated."""
+    decode_f16 and the waveform oracle, one at a time, the kept audio concatenated. wave "f16":
+    oracle.codec.decode_f16 (f16 storage); "f32": oracle.codec.decode_f32_reference on the latent
+    widened from f16 (the reference's WAV_DTYPE = F32 stack)."""
     from .codec import decode_f16 as wave_f16
+    from .codec import decode_f32_reference as wave_f32
     codes = np.ascontiguousarray(codes, np.int32)
     spf = front_geo.upsample * codec_geo.hop
     parts = []
     for frm, to, length, drop, keep in document_windows(codes.shape[0], chunk, context):
         idx = np.minimum(np.arange(frm, frm + length), to - 1)
         lat = decode_f16(front_geo, front_hw, codes[idx][None])
+        if wave == "f32":
+            wav = wave_f32(codec_geo, codec_prep, lat[0].view(np.float16).astype(np.float32))
+            parts.append(np.asarray(wav[drop * spf:(drop + keep) * spf], np.float32))
+            continue
         wav = wave_f16(codec_geo, codec_prep, lat)[0]
         parts.append(wav[drop * spf:(drop + keep) * spf].view(np.float16).astype(np.float32))
     return np.concatenate(parts) if parts else np.zeros(0, np.float32)

@@ -18,7 +18,7 @@ def _causal(x, w, b, dil=1):
 
 
 def torch_decode(geo, w, latent):
-    """latent [frames, dim] -> [frames*hop], float64."""
+    """latent [frames, dim] -> [frames*hop], float64; tanh, or the clamp for geo.out_clamp."""
     x = torch.from_numpy(np.ascontiguousarray(latent.T)).double()[None]
     x = _causal(x, w.head_w, w.head_b)
     for i, blk in enumerate(w.blocks):
@@ -32,4 +32,6 @@ def torch_decode(geo, w, latent):
             u = u + _causal(_snake(h, *un["act2"]), un["w2"], un["b2"])
         x = u
     y = _causal(_snake(x, *w.out_act), w.out_w, w.out_b)
+    if getattr(geo, "out_clamp", False):
+        return torch.clamp(y, -1.0, 1.0)[0, 0].numpy()
     return torch.tanh(y)[0, 0].numpy()

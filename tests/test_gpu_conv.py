@@ -108,14 +108,18 @@ def test_transposed_conv_matches_definition(dev, cin, cout, length, stride):
         assert np.all(err <= np.abs(want) * 2.0 ** -10 + 1e-3)
 
 
-def test_tanh_output_conv_single_channel(dev):
-    """The decoder's output conv: 96 -> 1, k=7, tanh (direct kernel)."""
-    x, w, wb, b = _case(43, 2, 1500, 96, 1, 7)
+@pytest.mark.parametrize("cin,k,dil,length", [(96, 7, 1, 1500), (64, 7, 3, 777), (128, 7, 9, 300), (32, 3, 1, 129),
+                                               (40, 7, 1, 500)])
+def test_tanh_output_conv_single_channel(dev, cin, k, dil, length):
+    """The decoder's output conv, 96 -> 1, k=7, tanh, and the single-output-channel kernel's other
+    channel counts, dilations and lengths (partial last tiles)."""
+    x, w, wb, b = _case(43, 2, length, cin, 1, k)
     w_tm = nlc.tap_major_weight(wb)
     w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
-    y = to_host(nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=7, act="tanh"))
-    want = oracle.conv1d_nlc_f16(x, w_tap, b, 1, act_tanh=True)
+    y = to_host(nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil, act="tanh"))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, dil, act_tanh=True)
     _close(y, want, tol=2e-3)
+    _elementwise(y, want)
 
 
 def test_conv_rejects_bad_shapes(dev):

@@ -190,6 +190,28 @@ def test_document_decode_matches_oracle(dev, n, chunk, context):
                                                                             rel(got, want))
 
 
+@pytest.mark.parametrize("n,chunk,context", [(14, 4, 2), (5, 4, 2)])
+def test_document_decode_f32_wave_meets_the_reference_gate(dev, n, chunk, context):
+    """The document decode with an f32 waveform stack (dtts_codec_create_f32, the reference's
+    WAV_DTYPE) against the oracle's window-by-window decode through the f32 stack on the same f16
+    front-half latent: within validate.rs's codec.wav gate, max|d| <= 5e-3
+    (crates/qwen3tts/src/bin/validate.rs:315)."""
+    from dtts import codec, codec_front
+    from oracle import codec as ocodec
+    from oracle import codec_front as ofront
+    from _doc_ref import TINY, TINY_WAVE, wave_weights
+    hw, w = codec_front.random_weights(TINY, 65), wave_weights(65)
+    codes = synth.randint(65, "codes", (n, TINY.n_books), 0, TINY.book_size - 1)
+    front = codec_front.CodecFront(TINY, hw, dev)
+    wave = codec.Codec(TINY_WAVE, w, dev, dtype="f32")
+    got = codec_front.decode_document(front, wave, codes, chunk, context).cpu().numpy()
+    want = ofront.decode_document_f32(TINY, hw, TINY_WAVE, ocodec.prepare(TINY_WAVE, w), codes, chunk, context,
+                                      wave="f32")
+    assert got.shape == want.shape == (n * TINY.upsample * TINY_WAVE.hop,)
+    assert np.max(np.abs(got - want)) <= 5e-3, np.max(np.abs(got - want))
+    assert np.std(want) > 0.02
+
+
 def test_document_decode_equals_its_windows(dev):
     """The batched document decode keeps, bit for bit, what each padded window decoded on its own
     (one lane through dtts_codec_front_decode and dtts_codec_decode) gives for its chunk."""

@@ -43,3 +43,18 @@ def test_oracle_codec_chains_match_torch_f64():
     # f16 storage points through 14 activations: a few f16 ulps of the unit-range waveform
     assert np.max(np.abs(got16 - want16)) < 2e-2
     assert got16.shape == (lanes, frames * GEO.hop)
+
+
+def test_oracle_f32_chain_clamps_like_codec_forward():
+    """out_clamp: Codec::forward's clamp to [-1, 1] (codec.rs:433-436) in place of tanh, against
+    the float64 build; the output conv is scaled up so the clamp is reached."""
+    from dataclasses import replace
+    geo = replace(GEO, out_clamp=True)
+    w = codec.random_weights(geo, seed=6)
+    w.out_w = (w.out_w * 3.0).astype(np.float32)
+    prep = ocodec.prepare(geo, w)
+    latent = synth.normal(6, "latent", (10, geo.latent_dim))
+    want = _torch_decode(geo, w, latent)
+    got = ocodec.decode_f32_reference(geo, prep, latent)
+    assert np.max(np.abs(got - want)) < 1e-4
+    assert np.mean(np.abs(want) == 1.0) > 0.01  # the clamp is active
