@@ -32,6 +32,8 @@ SIGNATURES = {
     "dtts_snake_ncl_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_snake_nlc_f32": [_P, _P, _P, _P, _I64, _I64, _P],
     "dtts_snake_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _P],
+    "dtts_snake_folded_f32": [_P, _P, _I64, _P],
+    "dtts_snake_alpha_f32": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_conv1d_nlc_f16_ex": [_P, _P],
     "dtts_conv1d_nlc_f32_ex": [_P, _P],
     "dtts_causal_conv1d_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],

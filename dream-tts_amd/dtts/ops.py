@@ -61,6 +61,33 @@ def snake_beta_nlc(x, alpha, beta_recip, out=None):
     return y
 
 
+def snake_folded(x, out=None):
+    """`x + sin^2(x)`, f32, any contiguous shape. crates/tts-nn/src/fused.rs:501-508."""
+    _check(x, "snake_folded", (_F32,), "x")
+    y = torch.empty_like(x) if out is None else out
+    _check(y, "snake_folded", (_F32,), "out")
+    if y.numel() != x.numel():
+        raise DttsError(f"snake_folded: out has {y.numel()} elements for {x.numel()}")
+    call("dtts_snake_folded_f32", ptr(x), ptr(y), x.numel(), stream_handle())
+    return y
+
+
+def snake_alpha(x, alpha, out=None):
+    """`u + sin^2(u)`, `u = alpha[c] * x`, over NCL `[lanes, C, L]` f32.
+
+    crates/tts-nn/src/fused.rs:510-522 (lanes == 1 there) and tts_nn::snake, lib.rs:1075-1083."""
+    _check(x, "snake_alpha", (_F32,), "x")
+    if x.dim() != 3:
+        raise DttsError(f"snake_alpha: x must be [lanes, C, L], got {tuple(x.shape)}")
+    lanes, c, length = x.shape
+    _check(alpha, "snake_alpha", (_F32,), "alpha")
+    if alpha.numel() != c:
+        raise DttsError(f"snake_alpha: alpha has {alpha.numel()} elements for {c} channels")
+    y = torch.empty_like(x) if out is None else out
+    call("dtts_snake_alpha_f32", ptr(x), ptr(alpha), ptr(y), lanes, c, length, stream_handle())
+    return y
+
+
 # ---------------------------------------------------------------- a8-a11 norm, RoPE, KV cache
 
 def _pos_array(pos, n, name):

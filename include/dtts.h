@@ -63,6 +63,19 @@ int dtts_snake_nlc_f32(const float *x, const float *alpha, const float *brecip, 
 int dtts_snake_nlc_f16(const dtts_f16 *x, const float *alpha, const float *brecip, dtts_f16 *y,
                        int64_t rows, int64_t chan, hipStream_t stream);
 
+/* The folded snakes, f32 (x, y any layout / [lanes, chan, len]; x == y allowed; full-precision
+ * sine, as the SnakeBeta f32 forms):
+ *   dtts_snake_folded_f32: y = x + sin^2(x) over n elements, for inputs whose alpha is folded into
+ *     the preceding conv's output weights. Replaces fused::snake_folded / SnakeFolded
+ *     (crates/tts-nn/src/fused.rs:17-91, 501-508; kernel snake_folded_f32, mtl.rs:128-143).
+ *   dtts_snake_alpha_f32: u = alpha[c] * x, y = u + sin^2(u), the half-folded snake whose 1/alpha
+ *     lives in the next conv's input weights. Replaces fused::snake_alpha / SnakeAlpha
+ *     (fused.rs:93-184, 510-522; kernel snake_alpha_f32, mtl.rs:145-166) and tts_nn::snake
+ *     (lib.rs:1075-1083); the reference takes lanes == 1, any lane count here. */
+int dtts_snake_folded_f32(const float *x, float *y, int64_t n, hipStream_t stream);
+int dtts_snake_alpha_f32(const float *x, const float *alpha, float *y, int64_t lanes, int64_t chan, int64_t len,
+                         hipStream_t stream);
+
 /* ------------------------------------------------------------------ a3-a5 channels-last conv */
 
 /* One channels-last conv1d with its neighbours fused (the general form behind

@@ -100,6 +100,21 @@ def snake_nlc_f16(x_bits, alpha, brecip):
     return y
 
 
+def snake_folded_f32(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_snake_folded_f32(_ptr(x), _ptr(y), _I64(x.size))
+    return y
+
+
+def snake_alpha_f32(x, alpha):
+    x, a = _f32(x), _f32(alpha)
+    lanes, c, l = x.shape
+    y = np.empty_like(x)
+    lib().or_snake_alpha_f32(_ptr(x), _ptr(a), _ptr(y), _I64(lanes), _I64(c), _I64(l))
+    return y
+
+
 def snake_nlc_f64(x, alpha, brecip):
     x, a, r = _f64(x), _f64(alpha), _f64(brecip)
     c = x.shape[-1]

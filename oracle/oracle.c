@@ -131,6 +131,30 @@ void or_snake_ncl_f16(const uint16_t *x, const float *alpha, const float *brecip
         }
 }
 
+/* The folded snakes' candle forms: snake_folded's off-Metal `x + x.sin()?.sqr()?`
+ * (crates/tts-nn/src/fused.rs:501-508; SnakeFolded::cpu_fwd, fused.rs:25-40, is x + sin(x)^2 too)
+ * and tts_nn::snake's `u = x * alpha; u + u.sin().sqr()` (lib.rs:1080-1083; SnakeAlpha::cpu_fwd,
+ * fused.rs:105-129). */
+void or_snake_folded_f32(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float s = sinf(x[i]);
+        y[i] = x[i] + s * s;
+    }
+}
+
+void or_snake_alpha_f32(const float *x, const float *alpha, float *y, int64_t lanes, int64_t chan,
+                        int64_t len) {
+    for (int64_t b = 0; b < lanes; ++b)
+        for (int64_t c = 0; c < chan; ++c) {
+            const int64_t o = (b * chan + c) * len;
+            for (int64_t l = 0; l < len; ++l) {
+                const float u = x[o + l] * alpha[c];
+                const float s = sinf(u);
+                y[o + l] = u + s * s;
+            }
+        }
+}
+
 /* Double-precision form, the target the reference's accuracy tests measure against
  * (fused.rs:2356-2391). */
 void or_snake_nlc_f64(const double *x, const double *alpha, const double *brecip, double *y,

@@ -35,6 +35,9 @@ void or_snake_ncl_f16(const uint16_t *x, const float *alpha, const float *brecip
                       int64_t lanes, int64_t chan, int64_t len);
 void or_snake_nlc_f64(const double *x, const double *alpha, const double *brecip, double *y,
                       int64_t rows, int64_t chan);
+void or_snake_folded_f32(const float *x, float *y, int64_t n);
+void or_snake_alpha_f32(const float *x, const float *alpha, float *y, int64_t lanes, int64_t chan,
+                        int64_t len);
 
 /* ---- a7 im2col gather (bit-exact) ---- */
 void or_im2col_tap_major_f32(const float *x, float *cols, int64_t cin, int64_t len, int64_t k,

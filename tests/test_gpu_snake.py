@@ -122,3 +122,66 @@ def test_snake_rejects_bad_arguments(dev):
     a = torch.ones(7, device=dev)
     with pytest.raises(DttsError, match="alpha"):
         ops.snake_beta_nlc(x, a, a)
+
+
+# ---------------------------------------------------------------- the folded snakes
+
+@pytest.mark.parametrize("shape,offset", [((1, 7, 33), 0), ((1, 96, 131072), 0), ((4801,), 0), ((1, 96, 1003), 1),
+                                          ((3,), 0), ((0,), 0)])
+def test_snake_folded_f32(dev, shape, offset):
+    """snake_folded against the oracle (fused.rs:2429-2446's 1e-5 against the composed form) and
+    f64; offset 1 runs the unaligned scalar kernel, odd counts the vector kernel's tail."""
+    n = int(np.prod(shape))
+    x = synth.normal(25, "x", (n + offset,), 0, 2)
+    xd = to_dev(x, dev)[offset:]
+    got = to_host(ops.snake_folded(xd))
+    want = oracle.snake_folded_f32(x[offset:])
+    if n:
+        assert rel(got, want)[1] < 1e-5
+        xf = x[offset:].astype(np.float64)
+        assert np.max(np.abs(got - (xf + np.sin(xf) ** 2)) / np.maximum(np.abs(xf), 1.0)) < 2e-6
+
+
+@pytest.mark.parametrize("lanes,c,length", [(1, 7, 33), (1, 96, 131072), (1, 1536, 601), (3, 5, 17), (2, 24, 4801)])
+def test_snake_alpha_f32(dev, lanes, c, length):
+    x = synth.normal(26, "x", (lanes, c, length), 0, 2)
+    a = synth.normal(26, "alpha", (c,))
+    got = to_host(ops.snake_alpha(to_dev(x, dev), to_dev(a, dev)))
+    assert rel(got, oracle.snake_alpha_f32(x, a))[1] < 1e-5
+
+
+def test_folded_snakes_wide_sweep_accuracy(dev):
+    # crates/tts-nn/src/fused.rs:2227-2283 ("snake_folded", "snake (alpha)"): x over +-30, alpha
+    # 0.05..2.55; error scaled by max(|x|, 1) resp. max(|alpha x|, 1) below 2e-6.
+    c, length = 8, 4096
+    x = (-30.0 + 60.0 * (np.arange(c * length) % length) / (length - 1)).astype(np.float32).reshape(1, c, length)
+    al = np.array([0.05 + 2.5 * j / (c - 1) for j in range(c)], np.float32)
+    xd = x.astype(np.float64)
+    got = to_host(ops.snake_folded(to_dev(x, dev)))
+    assert np.max(np.abs(got - (xd + np.sin(xd) ** 2)) / np.maximum(np.abs(xd), 1.0)) < 2e-6
+    u = al.astype(np.float64)[None, :, None] * xd
+    got = to_host(ops.snake_alpha(to_dev(x, dev), to_dev(al, dev)))
+    assert np.max(np.abs(got - (u + np.sin(u) ** 2)) / np.maximum(np.abs(u), 1.0)) < 2e-6
+
+
+def test_folded_snakes_in_place_and_identities(dev):
+    """In place; alpha = 1 gives snake_folded bit for bit (the same sine of the same argument)."""
+    x = synth.normal(27, "x", (2, 96, 1000), 0, 2)
+    t = to_dev(x, dev)
+    ref = ops.snake_folded(t)
+    ones = torch.ones(96, device=dev)
+    assert torch.equal(ops.snake_alpha(t, ones), ref)
+    ops.snake_folded(t, out=t)
+    assert torch.equal(t, ref)
+
+
+def test_folded_snakes_reject_bad_arguments(dev):
+    from dtts import DttsError
+
+    with pytest.raises(DttsError, match="alpha"):
+        ops.snake_alpha(torch.zeros((1, 8, 4), device=dev), torch.ones(7, device=dev))
+    with pytest.raises(DttsError, match="dtype"):
+        ops.snake_folded(torch.zeros(8, dtype=torch.float16, device=dev))
+    from dtts._lib import call
+    with pytest.raises(DttsError, match="negative"):
+        call("dtts_snake_folded_f32", None, None, -1, None)

@@ -85,6 +85,43 @@ def test_snake_layouts_agree_and_zero_is_fixed():
     assert np.all(oracle.snake_nlc_f32(np.zeros((4, 7), np.float32), a, r) == 0)
 
 
+def _sweep(c, length, lo, hi):
+    return (lo + (hi - lo) * (np.arange(c * length) % length) / (length - 1)).astype(np.float32)
+
+
+def test_folded_snakes_match_double_precision_over_wide_sweep():
+    # crates/tts-nn/src/fused.rs:2227-2283 ("snake_folded", "snake (alpha)"): x over +-30, alpha
+    # 0.05..2.55, error scaled by max(|x|, 1) resp. max(|alpha x|, 1), bound 2e-6 (fused.rs:2332).
+    c, length = 8, 4096
+    x = _sweep(c, length, -30.0, 30.0).reshape(1, c, length)
+    al = np.array([0.05 + 2.5 * j / (c - 1) for j in range(c)], np.float32)
+    xd = x.astype(np.float64)
+    got = oracle.snake_folded_f32(x)
+    assert np.max(np.abs(got - (xd + np.sin(xd) ** 2)) / np.maximum(np.abs(xd), 1.0)) < 2e-6
+    u = al.astype(np.float64)[None, :, None] * xd
+    got = oracle.snake_alpha_f32(x, al)
+    assert np.max(np.abs(got - (u + np.sin(u) ** 2)) / np.maximum(np.abs(u), 1.0)) < 2e-6
+    # the output is u + sin^2(u), not x + sin^2(u) (SnakeBeta with r = 1): a dropped alpha fails
+    assert np.max(np.abs(got - (xd + np.sin(u) ** 2))) > 1.0
+
+
+def test_folded_snakes_reduce_to_each_other_and_to_snake_beta():
+    """snake_forms_agree (fused.rs:2429-2446) plus the identities that fix the forms exactly:
+    snake_alpha at alpha = 1 and SnakeBeta at alpha = 1, 1/beta = 1 are x + sin^2(x) bit for bit,
+    and snake_alpha(x, a) is snake_folded of the f32 product a x."""
+    x = synth.normal(3, "x", (2, 7, 33), 0, 2)
+    a = synth.normal(3, "a", (7,))
+    folded = oracle.snake_folded_f32(x)
+    composed = (x + np.sin(x) ** 2).astype(np.float32)  # numpy's f32 sin, the candle composed form
+    assert np.max(np.abs(folded - composed)) < 1e-5
+    one = np.ones(7, np.float32)
+    assert np.array_equal(oracle.snake_alpha_f32(x, one), folded)
+    assert np.array_equal(oracle.snake_ncl_f32(x, one, one), folded)
+    ax = (x * a[None, :, None]).astype(np.float32)
+    assert np.array_equal(oracle.snake_alpha_f32(x, a), oracle.snake_folded_f32(ax))
+    assert np.all(oracle.snake_folded_f32(np.zeros(5, np.float32)) == 0)
+
+
 def test_snake_f16_is_one_rounding_of_f32():
     x = synth.normal(2, "x", (64, 96), 0, 3)
     xb = synth.f16_bits(x)
