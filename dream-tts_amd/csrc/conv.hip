@@ -172,7 +172,7 @@ Choice choose(const dtts_conv_desc *d) {
     const int64_t halo = (d->k - 1) * d->dilation;
     const bool aligned16 = aligned(d->x, 16) && aligned(d->w, 16) && aligned(d->y, 16) &&
                            (!d->bias || aligned(d->bias, 16)) && (!d->residual || aligned(d->residual, 16)) &&
-                           (!d->y_pre || aligned(d->y_pre, 16));
+                           (!d->y_pre || aligned(d->y_pre, 16)) && (!d->out_scale || aligned(d->out_scale, 16));
     if (!aligned16 || d->cin % 32 != 0 || d->cout % 32 != 0 || d->k > 7) return c;
     if (d->k == 1) {
         c.kmax = 1;

@@ -134,6 +134,14 @@ __device__ __forceinline__ float conv_sum(float acc, float bias, const float *sc
     return t + res;
 }
 
+// The same with the scale already in hand (1 when there is none: t * 1 == t exactly).
+__device__ __forceinline__ float conv_sum_s(float acc, float bias, float scale, float res) {
+#pragma clang fp contract(off)
+    float t = acc + bias;
+    t = t * scale;
+    return t + res;
+}
+
 // XCD-aware tile order: dispatch slot b runs on XCD b % 8; each XCD takes a contiguous range of
 // tiles ordered (N group, lane, m, n within the group), N fastest within a group. An M tile's
 // window is fetched into one L2 and reused by the group's N tiles there, and a group's weight
@@ -181,6 +189,15 @@ __device__ __forceinline__ void wait_vmem_le() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+
+// The workgroup barrier between pipeline stages. __syncthreads() carries a workgroup release
+// fence, which the compiler lowers to s_waitcnt vmcnt(0) before the s_barrier: every vector-memory
+// operation of the wave has to finish, the loads of the stages still being prefetched too, so a
+// deeper pipeline degenerates into one full memory round trip per chunk. Here the caller has
+// already waited (vmcnt) for exactly the loads the barrier publishes -- its share of the next
+// stage -- and this waits for the wave's own LDS accesses only; later loads stay in flight.
+// The asm is also a compiler barrier for memory: no access moves across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Load instructions a wave issues per chunk, at least: instruction j of a region belongs to wave
 // j % nw, and the region has at least `inst` instructions.
@@ -503,7 +520,7 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
         if (st < nchunks) issue(st * Cfg::KC, st);
     wait_for_next(nchunks - 1);
     if constexpr (SNAKE_IN) snake_stage(0, 0);
-    __syncthreads();
+    stage_barrier();
     int st = 0;          // stage holding chunk c
     int st_new = S - 1;  // stage receiving chunk c + S - 1
     if constexpr (!SNAKE_IN && KT >= 3) {
@@ -562,8 +579,7 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
                     load(st, t + 1, fa[cur ^ 1], fb[cur ^ 1]);
                 } else if (more) {
                     wait_for_next(nchunks - 2 - c);
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    __syncthreads();
+                    stage_barrier();
                     load(st_next, 0, fa[cur ^ 1], fb[cur ^ 1]);
                 }
                 mma(fa[cur], fb[cur]);
@@ -589,7 +605,7 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
             wait_for_next(nchunks - 2 - c);
             if constexpr (SNAKE_IN) snake_stage((c + 1) * Cfg::KC, st_next);
         }
-        __syncthreads();
+        stage_barrier();
         st = st_next;
         st_new = st_new + 1 == S ? 0 : st_new + 1;
     }
@@ -633,11 +649,14 @@ __device__ __forceinline__ void wave_lds_order() {
 // stores move 16 coalesced bytes per lane. The whole tile's residual and bias vectors are
 // requested up front. `ld` is the output row length (cout), `n0` the tile's first output
 // channel, `lmax` the lane's length. Called after the main loop's closing barrier (smem free).
-template <typename Cfg>
-__device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
-                                              int l0, int n0, int lmax, int ld, const half_t *bias, const half_t *res,
-                                              half_t *y_pre, half_t *y, const float *a_out, int act,
-                                              const float *scale) {
+// PLAIN: no activation and no scale, known at compile time. The general form reads act and scale
+// at run time, but they are uniform over the tile: branching on them per element costs more scalar
+// instructions and branches than the epilogue's arithmetic, so the caller picks a form once.
+template <typename Cfg, bool PLAIN>
+__device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
+                                                   int l0, int n0, int lmax, int ld, const half_t *bias,
+                                                   const half_t *res, half_t *y_pre, half_t *y, const float *a_out,
+                                                   int act, const float *scale) {
     constexpr int CG = Cfg::WTN / 8;  // 8-channel groups per wave row
     constexpr int NG = 32 * CG / 64;  // groups per lane per 32-row block
     static_assert((32 * CG) % 64 == 0, "a 32-row block splits evenly over the lanes");
@@ -687,13 +706,32 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             const float4_t *src = reinterpret_cast<const float4_t *>(E + mr * Cfg::EPI_PITCH + cg * 8);
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-                v[q] = conv_sum(v[q], static_cast<float>(bb[u][q]), scale, n + q, static_cast<float>(rr[i][u][q]));
             const int64_t off = (row0 + l) * ld + n;
             half8_t h;
+            if constexpr (PLAIN) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], act));
+                for (int q = 0; q < 8; ++q)
+                    h[q] = static_cast<half_t>(conv_sum_s(v[q], static_cast<float>(bb[u][q]), 1.0f,
+                                                          static_cast<float>(rr[i][u][q])));
+            } else {
+                float sc[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+                if (scale) {
+                    const float4_t s0 = *reinterpret_cast<const float4_t *>(scale + n);
+                    const float4_t s1 = *reinterpret_cast<const float4_t *>(scale + n + 4);
+                    sc[0] = s0[0], sc[1] = s0[1], sc[2] = s0[2], sc[3] = s0[3];
+                    sc[4] = s1[0], sc[5] = s1[1], sc[6] = s1[2], sc[7] = s1[3];
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    v[q] = conv_sum_s(v[q], static_cast<float>(bb[u][q]), sc[q], static_cast<float>(rr[i][u][q]));
+                if (act == 0) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(v[q]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], act));
+                }
+            }
             if (y_pre) *reinterpret_cast<half8_t *>(y_pre + off) = h;
             if (a_out) {
                 const int c = n - n0;
@@ -710,6 +748,17 @@ __device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cf
             *reinterpret_cast<half8_t *>(y + off) = h;
         }
     }
+}
+
+template <typename Cfg>
+__device__ __forceinline__ void conv_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
+                                              int l0, int n0, int lmax, int ld, const half_t *bias, const half_t *res,
+                                              half_t *y_pre, half_t *y, const float *a_out, int act,
+                                              const float *scale) {
+    if (act == 0 && !scale)
+        conv_epilogue_form<Cfg, true>(acc, smem, row0, l0, n0, lmax, ld, bias, res, y_pre, y, a_out, 0, nullptr);
+    else
+        conv_epilogue_form<Cfg, false>(acc, smem, row0, l0, n0, lmax, ld, bias, res, y_pre, y, a_out, act, scale);
 }
 
 }  // namespace dtts

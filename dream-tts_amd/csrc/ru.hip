@@ -340,7 +340,7 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
         else if (c + 1 < Cfg::CHUNKS)
             wait_vmem();
         if (c + 1 < Cfg::CHUNKS) win_write(R[nxt], stage[nxt]);
-        __syncthreads();
+        stage_barrier();
     }
 
     // the residual rows of this lane's positions, four channels per load (consumed at the end)
