@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import re
 import os
 import sys
 import time
@@ -571,6 +572,107 @@ def pmc_counters(stages_json, csv_paths):
     return out
 
 
+def pmc_clock(csv_paths):
+    """Per-kernel clock and matrix-core figures from rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_BUSY_CU_CYCLES
+    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA --kernel-trace runs (every kernel with MFMA work, dtts's and
+    the vendor library's alike). Per dispatch: duration from its timestamps; the CU clock as
+    SQ_BUSY_CU_CYCLES / 256 CUs / duration (cycles the CUs were busy, so a lower bound of the shader
+    clock); the MFMA-busy share of the SIMDs; the matrix work done, 1024 FLOP per SIMD MFMA-busy
+    cycle (a 32x32x16 f16 MFMA is 32 busy cycles, a 16x16x32 one 16); and the peak that clock
+    allows, 256 CUs x 4 SIMDs x 1024 FLOP per cycle."""
+    import csv
+
+    disp = {}
+    for path in csv_paths:
+        for r in csv.DictReader(open(path)):
+            d = disp.setdefault((path, int(r["Dispatch_Id"])), {"name": r["Kernel_Name"],
+                                                                 "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+    out = {}
+    for d in disp.values():
+        if not d.get("SQ_INSTS_MFMA") or d["ns"] <= 0:
+            continue
+        name = d["name"].replace("void ", "").replace("dtts::", "").replace("(anonymous namespace)::", "")
+        if "Cijk" in name:  # the vendor library's: its macro tile and stream-K flag name it
+            mt = re.search(r"MT\d+x\d+x\d+", name)
+            name = ("Custom_" if name.startswith("Custom") else "") + "Cijk " + (mt.group(0) if mt else name[:40]) + \
+                (" SK" if "_SK" in name else "")
+        else:
+            name = name.split("(")[0]
+        k = out.setdefault(name, {"dispatches": 0, "us": 0.0, "cu_clock_ghz": 0.0, "mfma_busy": 0.0, "tflops": 0.0,
+                                  "clock_peak_tflops": 0.0})
+        f_cu = d["SQ_BUSY_CU_CYCLES"] / 256.0 / d["ns"]  # cycles per ns = GHz
+        k["dispatches"] += 1
+        k["us"] += d["ns"] / 1e3
+        k["cu_clock_ghz"] += f_cu
+        k["mfma_busy"] += d["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * d["SQ_BUSY_CU_CYCLES"])
+        k["tflops"] += d["SQ_VALU_MFMA_BUSY_CYCLES"] * 1024.0 / d["ns"] / 1e3
+        k["clock_peak_tflops"] += f_cu * 256 * 4 * 1024 / 1e3
+    for k in out.values():
+        n = k["dispatches"]
+        for f in ("us", "cu_clock_ghz", "mfma_busy", "tflops", "clock_peak_tflops"):
+            k[f] = round(k[f] / n, 3)
+        k["frac_of_nameplate"] = round(k["tflops"] / PEAK_TFLOPS_F16, 4)
+    return out
+
+
+def vendor_gemm(stages, lanes, dev, reps=10):
+    """The vendor library's f16 GEMM (torch.matmul -> hipBLASLt) on each conv stage's im2col'd shape:
+    M = lanes x positions, K = taps x cin, N = cout; a fused residual unit as its two GEMMs (K = 7C
+    and C). The GEMM alone, no im2col pass, no epilogue, f16 out -- a bound for a library route."""
+    import torch
+
+    shapes, cache, out = [], {}, []
+    for s in stages:
+        m = lanes * s["len"]
+        if s["kernel"].startswith("ru_nlc"):
+            g = [(m, s["k"] * s["cin"], s["cout"]), (m, s["cout"], s["cout"])]
+        elif s["cout"] == 1 or not s["kernel"].startswith("conv_nlc_f16_mfma"):
+            continue
+        else:
+            g = [(m, s["k"] * s["cin"], s["cout"])]
+        shapes.append((s, g))
+    for s, g in shapes:
+        total = 0.0
+        for (m, k, n) in g:
+            if (m, k, n) not in cache:
+                a = torch.randn(m, k, device=dev, dtype=torch.float16)
+                b = torch.randn(n, k, device=dev, dtype=torch.float16).t()
+                for _ in range(3):
+                    c = torch.matmul(a, b)
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record()
+                for _ in range(reps):
+                    c = torch.matmul(a, b)
+                ev[1].record()
+                torch.cuda.synchronize()
+                cache[(m, k, n)] = ev[0].elapsed_time(ev[1]) / reps
+                del a, b, c
+                torch.cuda.empty_cache()
+            total += cache[(m, k, n)]
+        out.append({"stage": s["name"], "kernel": s["kernel"], "dtts_ms": round(s["ms"], 4), "gemms": g,
+                    "vendor_gemm_ms": round(total, 4), "dtts_over_vendor": round(s["ms"] / total, 3),
+                    "flops": s["flops"]})
+        log(f"    {s['name']:22s} dtts {s['ms']:7.3f} ms   vendor GEMM {total:7.3f} ms   ratio {s['ms'] / total:5.2f}")
+    # a reference point for the library itself: a square GEMM, its best case
+    a = torch.randn(8192, 8192, device=dev, dtype=torch.float16)
+    b = torch.randn(8192, 8192, device=dev, dtype=torch.float16).t()
+    for _ in range(3):
+        c = torch.matmul(a, b)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(reps):
+        c = torch.matmul(a, b)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    out.append({"stage": "square 8192 (reference)", "kernel": None, "dtts_ms": None, "gemms": [(8192, 8192, 8192)],
+                "vendor_gemm_ms": round(ms, 4), "dtts_over_vendor": None, "flops": 2.0 * 8192 ** 3})
+    log(f"    square 8192^3 vendor GEMM {ms:7.3f} ms = {2.0 * 8192 ** 3 / ms / 1e9:.0f} TFLOP/s")
+    del a, b, c
+    return out
+
+
 WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
              "stack": workload_stack, "front": workload_front, "cfg5f32": workload_cfg5f32}
 
@@ -595,6 +697,12 @@ def main():
                     choices=["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5f32", "cfg5", "all"],
                     help="cfg5 (default) is the headline codec line; cfg1-4 time the other rows' ops; stack "
                          "times the decoder-stack decode step; front the codec front half and document decode")
+    ap.add_argument("--pmc-clock", nargs="+", metavar="CSV",
+                    help="digest rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_BUSY_CU_CYCLES SQ_VALU_MFMA_BUSY_CYCLES "
+                         "SQ_INSTS_MFMA --kernel-trace runs into per-kernel clock and MFMA figures (no GPU)")
+    ap.add_argument("--vendor-gemm", default=None, metavar="JSON",
+                    help="after the profile run, time the vendor f16 GEMM on every conv stage's im2col'd "
+                         "shape and write the comparison here")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -604,6 +712,9 @@ def main():
         return
     if args.pmc_counters:
         print(json.dumps(pmc_counters(args.pmc_counters[0], args.pmc_counters[1:]), indent=1))
+        return
+    if args.pmc_clock:
+        print(json.dumps(pmc_clock(args.pmc_clock), indent=1))
         return
 
     if args.gpus != 1:
@@ -689,6 +800,12 @@ def main():
     if args.stages_out:
         with open(args.stages_out, "w") as f:
             json.dump(dict(ms_per_step=ms, stages=runs[-1]), f, indent=1)
+
+    if args.vendor_gemm:
+        log("vendor GEMM on the stages' im2col'd shapes:")
+        with open(args.vendor_gemm, "w") as f:
+            json.dump({"lanes": args.lanes, "frames": args.frames,
+                       "stages": vendor_gemm(runs[-1], args.lanes, dev)}, f, indent=1)
 
     if args.copy_probe:
         src = torch.ones(1 << 29, dtype=torch.float16, device=dev)
