@@ -14,7 +14,8 @@
 // each own a 32 x 32 block and run v_mfma_f32_32x32x2_f32, tap t reading the window at row offset
 // t*dil. The 32 lanes of an accumulator row are 32 consecutive output channels of one position,
 // so the epilogue's loads and stores are 128-byte runs straight from the accumulators.
-// Fewer than 32 output channels (the codec's 96 -> 1 output conv) run a direct kernel.
+// A single output channel (the codec's 96 -> 1 output conv) runs a window kernel of its own;
+// other shapes off the tile (channel counts not multiples of 16 / 32) run a direct kernel.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -185,6 +186,81 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_direct(NlcF32Params p, int64
     }
 }
 
+// A single output channel (the waveform conv, cin -> 1): HBM-bound, every input element feeds k
+// products. A workgroup owns kNarrowBM positions of one lane, a thread one position. Per
+// 32-channel chunk the window (kNarrowBM + (k-1)*dil rows) is loaded into registers whole, then
+// stored to LDS (the prologue SnakeBeta applied on the way), rows 36 floats apart so the 16-byte
+// reads of 16 consecutive rows hit 16 disjoint bank quads; the chunk's k x 32 weights sit beside
+// it and are read as broadcasts. Products accumulate in f32 in (chunk, tap, channel) order.
+constexpr int kNarrowBM = 256, kNarrowKC = 32, kNarrowPitch = kNarrowKC + 4, kNarrowMaxHalo = 64;
+constexpr int kNarrowRows = kNarrowBM + kNarrowMaxHalo;
+constexpr int kNarrowVec = (kNarrowRows * (kNarrowKC / 4) + 255) / 256;  // window float4s per thread, at most
+
+__global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
+    __shared__ __attribute__((aligned(16))) float win[kNarrowRows * kNarrowPitch];
+    __shared__ __attribute__((aligned(16))) float wsh[7 * kNarrowKC];
+    const int tile = blockIdx.x;
+    const int lane_idx = tile / p.tiles_m;
+    const int l0 = (tile - lane_idx * p.tiles_m) * kNarrowBM;
+    const int rows = kNarrowBM + (p.k - 1) * p.dil;
+    const int nvec = rows * (kNarrowKC / 4);
+    const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
+    const int tid = threadIdx.x;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < p.cin; c0 += kNarrowKC) {
+        float4_t buf[kNarrowVec];
+#pragma unroll
+        for (int i = 0; i < kNarrowVec; ++i) {
+            const int v = tid + i * 256;
+            buf[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            const int r = v >> 3, q = v & 7;
+            const int s = l0 - p.pad_left + r;
+            if (v < nvec && s >= 0 && s < p.L)
+                buf[i] = *reinterpret_cast<const float4_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + q * 4);
+        }
+        if (c0 > 0) __syncthreads();  // every thread is done with the previous chunk's window
+        if (tid < p.k * kNarrowKC) {
+            const int t = tid / kNarrowKC, c = tid - t * kNarrowKC;
+            wsh[tid] = p.w[t * p.cin + c0 + c];
+        }
+#pragma unroll
+        for (int i = 0; i < kNarrowVec; ++i) {
+            const int v = tid + i * 256;
+            if (v < nvec) {
+                const int r = v >> 3, q = v & 7;
+                float4_t x = buf[i];
+                const int s = l0 - p.pad_left + r;
+                if (p.a_in && s >= 0 && s < p.L) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[j] = snake_f32(x[j], p.a_in[c0 + q * 4 + j], p.r_in[c0 + q * 4 + j]);
+                }
+                *reinterpret_cast<float4_t *>(win + r * kNarrowPitch + q * 4) = x;
+            }
+        }
+        __syncthreads();
+        for (int t = 0; t < p.k; ++t) {
+            const float *row = win + (tid + t * p.dil) * kNarrowPitch;
+            const float *wr = wsh + t * kNarrowKC;
+#pragma unroll
+            for (int q = 0; q < kNarrowKC / 4; ++q) {
+                const float4_t x = *reinterpret_cast<const float4_t *>(row + q * 4);
+                const float4_t w = *reinterpret_cast<const float4_t *>(wr + q * 4);
+                acc = __builtin_fmaf(x[0], w[0], acc);
+                acc = __builtin_fmaf(x[1], w[1], acc);
+                acc = __builtin_fmaf(x[2], w[2], acc);
+                acc = __builtin_fmaf(x[3], w[3], acc);
+            }
+        }
+    }
+    const int l = l0 + tid;
+    if (l >= p.L) return;
+    const int64_t off = static_cast<int64_t>(lane_idx) * p.L + l;
+    float v = conv_f32_epilogue(acc, 0, off, p);
+    if (p.y_pre) p.y_pre[off] = v;
+    if (p.a_out) v = snake_f32(v, p.a_out[0], p.r_out[0]);
+    p.y[off] = v;
+}
+
 template <int KMAX, int HMAX>
 hipError_t launch_nlc_f32(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
     p.tiles_n = (p.cout + kF32BN - 1) / kF32BN;
@@ -200,6 +276,11 @@ hipError_t launch_nlc_f32(NlcF32Params p, int64_t lanes, bool snake, hipStream_t
     return hipGetLastError();
 }
 
+bool nlc_f32_narrow(const dtts_conv_desc *d) {
+    return d->cout == 1 && d->cin % kNarrowKC == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= kNarrowMaxHalo &&
+           aligned(d->x, 16);
+}
+
 bool nlc_f32_tiled(const dtts_conv_desc *d) {
     return d->cin % kF32KC == 0 && d->cout % 32 == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= 64 &&
            aligned(d->x, 16) && aligned(d->w, 16);
@@ -208,6 +289,7 @@ bool nlc_f32_tiled(const dtts_conv_desc *d) {
 }  // namespace
 
 const char *conv_f32_kernel_name(const dtts_conv_desc *d) {
+    if (nlc_f32_narrow(d)) return "conv_nlc_f32_narrow";
     if (!nlc_f32_tiled(d)) return "conv_nlc_f32_direct";
     if (d->k == 1) return "conv_nlc_f32_mfma<1, 0";
     return d->k == 2 && d->dilation == 1 ? "conv_nlc_f32_mfma<2, 1" : "conv_nlc_f32_mfma<7, 64";
@@ -248,7 +330,12 @@ int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
     p.pad_left = static_cast<int>(d->pad_left);
     p.act = d->act;
     hipError_t e;
-    if (nlc_f32_tiled(d)) {
+    if (nlc_f32_narrow(d)) {
+        p.tiles_m = static_cast<int>((d->len + kNarrowBM - 1) / kNarrowBM);
+        DTTS_REQUIRE(d->lanes * p.tiles_m < (int64_t(1) << 31), "%s: too many tiles", name);
+        conv_nlc_f32_narrow<<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
+        e = hipGetLastError();
+    } else if (nlc_f32_tiled(d)) {
         DTTS_REQUIRE(d->lanes * ((d->cout + kF32BN - 1) / kF32BN) * ((d->len + kF32BM - 1) / kF32BM) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
         const bool snake = d->in_alpha != nullptr;

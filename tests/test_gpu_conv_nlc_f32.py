@@ -113,3 +113,41 @@ def test_transposed_conv_f32_matches_definition(dev, cin, cout, length, stride):
     for li in range(lanes):
         want = oracle.conv_transpose1d_causal_f64(x[li], w, b, stride)
         assert rel(got[li], want)[1] < 1e-5
+
+
+@pytest.mark.parametrize("lanes,cin,length,k,dil,pad,ops", [
+    (2, 96, 900, 7, 1, None, "tanh"), (3, 96, 1000, 7, 3, None, "clamp"), (1, 64, 257, 7, 9, None, "snake_res"),
+    (2, 32, 300, 3, 21, None, "pre_snake_out"), (1, 128, 513, 1, 1, None, "bias"), (2, 96, 700, 7, 2, 5, "tanh"),
+])
+def test_single_output_channel_f32(dev, lanes, cin, length, k, dil, pad, ops):
+    """cin -> 1 (the waveform conv at f32): the window kernel against the oracle and torch f64, with
+    each epilogue and prologue operand, several lanes, halos up to 64 and partial last tiles."""
+    pad = (k - 1) * dil if pad is None else pad
+    x, w, b = _case(105, lanes, length, cin, 1, k)
+    kw = dict(k=k, dilation=dil, pad_left=pad)
+    w_tm = to_dev(nlc.tap_major_weight(w), dev)
+    want = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil, pad_left=pad)
+    exact = _torch_f64(x, w, b, dil, pad)
+    if ops in ("tanh", "clamp"):
+        got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), act=ops, **kw))
+        f = np.tanh if ops == "tanh" else (lambda v: np.clip(v, -1, 1))
+        assert rel(got, f(want))[1] < 1e-5 and rel(got, f(exact))[1] < 1e-5
+    elif ops == "snake_res":
+        a1 = synth.uniform(105, "a1", (cin,), 0.5, 1.5)
+        r1 = (1.0 / a1).astype(np.float32)
+        res = synth.normal(105, "res", (lanes, length, 1))
+        got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), snake_in=(to_dev(a1, dev), to_dev(r1, dev)),
+                                 residual=to_dev(res, dev), **kw))
+        want = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil, pad_left=pad, snake=(a1, r1), res=res)
+        assert rel(got, want)[1] < 1e-5
+        assert rel(got, _torch_f64(x, w, b, dil, pad, snake=(a1, r1)) + res)[1] < 1e-5
+    elif ops == "pre_snake_out":
+        a2 = synth.uniform(105, "a2", (1,), 0.5, 1.5)
+        r2 = (1.0 / a2).astype(np.float32)
+        y_pre, y = nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), snake_out=(to_dev(a2, dev), to_dev(r2, dev)),
+                              want_pre=True, **kw)
+        assert rel(to_host(y_pre), want)[1] < 1e-5
+        assert rel(to_host(y), oracle.snake_nlc_f32(want, a2, r2))[1] < 1e-5
+    else:
+        got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), **kw))
+        assert rel(got, want)[1] < 1e-5 and rel(got, exact)[1] < 1e-5
