@@ -134,10 +134,13 @@ def test_conv_rejects_bad_shapes(dev):
 
 
 @pytest.mark.parametrize("lanes,c,length,dil,out_snake", [(2, 96, 3000, 9, True), (3, 96, 700, 1, False),
-                                                           (2, 192, 1100, 3, True), (1, 192, 257, 9, False)])
+                                                           (2, 192, 1100, 3, True), (1, 192, 257, 9, False),
+                                                           (2, 96, 900, 3, True), (2, 192, 600, 1, False),
+                                                           (2, 96, 500, 2, True), (1, 192, 300, 5, False)])
 def test_fused_residual_unit_matches_composed_chain(dev, lanes, c, length, dil, out_snake):
     """dtts_residual_unit_nlc_f16 against the oracle's unfused chain with the same f16 storage
-    points: h = conv7(snake1(x)); h2 = snake2(h); y = conv1(h2) + x; [snake_out(y)]."""
+    points: h = conv7(snake1(x)); h2 = snake2(h); y = conv1(h2) + x; [snake_out(y)]. The codec's
+    dilations (1, 3, 9) at both widths, and others (2, 5) a caller may pass."""
     k = 7
     x = synth.f16_bits(synth.normal(44, "x", (lanes, length, c)))
     w1 = synth.f16_bits(synth.normal(44, "w1", (c, c, k), 0, np.sqrt(1.0 / (c * k))))
