@@ -673,6 +673,43 @@ def vendor_gemm(stages, lanes, dev, reps=10):
     return out
 
 
+def achievable_peaks(dev, reps=20):
+    """What the box delivers, next to the spec-sheet peaks the rooflines use: HBM from a copy kernel
+    over 2 GiB (read + write counted; far past the 256 MB MALL), f16 and f32 matrix throughput from
+    the vendor library's square GEMMs (torch.matmul), each timed with HIP events after warm-up."""
+    import torch
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    src = torch.ones(1 << 30, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    ms = timed(lambda: torch.mul(src, 1.0, out=dst))
+    out["hbm_copy"] = {"gbs": round(2 * src.numel() * 2 / ms / 1e6, 1), "bytes_per_pass": 2 * src.numel() * 2,
+                       "frac_of_peak": round(2 * src.numel() * 2 / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    del src, dst
+    for name, dt, n, peak in (("gemm_f16", torch.float16, 8192, PEAK_TFLOPS_F16),
+                              ("gemm_f32", torch.float32, 8192, PEAK_TFLOPS_F32)):
+        a = torch.randn(n, n, device=dev, dtype=dt)
+        b = torch.randn(n, n, device=dev, dtype=dt)
+        ms = timed(lambda: torch.matmul(a, b))
+        tf = 2.0 * n ** 3 / ms / 1e9
+        out[name] = {"shape": [n, n, n], "tflops": round(tf, 1), "frac_of_peak": round(tf / peak, 4)}
+        del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 WORKLOADS = {"cfg1": workload_cfg1, "cfg2": workload_cfg2, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
              "stack": workload_stack, "front": workload_front, "cfg5f32": workload_cfg5f32}
 
@@ -703,6 +740,8 @@ def main():
     ap.add_argument("--vendor-gemm", default=None, metavar="JSON",
                     help="after the profile run, time the vendor f16 GEMM on every conv stage's im2col'd "
                          "shape and write the comparison here")
+    ap.add_argument("--peaks", action="store_true",
+                    help="measure the box's achievable HBM copy bandwidth and f16/f32 GEMM throughput, then exit")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 1 GiB copy kernel 3 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -729,6 +768,11 @@ def main():
     from dtts import codec, synth
 
     dev = torch.device("cuda:0")
+    if args.peaks:
+        print(json.dumps({"achievable_peaks": achievable_peaks(dev),
+                          "spec": {"hbm_gbs": PEAK_HBM_GBS, "f16_tflops": PEAK_TFLOPS_F16,
+                                   "f32_matrix_tflops": PEAK_TFLOPS_F32}}))
+        return
     if args.workload != "cfg5":
         for w in (["cfg1", "cfg2", "cfg3", "cfg4", "stack", "front", "cfg5f32"] if args.workload == "all"
                   else [args.workload]):

@@ -115,14 +115,15 @@ auto with_tile(int64_t lanes, int len, int cin, int cout, bool direct, F &&f) {
             if (cout % 96 == 0) return f(Tile<ConvTile<256, 96, 4, 1, 16, KMAX, HMAX, 2, kStageDirect>>{});
         }
         // k = 2 (the transposed convs) at 128-multiples: 2 x 2 waves of 128 x 64 when the input is
-        // wide (cin >= 768: more matrix work per staged chunk), else 2 x 2 waves of 64 x 64 with
-        // three 32-channel stages in flight (three workgroups per CU); at 96-multiples four waves of
-        // 32 x 96, three stages. Measured on the codec's four upsampling shapes: 10-20% over one
-        // 256 x 96 tile for all.
+        // wide (cin >= 768: more matrix work per staged chunk), else 2 x 2 waves of 64 x 64; at
+        // 96-multiples four waves of 32 x 96. Two 32-channel stages: with the epilogue's plain form
+        // the smaller footprint (more workgroups per CU) beats a third stage in flight, 9% at
+        // 128 x 128 and 16% at 128 x 96 on the codec's shapes (A/B; three stages stay better for
+        // k = 1). Measured on the codec's four upsampling shapes: 10-20% over one 256 x 96 tile.
         if constexpr (KMAX == 2) {
             if (cout % 128 == 0 && cin >= 768) return f(Tile<ConvTile<256, 128, 2, 2, 32, KMAX, HMAX, 2, kStageDirect>>{});
-            if (cout % 128 == 0) return f(Tile<ConvTile<128, 128, 2, 2, 32, KMAX, HMAX, 3, kStageDirect>>{});
-            if (cout % 96 == 0) return f(Tile<ConvTile<128, 96, 4, 1, 32, KMAX, HMAX, 3, kStageDirect>>{});
+            if (cout % 128 == 0) return f(Tile<ConvTile<128, 128, 2, 2, 32, KMAX, HMAX, 2, kStageDirect>>{});
+            if (cout % 96 == 0) return f(Tile<ConvTile<128, 96, 4, 1, 32, KMAX, HMAX, 2, kStageDirect>>{});
         }
         // k = 1 at 128-multiples: 2 x 2 waves of 64 x 64. Three 32-channel stages in flight (three
         // workgroups per CU) up to cin 2048; beyond, two 64-channel stages (fewer barriers per
@@ -253,6 +254,7 @@ int conv1d_nlc_f16(const dtts_conv_desc *d, hipStream_t stream) {
     const Choice ch = choose(d);
     hipError_t e;
     if (std::strcmp(ch.path, "narrow") == 0) {
+        DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) < (int64_t(1) << 31), "%s: too many tiles", name);
         e = conv_narrow_launch(d, stream);
     } else if (std::strcmp(ch.path, "mfma") == 0) {
         DTTS_REQUIRE(d->lanes * ((d->len + 255) / 256) * (d->cout / 32) < (int64_t(1) << 31),

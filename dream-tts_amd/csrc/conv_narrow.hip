@@ -1,9 +1,12 @@
 // Channels-last conv with a single output channel (the codec's 96 -> 1 waveform conv).
 //
-// HBM-bound: every input element is read once and feeds k products. A workgroup stages a
-// window of BM + (k-1)*dil positions x cin channels in LDS (row pitch padded by 8 halves so 16
-// consecutive rows hit 16 disjoint bank quads), then each thread reduces one output position
-// over k taps x cin channels (LDS sized per launch) with packed f16 dot products accumulating in f32.
+// HBM-bound: every input element is read once and feeds k products. A workgroup owns kBM
+// positions of one lane, a thread one position. Per 32-channel chunk the window (kBM + (k-1)*dil
+// rows) goes through registers into LDS (the prologue SnakeBeta applied on the way), rows 40
+// halves apart so the 16-byte reads of 16 consecutive rows hit 16 disjoint bank quads; the chunk's
+// k x 32 weights sit beside it, read as broadcasts. Packed f16 dot products accumulate in f32, in
+// (chunk, tap, channel) order. Staging a chunk at a time keeps the footprint at ~26 KB, so several
+// workgroups share a CU and one's loads overlap another's products.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -11,9 +14,11 @@ namespace dtts {
 namespace {
 
 constexpr int kBM = 256;
-constexpr int kMaxCin = 128;
+constexpr int kKC = 32;                // channels per chunk
+constexpr int kPitch = kKC + 8;        // LDS row pitch, halves
 constexpr int kMaxHalo = 64;
-constexpr int kMaxVec = (kBM + kMaxHalo) * (kMaxCin / 8) / 256;  // window vectors per thread, at most
+constexpr int kRows = kBM + kMaxHalo;
+constexpr int kMaxVec = (kRows * (kKC / 8) + 255) / 256;  // window vectors per thread, at most
 
 struct NarrowParams {
     const half_t *x;
@@ -30,64 +35,69 @@ struct NarrowParams {
 };
 
 __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
-    extern __shared__ __attribute__((aligned(16))) char dyn[];
-    const int pitch = p.cin + 8;
-    const int rows = kBM + (p.k - 1) * p.dil;
-    half_t *win = reinterpret_cast<half_t *>(dyn);
-    half_t *wsh = win + rows * pitch;
+    __shared__ __attribute__((aligned(16))) half_t win[kRows * kPitch];
+    __shared__ __attribute__((aligned(16))) half_t wsh[7 * kKC];
     const int lane_idx = blockIdx.x / p.tiles_m;
     const int l0 = (blockIdx.x - lane_idx * p.tiles_m) * kBM;
-    const int cv = p.cin / 8;  // 16-byte vectors per row
+    const int rows = kBM + (p.k - 1) * p.dil;
     const half_t *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
-    for (int i = threadIdx.x; i < p.k * p.cin; i += 256) wsh[i] = p.w[i];
-    // every 16-byte vector of the window is loaded before any is stored, so the loads' latencies
-    // overlap instead of adding up
-    const int nvec = rows * cv;
-    half8_t buf[kMaxVec];
+    const int tid = threadIdx.x;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < p.cin; c0 += kKC) {
+        const int cv = (p.cin - c0 < kKC ? p.cin - c0 : kKC) / 8;  // 16-byte vectors per row in this chunk
+        const int nvec = rows * cv;
+        // every vector of the chunk's window is loaded before any is stored, so the loads'
+        // latencies overlap instead of adding up
+        half8_t buf[kMaxVec];
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
-        const int v = threadIdx.x + i * 256;
-        buf[i] = half8_t{};
-        if (v < nvec) {
+        for (int i = 0; i < kMaxVec; ++i) {
+            const int v = tid + i * 256;
+            buf[i] = half8_t{};
             const int r = v / cv;
             const int s = l0 - p.pad_left + r;
-            if (s >= 0 && s < p.L)
-                buf[i] = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + (v - r * cv) * 8);
+            if (v < nvec && s >= 0 && s < p.L)
+                buf[i] = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + (v - r * cv) * 8);
         }
-    }
+        if (c0 > 0) __syncthreads();  // every thread is done with the previous chunk's window and weights
+        if (tid < p.k * cv * 8) {
+            const int t = tid / (cv * 8), c = tid - t * (cv * 8);
+            wsh[t * kKC + c] = p.w[t * p.cin + c0 + c];
+        }
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
-        const int v = threadIdx.x + i * 256;
-        if (v < nvec) {
-            const int r = v / cv;
-            const int q = v - r * cv;
-            half8_t h = buf[i];
-            if (p.a_in) {
+        for (int i = 0; i < kMaxVec; ++i) {
+            const int v = tid + i * 256;
+            if (v < nvec) {
+                const int r = v / cv;
+                const int q = v - r * cv;
+                half8_t h = buf[i];
+                if (p.a_in) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    h[j] = static_cast<half_t>(snake_f16out(static_cast<float>(h[j]), p.a_in[q * 8 + j], p.r_in[q * 8 + j]));
+                    for (int j = 0; j < 8; ++j) {
+                        const int c = c0 + q * 8 + j;
+                        h[j] = static_cast<half_t>(snake_f16out(static_cast<float>(h[j]), p.a_in[c], p.r_in[c]));
+                    }
+                }
+                *reinterpret_cast<half8_t *>(win + r * kPitch + q * 8) = h;
             }
-            *reinterpret_cast<half8_t *>(win + r * pitch + q * 8) = h;
+        }
+        __syncthreads();
+        for (int t = 0; t < p.k; ++t) {
+            const half_t *row = win + (tid + t * p.dil) * kPitch;
+            const half_t *wr = wsh + t * kKC;
+            for (int q = 0; q < cv; ++q) {
+                const half8_t xv = *reinterpret_cast<const half8_t *>(row + q * 8);
+                const half8_t wv = *reinterpret_cast<const half8_t *>(wr + q * 8);
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const half2_t a = {xv[j], xv[j + 1]};
+                    const half2_t b = {wv[j], wv[j + 1]};
+                    acc = __builtin_amdgcn_fdot2(a, b, acc, false);
+                }
+            }
         }
     }
-    __syncthreads();
-    const int l = l0 + threadIdx.x;
+    const int l = l0 + tid;
     if (l >= p.L) return;
-    float acc = 0.0f;
-    for (int t = 0; t < p.k; ++t) {
-        const half_t *row = win + (threadIdx.x + t * p.dil) * pitch;
-        const half_t *wr = wsh + t * p.cin;
-        for (int q = 0; q < cv; ++q) {
-            const half8_t xv = *reinterpret_cast<const half8_t *>(row + q * 8);
-            const half8_t wv = *reinterpret_cast<const half8_t *>(wr + q * 8);
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                const half2_t a = {xv[j], xv[j + 1]};
-                const half2_t b = {wv[j], wv[j + 1]};
-                acc = __builtin_amdgcn_fdot2(a, b, acc, false);
-            }
-        }
-    }
     const int64_t off = static_cast<int64_t>(lane_idx) * p.L + l;
     float v = acc;
     if (p.bias) v += static_cast<float>(p.bias[0]);
@@ -103,8 +113,8 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
 }  // namespace
 
 bool conv_narrow_eligible(const dtts_conv_desc *d) {
-    return d->cout == 1 && d->cin % 8 == 0 && d->cin <= kMaxCin && d->k <= 7 &&
-           (d->k - 1) * d->dilation <= kMaxHalo && aligned(d->x, 16) && aligned(d->w, 16);
+    return d->cout == 1 && d->cin % 8 == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= kMaxHalo &&
+           aligned(d->x, 16);
 }
 
 hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream) {
@@ -127,8 +137,7 @@ hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream) {
     p.act = d->act;
     p.tiles_m = static_cast<int>((d->len + kBM - 1) / kBM);
     const int64_t grid = d->lanes * p.tiles_m;
-    const size_t lds = (static_cast<size_t>(kBM + (p.k - 1) * p.dil) * (p.cin + 8) + static_cast<size_t>(p.k) * p.cin) * 2;
-    conv_nlc_f16_narrow<<<static_cast<unsigned>(grid), 256, lds, stream>>>(p);
+    conv_nlc_f16_narrow<<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
     return hipGetLastError();
 }
 

@@ -724,12 +724,23 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
                     v[q] = conv_sum_s(v[q], static_cast<float>(bb[u][q]), sc[q], static_cast<float>(rr[i][u][q]));
-                if (act == 0) {
+                // one branch on the (uniform) activation per eight values
+                switch (act) {
+                case 1:
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], 1));
+                    break;
+                case 2:
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], 2));
+                    break;
+                case 3:
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], 3));
+                    break;
+                default:
 #pragma unroll
                     for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(v[q]);
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(conv_act(v[q], act));
                 }
             }
             if (y_pre) *reinterpret_cast<half8_t *>(y_pre + off) = h;

@@ -122,6 +122,31 @@ def test_tanh_output_conv_single_channel(dev, cin, k, dil, length):
     _elementwise(y, want)
 
 
+@pytest.mark.parametrize("lanes,cin,length,k,dil", [(2, 96, 1000, 7, 1), (1, 40, 300, 5, 9), (3, 160, 257, 7, 3)])
+def test_single_channel_conv_operands(dev, lanes, cin, length, k, dil):
+    """The single-output-channel kernel with the prologue snake, residual, pre-snake store and output
+    SnakeBeta, then with the clamp: channel counts with a partial last 32-channel chunk, halos to 54."""
+    x, w, wb, b = _case(45, lanes, length, cin, 1, k)
+    res = synth.f16_bits(synth.normal(45, "res", (lanes, length, 1)))
+    a1 = synth.uniform(45, "a1", (cin,), 0.5, 1.5)
+    r1 = (1.0 / a1).astype(np.float32)
+    a2 = synth.uniform(45, "a2", (1,), 0.5, 1.5)
+    r2 = (1.0 / a2).astype(np.float32)
+    w_tm = nlc.tap_major_weight(wb)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    y_pre, y = nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil,
+                          snake_in=(to_dev(a1, dev), to_dev(r1, dev)), residual=to_dev(res, dev),
+                          snake_out=(to_dev(a2, dev), to_dev(r2, dev)), want_pre=True)
+    want_pre = oracle.conv1d_nlc_f16(x, w_tap, b, dil, snake=(a1, r1), res_bits=res)
+    _close(to_host(y_pre), want_pre)
+    _elementwise(to_host(y_pre), want_pre)
+    assert f16_ulp_diff(to_host(y), oracle.snake_nlc_f16(to_host(y_pre), a2, r2)) <= 1
+    got = to_host(nlc.conv1d(to_dev(x, dev), to_dev(w_tm, dev), to_dev(b, dev), k=k, dilation=dil, act="clamp"))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, dil, act="clamp")
+    _close(got, want)
+    _elementwise(got, want)
+
+
 def test_conv_rejects_bad_shapes(dev):
     from dtts import DttsError
 
