@@ -12,7 +12,7 @@ import torch
 import oracle
 from dtts import nlc, synth
 
-from _util import f16_ulp_diff, to_dev, to_host  # noqa: F401
+from _util import f16_ulp_diff, rel, to_dev, to_host  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -190,3 +190,53 @@ def test_fused_residual_unit_matches_composed_chain(dev, lanes, c, length, dil, 
         assert f16_ulp_diff(to_host(y), oracle.snake_nlc_f16(got_pre, *pairs[2])) <= 1
     else:
         assert np.array_equal(to_host(y), got_pre)
+
+
+@pytest.mark.parametrize("act", ["tanh", "clamp", "gelu"])
+@pytest.mark.parametrize("lanes,cin,cout,length,k,dil", [(2, 96, 96, 1100, 7, 3), (2, 64, 128, 300, 2, 1),
+                                                        (2, 128, 128, 257, 1, 1)])
+def test_general_epilogue_activation_and_scale(dev, act, lanes, cin, cout, length, k, dil):
+    """The tile's general epilogue form (an activation and/or a per-channel scale; the plain form
+    serves neither): each activation with and without the scale and the residual, at a k=7, a k=2
+    and a k=1 tile, and a scale off 16-byte alignment, which the direct kernel takes instead."""
+    x, w, wb, b = _case(46, lanes, length, cin, cout, k)
+    w_tm = to_dev(nlc.tap_major_weight(wb), dev)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    res = synth.f16_bits(synth.normal(46, "res", (lanes, length, cout)))
+    scale = synth.uniform(46, "scale", (cout,), 0.1, 2.0)
+    xd, bd = to_dev(x, dev), to_dev(b, dev)
+    got = to_host(nlc.conv1d(xd, w_tm, bd, k=k, dilation=dil, act=act))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, dil, act=act)
+    _close(got, want)
+    _elementwise(got, want)
+    got = to_host(nlc.conv1d(xd, w_tm, bd, k=k, dilation=dil, act=act, residual=to_dev(res, dev),
+                             scale=to_dev(scale, dev)))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, dil, act=act, res_bits=res, scale=scale)
+    _close(got, want)
+    _elementwise(got, want)
+    # the same scale one float past a 16-byte boundary: the direct kernel, the same values
+    buf = torch.zeros(cout + 4, dtype=torch.float32, device=dev)
+    buf[1:1 + cout] = to_dev(scale, dev)
+    got_u = to_host(nlc.conv1d(xd, w_tm, bd, k=k, dilation=dil, act=act, residual=to_dev(res, dev),
+                               scale=buf[1:1 + cout]))
+    _close(got_u, want)
+    _elementwise(got_u, want)
+
+
+@pytest.mark.parametrize("lanes,length", [(3, 1), (2, 5), (1, 256), (2, 513)])
+def test_single_channel_conv_short_and_exact_lengths(dev, lanes, length):
+    """The single-output-channel kernels, f16 and f32, at lengths shorter than the halo, one tile
+    exactly and one past a tile boundary."""
+    cin, k, dil = 96, 7, 9
+    x, w, wb, b = _case(47, lanes, length, cin, 1, k)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    got = to_host(nlc.conv1d(to_dev(x, dev), to_dev(nlc.tap_major_weight(wb), dev), to_dev(b, dev), k=k,
+                             dilation=dil, act="tanh"))
+    want = oracle.conv1d_nlc_f16(x, w_tap, b, dil, act_tanh=True)
+    assert got.shape == (lanes, length, 1)
+    _close(got, want, tol=2e-3)
+    xf = synth.from_f16_bits(x).astype(np.float32)
+    got32 = to_host(nlc.conv1d(to_dev(xf, dev), to_dev(nlc.tap_major_weight(w), dev), to_dev(synth.from_f16_bits(b).astype(np.float32), dev),
+                               k=k, dilation=dil, act="tanh"))
+    want32 = np.tanh(oracle.conv1d_nlc_f32(xf, oracle.tap_weight_f32(w), synth.from_f16_bits(b).astype(np.float32), dil))
+    assert rel(got32, want32)[1] < 1e-5
