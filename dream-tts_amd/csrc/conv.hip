@@ -206,6 +206,8 @@ const char *conv_kernel_name(const dtts_conv_desc *d) {
             snprintf(tail, sizeof(tail), ", %s, %d>", c.snake ? "true" : "false", d->k == Cfg::KMAX ? Cfg::KMAX : 0);
             return tile_kernel_name<Cfg>(buf, sizeof(buf), "conv_nlc_f16_mfma", tail);
         });
+    else if (std::strcmp(c.path, "narrow") == 0)
+        snprintf(buf, sizeof(buf), "%s", conv_narrow_kernel_name(d));
     else
         snprintf(buf, sizeof(buf), "conv_nlc_f16_%s", c.path);
     return buf;

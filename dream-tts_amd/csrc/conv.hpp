@@ -28,5 +28,6 @@ int residual_unit_nlc_f16(const dtts_ru_desc *d, hipStream_t stream);
 // The single-output-channel kernel (conv_narrow.hip).
 bool conv_narrow_eligible(const dtts_conv_desc *d);
 hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream);
+const char *conv_narrow_kernel_name(const dtts_conv_desc *d);  // the kernel a narrow launch runs
 
 }  // namespace dtts

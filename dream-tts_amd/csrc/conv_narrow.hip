@@ -3,10 +3,16 @@
 // HBM-bound: every input element is read once and feeds k products. A workgroup owns kBM
 // positions of one lane, a thread one position. Per 32-channel chunk the window (kBM + (k-1)*dil
 // rows) goes through registers into LDS (the prologue SnakeBeta applied on the way), rows 40
-// halves apart so the 16-byte reads of 16 consecutive rows hit 16 disjoint bank quads; the chunk's
-// k x 32 weights sit beside it, read as broadcasts. Packed f16 dot products accumulate in f32, in
-// (chunk, tap, channel) order. Staging a chunk at a time keeps the footprint at ~26 KB, so several
-// workgroups share a CU and one's loads overlap another's products.
+// halves apart so the 16-byte reads of 16 consecutive rows hit 16 disjoint bank quads. Packed f16
+// dot products accumulate in f32, in (chunk, tap, channel) order.
+//
+// Two kernels share that order, so their outputs agree bit for bit:
+//   conv_nlc_f16_narrow_k<K>  k = K (7: the codec's), 32-channel multiples, no prologue SnakeBeta.
+//       The next chunk's window is loaded into registers while the current one is on the dot
+//       products, into the other of two LDS windows (one barrier per chunk); the weights are
+//       uniform loads (scalar registers). ~51 KB of LDS: three workgroups per CU.
+//   conv_nlc_f16_narrow       any k <= 7, 8-channel multiples, optional prologue SnakeBeta: one
+//       window, loaded, stored and consumed a chunk at a time, the chunk's weights in LDS.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -33,6 +39,21 @@ struct NarrowParams {
     const float *r_out;
     int L, cin, k, dil, pad_left, act, tiles_m;
 };
+
+// The epilogue both kernels share: bias, residual, activation, f16 rounding, the optional plain
+// store and output SnakeBeta.
+__device__ __forceinline__ void narrow_store(const NarrowParams &p, int lane_idx, int l, float acc) {
+    const int64_t off = static_cast<int64_t>(lane_idx) * p.L + l;
+    float v = acc;
+    if (p.bias) v += static_cast<float>(p.bias[0]);
+    if (p.res) v += static_cast<float>(p.res[off]);
+    if (p.act == 1) v = tanhf(v);
+    if (p.act == 3) v = fminf(fmaxf(v, -1.0f), 1.0f);
+    half_t h = static_cast<half_t>(v);
+    if (p.y_pre) p.y_pre[off] = h;
+    if (p.a_out) h = static_cast<half_t>(snake_f16out(static_cast<float>(h), p.a_out[0], p.r_out[0]));
+    p.y[off] = h;
+}
 
 __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
     __shared__ __attribute__((aligned(16))) half_t win[kRows * kPitch];
@@ -97,20 +118,75 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
         }
     }
     const int l = l0 + tid;
-    if (l >= p.L) return;
-    const int64_t off = static_cast<int64_t>(lane_idx) * p.L + l;
-    float v = acc;
-    if (p.bias) v += static_cast<float>(p.bias[0]);
-    if (p.res) v += static_cast<float>(p.res[off]);
-    if (p.act == 1) v = tanhf(v);
-    if (p.act == 3) v = fminf(fmaxf(v, -1.0f), 1.0f);
-    half_t h = static_cast<half_t>(v);
-    if (p.y_pre) p.y_pre[off] = h;
-    if (p.a_out) h = static_cast<half_t>(snake_f16out(static_cast<float>(h), p.a_out[0], p.r_out[0]));
-    p.y[off] = h;
+    if (l < p.L) narrow_store(p, lane_idx, l, acc);
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void conv_nlc_f16_narrow_k(NarrowParams p) {
+    constexpr int SEGS = kKC / 8;
+    constexpr int NVEC = (kRows * SEGS + 255) / 256;
+    __shared__ __attribute__((aligned(16))) half_t win[2][kRows * kPitch];
+    const int lane_idx = blockIdx.x / p.tiles_m;
+    const int l0 = (blockIdx.x - lane_idx * p.tiles_m) * kBM;
+    const int nvec = (kBM + (K - 1) * p.dil) * SEGS;
+    const half_t *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
+    const half_t *__restrict__ w = p.w;
+    const int tid = threadIdx.x;
+    half8_t buf[NVEC];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < NVEC; ++i) {
+            const int v = tid + i * 256;
+            const int r = v / SEGS;
+            const int s = l0 - p.pad_left + r;
+            buf[i] = half8_t{};
+            if (v < nvec && s >= 0 && s < p.L)
+                buf[i] = *reinterpret_cast<const half8_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + (v % SEGS) * 8);
+        }
+    };
+    float acc = 0.0f;
+    load(0);
+    int st = 0;
+    for (int c0 = 0; c0 < p.cin; c0 += kKC, st ^= 1) {
+        // window st was last read two chunks ago, before the barrier that closed the last chunk
+#pragma unroll
+        for (int i = 0; i < NVEC; ++i) {
+            const int v = tid + i * 256;
+            if (v < nvec) *reinterpret_cast<half8_t *>(win[st] + (v / SEGS) * kPitch + (v % SEGS) * 8) = buf[i];
+        }
+        if (c0 + kKC < p.cin) load(c0 + kKC);
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < K; ++t) {
+            const half_t *row = win[st] + (tid + t * p.dil) * kPitch;
+#pragma unroll
+            for (int q = 0; q < SEGS; ++q) {
+                const half8_t xv = *reinterpret_cast<const half8_t *>(row + q * 8);
+                const half8_t wv = *reinterpret_cast<const half8_t *>(w + t * p.cin + c0 + q * 8);
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const half2_t a = {xv[j], xv[j + 1]};
+                    const half2_t b = {wv[j], wv[j + 1]};
+                    acc = __builtin_amdgcn_fdot2(a, b, acc, false);
+                }
+            }
+        }
+    }
+    const int l = l0 + tid;
+    if (l < p.L) narrow_store(p, lane_idx, l, acc);
+}
+
+// The specialised kernel's shapes: k = 7, 32-channel multiples, no prologue SnakeBeta, 16-byte
+// weight rows.
+bool narrow_k7(const dtts_conv_desc *d) {
+    return d->k == 7 && d->cin % kKC == 0 && !d->in_alpha && aligned(d->w, 16);
 }
 
 }  // namespace
+
+const char *conv_narrow_kernel_name(const dtts_conv_desc *d) {
+    return narrow_k7(d) ? "conv_nlc_f16_narrow_k<7>" : "conv_nlc_f16_narrow";
+}
 
 bool conv_narrow_eligible(const dtts_conv_desc *d) {
     return d->cout == 1 && d->cin % 8 == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= kMaxHalo &&
@@ -137,7 +213,10 @@ hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream) {
     p.act = d->act;
     p.tiles_m = static_cast<int>((d->len + kBM - 1) / kBM);
     const int64_t grid = d->lanes * p.tiles_m;
-    conv_nlc_f16_narrow<<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
+    if (narrow_k7(d))
+        conv_nlc_f16_narrow_k<7><<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
+    else
+        conv_nlc_f16_narrow<<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
     return hipGetLastError();
 }
 

@@ -147,6 +147,37 @@ def test_single_channel_conv_operands(dev, lanes, cin, length, k, dil):
     _elementwise(got, want)
 
 
+@pytest.mark.parametrize("lanes,cin,length,dil", [(2, 96, 1000, 1), (1, 64, 300, 9), (3, 160, 257, 3)])
+def test_single_channel_k7_kernels_agree(dev, lanes, cin, length, dil):
+    """The k = 7 single-output-channel kernel (32-channel multiples, no prologue SnakeBeta) with the
+    residual, pre-snake store and output SnakeBeta against the oracle, and bit for bit against the
+    generic kernel on the same operands (weights 8 bytes past a 16-byte boundary take that one)."""
+    k = 7
+    x, w, wb, b = _case(48, lanes, length, cin, 1, k)
+    res = synth.f16_bits(synth.normal(48, "res", (lanes, length, 1)))
+    a2 = synth.uniform(48, "a2", (1,), 0.5, 1.5)
+    r2 = (1.0 / a2).astype(np.float32)
+    w_tm = nlc.tap_major_weight(wb)
+    w_tap = oracle.tap_weight_f32(synth.from_f16_bits(wb)).astype(np.float16).view(np.uint16)
+    wd = to_dev(w_tm, dev)
+    wbuf = torch.zeros(w_tm.size + 4, dtype=torch.float16, device=dev)
+    wbuf[4:4 + w_tm.size] = wd.reshape(-1)
+    w_off = wbuf[4:4 + w_tm.size].view(wd.shape)
+    assert w_off.data_ptr() % 16 == 8
+    outs = []
+    for wt in (wd, w_off):
+        outs.append([to_host(t) for t in nlc.conv1d(to_dev(x, dev), wt, to_dev(b, dev), k=k, dilation=dil,
+                                                     residual=to_dev(res, dev), snake_out=(to_dev(a2, dev), to_dev(r2, dev)),
+                                                     want_pre=True)])
+    (pre_f, y_f), (pre_g, y_g) = outs
+    assert np.array_equal(pre_f.view(np.uint16), pre_g.view(np.uint16))
+    assert np.array_equal(y_f.view(np.uint16), y_g.view(np.uint16))
+    want_pre = oracle.conv1d_nlc_f16(x, w_tap, b, dil, res_bits=res)
+    _close(pre_f, want_pre)
+    _elementwise(pre_f, want_pre)
+    assert f16_ulp_diff(y_f, oracle.snake_nlc_f16(pre_f, a2, r2)) <= 1
+
+
 def test_conv_rejects_bad_shapes(dev):
     from dtts import DttsError
 
