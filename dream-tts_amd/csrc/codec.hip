@@ -36,9 +36,12 @@ struct dtts_codec {
 namespace dtts {
 namespace {
 
-// Stages whose residual-unit input is at least this wide store it snaked as well: the unit's
-// k7 conv then reads the snaked copy instead of recomputing SnakeBeta once per output tile.
+// Stages whose residual-unit input is wider than this store it snaked as well: the unit's k7 conv
+// then reads the snaked copy instead of recomputing SnakeBeta once per output tile. An f32 codec
+// stores it at every width: its SnakeBeta is the full-precision sine, which costs the matrix-bound
+// k7 conv more than the extra store costs the producer.
 constexpr int64_t kStoreSnakedAbove = 96;
+inline bool stores_snaked(bool f32, int64_t cout) { return f32 || cout > kStoreSnakedAbove; }
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -127,7 +130,7 @@ int codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, bo
         const int64_t cout = g.channels[i + 1];
         const int64_t rate = g.rates[i];
         float *pa = nullptr, *pr = nullptr;
-        if (cout > dtts::kStoreSnakedAbove) {
+        if (dtts::stores_snaked(f32, cout)) {
             const size_t bytes = sizeof(float) * static_cast<size_t>(rate * cout);
             hipError_t e = hipMalloc(&pa, bytes);
             if (e == hipSuccess) e = hipMalloc(&pr, bytes);
@@ -270,7 +273,7 @@ int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lan
             }
             return true;
         }();
-        const bool wide = !fused && cout > kStoreSnakedAbove;
+        const bool wide = !fused && stores_snaked(c->f32, cout);
         // TransConv: one causal conv of 2 taps over the snaked input, rate*cout phase columns
         char *u = pick(x, nullptr, nullptr);
         char *su = wide ? pick(x, u, nullptr) : nullptr;

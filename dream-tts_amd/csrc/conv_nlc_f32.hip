@@ -7,15 +7,18 @@
 //
 // xs is x, or SnakeBeta(x) applied as the window is staged (full-precision sinf; a padded tap
 // stays 0, as snake(0) = 0 gives). GEMM view per lane: M = positions, N = output channels,
-// K = (tap, channel). A workgroup owns 64 positions x 64 output channels of one lane; per
-// 16-channel chunk it stages the dilated window (64 + (k-1)*dil rows x 16 channels) and the
-// 64 x k x 16 weight slice in LDS (two buffers: chunk c+1 goes from registers into one while chunk
-// c+2's loads are in flight and chunk c is multiplied, one barrier per chunk). Four waves (2 x 2)
-// each own a 32 x 32 block and run v_mfma_f32_32x32x2_f32, tap t reading the window at row offset
-// t*dil. The 32 lanes of an accumulator row are 32 consecutive output channels of one position,
-// so the epilogue's loads and stores are 128-byte runs straight from the accumulators.
+// K = (tap, channel). A workgroup owns BM = 128 positions x BN output channels of one lane: BN 64
+// (2 x 2 waves of 64 x 32), 96 (4 x 1 waves of 32 x 96) or 32 (4 x 1 waves of 32 x 32), the widest
+// that divides cout. Per 8-channel chunk it stages the dilated window (128 + (k-1)*dil rows) and
+// the BN x k x 8 weight slice in LDS (two buffers: chunk c+1 goes from registers into one while
+// chunk c+2's loads are in flight and chunk c is multiplied, one barrier per chunk). The waves run
+// v_mfma_f32_32x32x2_f32; step s of a tap pairs channel s (lanes 0-31) with channel 4 + s (lanes
+// 32-63), so a lane's four operands of a tap are one 16-byte LDS read per 32-row or 32-column
+// block, and with k = KMAX the taps are unrolled and tap t+1's reads issue under tap t's MFMAs.
+// The 32 lanes of an accumulator row are 32 consecutive output channels of one position, so the
+// epilogue's loads and stores are 128-byte runs straight from the accumulators.
 // A single output channel (the codec's 96 -> 1 output conv) runs a window kernel of its own;
-// other shapes off the tile (channel counts not multiples of 16 / 32) run a direct kernel.
+// other shapes off the tile (channel counts not multiples of 8 / 32) run a direct kernel.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -30,7 +33,7 @@ struct NlcF32Params {
     int tiles_m, tiles_n, total, per_xcd;
 };
 
-constexpr int kF32BM = 64, kF32BN = 64, kF32KC = 16;
+constexpr int kF32BM = 128, kF32KC = 8;
 
 __device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off, const NlcF32Params &p) {
     float v = s;
@@ -42,50 +45,60 @@ __device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off,
     return v;
 }
 
-template <int KMAX, int HMAX, bool SNAKE>
-__global__ __launch_bounds__(256, 2) void conv_nlc_f32_mfma(NlcF32Params p) {
-    constexpr int XR = kF32BM + HMAX;                          // window rows
-    constexpr int XP = kF32KC + 1;                             // window row pitch (floats, odd: no bank conflicts)
-    constexpr int WP = KMAX * kF32KC + 1;                      // weight row pitch
-    constexpr int XN = (XR * kF32KC / 4 + 255) / 256;          // window float4s per thread
-    constexpr int WN = (kF32BN * KMAX * kF32KC / 4 + 255) / 256;  // weight float4s per thread
-    __shared__ float xs[2][XR * XP];
-    __shared__ float ws[2][kF32BN * WP];
+// BM x BN tile over WM x WN waves (wave tile (BM/WM) x (BN/WN) in 32 x 32 blocks); KT = KMAX when
+// k fills the class (taps unrolled, the next tap's operands read under the current tap's MFMAs),
+// 0 for fewer taps.
+template <int KMAX, int HMAX, int KT, int BN, int WM, int WN, bool SNAKE>
+__global__ __launch_bounds__(64 * WM * WN, 2) void conv_nlc_f32_mfma(NlcF32Params p) {
+    constexpr int BM = kF32BM, KC = kF32KC;
+    constexpr int NT = 64 * WM * WN;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int XR = BM + HMAX;               // window rows
+    constexpr int XP = KC + 4;                  // row pitch: 48 B, so 16 consecutive rows' 16-byte reads
+    constexpr int WP = KMAX * KC + 4;           //   hit 16 distinct bank groups (likewise 16 * odd here)
+    constexpr int C4 = KC / 4;                  // float4s per row of a chunk
+    constexpr int XN = (XR * C4 + NT - 1) / NT;            // window float4s per thread
+    constexpr int WV = (BN * KMAX * C4 + NT - 1) / NT;     // weight float4s per thread
+    constexpr int H = KC / 2;                   // MFMA steps per tap
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC == 8, "f32 tile shape");
+    __shared__ __attribute__((aligned(16))) float xs[2][XR * XP];
+    __shared__ __attribute__((aligned(16))) float ws[2][BN * WP];
     const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (tile >= p.total) return;
     const int n_tile = tile % p.tiles_n;  // output channels fastest: neighbours share the window
     const int rest = tile / p.tiles_n;
     const int m_tile = rest % p.tiles_m;
     const int lane_idx = rest / p.tiles_m;
-    const int co0 = n_tile * kF32BN;
-    const int l0 = m_tile * kF32BM;
-    const int rows = kF32BM + (p.k - 1) * p.dil;
-    const int K = p.k * p.cin;
+    const int co0 = n_tile * BN;
+    const int l0 = m_tile * BM;
+    const int k = KT > 0 ? KT : p.k;
+    const int rows = BM + (k - 1) * p.dil;
+    const int K = k * p.cin;
     const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int kh = lane >> 5, lr = lane & 31;
-    const int nx = rows * (kF32KC / 4), nw = kF32BN * p.k * (kF32KC / 4);
+    const int nx = rows * C4, nw = BN * k * C4;
 
-    float4_t xr[XN], wr[WN];
+    float4_t xr[XN], wr[WV];
     auto load = [&](int c0) {
-        // window: row j holds positions l0 - pad_left + j, channels c0 .. c0+15 (four float4s)
+        // window: row j holds positions l0 - pad_left + j, channels c0 .. c0+7 (two float4s)
 #pragma unroll
         for (int i = 0; i < XN; ++i) {
-            const int e = tid + i * 256;
-            const int j = e >> 2, c4 = e & 3;
+            const int e = tid + i * NT;
+            const int j = e / C4, c4 = e % C4;
             const int s = l0 - p.pad_left + j;
             float4_t v = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
             if (e < nx && s >= 0 && s < p.L)
                 v = *reinterpret_cast<const float4_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + c4 * 4);
             xr[i] = v;
         }
-        // weights: 16 consecutive input channels of one (output channel, tap) are four float4s
+        // weights: 8 consecutive input channels of one (output channel, tap) are two float4s
 #pragma unroll
-        for (int i = 0; i < WN; ++i) {
-            const int e = tid + i * 256;
-            const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
-            const int t = q >> 2, c4 = q & 3;
+        for (int i = 0; i < WV; ++i) {
+            const int e = tid + i * NT;
+            const int m = e / (k * C4), q = e - (e / (k * C4)) * (k * C4);
+            const int t = q / C4, c4 = q % C4;
             float4_t v = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
             if (e < nw && co0 + m < p.cout)
                 v = *reinterpret_cast<const float4_t *>(p.w + static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 + c4 * 4);
@@ -95,68 +108,99 @@ __global__ __launch_bounds__(256, 2) void conv_nlc_f32_mfma(NlcF32Params p) {
     auto store = [&](int c0, int b) {
 #pragma unroll
         for (int i = 0; i < XN; ++i) {
-            const int e = tid + i * 256;
+            const int e = tid + i * NT;
             if (e < nx) {
-                const int j = e >> 2, c4 = e & 3;
-                const int s = l0 - p.pad_left + j;
-                float *dst = &xs[b][j * XP + c4 * 4];  // rows are XP floats apart (odd): scalar stores
+                const int j = e / C4, c4 = e % C4;
+                float4_t v = xr[i];
+                if constexpr (SNAKE) {
+                    const int s = l0 - p.pad_left + j;
+                    if (s >= 0 && s < p.L)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float v = xr[i][q];
-                    if constexpr (SNAKE)
-                        if (s >= 0 && s < p.L) v = snake_f32(v, p.a_in[c0 + c4 * 4 + q], p.r_in[c0 + c4 * 4 + q]);
-                    dst[q] = v;
+                        for (int q = 0; q < 4; ++q)
+                            v[q] = snake_f32(v[q], p.a_in[c0 + c4 * 4 + q], p.r_in[c0 + c4 * 4 + q]);
                 }
+                *reinterpret_cast<float4_t *>(&xs[b][j * XP + c4 * 4]) = v;
             }
         }
 #pragma unroll
-        for (int i = 0; i < WN; ++i) {
-            const int e = tid + i * 256;
+        for (int i = 0; i < WV; ++i) {
+            const int e = tid + i * NT;
             if (e < nw) {
-                const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
-                float *dst = &ws[b][m * WP + q * 4];
-                dst[0] = wr[i][0];
-                dst[1] = wr[i][1];
-                dst[2] = wr[i][2];
-                dst[3] = wr[i][3];
+                const int m = e / (k * C4), q = e - (e / (k * C4)) * (k * C4);
+                *reinterpret_cast<float4_t *>(&ws[b][m * WP + q * 4]) = wr[i];
             }
         }
     };
 
-    float16_t acc = float16_t{};
-    const int nchunks = p.cin / kF32KC;
+    float16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = float16_t{};
+    const int nchunks = p.cin / KC;
     load(0);
     store(0, 0);
-    if (nchunks > 1) load(kF32KC);
+    if (nchunks > 1) load(KC);
     __syncthreads();
     for (int c = 0; c < nchunks; ++c) {
         const int b = c & 1;
         if (c + 1 < nchunks) {
-            store((c + 1) * kF32KC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
-            if (c + 2 < nchunks) load((c + 2) * kF32KC);
+            store((c + 1) * KC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
+            if (c + 2 < nchunks) load((c + 2) * KC);
         }
-        for (int t = 0; t < p.k; ++t) {
-            // A[m][kk] = window[row m (+ tap offset)][channel kk]; B[kk][n] = w[n][tap t, channel kk]
-            const float *xa = xs[b] + (wm * 32 + lr + t * p.dil) * XP + kh;
-            const float *wb = ws[b] + (wn * 32 + lr) * WP + t * kF32KC + kh;
+        // operands of tap t: A[m][kk] = window[row m + t*dil][channel], B[kk][n] = w[n][tap t, channel]
+        auto frag = [&](int t, float4_t (&fa)[TM], float4_t (&fb)[TN]) {
 #pragma unroll
-            for (int ci = 0; ci < kF32KC; ci += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[ci], wb[ci], acc, 0, 0, 0);
+            for (int i = 0; i < TM; ++i)
+                fa[i] = *reinterpret_cast<const float4_t *>(xs[b] + (wm * WTM + i * 32 + lr + t * p.dil) * XP + kh * 4);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                fb[j] = *reinterpret_cast<const float4_t *>(ws[b] + (wn * WTN + j * 32 + lr) * WP + t * KC + kh * 4);
+        };
+        auto mma = [&](const float4_t (&fa)[TM], const float4_t (&fb)[TN]) {
+#pragma unroll
+            for (int st = 0; st < H; ++st)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st], acc[i][j], 0, 0, 0);
+        };
+        if constexpr (KT > 0) {
+            float4_t fa[2][TM], fb[2][TN];
+            frag(0, fa[0], fb[0]);
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+                if (t + 1 < KT) frag(t + 1, fa[(t + 1) & 1], fb[(t + 1) & 1]);
+                mma(fa[t & 1], fb[t & 1]);
+            }
+        } else {
+            for (int t = 0; t < k; ++t) {
+                float4_t fa[TM], fb[TN];
+                frag(t, fa, fb);
+                mma(fa, fb);
+            }
         }
         __syncthreads();
     }
-    const int co = co0 + wn * 32 + lr;
-    if (co >= p.cout) return;
     const int64_t lbase = static_cast<int64_t>(lane_idx) * p.L;
-    const float a_o = p.a_out ? p.a_out[co] : 0.0f, r_o = p.a_out ? p.r_out[co] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int pos = l0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
-        if (pos >= p.L) continue;
-        const int64_t off = (lbase + pos) * p.cout + co;
-        float v = conv_f32_epilogue(acc[r], co, off, p);
-        if (p.y_pre) p.y_pre[off] = v;
-        if (p.a_out) v = snake_f32(v, a_o, r_o);
-        p.y[off] = v;
+    for (int j = 0; j < TN; ++j) {
+        const int co = co0 + wn * WTN + j * 32 + lr;
+        if (co >= p.cout) continue;
+        const float a_o = p.a_out ? p.a_out[co] : 0.0f, r_o = p.a_out ? p.r_out[co] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int pos = l0 + wm * WTM + i * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+                if (pos >= p.L) continue;
+                const int64_t off = (lbase + pos) * p.cout + co;
+                float v = conv_f32_epilogue(acc[i][j][r], co, off, p);
+                if (p.y_pre) p.y_pre[off] = v;
+                if (p.a_out) v = snake_f32(v, a_o, r_o);
+                p.y[off] = v;
+            }
     }
 }
 
@@ -261,19 +305,39 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
     p.y[off] = v;
 }
 
-template <int KMAX, int HMAX>
-hipError_t launch_nlc_f32(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
-    p.tiles_n = (p.cout + kF32BN - 1) / kF32BN;
+// The tile's output-channel width: the widest of 64, 96 and 32 that divides cout.
+int f32_tile_bn(int64_t cout) { return cout % 64 == 0 ? 64 : cout % 96 == 0 ? 96 : 32; }
+
+template <int KMAX, int HMAX, int KT, int BN, int WM, int WN>
+hipError_t launch_f32_tile(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
+    p.tiles_n = p.cout / BN;
     p.tiles_m = (p.L + kF32BM - 1) / kF32BM;
     const int64_t total = lanes * p.tiles_m * p.tiles_n;
     p.total = static_cast<int>(total);
     p.per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
     if (snake)
-        conv_nlc_f32_mfma<KMAX, HMAX, true><<<grid, 256, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(p);
     else
-        conv_nlc_f32_mfma<KMAX, HMAX, false><<<grid, 256, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(p);
     return hipGetLastError();
+}
+
+template <int KMAX, int HMAX, int KT>
+hipError_t launch_nlc_f32(const NlcF32Params &p, int64_t lanes, bool snake, hipStream_t stream) {
+    switch (f32_tile_bn(p.cout)) {
+    case 64: return launch_f32_tile<KMAX, HMAX, KT, 64, 2, 2>(p, lanes, snake, stream);
+    case 96: return launch_f32_tile<KMAX, HMAX, KT, 96, 4, 1>(p, lanes, snake, stream);
+    default: return launch_f32_tile<KMAX, HMAX, KT, 32, 4, 1>(p, lanes, snake, stream);
+    }
+}
+
+// (KMAX, HMAX, KT) of the class a tiled shape runs in: k = 1, k = 2 without dilation, k = 7, or
+// fewer taps (KMAX 7, taps at run time)
+void f32_class(const dtts_conv_desc *d, int &kmax, int &hmax, int &kt) {
+    if (d->k == 1) kmax = 1, hmax = 0, kt = 1;
+    else if (d->k == 2 && d->dilation == 1) kmax = 2, hmax = 1, kt = 2;
+    else kmax = 7, hmax = 64, kt = d->k == 7 ? 7 : 0;
 }
 
 bool nlc_f32_narrow(const dtts_conv_desc *d) {
@@ -291,8 +355,13 @@ bool nlc_f32_tiled(const dtts_conv_desc *d) {
 const char *conv_f32_kernel_name(const dtts_conv_desc *d) {
     if (nlc_f32_narrow(d)) return "conv_nlc_f32_narrow";
     if (!nlc_f32_tiled(d)) return "conv_nlc_f32_direct";
-    if (d->k == 1) return "conv_nlc_f32_mfma<1, 0";
-    return d->k == 2 && d->dilation == 1 ? "conv_nlc_f32_mfma<2, 1" : "conv_nlc_f32_mfma<7, 64";
+    static thread_local char buf[96];
+    int kmax, hmax, kt;
+    f32_class(d, kmax, hmax, kt);
+    const int bn = f32_tile_bn(d->cout);
+    snprintf(buf, sizeof(buf), "conv_nlc_f32_mfma<%d, %d, %d, %d, %d, %d", kmax, hmax, kt, bn, bn == 64 ? 2 : 4,
+             bn == 64 ? 2 : 1);
+    return buf;
 }
 
 int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
@@ -336,15 +405,19 @@ int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
         conv_nlc_f32_narrow<<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
         e = hipGetLastError();
     } else if (nlc_f32_tiled(d)) {
-        DTTS_REQUIRE(d->lanes * ((d->cout + kF32BN - 1) / kF32BN) * ((d->len + kF32BM - 1) / kF32BM) < (int64_t(1) << 31),
+        DTTS_REQUIRE(d->lanes * (d->cout / f32_tile_bn(d->cout)) * ((d->len + kF32BM - 1) / kF32BM) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
         const bool snake = d->in_alpha != nullptr;
-        if (d->k == 1)
-            e = launch_nlc_f32<1, 0>(p, d->lanes, snake, stream);
-        else if (d->k == 2 && d->dilation == 1)
-            e = launch_nlc_f32<2, 1>(p, d->lanes, snake, stream);
+        int kmax, hmax, kt;
+        f32_class(d, kmax, hmax, kt);
+        if (kmax == 1)
+            e = launch_nlc_f32<1, 0, 1>(p, d->lanes, snake, stream);
+        else if (kmax == 2)
+            e = launch_nlc_f32<2, 1, 2>(p, d->lanes, snake, stream);
+        else if (kt == 7)
+            e = launch_nlc_f32<7, 64, 7>(p, d->lanes, snake, stream);
         else
-            e = launch_nlc_f32<7, 64>(p, d->lanes, snake, stream);
+            e = launch_nlc_f32<7, 64, 0>(p, d->lanes, snake, stream);
     } else {
         const int64_t total = d->lanes * d->len * d->cout;
         conv_nlc_f32_direct<<<grid_for(total, 256, 16), 256, 0, stream>>>(p, total);

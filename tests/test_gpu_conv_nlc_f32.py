@@ -46,6 +46,8 @@ def _torch_f64(x, w, b, dil, pad_left, snake=None):
     (1, 64, 96, 4097, 1, 1),
     (3, 96, 96, 700, 7, 9), (2, 192, 192, 513, 7, 3), (2, 384, 384, 300, 7, 1),   # codec stages
     (2, 768, 768, 250, 1, 1), (2, 1024, 1536, 60, 7, 1), (2, 96, 1, 900, 7, 1),
+    (2, 64, 160, 300, 7, 3), (1, 32, 32, 500, 1, 1), (1, 64, 64, 400, 5, 2),     # each tile width (32, 64, 96)
+    (2, 96, 96, 333, 3, 4), (1, 40, 64, 129, 2, 3),                               # and taps below 7
 ])
 def test_causal_conv_f32_matches_oracle_and_torch(dev, lanes, cin, cout, length, k, dil):
     x, w, b = _case(100, lanes, length, cin, cout, k)
@@ -65,7 +67,8 @@ def test_centered_pad_f32(dev):
     assert rel(got, _torch_f64(x, w, b, 3, 9))[1] < 1e-5
 
 
-@pytest.mark.parametrize("lanes,c,length,k,dil", [(2, 96, 3000, 7, 9), (1, 192, 1100, 1, 1), (2, 384, 300, 7, 3)])
+@pytest.mark.parametrize("lanes,c,length,k,dil", [(2, 96, 3000, 7, 9), (1, 192, 1100, 1, 1), (2, 384, 300, 7, 3),
+                                                   (1, 160, 700, 7, 1), (2, 64, 400, 5, 3)])
 def test_fused_snake_residual_f32(dev, lanes, c, length, k, dil):
     """NlcConv's has_snake / has_res (nlc::snake_conv_residual, nlc.rs:40-68) plus the epilogue
     SnakeBeta and y_pre the codec uses."""
@@ -99,7 +102,7 @@ def test_activations_and_scale_f32(dev):
 
 
 @pytest.mark.parametrize("cin,cout,length,stride", [(1536, 768, 20, 8), (768, 384, 40, 5), (384, 192, 64, 4),
-                                                    (192, 96, 128, 3), (8, 6, 12, 2), (12, 8, 9, 5)])
+                                                    (192, 96, 128, 3), (8, 6, 12, 2), (12, 8, 9, 5), (16, 16, 50, 2)])
 def test_transposed_conv_f32_matches_definition(dev, cin, cout, length, stride):
     """The polyphase transposed conv at f32 against the scatter definition (nlc.rs:329-360 shapes
     and the codec's four)."""
