@@ -183,24 +183,41 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void conv_nlc_f32_mfma(NlcF32Param
         }
         __syncthreads();
     }
+    // each 32 x 32 block's residuals are requested together before its stores (res may alias the
+    // outputs, so a load issued after a store waits for it: one memory round trip per block,
+    // not per value)
     const int64_t lbase = static_cast<int64_t>(lane_idx) * p.L;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int co = co0 + wn * WTN + j * 32 + lr;
         if (co >= p.cout) continue;
         const float a_o = p.a_out ? p.a_out[co] : 0.0f, r_o = p.a_out ? p.r_out[co] : 0.0f;
+        const float bias = p.bias ? p.bias[co] : 0.0f, scale = p.scale ? p.scale[co] : 1.0f;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
+            const int pos0 = l0 + wm * WTM + i * 32 + kh * 4;
+            float rv[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int pos = l0 + wm * WTM + i * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+                const int pos = pos0 + (r >> 2) * 8 + (r & 3);
+                rv[r] = p.res && pos < p.L ? p.res[(lbase + pos) * p.cout + co] : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int pos = pos0 + (r >> 2) * 8 + (r & 3);
                 if (pos >= p.L) continue;
                 const int64_t off = (lbase + pos) * p.cout + co;
-                float v = conv_f32_epilogue(acc[i][j][r], co, off, p);
+                // as conv_f32_epilogue: bias, scale, residual, activation
+                float v = acc[i][j][r] + bias;
+                if (p.scale) v = scale * v;
+                if (p.res) v += rv[r];
+                if (p.act == 1) v = tanhf(v);
+                if (p.act == 3) v = fminf(fmaxf(v, -1.0f), 1.0f);
                 if (p.y_pre) p.y_pre[off] = v;
                 if (p.a_out) v = snake_f32(v, a_o, r_o);
                 p.y[off] = v;
             }
+        }
     }
 }
 
