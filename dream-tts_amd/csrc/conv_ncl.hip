@@ -5,11 +5,15 @@
 //
 // xs is x or SnakeBeta(x) (full-precision sinf; f32 outputs are held to 1e-5). GEMM view per
 // lane: M = output channels, N = positions, K = (tap, channel). A workgroup owns 64 channels x
-// 64 positions; per 16-channel chunk it stages the dilated window of x (16 rows x
-// 64 + (k-1)*dil positions) and the 64 x k x 16 weight slice in LDS (two buffers, the next
-// chunk prefetched through registers), then four waves (2 x 2) run v_mfma_f32_32x32x2_f32, each
-// tap reading the window at offset t*dil. The epilogue writes straight from the accumulators:
-// the 32 lanes of a C column are 32 consecutive positions.
+// 64 positions; per KC-channel chunk (8 for k = 7, 16 for k = 1) it stages the dilated window of
+// x position-major (64 + (k-1)*dil rows of KC channels, transposed as it is stored) and the
+// 64 x k x KC weight slice in LDS (two buffers, the next chunk prefetched through registers),
+// then four waves (2 x 2) run v_mfma_f32_32x32x2_f32, each tap reading the window at row offset
+// t*dil. MFMA step s pairs channel s (lanes 0-31) with channel KC/2 + s (lanes 32-63), so a
+// lane's operands of a tap are consecutive floats of one row: 16-byte LDS reads for both the
+// weights and the window; with k = KMAX the taps are unrolled and tap t+1's reads issue under
+// tap t's MFMAs. The epilogue writes straight from the accumulators: the 32 lanes of a C column
+// are 32 consecutive positions.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -24,21 +28,26 @@ struct NclParams {
     int tiles_m, tiles_n, total, per_xcd;
 };
 
-constexpr int kBM = 64, kBN = 64, kKC = 16;
+constexpr int kBM = 64, kBN = 64;
 
 // One workgroup = 64 output channels x 64 positions of one lane; four waves (2 x 2), each one
-// 32 x 32 accumulator block. Per 16-channel chunk the window (16 rows x 64 + (k-1)*dil
-// positions, SnakeBeta applied as it is staged) and the 64 x k x 16 weight slice sit in one of
-// two LDS buffers: chunk c+1 is stored from registers into the other buffer while chunk c+2 is
-// loaded into registers and chunk c is multiplied, one barrier per chunk.
-template <int KMAX, int HMAX, bool SNAKE>
+// 32 x 32 accumulator block. Per KC-channel chunk the window (64 + (k-1)*dil positions x KC
+// channels, SnakeBeta applied as it is staged) and the 64 x k x KC weight slice sit in one of two
+// LDS buffers: chunk c+1 is stored from registers into the other buffer while chunk c+2 is
+// loaded into registers and chunk c is multiplied, one barrier per chunk. KT = KMAX when k fills
+// the class (taps unrolled), 0 for fewer taps.
+template <int KMAX, int HMAX, int KT, int KC, bool SNAKE>
 __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
-    constexpr int XW = kBN + HMAX;                           // window positions per channel row
-    constexpr int WP = KMAX * kKC + 1;                       // weight row pitch (floats); +1 spreads the banks
-    constexpr int XN = (kKC * XW + 255) / 256;               // window elements per thread
-    constexpr int WN = (kBM * KMAX * kKC / 4 + 255) / 256;   // weight float4s per thread
-    __shared__ float xs[2][kKC * XW];
-    __shared__ float ws[2][kBM * WP];
+    constexpr int XR = kBN + HMAX;                             // window positions
+    constexpr int XP = KC + 4;                                 // window row (one position) pitch, floats
+    constexpr int WP = KMAX * KC + 4;                          // weight row pitch: 16-byte aligned rows
+    constexpr int C4 = KC / 4;
+    constexpr int XE = (KC * XR + 255) / 256;                  // window elements per thread
+    constexpr int WV = (kBM * KMAX * C4 + 255) / 256;          // weight float4s per thread
+    constexpr int H = KC / 2, HV = H / 4;                      // MFMA steps per tap, float4s per operand
+    static_assert(KC % 8 == 0, "chunk width");
+    __shared__ __attribute__((aligned(16))) float xs[2][XR * XP];
+    __shared__ __attribute__((aligned(16))) float ws[2][kBM * WP];
     const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (tile >= p.total) return;
     const int m_tile = tile % p.tiles_m;  // output channels fastest: neighbours share the window
@@ -47,19 +56,22 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
     const int lane_idx = rest / p.tiles_n;
     const int co0 = m_tile * kBM;
     const int l0 = n_tile * kBN;
-    const int rows = kBN + (p.k - 1) * p.dil;
-    const int K = p.k * p.cin;
+    const int k = KT > 0 ? KT : p.k;
+    const int rows = kBN + (k - 1) * p.dil;
+    const int K = k * p.cin;
     const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.cin * p.L;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int kh = lane >> 5, lr = lane & 31;
-    const int nx = kKC * rows, nw = kBM * p.k * kKC / 4;
+    const int nx = KC * rows, nw = kBM * k * C4;
 
-    float xr[XN];
-    float4_t wr[WN];
+    float xr[XE];
+    float4_t wr[WV];
     auto load = [&](int c0) {
+        // window: element e is channel e / rows at position e % rows, so consecutive threads read
+        // consecutive positions of one channel row
 #pragma unroll
-        for (int i = 0; i < XN; ++i) {
+        for (int i = 0; i < XE; ++i) {
             const int e = tid + i * 256;
             const int ci = e / rows, j = e - (e / rows) * rows;
             const int s = l0 - p.pad_left + j;
@@ -67,12 +79,12 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
             if (e < nx && s >= 0 && s < p.L) v = xl[static_cast<int64_t>(c0 + ci) * p.L + s];
             xr[i] = v;
         }
-        // weights: 16 consecutive input channels of one (output channel, tap) are 4 float4s
+        // weights: KC consecutive input channels of one (output channel, tap) are KC/4 float4s
 #pragma unroll
-        for (int i = 0; i < WN; ++i) {
+        for (int i = 0; i < WV; ++i) {
             const int e = tid + i * 256;
-            const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
-            const int t = q >> 2, c4 = q & 3;
+            const int m = e / (k * C4), q = e - (e / (k * C4)) * (k * C4);
+            const int t = q / C4, c4 = q % C4;
             wr[i] = e < nw ? *reinterpret_cast<const float4_t *>(p.w + static_cast<int64_t>(co0 + m) * K + t * p.cin + c0 +
                                                                c4 * 4)
                            : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -80,62 +92,90 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
     };
     auto store = [&](int c0, int b) {
 #pragma unroll
-        for (int i = 0; i < XN; ++i) {
+        for (int i = 0; i < XE; ++i) {
             const int e = tid + i * 256;
             if (e < nx) {
                 const int ci = e / rows, j = e - (e / rows) * rows;
-                const int s = l0 - p.pad_left + j;
                 float v = xr[i];
-                if constexpr (SNAKE)
+                if constexpr (SNAKE) {
+                    const int s = l0 - p.pad_left + j;
                     if (s >= 0 && s < p.L) v = snake_f32(v, p.a_in[c0 + ci], p.r_in[c0 + ci]);
-                xs[b][ci * XW + j] = v;
+                }
+                xs[b][j * XP + ci] = v;  // transposed: row = position
             }
         }
 #pragma unroll
-        for (int i = 0; i < WN; ++i) {
+        for (int i = 0; i < WV; ++i) {
             const int e = tid + i * 256;
             if (e < nw) {
-                const int m = e / (p.k * 4), q = e - (e / (p.k * 4)) * (p.k * 4);
-                float *dst = &ws[b][m * WP + q * 4];  // rows are WP floats apart (odd): scalar stores
-                dst[0] = wr[i][0];
-                dst[1] = wr[i][1];
-                dst[2] = wr[i][2];
-                dst[3] = wr[i][3];
+                const int m = e / (k * C4), q = e - (e / (k * C4)) * (k * C4);
+                *reinterpret_cast<float4_t *>(&ws[b][m * WP + q * 4]) = wr[i];
             }
         }
     };
 
     float16_t acc = float16_t{};
-    const int nchunks = p.cin / kKC;
+    const int nchunks = p.cin / KC;
     load(0);
     store(0, 0);
-    if (nchunks > 1) load(kKC);
+    if (nchunks > 1) load(KC);
     __syncthreads();
     for (int c = 0; c < nchunks; ++c) {
         const int b = c & 1;
         if (c + 1 < nchunks) {
-            store((c + 1) * kKC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
-            if (c + 2 < nchunks) load((c + 2) * kKC);
+            store((c + 1) * KC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
+            if (c + 2 < nchunks) load((c + 2) * KC);
         }
-        for (int t = 0; t < p.k; ++t) {
-            const float *wa = ws[b] + (wm * 32 + lr) * WP + t * kKC + kh;
-            const float *xb = xs[b] + kh * XW + wn * 32 + lr + t * p.dil;
+        // A[m][kk] = w[co0 + m][tap t, channel kk]; B[kk][n] = window[position n + t*dil][channel kk]
+        auto frag = [&](int t, float4_t (&fa)[HV], float4_t (&fb)[HV]) {
+            const float *wa = ws[b] + (wm * 32 + lr) * WP + t * KC + kh * H;
+            const float *xb = xs[b] + (wn * 32 + lr + t * p.dil) * XP + kh * H;
 #pragma unroll
-            for (int ci = 0; ci < kKC; ci += 2)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[ci], xb[ci * XW], acc, 0, 0, 0);
+            for (int h = 0; h < HV; ++h) {
+                fa[h] = *reinterpret_cast<const float4_t *>(wa + 4 * h);
+                fb[h] = *reinterpret_cast<const float4_t *>(xb + 4 * h);
+            }
+        };
+        auto mma = [&](const float4_t (&fa)[HV], const float4_t (&fb)[HV]) {
+#pragma unroll
+            for (int st = 0; st < H; ++st)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[st >> 2][st & 3], fb[st >> 2][st & 3], acc, 0, 0, 0);
+        };
+        if constexpr (KT > 0) {
+            float4_t fa[2][HV], fb[2][HV];
+            frag(0, fa[0], fb[0]);
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+                if (t + 1 < KT) frag(t + 1, fa[(t + 1) & 1], fb[(t + 1) & 1]);
+                mma(fa[t & 1], fb[t & 1]);
+            }
+        } else {
+            for (int t = 0; t < k; ++t) {
+                float4_t fa[HV], fb[HV];
+                frag(t, fa, fb);
+                mma(fa, fb);
+            }
         }
         __syncthreads();
     }
     const int64_t ybase = static_cast<int64_t>(lane_idx) * p.cout * p.L;
     const int pos = l0 + wn * 32 + lr;
     if (pos >= p.L) return;
+    // the block's residuals are requested together before its stores (res may alias the
+    // outputs, so a load issued after a store would wait for it)
+    float rv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+        rv[r] = p.res ? p.res[ybase + static_cast<int64_t>(co) * p.L + pos] : 0.0f;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
         const int64_t off = ybase + static_cast<int64_t>(co) * p.L + pos;
         float v = acc[r];
         if (p.bias) v += p.bias[co];
-        if (p.res) v += p.res[off];
+        if (p.res) v += rv[r];
         if (p.act == 1) v = tanhf(v);
         if (p.y_pre) p.y_pre[off] = v;
         if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
@@ -185,7 +225,7 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float *x, float *cols
     }
 }
 
-template <int KMAX, int HMAX>
+template <int KMAX, int HMAX, int KT, int KC>
 hipError_t launch_ncl(NclParams p, int64_t lanes, bool snake, hipStream_t stream) {
     p.tiles_m = p.cout / kBM;
     p.tiles_n = (p.L + kBN - 1) / kBN;
@@ -194,9 +234,9 @@ hipError_t launch_ncl(NclParams p, int64_t lanes, bool snake, hipStream_t stream
     p.per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
     if (snake)
-        conv_ncl_f32_mfma<KMAX, HMAX, true><<<grid, 256, 0, stream>>>(p);
+        conv_ncl_f32_mfma<KMAX, HMAX, KT, KC, true><<<grid, 256, 0, stream>>>(p);
     else
-        conv_ncl_f32_mfma<KMAX, HMAX, false><<<grid, 256, 0, stream>>>(p);
+        conv_ncl_f32_mfma<KMAX, HMAX, KT, KC, false><<<grid, 256, 0, stream>>>(p);
     return hipGetLastError();
 }
 
@@ -238,13 +278,18 @@ extern "C" int dtts_conv1d_ncl_f32_ex(const dtts_conv_desc *d, hipStream_t strea
     p.act = d->act;
     const int64_t halo = (d->k - 1) * d->dilation;
     hipError_t e;
-    if (d->cin % dtts::kKC == 0 && d->cout % dtts::kBM == 0 && d->k <= 7 && halo <= 64 && dtts::aligned(d->w, 16)) {
+    // the tile's classes: k = 1 on 16-channel chunks, k <= 7 on 8-channel chunks
+    const int64_t kc = d->k == 1 ? 16 : 8;
+    if (d->cin % kc == 0 && d->cout % dtts::kBM == 0 && d->k <= 7 && halo <= 64 && dtts::aligned(d->w, 16)) {
         DTTS_REQUIRE(d->lanes * (d->cout / dtts::kBM) * ((d->len + dtts::kBN - 1) / dtts::kBN) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
+        const bool snake = d->in_alpha != nullptr;
         if (d->k == 1)
-            e = dtts::launch_ncl<1, 0>(p, d->lanes, d->in_alpha != nullptr, stream);
+            e = dtts::launch_ncl<1, 0, 1, 16>(p, d->lanes, snake, stream);
+        else if (d->k == 7)
+            e = dtts::launch_ncl<7, 64, 7, 8>(p, d->lanes, snake, stream);
         else
-            e = dtts::launch_ncl<7, 64>(p, d->lanes, d->in_alpha != nullptr, stream);
+            e = dtts::launch_ncl<7, 64, 0, 8>(p, d->lanes, snake, stream);
     } else {
         const int64_t total = d->lanes * d->cout * d->len;
         dtts::conv_ncl_f32_direct<<<dtts::grid_for(total, 256, 16), 256, 0, stream>>>(p, total);
