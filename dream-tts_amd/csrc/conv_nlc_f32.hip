@@ -7,9 +7,10 @@
 //
 // xs is x, or SnakeBeta(x) applied as the window is staged (full-precision sinf; a padded tap
 // stays 0, as snake(0) = 0 gives). GEMM view per lane: M = positions, N = output channels,
-// K = (tap, channel). A workgroup owns BM = 128 positions x BN output channels of one lane: BN 64
-// (2 x 2 waves of 64 x 32), 96 (4 x 1 waves of 32 x 96) or 32 (4 x 1 waves of 32 x 32), the widest
-// that divides cout. Per 8-channel chunk it stages the dilated window (128 + (k-1)*dil rows) and
+// K = (tap, channel). A workgroup owns BM positions x BN output channels of one lane: BN 64
+// (k = 7: 256 positions over 4 x 2 waves of 64 x 32, four waves per SIMD; otherwise 128 over 2 x 2),
+// 96 (128 over 4 x 1 waves of 32 x 96) or 32 (128 over 4 x 1 waves of 32 x 32), the widest BN that
+// divides cout. Per 8-channel chunk it stages the dilated window (BM + (k-1)*dil rows) and
 // the BN x k x 8 weight slice in LDS (two buffers: chunk c+1 goes from registers into one while
 // chunk c+2's loads are in flight and chunk c is multiplied, one barrier per chunk). The waves run
 // v_mfma_f32_32x32x2_f32; step s of a tap pairs channel s (lanes 0-31) with channel 4 + s (lanes
@@ -33,7 +34,7 @@ struct NlcF32Params {
     int tiles_m, tiles_n, total, per_xcd;
 };
 
-constexpr int kF32BM = 128, kF32KC = 8;
+constexpr int kF32KC = 8;
 
 __device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off, const NlcF32Params &p) {
     float v = s;
@@ -48,9 +49,9 @@ __device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off,
 // BM x BN tile over WM x WN waves (wave tile (BM/WM) x (BN/WN) in 32 x 32 blocks); KT = KMAX when
 // k fills the class (taps unrolled, the next tap's operands read under the current tap's MFMAs),
 // 0 for fewer taps.
-template <int KMAX, int HMAX, int KT, int BN, int WM, int WN, bool SNAKE>
-__global__ __launch_bounds__(64 * WM * WN, 2) void conv_nlc_f32_mfma(NlcF32Params p) {
-    constexpr int BM = kF32BM, KC = kF32KC;
+template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN, bool SNAKE>
+__global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(NlcF32Params p) {
+    constexpr int KC = kF32KC;
     constexpr int NT = 64 * WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
     constexpr int XR = BM + HMAX;               // window rows
@@ -324,28 +325,32 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
 
 // The tile's output-channel width: the widest of 64, 96 and 32 that divides cout.
 int f32_tile_bn(int64_t cout) { return cout % 64 == 0 ? 64 : cout % 96 == 0 ? 96 : 32; }
+// Its rows: 256 for the 64-wide k = 7 tile, 128 otherwise.
+int f32_tile_bm(int kmax, int bn) { return kmax == 7 && bn == 64 ? 256 : 128; }
 
-template <int KMAX, int HMAX, int KT, int BN, int WM, int WN>
+template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN>
 hipError_t launch_f32_tile(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
     p.tiles_n = p.cout / BN;
-    p.tiles_m = (p.L + kF32BM - 1) / kF32BM;
+    p.tiles_m = (p.L + BM - 1) / BM;
     const int64_t total = lanes * p.tiles_m * p.tiles_n;
     p.total = static_cast<int>(total);
     p.per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
     if (snake)
-        conv_nlc_f32_mfma<KMAX, HMAX, KT, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(p);
     else
-        conv_nlc_f32_mfma<KMAX, HMAX, KT, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(p);
     return hipGetLastError();
 }
 
 template <int KMAX, int HMAX, int KT>
 hipError_t launch_nlc_f32(const NlcF32Params &p, int64_t lanes, bool snake, hipStream_t stream) {
     switch (f32_tile_bn(p.cout)) {
-    case 64: return launch_f32_tile<KMAX, HMAX, KT, 64, 2, 2>(p, lanes, snake, stream);
-    case 96: return launch_f32_tile<KMAX, HMAX, KT, 96, 4, 1>(p, lanes, snake, stream);
-    default: return launch_f32_tile<KMAX, HMAX, KT, 32, 4, 1>(p, lanes, snake, stream);
+    case 64:  // the k = 7 class on 256 rows over 4 x 2 waves (four waves per SIMD), the others on 128
+        if constexpr (KMAX == 7) return launch_f32_tile<KMAX, HMAX, KT, 256, 64, 4, 2>(p, lanes, snake, stream);
+        else return launch_f32_tile<KMAX, HMAX, KT, 128, 64, 2, 2>(p, lanes, snake, stream);
+    case 96: return launch_f32_tile<KMAX, HMAX, KT, 128, 96, 4, 1>(p, lanes, snake, stream);
+    default: return launch_f32_tile<KMAX, HMAX, KT, 128, 32, 4, 1>(p, lanes, snake, stream);
     }
 }
 
@@ -375,9 +380,9 @@ const char *conv_f32_kernel_name(const dtts_conv_desc *d) {
     static thread_local char buf[96];
     int kmax, hmax, kt;
     f32_class(d, kmax, hmax, kt);
-    const int bn = f32_tile_bn(d->cout);
-    snprintf(buf, sizeof(buf), "conv_nlc_f32_mfma<%d, %d, %d, %d, %d, %d", kmax, hmax, kt, bn, bn == 64 ? 2 : 4,
-             bn == 64 ? 2 : 1);
+    const int bn = f32_tile_bn(d->cout), bm = f32_tile_bm(kmax, bn);
+    const int wm = bn == 64 ? bm / 64 : 4, wn = bn == 64 ? 2 : 1;
+    snprintf(buf, sizeof(buf), "conv_nlc_f32_mfma<%d, %d, %d, %d, %d, %d, %d", kmax, hmax, kt, bm, bn, wm, wn);
     return buf;
 }
 
@@ -422,7 +427,7 @@ int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
         conv_nlc_f32_narrow<<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
         e = hipGetLastError();
     } else if (nlc_f32_tiled(d)) {
-        DTTS_REQUIRE(d->lanes * (d->cout / f32_tile_bn(d->cout)) * ((d->len + kF32BM - 1) / kF32BM) < (int64_t(1) << 31),
+        DTTS_REQUIRE(d->lanes * (d->cout / f32_tile_bn(d->cout)) * ((d->len + 127) / 128) < (int64_t(1) << 31),
                      "%s: too many tiles", name);
         const bool snake = d->in_alpha != nullptr;
         int kmax, hmax, kt;
