@@ -10,12 +10,14 @@
 // K = (tap, channel). A workgroup owns BM positions x BN output channels of one lane: BN 64
 // (k = 7: 256 positions over 4 x 2 waves of 64 x 32, four waves per SIMD; otherwise 128 over 2 x 2),
 // 96 (128 over 4 x 1 waves of 32 x 96) or 32 (128 over 4 x 1 waves of 32 x 32), the widest BN that
-// divides cout. Per 8-channel chunk it stages the dilated window (BM + (k-1)*dil rows) and
-// the BN x k x 8 weight slice in LDS (two buffers: chunk c+1 goes from registers into one while
-// chunk c+2's loads are in flight and chunk c is multiplied, one barrier per chunk). The waves run
-// v_mfma_f32_32x32x2_f32; step s of a tap pairs channel s (lanes 0-31) with channel 4 + s (lanes
-// 32-63), so a lane's four operands of a tap are one 16-byte LDS read per 32-row or 32-column
-// block, and with k = KMAX the taps are unrolled and tap t+1's reads issue under tap t's MFMAs.
+// divides cout. Per KC-channel chunk (8; 16 at k = 1) it stages the dilated window
+// (BM + (k-1)*dil rows) and the BN x k x KC weight slice in LDS (two buffers: chunk c+1 goes from
+// registers into one while chunk c+2's loads are in flight and chunk c is multiplied, one barrier
+// per chunk). The waves run
+// v_mfma_f32_32x32x2_f32; step s of a tap pairs channel s (lanes 0-31) with channel KC/2 + s
+// (lanes 32-63), so a lane's operands of a tap are 16-byte LDS reads (one per 32-row or 32-column
+// block at KC = 8), and with k = KMAX the taps are unrolled and tap t+1's reads issue under tap
+// t's MFMAs.
 // The 32 lanes of an accumulator row are 32 consecutive output channels of one position, so the
 // epilogue's loads and stores are 128-byte runs straight from the accumulators.
 // A single output channel (the codec's 96 -> 1 output conv) runs a window kernel of its own;
@@ -49,9 +51,8 @@ __device__ __forceinline__ float conv_f32_epilogue(float s, int co, int64_t off,
 // BM x BN tile over WM x WN waves (wave tile (BM/WM) x (BN/WN) in 32 x 32 blocks); KT = KMAX when
 // k fills the class (taps unrolled, the next tap's operands read under the current tap's MFMAs),
 // 0 for fewer taps.
-template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN, bool SNAKE>
+template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN, int KC, bool SNAKE>
 __global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(NlcF32Params p) {
-    constexpr int KC = kF32KC;
     constexpr int NT = 64 * WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
     constexpr int XR = BM + HMAX;               // window rows
@@ -60,8 +61,9 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(N
     constexpr int C4 = KC / 4;                  // float4s per row of a chunk
     constexpr int XN = (XR * C4 + NT - 1) / NT;            // window float4s per thread
     constexpr int WV = (BN * KMAX * C4 + NT - 1) / NT;     // weight float4s per thread
-    constexpr int H = KC / 2;                   // MFMA steps per tap
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC == 8, "f32 tile shape");
+    constexpr int H = KC / 2;                   // MFMA steps per tap; step s pairs channels s and H + s
+    constexpr int HV = H / 4;                   // float4s per operand block and tap
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KC % 8 == 0, "f32 tile shape");
     __shared__ __attribute__((aligned(16))) float xs[2][XR * XP];
     __shared__ __attribute__((aligned(16))) float ws[2][BN * WP];
     const int tile = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
@@ -149,26 +151,37 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(N
             store((c + 1) * KC, b ^ 1);  // that buffer was last read by chunk c-1, before the barrier
             if (c + 2 < nchunks) load((c + 2) * KC);
         }
-        // operands of tap t: A[m][kk] = window[row m + t*dil][channel], B[kk][n] = w[n][tap t, channel]
-        auto frag = [&](int t, float4_t (&fa)[TM], float4_t (&fb)[TN]) {
+        // operands of tap t: A[m][kk] = window[row m + t*dil][channel], B[kk][n] = w[n][tap t, channel];
+        // a lane's H operands of a block are HV float4s
+        typedef float4_t FragA[TM][HV];
+        typedef float4_t FragB[TN][HV];
+        auto frag = [&](int t, FragA &fa, FragB &fb) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-                fa[i] = *reinterpret_cast<const float4_t *>(xs[b] + (wm * WTM + i * 32 + lr + t * p.dil) * XP + kh * 4);
+            for (int i = 0; i < TM; ++i) {
+                const float *xa = xs[b] + (wm * WTM + i * 32 + lr + t * p.dil) * XP + kh * H;
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                fb[j] = *reinterpret_cast<const float4_t *>(ws[b] + (wn * WTN + j * 32 + lr) * WP + t * KC + kh * 4);
+                for (int h = 0; h < HV; ++h) fa[i][h] = *reinterpret_cast<const float4_t *>(xa + 4 * h);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float *wb = ws[b] + (wn * WTN + j * 32 + lr) * WP + t * KC + kh * H;
+#pragma unroll
+                for (int h = 0; h < HV; ++h) fb[j][h] = *reinterpret_cast<const float4_t *>(wb + 4 * h);
+            }
         };
-        auto mma = [&](const float4_t (&fa)[TM], const float4_t (&fb)[TN]) {
+        auto mma = [&](const FragA &fa, const FragB &fb) {
 #pragma unroll
             for (int st = 0; st < H; ++st)
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st >> 2][st & 3], fb[j][st >> 2][st & 3],
+                                                                         acc[i][j], 0, 0, 0);
         };
         if constexpr (KT > 0) {
-            float4_t fa[2][TM], fb[2][TN];
+            FragA fa[2];
+            FragB fb[2];
             frag(0, fa[0], fb[0]);
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
@@ -177,7 +190,8 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(N
             }
         } else {
             for (int t = 0; t < k; ++t) {
-                float4_t fa[TM], fb[TN];
+                FragA fa;
+                FragB fb;
                 frag(t, fa, fb);
                 mma(fa, fb);
             }
@@ -327,8 +341,11 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
 int f32_tile_bn(int64_t cout) { return cout % 64 == 0 ? 64 : cout % 96 == 0 ? 96 : 32; }
 // Its rows: 256 for the 64-wide k = 7 tile, 128 otherwise.
 int f32_tile_bm(int kmax, int bn) { return kmax == 7 && bn == 64 ? 256 : 128; }
+// Channels per chunk: 16 for k = 1 (half the barriers of 8; 7-9% faster on the codec's k = 1
+// shapes), 8 otherwise.
+constexpr int f32_tile_kc(int kmax) { return kmax == 1 ? 16 : kF32KC; }
 
-template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN>
+template <int KMAX, int HMAX, int KT, int BM, int BN, int WM, int WN, int KC = kF32KC>
 hipError_t launch_f32_tile(NlcF32Params p, int64_t lanes, bool snake, hipStream_t stream) {
     p.tiles_n = p.cout / BN;
     p.tiles_m = (p.L + BM - 1) / BM;
@@ -337,20 +354,21 @@ hipError_t launch_f32_tile(NlcF32Params p, int64_t lanes, bool snake, hipStream_
     p.per_xcd = static_cast<int>((total + 7) / 8);
     const unsigned grid = static_cast<unsigned>(int64_t(p.per_xcd) * 8);
     if (snake)
-        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, true><<<grid, 64 * WM * WN, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, KC, true><<<grid, 64 * WM * WN, 0, stream>>>(p);
     else
-        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, false><<<grid, 64 * WM * WN, 0, stream>>>(p);
+        conv_nlc_f32_mfma<KMAX, HMAX, KT, BM, BN, WM, WN, KC, false><<<grid, 64 * WM * WN, 0, stream>>>(p);
     return hipGetLastError();
 }
 
 template <int KMAX, int HMAX, int KT>
 hipError_t launch_nlc_f32(const NlcF32Params &p, int64_t lanes, bool snake, hipStream_t stream) {
+    constexpr int KC = f32_tile_kc(KMAX);
     switch (f32_tile_bn(p.cout)) {
     case 64:  // the k = 7 class on 256 rows over 4 x 2 waves (four waves per SIMD), the others on 128
-        if constexpr (KMAX == 7) return launch_f32_tile<KMAX, HMAX, KT, 256, 64, 4, 2>(p, lanes, snake, stream);
-        else return launch_f32_tile<KMAX, HMAX, KT, 128, 64, 2, 2>(p, lanes, snake, stream);
-    case 96: return launch_f32_tile<KMAX, HMAX, KT, 128, 96, 4, 1>(p, lanes, snake, stream);
-    default: return launch_f32_tile<KMAX, HMAX, KT, 128, 32, 4, 1>(p, lanes, snake, stream);
+        if constexpr (KMAX == 7) return launch_f32_tile<KMAX, HMAX, KT, 256, 64, 4, 2, KC>(p, lanes, snake, stream);
+        else return launch_f32_tile<KMAX, HMAX, KT, 128, 64, 2, 2, KC>(p, lanes, snake, stream);
+    case 96: return launch_f32_tile<KMAX, HMAX, KT, 128, 96, 4, 1, KC>(p, lanes, snake, stream);
+    default: return launch_f32_tile<KMAX, HMAX, KT, 128, 32, 4, 1, KC>(p, lanes, snake, stream);
     }
 }
 
@@ -368,8 +386,8 @@ bool nlc_f32_narrow(const dtts_conv_desc *d) {
 }
 
 bool nlc_f32_tiled(const dtts_conv_desc *d) {
-    return d->cin % kF32KC == 0 && d->cout % 32 == 0 && d->k <= 7 && (d->k - 1) * d->dilation <= 64 &&
-           aligned(d->x, 16) && aligned(d->w, 16);
+    return d->cin % f32_tile_kc(d->k == 1 ? 1 : 7) == 0 && d->cout % 32 == 0 && d->k <= 7 &&
+           (d->k - 1) * d->dilation <= 64 && aligned(d->x, 16) && aligned(d->w, 16);
 }
 
 }  // namespace
@@ -382,7 +400,8 @@ const char *conv_f32_kernel_name(const dtts_conv_desc *d) {
     f32_class(d, kmax, hmax, kt);
     const int bn = f32_tile_bn(d->cout), bm = f32_tile_bm(kmax, bn);
     const int wm = bn == 64 ? bm / 64 : 4, wn = bn == 64 ? 2 : 1;
-    snprintf(buf, sizeof(buf), "conv_nlc_f32_mfma<%d, %d, %d, %d, %d, %d, %d", kmax, hmax, kt, bm, bn, wm, wn);
+    snprintf(buf, sizeof(buf), "conv_nlc_f32_mfma<%d, %d, %d, %d, %d, %d, %d, %d", kmax, hmax, kt, bm, bn, wm, wn,
+             f32_tile_kc(kmax));
     return buf;
 }
 
