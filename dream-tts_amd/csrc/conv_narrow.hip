@@ -7,12 +7,13 @@
 // dot products accumulate in f32, in (chunk, tap, channel) order.
 //
 // Two kernels share that order, so their outputs agree bit for bit:
-//   conv_nlc_f16_narrow_k<K>  k = K (7: the codec's), 32-channel multiples, no prologue SnakeBeta.
-//       The next chunk's window is loaded into registers while the current one is on the dot
-//       products, into the other of two LDS windows (one barrier per chunk); the weights are
-//       uniform loads (scalar registers). ~51 KB of LDS: three workgroups per CU.
+//   conv_nlc_f16_narrow_k<K, SNAKE>  k = K (7: the codec's), 32-channel multiples, the prologue
+//       SnakeBeta optional. The next chunk's window is loaded into registers while the current
+//       one is on the dot products, into the other of two LDS windows (one barrier per chunk); the
+//       weights are uniform loads (scalar registers). ~51 KB of LDS: three workgroups per CU.
 //   conv_nlc_f16_narrow       any k <= 7, 8-channel multiples, optional prologue SnakeBeta: one
 //       window, loaded, stored and consumed a chunk at a time, the chunk's weights in LDS.
+// Both apply the prologue SnakeBeta through snake_f16out, as the standalone snake does.
 #include "conv.hpp"
 #include "snake.hpp"
 
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow(NarrowParams p) {
     if (l < p.L) narrow_store(p, lane_idx, l, acc);
 }
 
-template <int K>
+template <int K, bool SNAKE>
 __global__ __launch_bounds__(256) void conv_nlc_f16_narrow_k(NarrowParams p) {
     constexpr int SEGS = kKC / 8;
     constexpr int NVEC = (kRows * SEGS + 255) / 256;
@@ -148,11 +149,30 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow_k(NarrowParams p) {
     load(0);
     int st = 0;
     for (int c0 = 0; c0 < p.cin; c0 += kKC, st ^= 1) {
+        // the thread's 8 channels of this chunk (segment tid % SEGS of every row it stages)
+        float ka[8], kr[8];
+        if constexpr (SNAKE) {
+            const int c = c0 + (tid % SEGS) * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ka[j] = p.a_in[c + j];
+                kr[j] = p.r_in[c + j];
+            }
+        }
         // window st was last read two chunks ago, before the barrier that closed the last chunk
 #pragma unroll
         for (int i = 0; i < NVEC; ++i) {
             const int v = tid + i * 256;
-            if (v < nvec) *reinterpret_cast<half8_t *>(win[st] + (v / SEGS) * kPitch + (v % SEGS) * 8) = buf[i];
+            if (v < nvec) {
+                half8_t h = buf[i];
+                if constexpr (SNAKE) {
+                    // rows outside the sequence hold 0, which SnakeBeta keeps 0
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        h[j] = static_cast<half_t>(snake_f16out(static_cast<float>(h[j]), ka[j], kr[j]));
+                }
+                *reinterpret_cast<half8_t *>(win[st] + (v / SEGS) * kPitch + (v % SEGS) * 8) = h;
+            }
         }
         if (c0 + kKC < p.cin) load(c0 + kKC);
         __syncthreads();
@@ -176,16 +196,14 @@ __global__ __launch_bounds__(256) void conv_nlc_f16_narrow_k(NarrowParams p) {
     if (l < p.L) narrow_store(p, lane_idx, l, acc);
 }
 
-// The specialised kernel's shapes: k = 7, 32-channel multiples, no prologue SnakeBeta, 16-byte
-// weight rows.
-bool narrow_k7(const dtts_conv_desc *d) {
-    return d->k == 7 && d->cin % kKC == 0 && !d->in_alpha && aligned(d->w, 16);
-}
+// The specialised kernel's shapes: k = 7, 32-channel multiples, 16-byte weight rows.
+bool narrow_k7(const dtts_conv_desc *d) { return d->k == 7 && d->cin % kKC == 0 && aligned(d->w, 16); }
 
 }  // namespace
 
 const char *conv_narrow_kernel_name(const dtts_conv_desc *d) {
-    return narrow_k7(d) ? "conv_nlc_f16_narrow_k<7>" : "conv_nlc_f16_narrow";
+    if (!narrow_k7(d)) return "conv_nlc_f16_narrow";
+    return d->in_alpha ? "conv_nlc_f16_narrow_k<7, true>" : "conv_nlc_f16_narrow_k<7, false>";
 }
 
 bool conv_narrow_eligible(const dtts_conv_desc *d) {
@@ -213,8 +231,10 @@ hipError_t conv_narrow_launch(const dtts_conv_desc *d, hipStream_t stream) {
     p.act = d->act;
     p.tiles_m = static_cast<int>((d->len + kBM - 1) / kBM);
     const int64_t grid = d->lanes * p.tiles_m;
-    if (narrow_k7(d))
-        conv_nlc_f16_narrow_k<7><<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
+    if (narrow_k7(d) && d->in_alpha)
+        conv_nlc_f16_narrow_k<7, true><<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
+    else if (narrow_k7(d))
+        conv_nlc_f16_narrow_k<7, false><<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
     else
         conv_nlc_f16_narrow<<<static_cast<unsigned>(grid), 256, 0, stream>>>(p);
     return hipGetLastError();

@@ -28,8 +28,10 @@ __device__ __forceinline__ half_t snake_f16k(half_t x, float ka, float r) {
     return static_cast<half_t>(__builtin_fmaf(r, s * s, xf));
 }
 
-// The same value from a and an f32 x that holds an f16 (every caller rounds x to f16 first), so
-// fused and standalone snakes store identical f16 bits.
+// The same value from a and an f32 x that holds an f16 (every caller rounds x to f16 first). Fused
+// and standalone snakes compute the same formula; where the compiler rounds the final fma to f16
+// directly (one rounding) in one kernel and through f32 (two) in another, results within a
+// hair of an f16 rounding midpoint differ by one ulp (a few elements per million, measured).
 __device__ __forceinline__ float snake_f16out(float x, float a, float r) {
     const float s = sin_rev_f16out(x * (a * kInv2Pi));
     return __builtin_fmaf(r, s * s, x);
