@@ -119,6 +119,18 @@ def test_stack_talker_widths(dev):
     p.step(synth.randint(94, "stack.talker.pos", (lanes,), 0, 255).astype(np.int32), graph=True)
 
 
+def test_stack_talker_long_cache_graph_replays(dev):
+    """The talker's widths at its cache capacity (2048): 1-4 chunks per (lane, kv head), spans
+    ending on and either side of chunk boundaries; an eager step, then graph replays as the
+    positions advance."""
+    geo = with_layers(replace(stack.TALKER, capacity=2048), 2)
+    lanes = 8
+    p = Pair(dev, geo, 97, lanes, 2048, tol=1e-3)
+    start = np.array([2040, 1535, 1536, 511, 512, 1024, 7, 1900], np.int32)
+    for s in range(4):
+        p.step(start + s, graph=(s > 0))
+
+
 def test_stack_rejects_bad_arguments(dev):
     geo = SMALL
     layers, fn = stack.random_weights(geo, 95)
