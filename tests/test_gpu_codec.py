@@ -79,3 +79,36 @@ def test_codec_profile_covers_every_launch(dev):
     assert all(s["ms"] > 0 for s in stages)
     assert stages[0]["name"] == "head" and stages[-1]["name"] == "out"
     assert sum(s["flops"] for s in stages) == pytest.approx(2 * 8 * geo.flops_per_frame(), rel=1e-9)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_codec_empty_and_single_frame_decodes(dev, dtype):
+    """No lanes or no frames: nothing is enqueued and nothing is written. One lane of one frame
+    (every conv's grid a single, mostly padded tile) matches the oracle chain under the bar above
+    (f16), or, f32, the oracle's f32 route and float64 within the reference's 5e-3 gate."""
+    geo = SMALL
+    w = _weights(geo, 10)
+    model = codec.Codec(geo, w, dev, dtype=dtype)
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    for lanes, frames in ((0, 5), (2, 0)):
+        lat = torch.zeros((lanes, frames, geo.latent_dim), dtype=tdt, device=dev)
+        out = torch.full((lanes, frames * geo.hop), 7.0, dtype=tdt, device=dev)
+        assert model.decode(lat, out=out).shape == (lanes, frames * geo.hop)
+    canary = torch.full((3, geo.hop), 7.0, dtype=tdt, device=dev)
+    model.decode(torch.zeros((1, 0, geo.latent_dim), dtype=tdt, device=dev), out=canary[:1, :0])
+    torch.cuda.synchronize()
+    assert bool((canary == 7.0).all())
+
+    latent = synth.f16_bits(synth.normal(10, "latent", (1, 1, geo.latent_dim)))
+    lat32 = synth.from_f16_bits(latent)
+    exact = torch_decode(geo, w, lat32[0])[None]
+    if dtype == "f16":
+        got = synth.from_f16_bits(to_host(model.decode(to_dev(latent, dev))))
+        want = synth.from_f16_bits(ocodec.decode_f16(geo, ocodec.prepare(geo, w), latent))
+        max_f16 = float(np.max(np.abs(want - exact)))
+        assert np.max(np.abs(got - want)) <= max(2e-2, 1.5 * max_f16)
+    else:  # the reference's codec.wav gate (validate.rs:315), against its f32 route and float64
+        got = to_host(model.decode(torch.from_numpy(lat32).to(dev)))
+        want = ocodec.decode_f32_reference(geo, ocodec.prepare(geo, w), lat32[0])[None]
+        assert np.max(np.abs(got - want)) <= 5e-3 and np.max(np.abs(got - exact)) <= 5e-3
+    assert got.shape == (1, geo.hop) and np.isfinite(got).all()
