@@ -51,13 +51,23 @@ def dominant(stages_runs):
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with its family and model numbers (which identify the
+    generation where a VM shortens the name) and the logical CPUs the system reports."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model") and key not in fields:
+                fields[key] = val.strip()
+            if len(fields) == 3:
+                break
     except OSError:
-        pass
-    return None
+        return None
+    if "model name" not in fields:
+        return None
+    return (f"{fields['model name']} (family {fields.get('cpu family', '?')}, model {fields.get('model', '?')}, "
+            f"{os.cpu_count()} logical CPUs)")
 
 
 def kernel_rooflines(by):
