@@ -487,6 +487,16 @@ def workload_cfg5f32(dev, args):
 # ---------------------------------------------------------------- rocprofv3 counter digest
 
 COPY_PROBE_BYTES = 1 << 30  # --copy-probe: a mul kernel reading and writing 1 GiB
+# The runs a --pmc-summary digest comes from (from the repository root on the GPU box, after
+# `cd /tmp && export TMPDIR=/tmp`; paths relative to the repository), recorded in the digest.
+PMC_COMMANDS = [
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o fetch -- python3 bench.py "
+    "--no-cpu-baseline --steps 1 --warmup 0 --profile-runs 1 --copy-probe --stages-out gpurun_out/stages.json",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o write -- python3 bench.py "
+    "--no-cpu-baseline --steps 1 --warmup 0 --profile-runs 1 --copy-probe",
+    "python3 bench.py --pmc-summary gpurun_out/prof_fetch/fetch_counter_collection.csv "
+    "gpurun_out/prof_write/write_counter_collection.csv gpurun_out/stages.json",
+]
 
 
 def pmc_summary(fetch_csv, write_csv, stages_json):
@@ -515,7 +525,7 @@ def pmc_summary(fetch_csv, write_csv, stages_json):
         raise SystemExit("pmc-summary: fewer dtts dispatches than stages")
     # the last n dispatches are the profile run's: one plan over all lanes on one stream, in stage
     # order (the timed decode before it interleaves its two half-batch plans)
-    out = {"fetch_scale": cf, "write_scale": cw, "kernels": {}, "stages": []}
+    out = {"commands": PMC_COMMANDS, "fetch_scale": cf, "write_scale": cw, "kernels": {}, "stages": []}
     for st, f, w in zip(stages, fd[-n:], wd[-n:]):
         rd, wb = float(f["Counter_Value"]) * 1024 * cf, float(w["Counter_Value"]) * 1024 * cw
         out["stages"].append({"name": st["name"], "kernel": st["kernel"], "fetch_bytes": rd, "write_bytes": wb,
