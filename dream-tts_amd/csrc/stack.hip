@@ -543,6 +543,187 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     }
 }
 
+// The same attention on the f32 matrix cores (v_mfma_f32_32x32x2_f32), one wave per (lane bi,
+// head h, 32 consecutive queries ti0 ..): the score block of 32 keys x the 32 queries is K . Q^T,
+// so a lane holds 16 keys of one query (its lane index mod 32). MFMA step s pairs dimension s
+// (lanes 0-31) with dimension D/2 + s (lanes 32-63): a lane's operands are D/2 contiguous floats
+// of its query row and of its key row, loaded once per block with 16-byte loads, the next block's
+// keys while the current one multiplies. The scores go to LDS ([key][query], rows 34 floats
+// apart), masked to -inf outside each query's range; then softmax_last_dim as candle computes it
+// (max, exp(s - max), sum, probs = e / sum), in place; then out^T = V^T . P^T in 32-dimension
+// blocks, two keys per step (key s and s + 16 of a 32-key block), each lane one dimension. The
+// dot products are summed in the matrix cores' order rather than dimension order; the f32
+// tolerance of the prefill's parity holds either way. LDS: the block's keys x 34 floats.
+constexpr int kPrefillMfmaPitch = 34;         // 16 rows x 34 floats = 32 banks apart (mod 64)
+constexpr int kPrefillMfmaMaxLds = 64 * 1024;  // longer key ranges take prefill_attention
+constexpr int kPrefillMfmaMinT = 16;           // fewer queries leave most of a 32-query block idle
+
+template <int D>
+__global__ __launch_bounds__(64) void prefill_attention_mfma(const float *q, const half_t *kc, const half_t *vc,
+                                                             const float *kf, const float *vf, half_t *out, int t,
+                                                             int start, int heads, int n_kv, int cap, int window,
+                                                             float scale) {
+#pragma clang fp contract(off)
+    extern __shared__ __attribute__((aligned(16))) float sc[];  // [keys][kPrefillMfmaPitch]
+    constexpr int H = D / 2, NDB = D / 32, P = kPrefillMfmaPitch;
+    static_assert(D == 64 || D == 128, "head dim");
+    const int lane = threadIdx.x, l32 = lane & 31, hf = lane >> 5;
+    const int qblocks = (t + 31) / 32;
+    const int h = blockIdx.x % heads, qb = (blockIdx.x / heads) % qblocks, bi = blockIdx.x / (heads * qblocks);
+    const int ti0 = qb * 32;
+    const int nq = t - ti0 < 32 ? t - ti0 : 32;
+    const int kh = h / (heads / n_kv);
+    auto lo_of = [&](int ti) { return window > 0 && start + ti + 1 > window ? start + ti + 1 - window : 0; };
+    const int lo = lo_of(ti0), hi = start + ti0 + nq - 1;  // the union of the block's key ranges
+    const int nb = (hi - lo + 32) / 32;
+    const half_t *kcr = kc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
+    const half_t *vcr = vc + (static_cast<int64_t>(bi) * n_kv + kh) * cap * D;
+    const float *kfr = kf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
+    const float *vfr = vf + (static_cast<int64_t>(bi) * n_kv + kh) * t * D;
+    const bool qok = l32 < nq;
+    const int tq = ti0 + l32;  // this lane's query
+    float qv[H];
+    {
+        const float *qr = q + ((static_cast<int64_t>(bi) * heads + h) * t + (qok ? tq : ti0)) * D + hf * H;
+#pragma unroll
+        for (int e = 0; e < H; e += 4) {
+            const float4_t v = *reinterpret_cast<const float4_t *>(qr + e);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) qv[e + c] = qok ? v[c] : 0.0f;
+        }
+    }
+    // key row j's dims hf*H .. hf*H + H - 1 as f32 (zeros past the range)
+    auto load_k = [&](int j, float (&kv)[H]) {
+        if (j > hi) {
+#pragma unroll
+            for (int e = 0; e < H; ++e) kv[e] = 0.0f;
+        } else if (j < start) {
+            const half_t *kr = kcr + static_cast<int64_t>(j) * D + hf * H;
+#pragma unroll
+            for (int e = 0; e < H; e += 8) {
+                const half8_t v = *reinterpret_cast<const half8_t *>(kr + e);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) kv[e + c] = static_cast<float>(v[c]);
+            }
+        } else {
+            const float *kr = kfr + static_cast<int64_t>(j - start) * D + hf * H;
+#pragma unroll
+            for (int e = 0; e < H; e += 4) {
+                const float4_t v = *reinterpret_cast<const float4_t *>(kr + e);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kv[e + c] = v[c];
+            }
+        }
+    };
+    float mx = -INFINITY;  // over this lane's rows of its query's scores
+    auto score_block = [&](int b, const float (&kv)[H]) {
+        float16_t acc = {};
+#pragma unroll
+        for (int s = 0; s < H; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[s], qv[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int i = 32 * b + 8 * (v >> 2) + 4 * hf + (v & 3);  // key lo + i
+            const int j = lo + i;
+            const bool in = qok && j <= start + tq && j >= lo_of(tq);
+            float x = acc[v];
+            if (scale != 1.0f) x = x * scale;
+            sc[i * P + l32] = in ? x : -INFINITY;
+            if (in) mx = fmaxf(mx, x);
+        }
+    };
+    {
+        float k0[H], k1[H];
+        load_k(lo + l32, k0);
+        for (int b = 0; b < nb; b += 2) {
+            if (b + 1 < nb) load_k(lo + 32 * (b + 1) + l32, k1);
+            score_block(b, k0);
+            if (b + 1 < nb) {
+                if (b + 2 < nb) load_k(lo + 32 * (b + 2) + l32, k0);
+                score_block(b + 1, k1);
+            }
+        }
+    }
+    // softmax over the query's keys: lane (query l32, half hf) takes every second key
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int i = hf; i < 32 * nb; i += 2) {
+        const float e = qok ? expf(sc[i * P + l32] - mx) : 0.0f;  // exactly 0 outside the range
+        sc[i * P + l32] = e;
+        sum += e;
+    }
+    sum += __shfl_xor(sum, 32, 64);
+    for (int i = hf; i < 32 * nb; i += 2) sc[i * P + l32] = qok ? sc[i * P + l32] / sum : 0.0f;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // out^T[d][query] = sum over keys of v[key][d] p[query][key]; lane: dimension l32 of each block
+    auto load_v = [&](int b, float (&vv)[NDB][16]) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int j = lo + 32 * b + s + 16 * hf;
+            if (j > hi) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) vv[db][s] = 0.0f;
+            } else if (j < start) {
+                const half_t *vr = vcr + static_cast<int64_t>(j) * D + l32;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) vv[db][s] = static_cast<float>(vr[32 * db]);
+            } else {
+                const float *vr = vfr + static_cast<int64_t>(j - start) * D + l32;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) vv[db][s] = vr[32 * db];
+            }
+        }
+    };
+    float16_t o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = float16_t{};
+    auto pv_block = [&](int b, const float (&vv)[NDB][16]) {
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float p = sc[(32 * b + s + 16 * hf) * P + l32];
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[db][s], p, o[db], 0, 0, 0);
+        }
+    };
+    {
+        float v0[NDB][16], v1[NDB][16];
+        load_v(0, v0);
+        for (int b = 0; b < nb; b += 2) {
+            if (b + 1 < nb) load_v(b + 1, v1);
+            pv_block(b, v0);
+            if (b + 1 < nb) {
+                if (b + 2 < nb) load_v(b + 2, v0);
+                pv_block(b + 1, v1);
+            }
+        }
+    }
+    if (!qok) return;
+    half_t *dst = out + (static_cast<int64_t>(bi) * t + tq) * heads * D + h * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            half4_t r;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) r[c] = static_cast<half_t>(o[db][4 * g + c]);
+            *reinterpret_cast<half4_t *>(dst + 32 * db + 8 * g + 4 * hf) = r;
+        }
+}
+
+// The largest key range of any 32-query block of a prefill (prefill_attention_mfma's LDS rows).
+int prefill_block_keys(int t, int start, int window) {
+    int most = 0;
+    for (int ti0 = 0; ti0 < t; ti0 += 32) {
+        const int nq = t - ti0 < 32 ? t - ti0 : 32;
+        const int lo = window > 0 && start + ti0 + 1 > window ? start + ti0 + 1 - window : 0;
+        const int n = start + ti0 + nq - lo;
+        most = n > most ? n : most;
+    }
+    return most;
+}
+
 // Up to this many rows the prefill's projections run on the A-sharing kernel (its k ranges keep
 // the weights streaming at decode's rate); past it, on the tile kernel.
 constexpr int kPrefillMaxLdsRows = 128;
@@ -652,6 +833,12 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     const int per_wave = (keys + hd) * 4 * qp;  // LDS bytes: the scores and the queries
     const int wpb = per_wave * 4 <= 65536 ? 4 : (per_wave * 2 <= 65536 ? 2 : 1);
     const int att_waves = lanes * ((t + qp - 1) / qp) * heads;
+    // 32-query blocks on the matrix cores when there are enough queries and every block's keys
+    // fit its LDS
+    const size_t mfma_lds = static_cast<size_t>((prefill_block_keys(t, start, static_cast<int>(g.window)) + 31) / 32) *
+                            32 * kPrefillMfmaPitch * sizeof(float);
+    const bool attn_mfma = t >= kPrefillMfmaMinT && (hd == 64 || hd == 128) && mfma_lds <= kPrefillMfmaMaxLds;
+    const unsigned mfma_blocks = static_cast<unsigned>(lanes * ((t + 31) / 32) * heads);
     Partials pending{};
     const half_t *pending16 = nullptr;
     bool pending_round = false;
@@ -684,7 +871,13 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
 #define DTTS_PREFILL_ATTN(D_, QP_)                                                                                   \
     prefill_attention<D_, QP_><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, lanes, t, start, heads, n_kv, \
                                                                  cap, static_cast<int>(g.window), scale, keys, wpb)
-        if (hd == 128) {
+        if (attn_mfma && hd == 128) {
+            prefill_attention_mfma<128><<<mfma_blocks, 64, mfma_lds, stream>>>(
+                q, kc, vc, kf, vf, a16, t, start, heads, n_kv, cap, static_cast<int>(g.window), scale);
+        } else if (attn_mfma) {
+            prefill_attention_mfma<64><<<mfma_blocks, 64, mfma_lds, stream>>>(
+                q, kc, vc, kf, vf, a16, t, start, heads, n_kv, cap, static_cast<int>(g.window), scale);
+        } else if (hd == 128) {
             if (qp == 4)
                 DTTS_PREFILL_ATTN(128, 4);
             else if (qp == 2)

@@ -17,7 +17,7 @@ import torch
 import oracle
 from dtts import DttsError, stack, synth
 
-from _stack_ref import SMALL, WINDOWED, inputs
+from _stack_ref import SMALL, WINDOWED, inputs, stack_prefill_f64
 from _util import rel, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
@@ -60,6 +60,9 @@ def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
     (SMALL, 43, 3, 0, 16),      # 129 rows: the first count on the tile kernel
     (SMALL, 3, 50, 0, 64),      # 150 rows: the tile kernel's f16 outputs
     (WINDOWED, 5, 30, 2, 32),   # 150 rows, windowed
+    # t >= 16: 32-query blocks on the f32 matrix cores
+    (LONG, 2, 100, 20, 160),    # a 20-key f16 prefix: the first key block crosses start; a 4-query last block
+    (replace(WINDOWED, capacity=96), 2, 70, 9, 96),  # D = 64, windows of 5 inside 32-query blocks, scaled scores
 ])
 def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
     layers, fn, x, kc, vc, st, state = _setup(dev, geo, 95, lanes, t, cap)
@@ -70,6 +73,28 @@ def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
     torch.cuda.synchronize()
     got = to_host(got)
     assert rel(got, want)[1] < 5e-4, rel(got, want)
+    _check(geo, state, kb, vb, kc, vc, start, t)
+
+
+def test_prefill_talker_widths(dev):
+    """The talker's widths (dim 2048, 16/8 heads, D 128, ffn 6144), 2 of its 28 layers, 2 lanes x
+    64 prompt positions: two 32-query blocks per (lane, head) on the matrix cores. Bar 1e-3 against
+    the oracle, as for the decode step at these widths (an f16 rounding on the other side of a tie
+    separates outputs by up to an f16 ulp of the rounded activation, 4.9e-4 relative), and the GPU
+    no further from a float64 evaluation with the same f16 rounding points than the oracle is,
+    within 2e-4."""
+    geo = replace(stack.TALKER, layers=2, capacity=128)
+    lanes, t, start = 2, 64, 0
+    layers, fn, x, kc, vc, st, state = _setup(dev, geo, 96, lanes, t, 128)
+    kb, vb = [k.copy() for k in kc], [v.copy() for v in vc]
+    exact, _, _ = stack_prefill_f64(geo, layers, fn, x, kc, vc, start)
+    want = oracle.stack_prefill_f32(geo, layers, fn, x, kc, vc, start)
+    got = to_host(st.prefill(to_dev(x, dev), state, start))
+    torch.cuda.synchronize()
+    d_oracle, d_gpu, d_both = rel(want, exact)[1], rel(got, exact)[1], rel(got, want)[1]
+    print(f"max-rel: oracle-f64 {d_oracle:.2e}, gpu-f64 {d_gpu:.2e}, gpu-oracle {d_both:.2e}")
+    assert d_both < 1e-3
+    assert d_gpu <= d_oracle + 2e-4
     _check(geo, state, kb, vb, kc, vc, start, t)
 
 
