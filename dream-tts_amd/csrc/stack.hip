@@ -572,7 +572,10 @@ __global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q,
     static_assert(D == 64 || D == 128, "head dim");
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
     const int qblocks = (t + 31) / 32;
-    const int h = blockIdx.x % heads, qb = (blockIdx.x / heads) % qblocks, bi = blockIdx.x / (heads * qblocks);
+    // the query blocks of lane bi in an order rotated by bi: consecutive workgroups, which land on
+    // different CUs, mix long and short key ranges
+    const int h = blockIdx.x % heads, bi = blockIdx.x / (heads * qblocks);
+    const int qb = ((blockIdx.x / heads) % qblocks + bi) % qblocks;
     const int ti0 = qb * 32;
     const int nq = t - ti0 < 32 ? t - ti0 : 32;
     const int kh = h / (heads / n_kv);
