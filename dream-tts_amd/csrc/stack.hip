@@ -543,31 +543,32 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
     }
 }
 
-// The same attention on the f32 matrix cores (v_mfma_f32_32x32x2_f32), one workgroup of two
+// The same attention on the f32 matrix cores (v_mfma_f32_32x32x2_f32), one workgroup of NW
 // waves per (lane bi, head h, 32 consecutive queries ti0 ..), the waves taking alternate blocks
 // of 32 keys. A score block is K . Q^T, so a lane holds 16 keys of one query (its lane index mod
 // 32); MFMA step s pairs dimension s (lanes 0-31) with dimension D/2 + s (lanes 32-63), so a
 // lane's operands are D/2 contiguous floats of its key row and of its query row (16-byte loads).
 // The scores go to LDS ([key][query], rows 34 floats apart), masked to -inf outside each query's
 // range; then softmax_last_dim as candle computes it (max, exp(s - max), sum, probs = e / sum),
-// the two waves' maxima and sums combined through LDS (wave 0's sum + wave 1's); then each wave's
+// the waves' maxima and sums combined through LDS (the sums in wave order); then each wave's
 // out^T = V^T . P^T over its key blocks in 32-dimension blocks, two keys per step (key s and
-// s + 16 of a block), and wave 0 adds wave 1's partial. The dot products are summed in the matrix
+// s + 16 of a block), and wave 0 adds the others' partials in wave order. The dot products are summed in the matrix
 // cores' order rather than dimension order; the prefill's f32 tolerance holds either way. A
 // block's keys (or values) load under the previous block's MFMAs, within two waves per SIMD's
-// registers. LDS: the keys x 34 floats, at least the partial output's D x 32 floats.
+// registers. LDS: the keys x 34 floats, at least (NW - 1) partial outputs of D x 32 floats.
 constexpr int kPrefillMfmaPitch = 34;          // 16 rows x 34 floats = 32 banks apart (mod 64)
 constexpr int kPrefillMfmaMaxLds = 64 * 1024;  // longer key ranges take prefill_attention
 constexpr int kPrefillMfmaMinT = 16;           // fewer queries leave most of a 32-query block idle
+constexpr int kPrefillMfmaWaves = 2;           // waves per 32-query block, on alternate key blocks (4: slower)
 
-template <int D>
-__global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q, const half_t *kc, const half_t *vc,
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void prefill_attention_mfma(const float *q, const half_t *kc, const half_t *vc,
                                                                  const float *kf, const float *vf, half_t *out, int t,
                                                                  int start, int heads, int n_kv, int cap, int window,
                                                                  float scale) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sc[];  // [keys][kPrefillMfmaPitch], then wave 1's output
-    __shared__ float red[2][2][32];                              // [max | sum][wave][query]
+    __shared__ float red[2][NW][32];                             // [max | sum][wave][query]
     constexpr int H = D / 2, NDB = D / 32, P = kPrefillMfmaPitch;
     static_assert(D == 64 || D == 128, "head dim");
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
@@ -641,23 +642,25 @@ __global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q,
         // the wave's blocks w, w + 2, ...: the next one's keys load under the current one's MFMAs
         float k0[H], k1[H];
         if (w < nb) load_k(lo + 32 * w + l32, k0);
-        for (int b = w; b < nb; b += 4) {
-            if (b + 2 < nb) load_k(lo + 32 * (b + 2) + l32, k1);
+        for (int b = w; b < nb; b += 2 * NW) {
+            if (b + NW < nb) load_k(lo + 32 * (b + NW) + l32, k1);
             score_block(b, k0);
-            if (b + 2 < nb) {
-                if (b + 4 < nb) load_k(lo + 32 * (b + 4) + l32, k0);
-                score_block(b + 2, k1);
+            if (b + NW < nb) {
+                if (b + 2 * NW < nb) load_k(lo + 32 * (b + 2 * NW) + l32, k0);
+                score_block(b + NW, k1);
             }
         }
     }
     // softmax over the query's keys: each wave over its own blocks' rows, lane (query l32, half
-    // hf) taking every second row; the two waves' maxima and sums meet in LDS
+    // hf) taking every second row; the waves' maxima and sums meet in LDS
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     if (hf == 0) red[0][w][l32] = mx;
     __syncthreads();
-    mx = fmaxf(red[0][0][l32], red[0][1][l32]);
+    mx = red[0][0][l32];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) mx = fmaxf(mx, red[0][u][l32]);
     float sum = 0.0f;
-    for (int b = w; b < nb; b += 2)
+    for (int b = w; b < nb; b += NW)
         for (int r = hf; r < 32; r += 2) {
             const int i = 32 * b + r;
             const float e = qok ? expf(sc[i * P + l32] - mx) : 0.0f;  // exactly 0 outside the range
@@ -667,8 +670,10 @@ __global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q,
     sum += __shfl_xor(sum, 32, 64);
     if (hf == 0) red[1][w][l32] = sum;
     __syncthreads();
-    sum = red[1][0][l32] + red[1][1][l32];
-    for (int b = w; b < nb; b += 2)
+    sum = red[1][0][l32];
+#pragma unroll
+    for (int u = 1; u < NW; ++u) sum += red[1][u][l32];  // in wave order
+    for (int b = w; b < nb; b += NW)
         for (int r = hf; r < 32; r += 2) {
             const int i = 32 * b + r;
             sc[i * P + l32] = qok ? sc[i * P + l32] / sum : 0.0f;
@@ -709,25 +714,35 @@ __global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q,
     {
         float v0[NDB][16], v1[NDB][16];
         if (w < nb) load_v(w, v0);
-        for (int b = w; b < nb; b += 4) {
-            if (b + 2 < nb) load_v(b + 2, v1);
+        for (int b = w; b < nb; b += 2 * NW) {
+            if (b + NW < nb) load_v(b + NW, v1);
             pv_block(b, v0);
-            if (b + 2 < nb) {
-                if (b + 4 < nb) load_v(b + 4, v0);
-                pv_block(b + 2, v1);
+            if (b + NW < nb) {
+                if (b + 2 * NW < nb) load_v(b + 2 * NW, v0);
+                pv_block(b + NW, v1);
             }
         }
     }
-    // wave 1's partial to LDS once both waves are done with the probabilities; wave 0 adds it
+    // the other waves' partials to LDS once every wave is done with the probabilities; wave 0 adds
+    // them in wave order
     __syncthreads();
-    if (w == 1) {
+    if (w > 0) {
+        float *mine = sc + (w - 1) * D * 32;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sc[(db * 16 + v) * 64 + lane] = o[db][v];
+            for (int v = 0; v < 16; ++v) mine[(db * 16 + v) * 64 + lane] = o[db][v];
     }
     __syncthreads();
-    if (w == 1 || !qok) return;
+    if (w > 0 || !qok) return;
+#pragma unroll
+    for (int u = 1; u < NW; ++u) {
+        const float *part = sc + (u - 1) * D * 32;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[db][v] = o[db][v] + part[(db * 16 + v) * 64 + lane];
+    }
     half_t *dst = out + (static_cast<int64_t>(bi) * t + tq) * heads * D + h * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -735,7 +750,7 @@ __global__ __launch_bounds__(128, 2) void prefill_attention_mfma(const float *q,
         for (int g = 0; g < 4; ++g) {
             half4_t r;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) r[c] = static_cast<half_t>(o[db][4 * g + c] + sc[(db * 16 + 4 * g + c) * 64 + lane]);
+            for (int c = 0; c < 4; ++c) r[c] = static_cast<half_t>(o[db][4 * g + c]);
             *reinterpret_cast<half4_t *>(dst + 32 * db + 8 * g + 4 * hf) = r;
         }
 }
@@ -866,9 +881,8 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     const size_t mfma_lds = static_cast<size_t>((prefill_block_keys(t, start, static_cast<int>(g.window)) + 31) / 32) *
                             32 * kPrefillMfmaPitch * sizeof(float);
     const bool attn_mfma = t >= kPrefillMfmaMinT && (hd == 64 || hd == 128) && mfma_lds <= kPrefillMfmaMaxLds;
-    const size_t mfma_lds_launch = mfma_lds > static_cast<size_t>(hd) * 32 * sizeof(float)
-                                       ? mfma_lds
-                                       : static_cast<size_t>(hd) * 32 * sizeof(float);  // wave 1's partial output
+    const size_t mfma_parts = static_cast<size_t>(kPrefillMfmaWaves - 1) * hd * 32 * sizeof(float);  // waves 1.. partials
+    const size_t mfma_lds_launch = mfma_lds > mfma_parts ? mfma_lds : mfma_parts;
     const unsigned mfma_blocks = static_cast<unsigned>(lanes * ((t + 31) / 32) * heads);
     Partials pending{};
     const half_t *pending16 = nullptr;
@@ -903,10 +917,10 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     prefill_attention<D_, QP_><<<at_blocks, 256, lds, stream>>>(q, kc, vc, kf, vf, a16, lanes, t, start, heads, n_kv, \
                                                                  cap, static_cast<int>(g.window), scale, keys, wpb)
         if (attn_mfma && hd == 128) {
-            prefill_attention_mfma<128><<<mfma_blocks, 128, mfma_lds_launch, stream>>>(
+            prefill_attention_mfma<128, kPrefillMfmaWaves><<<mfma_blocks, 64 * kPrefillMfmaWaves, mfma_lds_launch, stream>>>(
                 q, kc, vc, kf, vf, a16, t, start, heads, n_kv, cap, static_cast<int>(g.window), scale);
         } else if (attn_mfma) {
-            prefill_attention_mfma<64><<<mfma_blocks, 128, mfma_lds_launch, stream>>>(
+            prefill_attention_mfma<64, kPrefillMfmaWaves><<<mfma_blocks, 64 * kPrefillMfmaWaves, mfma_lds_launch, stream>>>(
                 q, kc, vc, kf, vf, a16, t, start, heads, n_kv, cap, static_cast<int>(g.window), scale);
         } else if (hd == 128) {
             if (qp == 4)
