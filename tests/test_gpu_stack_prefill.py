@@ -63,6 +63,8 @@ def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
     # t >= 16: 32-query blocks on the f32 matrix cores
     (LONG, 2, 100, 20, 160),    # a 20-key f16 prefix: the first key block crosses start; a 4-query last block
     (replace(WINDOWED, capacity=96), 2, 70, 9, 96),  # D = 64, windows of 5 inside 32-query blocks, scaled scores
+    (replace(SMALL, capacity=512), 1, 64, 380, 512),  # 444 keys: 14 key blocks, 61 KB of scores, the most it takes
+    (replace(SMALL, capacity=512), 1, 40, 460, 512),  # 500 keys: past its LDS, the per-wave kernel again
 ])
 def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
     layers, fn, x, kc, vc, st, state = _setup(dev, geo, 95, lanes, t, cap)
