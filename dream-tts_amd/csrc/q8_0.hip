@@ -24,9 +24,13 @@ namespace {
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 
+// Activation modes (the DTTS_Q8_* values).
+constexpr int kA16 = DTTS_Q8_W8A16, kA8 = DTTS_Q8_W8A8, kA32 = DTTS_Q8_W8A32;
+
+template <typename XT>
 struct Q8Params {
-    const half_t *x;       // [m, k]
-    const uint8_t *w;      // [n][k/32] blocks of 34 bytes
+    const XT *x;           // [m, k], f16 or f32
+    const uint8_t *w;      // [n][k/32] blocks of 34 bytes (or the packed layout)
     float *y;              // [m, n]
     int m, k, n, ks, slab_blocks;
 };
@@ -44,8 +48,87 @@ __device__ __forceinline__ void load_wblock(const uint8_t *blk, int g, uint64_t 
     d = static_cast<float>(h);
 }
 
-template <int MB, bool A8>
-__global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params p) {
+// 8 consecutive activations as f32 (f16 widens exactly), zero when the row is absent.
+__device__ __forceinline__ void load_x8(const half_t *p, bool valid, float v[8]) {
+    half8_t h = valid ? *reinterpret_cast<const half8_t *>(p) : half8_t{};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(h[j]);
+}
+__device__ __forceinline__ void load_x8(const float *p, bool valid, float v[8]) {
+    float4v a = float4v{0.f, 0.f, 0.f, 0.f}, b = a;
+    if (valid) {
+        a = *reinterpret_cast<const float4v *>(p);
+        b = *reinterpret_cast<const float4v *>(p + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = a[j];
+        v[4 + j] = b[j];
+    }
+}
+
+// Q8_0 quantization of one 32-block of activations held 8 per lane by the four lanes XOR-ed
+// together by X1 and X2 (amax/127, round half away from zero, the scale rounded to f16):
+// exactly the weight quantizer's rule, applied to the values as given (f32 activations are
+// quantized directly, with no f16 rounding first).
+template <int X1, int X2>
+__device__ __forceinline__ uint64_t quant_block8(const float v[8], float &dx) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, X1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, X2, 64));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint64_t qa = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = static_cast<int>(roundf(v[j] * id));
+        qa |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<int8_t>(q))) << (8 * j);
+    }
+    dx = static_cast<float>(static_cast<half_t>(d));
+    return qa;
+}
+
+// W8A32: one 32-block of f32 activations as two f16 terms for the f16 matrix cores. The block is
+// scaled by 2^e so its amax lies in [2^14, 2^15) (f16 range, and lo = s - f16(s) kept normal for
+// the block's large entries), then s = hi + lo with hi = f16(s) and lo = f16(s - hi); s - hi is
+// exact in f32, so the pair carries s to 2^-22 of the block's amax. inv = 2^-e undoes the scale.
+template <int X1, int X2>
+__device__ __forceinline__ void split_block8(const float v[8], half8_t &hi, half8_t &lo, float &inv) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, X1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, X2, 64));
+    int e = 0;
+    if (amax > 0.0f) {
+        int ex;
+        frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+        e = min(max(15 - ex, -126), 126);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float s = ldexpf(v[j], e);
+        const half_t h = static_cast<half_t>(s);
+        hi[j] = h;
+        lo[j] = static_cast<half_t>(s - static_cast<float>(h));
+    }
+    inv = ldexpf(1.0f, -e);
+}
+
+// The lane's 8 int8 weights as exact f16 values.
+__device__ __forceinline__ half8_t widen_w8(uint64_t q8) {
+    half8_t wv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[j] = static_cast<half_t>(static_cast<float>(static_cast<int8_t>((q8 >> (8 * j)) & 0xff)));
+    return wv;
+}
+
+template <int MB, int MODE, typename XT>
+__global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params<XT> p) {
+    static_assert(MODE != kA16 || sizeof(XT) == 2, "W8A16 takes f16 activations");
+    static_assert(MODE != kA32 || sizeof(XT) == 4, "W8A32 takes f32 activations");
     extern __shared__ __attribute__((aligned(16))) float red[];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -59,7 +142,7 @@ __global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params p) {
     float4v acc[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[mb] = float4v{0.f, 0.f, 0.f, 0.f};
-    const half_t *xr[MB];
+    const XT *xr[MB];
     bool xrow[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -73,44 +156,38 @@ __global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params p) {
         load_wblock(wrow + static_cast<int64_t>(b) * 34, g, q8, dw);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-            half8_t xv = *reinterpret_cast<const half8_t *>(xr[mb] + b * 32);
-            if (!xrow[mb]) xv = half8_t{};
-            if constexpr (A8) {
-                // Q8_0 quantization of this row's block: amax over the 4 lanes holding it
-                float v[8], amax = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    v[j] = static_cast<float>(xv[j]);
-                    amax = fmaxf(amax, fabsf(v[j]));
-                }
-                amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-                const float d = amax / 127.0f;
-                const float id = d != 0.0f ? 1.0f / d : 0.0f;
-                uint64_t qa = 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int q = static_cast<int>(roundf(v[j] * id));
-                    qa |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<int8_t>(q))) << (8 * j);
-                }
-                const float dx = static_cast<float>(static_cast<half_t>(d));
-                const int4v dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(qa), static_cast<long>(q8),
-                                                                         int4v{0, 0, 0, 0}, 0, 0, 0);
-                // the C fragment holds rows 4g + i; their scales live in lanes 4g + i
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float dxi = __shfl(dx, g * 4 + i, 64);
-                    const float t = (static_cast<float>(dot[i]) * dw) * dxi;
-                    acc[mb][i] += t;
-                }
-            } else {
-                half8_t wv;
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    wv[j] = static_cast<half_t>(static_cast<float>(static_cast<int8_t>((q8 >> (8 * j)) & 0xff)));
-                const float4v part = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            if constexpr (MODE == kA16) {
+                half8_t xv = *reinterpret_cast<const half8_t *>(xr[mb] + b * 32);
+                if (!xrow[mb]) xv = half8_t{};
+                const float4v part = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, widen_w8(q8), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mb][i] += part[i] * dw;
+            } else {
+                float v[8];
+                load_x8(xr[mb] + b * 32, xrow[mb], v);
+                if constexpr (MODE == kA8) {
+                    // Q8_0 quantization of this row's block: amax over the 4 lanes holding it
+                    float dx;
+                    const uint64_t qa = quant_block8<16, 32>(v, dx);
+                    const int4v dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(qa), static_cast<long>(q8),
+                                                                             int4v{0, 0, 0, 0}, 0, 0, 0);
+                    // the C fragment holds rows 4g + i; their scales live in lanes 4g + i
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float dxi = __shfl(dx, g * 4 + i, 64);
+                        const float t = (static_cast<float>(dot[i]) * dw) * dxi;
+                        acc[mb][i] += t;
+                    }
+                } else {
+                    half8_t hi, lo;
+                    float inv;
+                    split_block8<16, 32>(v, hi, lo, inv);
+                    const half8_t wv = widen_w8(q8);
+                    float4v part = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, wv, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, wv, part, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[mb][i] += (part[i] * dw) * __shfl(inv, g * 4 + i, 64);
+                }
             }
         }
     }
@@ -131,25 +208,43 @@ __global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params p) {
     }
 }
 
+// LDS of the A-sharing kernel: the activation slab of MB*16 rows by NB blocks as f16 (W8A16),
+// int8 codes plus f32 scales (W8A8), or f16 hi and lo slabs plus f32 inverse scales (W8A32).
+constexpr int q8_pitch(int nb) { return nb * 32 + 8; }    // f16 slab row: 16 bytes of padding spread the fragment reads over banks
+constexpr int q8_pitch8(int nb) { return nb * 32 + 16; }  // int8 slab row, likewise
+constexpr size_t q8_lds_bytes(int mb, int nb, int mode) {
+    return mode == kA16   ? static_cast<size_t>(mb) * 16 * q8_pitch(nb) * 2
+           : mode == kA8 ? static_cast<size_t>(mb) * 16 * q8_pitch8(nb) + static_cast<size_t>(nb) * mb * 16 * 4
+                          : static_cast<size_t>(mb) * 16 * q8_pitch(nb) * 2 * 2 + static_cast<size_t>(nb) * mb * 16 * 4;
+}
+constexpr size_t kQ8MaxLds = 160 * 1024;  // gfx950's LDS per workgroup
+
 // The A-sharing form (with a workspace): a workgroup of 4 waves owns 64 columns (16 per wave)
 // and a k range of NB blocks. The activation slab A[0:m, range] is read once per workgroup into
 // LDS, where the four waves read their fragments; each lane's NB weight blocks are all requested
 // before the slab is staged. For W8A8 the slab is quantised once while it is staged (int8 values
-// and f16-rounded scales in LDS) instead of once per 16-column wave. The block arithmetic is
-// gemm_q8_0's; with several ranges each
-// workgroup writes its partial [m, 64] tile to part[range] and q8_merge sums the ranges in order.
+// and f16-rounded scales in LDS) instead of once per 16-column wave; for W8A32 it is split once
+// into its scaled f16 hi and lo terms. The block arithmetic is gemm_q8_0's; with several ranges
+// each workgroup writes its partial [m, 64] tile to part[range] and q8_merge sums the ranges in
+// order.
 // PACKED: the weights are in dtts_q8_0_repack's layout, where a lane's 8 quantised weights of
 // consecutive blocks are contiguous (NB/2 16-byte loads) and the row's scales follow (NB/8
 // loads), instead of 5 two-byte loads per 34-byte block.
-template <int MB, int NB, bool A8, bool PACKED = false>
-__global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params p, float *part) {
+template <int MB, int NB, int MODE, bool PACKED, typename XT>
+__global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params<XT> p, float *part) {
+    static_assert(MODE != kA16 || sizeof(XT) == 2, "W8A16 takes f16 activations");
+    static_assert(MODE != kA32 || sizeof(XT) == 4, "W8A32 takes f32 activations");
     constexpr int KR = NB * 32;       // elements of a slab row
-    constexpr int PITCH = KR + 8;     // f16 slab: 16 bytes of padding spread the fragment reads over banks
-    constexpr int PITCH8 = KR + 16;   // int8 slab (W8A8), likewise
+    constexpr int PITCH = q8_pitch(NB);
+    constexpr int PITCH8 = q8_pitch8(NB);
     constexpr int SEGS = KR / 8;      // 8-element segments per slab row
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr size_t LDS = q8_lds_bytes(MB, NB, MODE);
+    static_assert(LDS <= kQ8MaxLds, "slab exceeds the LDS");
+    __shared__ __attribute__((aligned(16))) unsigned char smem[LDS];
     half_t *as = reinterpret_cast<half_t *>(smem);
-    float *scale = reinterpret_cast<float *>(smem + MB * 16 * PITCH8);  // W8A8: [NB][MB * 16] f16-rounded scales
+    half_t *as_lo = as + MB * 16 * PITCH;  // W8A32: the lo slab follows the hi slab
+    // [NB][MB * 16] per-row block scales: W8A8's f16-rounded d_x, W8A32's 2^-e
+    float *scale = reinterpret_cast<float *>(smem + (MODE == kA8 ? MB * 16 * PITCH8 : MB * 16 * PITCH * 4));
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, r = lane & 15;
     const int nblocks = p.k / 32;
@@ -183,30 +278,28 @@ __global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params p, float *part) {
     // quad shuffles below see all four lanes of a block.
     for (int e = tid; e < MB * 16 * SEGS; e += 256) {
         const int row = e / SEGS, sg = e - (e / SEGS) * SEGS;
-        half8_t v = half8_t{};
-        if (row < p.m) v = *reinterpret_cast<const half8_t *>(p.x + static_cast<int64_t>(row) * p.k + b0 * 32 + sg * 8);
-        if constexpr (A8) {
-            // the row's block quantised once per workgroup (4 consecutive threads hold it)
-            float f[8], amax = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f[j] = static_cast<float>(v[j]);
-                amax = fmaxf(amax, fabsf(f[j]));
-            }
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-            const float d = amax / 127.0f;
-            const float id = d != 0.0f ? 1.0f / d : 0.0f;
-            uint64_t qa = 0;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int q = static_cast<int>(roundf(f[j] * id));
-                qa |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<int8_t>(q))) << (8 * j);
-            }
-            *reinterpret_cast<uint64_t *>(smem + row * PITCH8 + sg * 8) = qa;
-            if ((sg & 3) == 0) scale[(sg >> 2) * (MB * 16) + row] = static_cast<float>(static_cast<half_t>(d));
-        } else {
+        const XT *src = p.x + static_cast<int64_t>(row < p.m ? row : 0) * p.k + b0 * 32 + sg * 8;
+        if constexpr (MODE == kA16) {
+            half8_t v = half8_t{};
+            if (row < p.m) v = *reinterpret_cast<const half8_t *>(src);
             *reinterpret_cast<half8_t *>(as + row * PITCH + sg * 8) = v;
+        } else {
+            float f[8];
+            load_x8(src, row < p.m, f);
+            if constexpr (MODE == kA8) {
+                // the row's block quantised once per workgroup (4 consecutive threads hold it)
+                float dx;
+                const uint64_t qa = quant_block8<1, 2>(f, dx);
+                *reinterpret_cast<uint64_t *>(smem + row * PITCH8 + sg * 8) = qa;
+                if ((sg & 3) == 0) scale[(sg >> 2) * (MB * 16) + row] = dx;
+            } else {
+                half8_t hi, lo;
+                float inv;
+                split_block8<1, 2>(f, hi, lo, inv);
+                *reinterpret_cast<half8_t *>(as + row * PITCH + sg * 8) = hi;
+                *reinterpret_cast<half8_t *>(as_lo + row * PITCH + sg * 8) = lo;
+                if ((sg & 3) == 0) scale[(sg >> 2) * (MB * 16) + row] = inv;
+            }
         }
     }
     __syncthreads();
@@ -217,7 +310,7 @@ __global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params p, float *part) {
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-            if constexpr (A8) {
+            if constexpr (MODE == kA8) {
                 const uint64_t qa = *reinterpret_cast<const uint64_t *>(smem + (mb * 16 + r) * PITCH8 + b * 32 + g * 8);
                 const int4v dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(static_cast<long>(qa), static_cast<long>(q8[b]),
                                                                          int4v{0, 0, 0, 0}, 0, 0, 0);
@@ -228,15 +321,20 @@ __global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params p, float *part) {
                     const float t = (static_cast<float>(dot[i]) * dw[b]) * dx[i];
                     acc[mb][i] += t;
                 }
-            } else {
+            } else if constexpr (MODE == kA16) {
                 const half8_t xv = *reinterpret_cast<const half8_t *>(as + (mb * 16 + r) * PITCH + b * 32 + g * 8);
-                half8_t wv;
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    wv[j] = static_cast<half_t>(static_cast<float>(static_cast<int8_t>((q8[b] >> (8 * j)) & 0xff)));
-                const float4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, wv, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const float4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, widen_w8(q8[b]), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mb][i] += pr[i] * dw[b];
+            } else {
+                const half8_t xh = *reinterpret_cast<const half8_t *>(as + (mb * 16 + r) * PITCH + b * 32 + g * 8);
+                const half8_t xl = *reinterpret_cast<const half8_t *>(as_lo + (mb * 16 + r) * PITCH + b * 32 + g * 8);
+                const half8_t wv = widen_w8(q8[b]);
+                float4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wv, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wv, pr, 0, 0, 0);
+                const float4v inv = *reinterpret_cast<const float4v *>(scale + b * (MB * 16) + mb * 16 + g * 4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb][i] += (pr[i] * dw[b]) * inv[i];
             }
         }
     }
@@ -345,47 +443,193 @@ extern "C" int dtts_q8_0_dequantize_f32(const void *blocks, float *w, int64_t ro
     return DTTS_OK;
 }
 
-extern "C" int dtts_gemm_q8_0(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
-                              int32_t mode, hipStream_t stream) {
-    const char *name = "dtts_gemm_q8_0";
+namespace dtts {
+namespace {
+
+const char *mode_name(int32_t mode) {
+    return mode == DTTS_Q8_W8A16 ? "W8A16" : mode == DTTS_Q8_W8A8 ? "W8A8" : mode == DTTS_Q8_W8A32 ? "W8A32" : "?";
+}
+
+// The modes each activation type takes: f16 x runs W8A16 (its product is exact already) or W8A8;
+// f32 x runs W8A8 (quantized from f32 directly) or W8A32.
+template <typename XT>
+bool mode_ok(int32_t mode) {
+    if (sizeof(XT) == 2) return mode == DTTS_Q8_W8A16 || mode == DTTS_Q8_W8A8;
+    return mode == DTTS_Q8_W8A8 || mode == DTTS_Q8_W8A32;
+}
+
+template <typename XT>
+int q8_plain(const char *name, const XT *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+             int32_t mode, hipStream_t stream) {
     DTTS_REQUIRE(m >= 0 && k > 0 && n > 0 && k % 32 == 0, "%s: bad shape (%lld, %lld, %lld)", name, (long long)m,
                  (long long)k, (long long)n);
-    DTTS_REQUIRE(mode == DTTS_Q8_W8A16 || mode == DTTS_Q8_W8A8, "%s: mode %d unknown", name, mode);
+    DTTS_REQUIRE(mode_ok<XT>(mode), "%s: mode %d (%s) not taken with %s activations", name, mode, mode_name(mode),
+                 sizeof(XT) == 2 ? "f16" : "f32");
     if (m == 0) return DTTS_OK;
     DTTS_REQUIRE(x && blocks && y, "%s: null pointer", name);
     DTTS_REQUIRE(m <= 64, "%s: m = %lld > 64 (decode shapes only)", name, (long long)m);
     DTTS_REQUIRE(n % 16 == 0, "%s: n = %lld not a multiple of 16", name, (long long)n);
-    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(blocks, 2), "%s: x must be 16-byte aligned", name);
+    DTTS_REQUIRE(aligned(x, 16) && aligned(blocks, 2), "%s: x must be 16-byte aligned", name);
     DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
-    dtts::Q8Params p{};
-    p.x = reinterpret_cast<const half_t *>(x);
+    Q8Params<XT> p{};
+    p.x = x;
     p.w = static_cast<const uint8_t *>(blocks);
     p.y = y;
     p.m = static_cast<int>(m);
     p.k = static_cast<int>(k);
     p.n = static_cast<int>(n);
     const int64_t groups = n / 16;
-    p.ks = dtts::pick_ks_blocks(groups, k / 32);
+    p.ks = pick_ks_blocks(groups, k / 32);
     p.slab_blocks = static_cast<int>(k / 32 / p.ks);
     const int mb = static_cast<int>((m + 15) / 16);
     const unsigned threads = static_cast<unsigned>(64 * p.ks);
     const size_t lds = static_cast<size_t>(p.ks) * mb * 256 * 4;
     const unsigned grid = static_cast<unsigned>(groups);
-    const bool a8 = mode == DTTS_Q8_W8A8;
-#define DTTS_Q8_LAUNCH(MB)                                                                                            \
-    if (a8)                                                                                                           \
-        dtts::gemm_q8_0<MB, true><<<grid, threads, lds, stream>>>(p);                                                 \
-    else                                                                                                              \
-        dtts::gemm_q8_0<MB, false><<<grid, threads, lds, stream>>>(p);
+    auto launch = [&](auto mbc) {
+        constexpr int MB = decltype(mbc)::value;
+        if constexpr (sizeof(XT) == 2) {
+            if (mode == DTTS_Q8_W8A8)
+                gemm_q8_0<MB, kA8, XT><<<grid, threads, lds, stream>>>(p);
+            else
+                gemm_q8_0<MB, kA16, XT><<<grid, threads, lds, stream>>>(p);
+        } else {
+            if (mode == DTTS_Q8_W8A8)
+                gemm_q8_0<MB, kA8, XT><<<grid, threads, lds, stream>>>(p);
+            else
+                gemm_q8_0<MB, kA32, XT><<<grid, threads, lds, stream>>>(p);
+        }
+    };
     switch (mb) {
-        case 1: DTTS_Q8_LAUNCH(1) break;
-        case 2: DTTS_Q8_LAUNCH(2) break;
-        case 3: DTTS_Q8_LAUNCH(3) break;
-        default: DTTS_Q8_LAUNCH(4) break;
+        case 1: launch(std::integral_constant<int, 1>{}); break;
+        case 2: launch(std::integral_constant<int, 2>{}); break;
+        case 3: launch(std::integral_constant<int, 3>{}); break;
+        default: launch(std::integral_constant<int, 4>{}); break;
     }
-#undef DTTS_Q8_LAUNCH
     DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
+}
+
+template <int MB, int NB, int MODE, typename XT>
+void q8_lds_kernel(bool packed, dim3 grid, hipStream_t stream, const Q8Params<XT> &p, float *part) {
+    // pick_q8_nb keeps the f16 slab within 64 KB: other (MB, NB) pairs are never launched
+    if constexpr (q8_lds_bytes(MB, NB, MODE) <= kQ8MaxLds && q8_lds_bytes(MB, NB, kA16) <= 65536) {
+        if (packed)
+            gemm_q8_lds<MB, NB, MODE, true, XT><<<grid, 256, 0, stream>>>(p, part);
+        else
+            gemm_q8_lds<MB, NB, MODE, false, XT><<<grid, 256, 0, stream>>>(p, part);
+    }
+}
+
+template <int MB, int NB, typename XT>
+void q8_lds_modes(int32_t mode, bool packed, dim3 grid, hipStream_t stream, const Q8Params<XT> &p, float *part) {
+    if (mode == DTTS_Q8_W8A8)
+        q8_lds_kernel<MB, NB, kA8, XT>(packed, grid, stream, p, part);
+    else if constexpr (sizeof(XT) == 2)
+        q8_lds_kernel<MB, NB, kA16, XT>(packed, grid, stream, p, part);
+    else
+        q8_lds_kernel<MB, NB, kA32, XT>(packed, grid, stream, p, part);
+}
+
+template <int MB, typename XT>
+void q8_lds_nb(int nb, int32_t mode, bool packed, dim3 grid, hipStream_t stream, const Q8Params<XT> &p, float *part) {
+    if (nb == 32)
+        q8_lds_modes<MB, 32, XT>(mode, packed, grid, stream, p, part);
+    else if (nb == 16)
+        q8_lds_modes<MB, 16, XT>(mode, packed, grid, stream, p, part);
+    else
+        q8_lds_modes<MB, 8, XT>(mode, packed, grid, stream, p, part);
+}
+
+// Whether the A-sharing kernel's slab fits the LDS for this (m, nb, mode): pick_q8_nb bounds the
+// f16 slab by 64 KB, so W8A16 and W8A8 always fit and W8A32 (two f16 slabs) stays within 134 KB.
+bool q8_lds_fits(int64_t m, int nb, int32_t mode) {
+    const int mb = static_cast<int>((m + 15) / 16);
+    return mb >= 1 && mb <= 4 && q8_lds_bytes(mb, nb, mode) <= kQ8MaxLds;
+}
+
+template <typename XT>
+int q8_lds_launch(const char *name, const XT *x, const void *w, float *y, int64_t m, int64_t k, int64_t n,
+                  int32_t mode, int nb, void *workspace, bool packed, hipStream_t stream) {
+    const int64_t ranges = k / 32 / nb;
+    const size_t need = ranges > 1 ? static_cast<size_t>(ranges * m * n) * sizeof(float) : 0;
+    DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
+    DTTS_REQUIRE(q8_lds_fits(m, nb, mode), "%s: no slab layout for m = %lld", name, (long long)m);
+    Q8Params<XT> p{};
+    p.x = x;
+    p.w = static_cast<const uint8_t *>(w);
+    p.y = y;
+    p.m = static_cast<int>(m);
+    p.k = static_cast<int>(k);
+    p.n = static_cast<int>(n);
+    float *part = need ? static_cast<float *>(workspace) : nullptr;
+    const int mb = static_cast<int>((m + 15) / 16);
+    const dim3 grid(static_cast<unsigned>(n / 64), static_cast<unsigned>(ranges));
+    switch (mb) {
+        case 1: q8_lds_nb<1, XT>(nb, mode, packed, grid, stream, p, part); break;
+        case 2: q8_lds_nb<2, XT>(nb, mode, packed, grid, stream, p, part); break;
+        case 3: q8_lds_nb<3, XT>(nb, mode, packed, grid, stream, p, part); break;
+        default: q8_lds_nb<4, XT>(nb, mode, packed, grid, stream, p, part); break;
+    }
+    DTTS_LAUNCH_CHECK(name);
+    if (part) {
+        q8_merge<<<grid_for(m * n, 256), 256, 0, stream>>>(part, y, m * n, static_cast<int>(ranges));
+        DTTS_LAUNCH_CHECK(name);
+    }
+    return DTTS_OK;
+}
+
+template <typename XT>
+int q8_ws(const char *name, const XT *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n, int32_t mode,
+          void *workspace, size_t ws_bytes, hipStream_t stream, const char *plain_name) {
+    DTTS_REQUIRE(m >= 0 && k > 0 && n > 0 && k % 32 == 0, "%s: bad shape (%lld, %lld, %lld)", name, (long long)m,
+                 (long long)k, (long long)n);
+    DTTS_REQUIRE(mode_ok<XT>(mode), "%s: mode %d (%s) not taken with %s activations", name, mode, mode_name(mode),
+                 sizeof(XT) == 2 ? "f16" : "f32");
+    if (m == 0) return DTTS_OK;
+    // On the GGML layout the A-sharing kernel pays for its 2-byte weight loads only once a slab
+    // serves more than 16 rows (measured at m = 1, 8 and 48); below that, and without room for
+    // the ranges, the workspace-free kernel runs.
+    const int nb = m > 16 ? pick_q8_nb(m, k, n) : 0;
+    const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
+    if (!nb || (need && (!workspace || ws_bytes < need)))
+        return q8_plain(plain_name, x, blocks, y, m, k, n, mode, stream);
+    DTTS_REQUIRE(x && blocks && y, "%s: null pointer", name);
+    DTTS_REQUIRE(aligned(x, 16) && aligned(blocks, 2) && (!need || aligned(workspace, 16)),
+                 "%s: x and the workspace must be 16-byte aligned", name);
+    return q8_lds_launch(name, x, blocks, y, m, k, n, mode, nb, workspace, false, stream);
+}
+
+template <typename XT>
+int q8_packed(const char *name, const XT *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
+              int32_t mode, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    DTTS_REQUIRE(m >= 0 && k > 0 && n > 0 && k % 256 == 0 && n % 64 == 0,
+                 "%s: bad shape (%lld, %lld, %lld): k a multiple of 256, n of 64", name, (long long)m, (long long)k,
+                 (long long)n);
+    DTTS_REQUIRE(mode_ok<XT>(mode), "%s: mode %d (%s) not taken with %s activations", name, mode, mode_name(mode),
+                 sizeof(XT) == 2 ? "f16" : "f32");
+    if (m == 0) return DTTS_OK;
+    DTTS_REQUIRE(m <= 64, "%s: m = %lld > 64 (decode shapes only)", name, (long long)m);
+    DTTS_REQUIRE(x && packed && y, "%s: null pointer", name);
+    const int nb = pick_q8_nb(m, k, n);
+    const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
+    DTTS_REQUIRE(nb > 0, "%s: shape not supported", name);
+    DTTS_REQUIRE(!need || (workspace && ws_bytes >= need), "%s: workspace %zu bytes < %zu needed", name, ws_bytes, need);
+    DTTS_REQUIRE(aligned(x, 16) && aligned(packed, 16) && (!need || aligned(workspace, 16)),
+                 "%s: x, packed and the workspace must be 16-byte aligned", name);
+    return q8_lds_launch(name, x, packed, y, m, k, n, mode, nb, workspace, true, stream);
+}
+
+}  // namespace
+}  // namespace dtts
+
+extern "C" int dtts_gemm_q8_0(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                              int32_t mode, hipStream_t stream) {
+    return dtts::q8_plain("dtts_gemm_q8_0", reinterpret_cast<const half_t *>(x), blocks, y, m, k, n, mode, stream);
+}
+
+extern "C" int dtts_gemm_q8_0_f32(const float *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                                  int32_t mode, hipStream_t stream) {
+    return dtts::q8_plain("dtts_gemm_q8_0_f32", x, blocks, y, m, k, n, mode, stream);
 }
 
 extern "C" size_t dtts_gemm_q8_0_workspace_bytes(int64_t m, int64_t k, int64_t n) {
@@ -395,83 +639,16 @@ extern "C" size_t dtts_gemm_q8_0_workspace_bytes(int64_t m, int64_t k, int64_t n
     return ranges > 1 ? static_cast<size_t>(ranges * m * n) * sizeof(float) : 0;
 }
 
-namespace dtts {
-namespace {
-
-int q8_lds_launch(const char *name, const dtts_f16 *x, const void *w, float *y, int64_t m, int64_t k, int64_t n,
-                  int32_t mode, int nb, void *workspace, bool packed, hipStream_t stream) {
-    const int64_t ranges = k / 32 / nb;
-    const size_t need = ranges > 1 ? static_cast<size_t>(ranges * m * n) * sizeof(float) : 0;
-    DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
-    Q8Params p{};
-    p.x = reinterpret_cast<const half_t *>(x);
-    p.w = static_cast<const uint8_t *>(w);
-    p.y = y;
-    p.m = static_cast<int>(m);
-    p.k = static_cast<int>(k);
-    p.n = static_cast<int>(n);
-    float *part = need ? static_cast<float *>(workspace) : nullptr;
-    const int mb = static_cast<int>((m + 15) / 16);
-    const size_t lds = mode == DTTS_Q8_W8A8 ? static_cast<size_t>(mb) * 16 * (nb * 32 + 16) + nb * mb * 16 * 4
-                                            : static_cast<size_t>(mb) * 16 * (nb * 32 + 8) * 2;
-    const dim3 grid(static_cast<unsigned>(n / 64), static_cast<unsigned>(ranges));
-    const bool a8 = mode == DTTS_Q8_W8A8;
-#define DTTS_Q8L(MB, NB)                                                                              \
-    if (packed) {                                                                                     \
-        if (a8)                                                                                       \
-            gemm_q8_lds<MB, NB, true, true><<<grid, 256, lds, stream>>>(p, part);                     \
-        else                                                                                          \
-            gemm_q8_lds<MB, NB, false, true><<<grid, 256, lds, stream>>>(p, part);                    \
-    } else if (a8) {                                                                                  \
-        gemm_q8_lds<MB, NB, true, false><<<grid, 256, lds, stream>>>(p, part);                        \
-    } else {                                                                                          \
-        gemm_q8_lds<MB, NB, false, false><<<grid, 256, lds, stream>>>(p, part);                       \
-    }
-#define DTTS_Q8L_NB(MB)         \
-    if (nb == 32) {             \
-        DTTS_Q8L(MB, 32)        \
-    } else if (nb == 16) {      \
-        DTTS_Q8L(MB, 16)        \
-    } else {                    \
-        DTTS_Q8L(MB, 8)         \
-    }
-    switch (mb) {
-        case 1: DTTS_Q8L_NB(1) break;
-        case 2: DTTS_Q8L_NB(2) break;
-        case 3: DTTS_Q8L_NB(3) break;
-        default: DTTS_Q8L_NB(4) break;
-    }
-#undef DTTS_Q8L_NB
-#undef DTTS_Q8L
-    DTTS_LAUNCH_CHECK(name);
-    if (part) {
-        q8_merge<<<grid_for(m * n, 256), 256, 0, stream>>>(part, y, m * n, static_cast<int>(ranges));
-        DTTS_LAUNCH_CHECK(name);
-    }
-    return DTTS_OK;
-}
-
-}  // namespace
-}  // namespace dtts
-
 extern "C" int dtts_gemm_q8_0_ws(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
                                  int32_t mode, void *workspace, size_t ws_bytes, hipStream_t stream) {
-    const char *name = "dtts_gemm_q8_0_ws";
-    DTTS_REQUIRE(m >= 0 && k > 0 && n > 0 && k % 32 == 0, "%s: bad shape (%lld, %lld, %lld)", name, (long long)m,
-                 (long long)k, (long long)n);
-    DTTS_REQUIRE(mode == DTTS_Q8_W8A16 || mode == DTTS_Q8_W8A8, "%s: mode %d unknown", name, mode);
-    if (m == 0) return DTTS_OK;
-    // On the GGML layout the A-sharing kernel pays for its 2-byte weight loads only once a slab
-    // serves more than 16 rows (measured at m = 1, 8 and 48); below that, and without room for
-    // the ranges, the workspace-free kernel runs.
-    const int nb = m > 16 ? dtts::pick_q8_nb(m, k, n) : 0;
-    const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
-    if (!nb || (need && (!workspace || ws_bytes < need)))
-        return dtts_gemm_q8_0(x, blocks, y, m, k, n, mode, stream);
-    DTTS_REQUIRE(x && blocks && y, "%s: null pointer", name);
-    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(blocks, 2) && (!need || dtts::aligned(workspace, 16)),
-                 "%s: x and the workspace must be 16-byte aligned", name);
-    return dtts::q8_lds_launch(name, x, blocks, y, m, k, n, mode, nb, workspace, false, stream);
+    return dtts::q8_ws("dtts_gemm_q8_0_ws", reinterpret_cast<const half_t *>(x), blocks, y, m, k, n, mode, workspace,
+                       ws_bytes, stream, "dtts_gemm_q8_0");
+}
+
+extern "C" int dtts_gemm_q8_0_ws_f32(const float *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                                     int32_t mode, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    return dtts::q8_ws("dtts_gemm_q8_0_ws_f32", x, blocks, y, m, k, n, mode, workspace, ws_bytes, stream,
+                       "dtts_gemm_q8_0_f32");
 }
 
 extern "C" size_t dtts_q8_0_packed_bytes(int64_t rows, int64_t k) {
@@ -493,19 +670,11 @@ extern "C" int dtts_q8_0_repack(const void *blocks, void *packed, int64_t rows, 
 
 extern "C" int dtts_gemm_q8_0_packed(const dtts_f16 *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
                                      int32_t mode, void *workspace, size_t ws_bytes, hipStream_t stream) {
-    const char *name = "dtts_gemm_q8_0_packed";
-    DTTS_REQUIRE(m >= 0 && k > 0 && n > 0 && k % 256 == 0 && n % 64 == 0,
-                 "%s: bad shape (%lld, %lld, %lld): k a multiple of 256, n of 64", name, (long long)m, (long long)k,
-                 (long long)n);
-    DTTS_REQUIRE(mode == DTTS_Q8_W8A16 || mode == DTTS_Q8_W8A8, "%s: mode %d unknown", name, mode);
-    if (m == 0) return DTTS_OK;
-    DTTS_REQUIRE(m <= 64, "%s: m = %lld > 64 (decode shapes only)", name, (long long)m);
-    DTTS_REQUIRE(x && packed && y, "%s: null pointer", name);
-    const int nb = dtts::pick_q8_nb(m, k, n);
-    const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
-    DTTS_REQUIRE(nb > 0, "%s: shape not supported", name);
-    DTTS_REQUIRE(!need || (workspace && ws_bytes >= need), "%s: workspace %zu bytes < %zu needed", name, ws_bytes, need);
-    DTTS_REQUIRE(dtts::aligned(x, 16) && dtts::aligned(packed, 16) && (!need || dtts::aligned(workspace, 16)),
-                 "%s: x, packed and the workspace must be 16-byte aligned", name);
-    return dtts::q8_lds_launch(name, x, packed, y, m, k, n, mode, nb, workspace, true, stream);
+    return dtts::q8_packed("dtts_gemm_q8_0_packed", reinterpret_cast<const half_t *>(x), packed, y, m, k, n, mode,
+                           workspace, ws_bytes, stream);
+}
+
+extern "C" int dtts_gemm_q8_0_packed_f32(const float *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
+                                         int32_t mode, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    return dtts::q8_packed("dtts_gemm_q8_0_packed_f32", x, packed, y, m, k, n, mode, workspace, ws_bytes, stream);
 }

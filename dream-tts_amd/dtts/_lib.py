@@ -104,6 +104,9 @@ SIGNATURES = {
     "dtts_q8_0_packed_bytes": [_I64, _I64],
     "dtts_q8_0_repack": [_P, _P, _I64, _I64, _P],
     "dtts_gemm_q8_0_packed": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
+    "dtts_gemm_q8_0_f32": [_P, _P, _P, _I64, _I64, _I64, _I32, _P],
+    "dtts_gemm_q8_0_ws_f32": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
+    "dtts_gemm_q8_0_packed_f32": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],

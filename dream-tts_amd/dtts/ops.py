@@ -352,35 +352,48 @@ def q8_0_repack(blocks, k):
     return out
 
 
+_Q8_MODES = {"w8a16": 0, "w8a8": 1, "w8a32": 2}
+
+
+def _q8_x(x, name):
+    """x [m, k] f16 or f32 (Proj::forward hands QMatMul f32, crates/tts-nn/src/lib.rs:509-531):
+    the entry-point suffix for its dtype."""
+    _check(x, name, (_F16, _F32), "x")
+    if x.dim() != 2:
+        raise DttsError(f"{name}: x must be 2-D, got {tuple(x.shape)}")
+    return "_f32" if x.dtype == _F32 else ""
+
+
 def q8_0_matmul_packed(x, packed, n, mode="w8a16", workspace=None):
-    """dtts_gemm_q8_0_packed: x [m, k] f16 times a repacked Q8_0 weight [n, k] -> y [m, n] f32."""
-    _mat(x, "q8_0_matmul_packed", "x", _F16)
+    """dtts_gemm_q8_0_packed{,_f32}: x [m, k] f16 or f32 times a repacked Q8_0 weight [n, k] ->
+    y [m, n] f32."""
+    sfx = _q8_x(x, "q8_0_matmul_packed")
     m, k = x.shape
     y = torch.empty((m, n), dtype=_F32, device=x.device)
     if workspace is None:
         workspace = torch.empty(max(q8_0_workspace_bytes(m, k, n), 16), dtype=torch.uint8, device=x.device)
-    call("dtts_gemm_q8_0_packed", ptr(x), ptr(packed), ptr(y), m, k, n, {"w8a16": 0, "w8a8": 1}[mode], ptr(workspace),
+    call("dtts_gemm_q8_0_packed" + sfx, ptr(x), ptr(packed), ptr(y), m, k, n, _Q8_MODES[mode], ptr(workspace),
          workspace.numel(), stream_handle())
     return y
 
 
 def q8_0_matmul(x, blocks, mode="w8a16", workspace=None):
-    """QMatMul::forward on a Q8_0 weight [n, k]: x [m, k] f16 -> y [m, n] f32. With a workspace
-    (a device uint8 tensor, or "auto" to allocate one) the A-sharing kernel runs
-    (dtts_gemm_q8_0_ws)."""
-    _mat(x, "q8_0_matmul", "x", _F16)
+    """QMatMul::forward on a Q8_0 weight [n, k]: x [m, k] f16 or f32 -> y [m, n] f32 (f32 x goes
+    to the _f32 entry points, whose W8A8 quantizes it directly). With a workspace (a device uint8
+    tensor, or "auto" to allocate one) the A-sharing kernel runs (dtts_gemm_q8_0_ws{,_f32})."""
+    sfx = _q8_x(x, "q8_0_matmul")
     m, k = x.shape
     n = blocks.shape[0]
     if blocks.dtype != torch.uint8 or not blocks.is_cuda or blocks.numel() != n * (k // 32) * 34:
         raise DttsError("q8_0_matmul: blocks must be device uint8 [n, k/32, 34]")
     y = torch.empty((m, n), dtype=_F32, device=x.device)
-    md = {"w8a16": 0, "w8a8": 1}[mode]
+    md = _Q8_MODES[mode]
     if workspace is None:
-        call("dtts_gemm_q8_0", ptr(x), ptr(blocks), ptr(y), m, k, n, md, stream_handle())
+        call("dtts_gemm_q8_0" + sfx, ptr(x), ptr(blocks), ptr(y), m, k, n, md, stream_handle())
         return y
     if isinstance(workspace, str):
         workspace = torch.empty(max(q8_0_workspace_bytes(m, k, n), 16), dtype=torch.uint8, device=x.device)
-    call("dtts_gemm_q8_0_ws", ptr(x), ptr(blocks), ptr(y), m, k, n, md, ptr(workspace), workspace.numel(),
+    call("dtts_gemm_q8_0_ws" + sfx, ptr(x), ptr(blocks), ptr(y), m, k, n, md, ptr(workspace), workspace.numel(),
          stream_handle())
     return y
 

@@ -548,6 +548,8 @@ int dtts_swiglu_mul_f32(const float *g, const float *u, float *y, int64_t n, hip
  * int8 qs[32]}; w[n, c] = qs[n][c/32][c%32] * d[n][c/32]. */
 #define DTTS_Q8_W8A16 0 /* f16 activations times the exact int8 weights, scaled per block */
 #define DTTS_Q8_W8A8 1  /* activations quantized to Q8_0 per 32-block first (candle CPU's vec_dot) */
+#define DTTS_Q8_W8A32 2 /* f32 activations times the exact int8 weights, scaled per block, at f32
+                           precision (the unquantized-activation product); f32 entry points only */
 
 /* Host: quantize f32 [rows, k] (k % 32 == 0) into blocks: d = amax/127, qs = round-half-away(x/d)
  * with the f32 reciprocal, d stored as f16 (BlockQ8_0::from_float). blocks holds rows*k/32*34
@@ -584,6 +586,20 @@ int dtts_q8_0_repack(const void *blocks, void *packed, int64_t rows, int64_t k, 
  * m <= 64; the workspace (dtts_gemm_q8_0_workspace_bytes) is required when nonzero. */
 int dtts_gemm_q8_0_packed(const dtts_f16 *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
                           int32_t mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* The f32-activation forms of the three above, with Proj::forward's own interface: it hands
+ * QMatMul::forward the f32 hidden state and takes f32 back for every weight kind
+ * (crates/tts-nn/src/lib.rs:509-531, `Proj::Quant(q) => q.forward(x)`). x is f32 [m, k], 16-byte
+ * aligned; shapes, workspace and routing as the f16 forms. mode DTTS_Q8_W8A8 quantizes the f32
+ * activations per 32-block directly (no f16 rounding first), as candle's CPU QMatMul receives
+ * them; DTTS_Q8_W8A32 is the unquantized f32 product. DTTS_Q8_W8A16 is refused here (it names an
+ * f16 operand). */
+int dtts_gemm_q8_0_f32(const float *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                       int32_t mode, hipStream_t stream);
+int dtts_gemm_q8_0_ws_f32(const float *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
+                          int32_t mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
+int dtts_gemm_q8_0_packed_f32(const float *x, const void *packed, float *y, int64_t m, int64_t k, int64_t n,
+                              int32_t mode, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------ codec decoder stack */
 

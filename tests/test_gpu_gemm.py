@@ -156,3 +156,94 @@ def test_q8_0_packed_layout(dev, m, k, n):
     if m > 16:
         for mode, got in (("w8a8", got8), ("w8a16", got16)):
             assert np.array_equal(got, to_host(ops.q8_0_matmul(xd, bd, mode, workspace="auto"))), mode
+
+
+# ---------------------------------------------------------------- Q8_0 on f32 activations
+# Proj::forward hands QMatMul::forward the f32 hidden state (crates/tts-nn/src/lib.rs:509-531).
+# Bars: W8A8 max-rel <= 1e-5 against the oracle's vec_dot restatement on the same f32 values
+# (no f16 rounding first); W8A32 max-rel <= 1e-5 against float64 on the dequantized weights.
+
+def _q8_f32_paths(xd, bd, packed, n, mode):
+    return {
+        "plain": ops.q8_0_matmul(xd, bd, mode),
+        "ws": ops.q8_0_matmul(xd, bd, mode, workspace="auto"),
+        "packed": ops.q8_0_matmul_packed(xd, packed, n, mode),
+    }
+
+
+@pytest.mark.parametrize("m,k,n", Q8_SHAPES + [(33, 512, 128), (64, 1024, 1024)])
+def test_q8_0_f32_activations(dev, m, k, n):
+    w = synth.normal(86, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    x = synth.normal(86, "x32", (m, k)).astype(np.float32)
+    assert not np.array_equal(x, synth.from_f16_bits(synth.f16_bits(x)))  # not f16 values
+    xd, bd = torch.from_numpy(x).to(dev), torch.from_numpy(blocks).to(dev)
+    packed = ops.q8_0_repack(bd, k)
+    want8 = oracle.q8_0_matmul_w8a8(x, blocks)
+    want32 = oracle.q8_0_matmul_f64(x, blocks)
+    got8 = {p: to_host(y) for p, y in _q8_f32_paths(xd, bd, packed, n, "w8a8").items()}
+    got32 = {p: to_host(y) for p, y in _q8_f32_paths(xd, bd, packed, n, "w8a32").items()}
+    for p in got8:
+        assert rel(got8[p], want8)[1] <= 1e-5, (p, rel(got8[p], want8))
+        assert rel(got32[p], want32)[1] <= 1e-5, (p, rel(got32[p], want32))
+    if m > 16:  # the A-sharing kernel behind both: the same sums bit for bit
+        assert np.array_equal(got8["ws"], got8["packed"]) and np.array_equal(got32["ws"], got32["packed"])
+
+
+def test_q8_0_f32_w8a8_near_ties(dev):
+    """f32 activations just below an x.5 tie that f16 rounding lands on (test_oracle_gemm_q8's
+    block): every path quantizes the f32 values, matching the oracle, and lands far from the
+    f16-first route."""
+    from test_oracle_gemm_q8 import near_tie_activations
+
+    m, k, n = 48, 1024, 1024
+    x = near_tie_activations(m, k)
+    w = synth.normal(87, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    xd, bd = torch.from_numpy(x).to(dev), torch.from_numpy(blocks).to(dev)
+    want = oracle.q8_0_matmul_w8a8(x, blocks)
+    via_f16 = oracle.q8_0_matmul_w8a8(synth.from_f16_bits(synth.f16_bits(x)), blocks)
+    assert rel(via_f16, want)[1] > 1e-3
+    for p, y in _q8_f32_paths(xd, bd, ops.q8_0_repack(bd, k), n, "w8a8").items():
+        got = to_host(y)
+        assert rel(got, want)[1] <= 1e-5, p
+        assert rel(got, via_f16)[1] > 1e-3, p
+
+
+def test_q8_0_w8a32_dynamic_range(dev):
+    """W8A32 scales each activation block by a power of two before its f16 hi + lo split: rows far
+    outside f16's range (1e6, 1e30) or deep in its subnormals (1e-6, 1e-30), a row whose blocks
+    differ by 1e12, and a zero row all meet 1e-5 of their own row's magnitude."""
+    m, k, n = 48, 1024, 1024
+    x = synth.normal(88, "x32", (m, k)).astype(np.float32)
+    scales = np.ones(m, np.float32)
+    scales[1:6] = [1e6, 1e30, 1e-6, 1e-30, 6e4]
+    x *= scales[:, None]
+    x[6, 512:] *= np.float32(1e12)
+    x[7] = 0.0
+    w = synth.normal(88, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    xd, bd = torch.from_numpy(x).to(dev), torch.from_numpy(blocks).to(dev)
+    want = oracle.q8_0_matmul_f64(x, blocks)
+    for p, y in _q8_f32_paths(xd, bd, ops.q8_0_repack(bd, k), n, "w8a32").items():
+        got = to_host(y)
+        assert np.all(got[7] == 0.0), p
+        for r in range(m):
+            if r == 7:
+                continue
+            err = np.max(np.abs(got[r].astype(np.float64) - want[r])) / np.max(np.abs(want[r]))
+            assert err <= 1e-5, (p, r, err)
+
+
+def test_q8_0_mode_and_dtype_refusals(dev):
+    """W8A16 names an f16 operand (refused for f32 x); W8A32 is an f32 mode (refused for f16 x)."""
+    k, n = 256, 64
+    bd = torch.from_numpy(ops.q8_0_quantize(synth.normal(89, "w", (n, k), 0, 0.02))).to(dev)
+    x32 = torch.ones((8, k), dtype=torch.float32, device=dev)
+    x16 = x32.half()
+    for xx, mode in ((x32, "w8a16"), (x16, "w8a32")):
+        for ws in (None, "auto"):
+            with pytest.raises(ops.DttsError, match="not taken with"):
+                ops.q8_0_matmul(xx, bd, mode, workspace=ws)
+        with pytest.raises(ops.DttsError, match="not taken with"):
+            ops.q8_0_matmul_packed(xx, ops.q8_0_repack(bd, k), n, mode)

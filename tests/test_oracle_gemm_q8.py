@@ -104,3 +104,43 @@ def test_q8_0_w8a8_close_to_unquantized_activations():
     got = oracle.q8_0_matmul_w8a8(x, blocks)
     want = oracle.q8_0_matmul_f64(x, blocks)
     assert oracle.abs_and_rel(got, want)[1] < 2e-2  # activation quantization noise, ~1/254 per term
+
+
+# f32 activations just below an x.5 tie that f16 rounding lands on: in a block whose amax is 127
+# (d = 1, id = 1) each f32 value quantizes toward zero and its f16 image (2.5, 4.5, -6.5, ...)
+# away from zero. Proj::forward hands QMatMul::forward the f32 hidden state
+# (crates/tts-nn/src/lib.rs:509-531), so a route that rounds x to f16 first gets other codes.
+NEAR_TIE = np.array([127.0, 2.4999, 4.4999, -6.4999, 0.49999, 10.4999, -1.4999, 126.4999], np.float32)
+NEAR_TIE_CODES_F32 = np.array([127, 2, 4, -6, 0, 10, -1, 126], np.int32)
+NEAR_TIE_CODES_F16 = np.array([127, 3, 5, -7, 1, 11, -2, 127], np.int32)
+
+
+def near_tie_activations(m, k, seed=74):
+    """[m, k] f32 ~ N(0, 1) whose first block in every row opens with NEAR_TIE (amax 127)."""
+    x = synth.normal(seed, "x.neartie", (m, k)).astype(np.float32)
+    x[:, :8] = NEAR_TIE
+    return x
+
+
+def test_q8_0_w8a8_quantizes_f32_activations_without_f16_rounding():
+    x = near_tie_activations(4, 64)
+    x16 = synth.from_f16_bits(synth.f16_bits(x))
+    codes = oracle.q8_0_quantize(x)[:, 0, 2:10].view(np.int8).astype(np.int32)
+    codes16 = oracle.q8_0_quantize(x16)[:, 0, 2:10].view(np.int8).astype(np.int32)
+    assert np.array_equal(codes, np.tile(NEAR_TIE_CODES_F32, (4, 1)))
+    assert np.array_equal(codes16, np.tile(NEAR_TIE_CODES_F16, (4, 1)))
+    # the W8A8 product on the f32 values is the one the oracle's vec_dot restatement gives, and
+    # the f16-first route misses it by far more than the 1e-5 parity bar
+    w = synth.normal(74, "w.neartie", (64, 64), 0, 0.02)
+    blocks = oracle.q8_0_quantize(w)
+    y = oracle.q8_0_matmul_w8a8(x, blocks)
+    y16 = oracle.q8_0_matmul_w8a8(x16, blocks)
+    assert oracle.abs_and_rel(y16, y)[1] > 1e-3
+    # and it is the exact block arithmetic: integer dots of those codes times the f16 scales
+    xq = oracle.q8_0_quantize(x)
+    qx = xq[..., 2:].view(np.int8).astype(np.int64)
+    dx = synth.from_f16_bits(xq[..., :2].copy().view(np.uint16)[..., 0]).astype(np.float64)
+    qw = blocks[..., 2:].view(np.int8).astype(np.int64)
+    dw = synth.from_f16_bits(blocks[..., :2].copy().view(np.uint16)[..., 0]).astype(np.float64)
+    want = np.einsum("mbj,nbj->mnb", qx, qw).astype(np.float64) * dx[:, None, :] * dw[None, :, :]
+    assert np.max(np.abs(y - want.sum(-1))) <= 1e-5 * np.max(np.abs(want.sum(-1)))
