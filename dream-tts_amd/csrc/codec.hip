@@ -14,6 +14,7 @@
 // Every tensor stored is one the unfused chain would store (f16), so the arithmetic matches the
 // composed form up to summation order.
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -28,6 +29,11 @@ struct dtts_codec {
     // other's (measured: 19.58 -> 19.06 ms for config 5).
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    // Held from the fork record through the join wait, so that decodes from several host threads
+    // each wait on their own fork and join: without it one thread's record could land between
+    // another's record and wait, and that decode's second half would start on the wrong
+    // stream's work.
+    mutable std::mutex split_lock;
     // act1 of unit 0 of each block, repeated over the TransConv's `rate` output phases (the
     // TransConv's output channel p*C + c is channel c of phase p).
     std::vector<float *> phase_alpha, phase_brecip;
@@ -400,6 +406,7 @@ int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *la
             if ((rc = run_stage(st, c->f32, stream)) != DTTS_OK) return rc;
         return DTTS_OK;
     }
+    std::lock_guard<std::mutex> hold(c->split_lock);
     // fork: the side stream starts after everything the caller enqueued before this decode
     DTTS_HIP_CHECK(hipEventRecord(c->fork, stream), name);
     DTTS_HIP_CHECK(hipStreamWaitEvent(c->side, c->fork, 0), name);

@@ -557,9 +557,14 @@ __global__ __launch_bounds__(256) void prefill_attention(const float *q, const h
 // block's keys (or values) load under the previous block's MFMAs, within two waves per SIMD's
 // registers. LDS: the keys x 34 floats, at least (NW - 1) partial outputs of D x 32 floats.
 constexpr int kPrefillMfmaPitch = 34;          // 16 rows x 34 floats = 32 banks apart (mod 64)
-constexpr int kPrefillMfmaMaxLds = 64 * 1024;  // longer key ranges take prefill_attention
+constexpr int kPrefillMfmaMaxLds = 64 * 1024;  // dynamic + static LDS; longer key ranges take prefill_attention
 constexpr int kPrefillMfmaMinT = 16;           // fewer queries leave most of a 32-query block idle
 constexpr int kPrefillMfmaWaves = 2;           // waves per 32-query block, on alternate key blocks (4: slower)
+
+// The kernel's static LDS (its `red` array of maxima and sums), counted against kPrefillMfmaMaxLds
+// with the dynamic rows.
+template <int NW>
+constexpr size_t prefill_mfma_static_lds() { return 2 * NW * 32 * sizeof(float); }
 
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void prefill_attention_mfma(const float *q, const half_t *kc, const half_t *vc,
@@ -569,6 +574,7 @@ __global__ __launch_bounds__(64 * NW, 2) void prefill_attention_mfma(const float
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float sc[];  // [keys][kPrefillMfmaPitch], then wave 1's output
     __shared__ float red[2][NW][32];                             // [max | sum][wave][query]
+    static_assert(sizeof(red) == prefill_mfma_static_lds<NW>(), "static LDS counted on the host");
     constexpr int H = D / 2, NDB = D / 32, P = kPrefillMfmaPitch;
     static_assert(D == 64 || D == 128, "head dim");
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
@@ -880,9 +886,11 @@ int enqueue_prefill(const dtts_stack &s, const float *x, float *out, const dtts_
     // fit its LDS
     const size_t mfma_lds = static_cast<size_t>((prefill_block_keys(t, start, static_cast<int>(g.window)) + 31) / 32) *
                             32 * kPrefillMfmaPitch * sizeof(float);
-    const bool attn_mfma = t >= kPrefillMfmaMinT && (hd == 64 || hd == 128) && mfma_lds <= kPrefillMfmaMaxLds;
     const size_t mfma_parts = static_cast<size_t>(kPrefillMfmaWaves - 1) * hd * 32 * sizeof(float);  // waves 1.. partials
     const size_t mfma_lds_launch = mfma_lds > mfma_parts ? mfma_lds : mfma_parts;
+    // the whole workgroup's LDS within 64 KB: 14 key blocks (448 keys) at most
+    const bool attn_mfma = t >= kPrefillMfmaMinT && (hd == 64 || hd == 128) &&
+                           mfma_lds_launch + prefill_mfma_static_lds<kPrefillMfmaWaves>() <= kPrefillMfmaMaxLds;
     const unsigned mfma_blocks = static_cast<unsigned>(lanes * ((t + 31) / 32) * heads);
     Partials pending{};
     const half_t *pending16 = nullptr;

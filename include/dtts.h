@@ -678,7 +678,9 @@ size_t dtts_codec_workspace_bytes(const dtts_codec *codec, int64_t lanes, int64_
  * the codec owns, forked from and joined back into `stream` with events, so the call is ordered
  * on `stream` like any other work (the two halves overlap each other's ramps and tails). The
  * workspace must hold dtts_codec_workspace_bytes bytes. Calls on one codec share its side stream
- * and events: order them (one host thread at a time). */
+ * and events under a lock the codec holds from the fork to the join, so several host threads may
+ * decode through one codec (each with its own workspace); their second halves then run one after
+ * another on the side stream. */
 int dtts_codec_decode(const dtts_codec *codec, const dtts_f16 *latent, dtts_f16 *audio,
                       int64_t lanes, int64_t frames, void *workspace, size_t workspace_bytes,
                       hipStream_t stream);

@@ -112,3 +112,48 @@ def test_codec_empty_and_single_frame_decodes(dev, dtype):
         want = ocodec.decode_f32_reference(geo, ocodec.prepare(geo, w), lat32[0])[None]
         assert np.max(np.abs(got - want)) <= 5e-3 and np.max(np.abs(got - exact)) <= 5e-3
     assert got.shape == (1, geo.hop) and np.isfinite(got).all()
+
+
+def test_codec_decode_from_two_host_threads(dev):
+    """Two host threads decode through one codec at once, each on its own stream with its own
+    workspace: every decode equals the single-thread decode of the same latent bit for bit (the
+    codec's lock keeps each call's fork and join events its own)."""
+    import threading
+
+    from dtts._lib import call, lib, ptr, stream_handle
+
+    geo, lanes, frames, reps = SMALL, 4, 24, 12
+    model = codec.Codec(geo, _weights(geo, 9), dev)
+    lats = [to_dev(synth.f16_bits(synth.normal(9, f"latent{i}", (lanes, frames, geo.latent_dim))), dev)
+            for i in range(2)]
+    want = [to_host(model.decode(lat)) for lat in lats]
+    need = int(lib().dtts_codec_workspace_bytes(model.handle, lanes, frames))
+    torch.cuda.synchronize()
+    got, errors = [None, None], []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream(device=dev)
+            with torch.cuda.stream(s):
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
+                audio = torch.empty((lanes, frames * geo.hop), dtype=torch.float16, device=dev)
+                outs = []
+                for _ in range(reps):
+                    call("dtts_codec_decode", model.handle, ptr(lats[i]), ptr(audio), lanes, frames, ptr(ws),
+                         need, stream_handle())
+                    outs.append(audio.clone())
+            s.synchronize()
+            got[i] = [to_host(o) for o in outs]
+        except Exception as e:  # reported on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        assert len(got[i]) == reps
+        for r, out in enumerate(got[i]):
+            assert np.array_equal(out, want[i]), (i, r)

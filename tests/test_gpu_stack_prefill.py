@@ -63,8 +63,11 @@ def _check(geo, state, kc_before, vc_before, kc_want, vc_want, start, t):
     # t >= 16: 32-query blocks on the f32 matrix cores
     (LONG, 2, 100, 20, 160),    # a 20-key f16 prefix: the first key block crosses start; a 4-query last block
     (replace(WINDOWED, capacity=96), 2, 70, 9, 96),  # D = 64, windows of 5 inside 32-query blocks, scaled scores
-    (replace(SMALL, capacity=512), 1, 64, 380, 512),  # 444 keys: 14 key blocks, 61 KB of scores, the most it takes
-    (replace(SMALL, capacity=512), 1, 40, 460, 512),  # 500 keys: past its LDS, the per-wave kernel again
+    # its LDS is the key blocks' scores (4352 B each) plus 512 B of static maxima and sums, within 64 KB
+    (replace(SMALL, capacity=512), 1, 64, 380, 512),  # 444 keys: 14 key blocks
+    (replace(SMALL, capacity=512), 1, 64, 384, 512),  # 448 keys: 14 full key blocks, 61,440 B, the most it takes
+    (replace(SMALL, capacity=512), 1, 64, 416, 512),  # 480 keys: 15 blocks (65,792 B), the per-wave kernel
+    (replace(SMALL, capacity=512), 1, 40, 460, 512),  # 500 keys: the per-wave kernel again
 ])
 def test_prefill_matches_oracle(dev, geo, lanes, t, start, cap):
     layers, fn, x, kc, vc, st, state = _setup(dev, geo, 95, lanes, t, cap)
