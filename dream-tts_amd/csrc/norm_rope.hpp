@@ -138,11 +138,12 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 // multiplies the roped q (Stack::forward's q * 1/sqrt(D) for such layers, crates/qwen3tts/src/
 // qwen3.rs:404-408), and is 1 otherwise. P: Positions or DevPositions. ys > 1: qkv is the sum,
 // in order, of ys partial arrays ystride elements apart (a projection's k-split partials);
-// round16 rounds that sum to f16 first.
-template <typename T, typename P>
+// round16 rounds that sum to f16 first. CT: the caches' element type (f16, or f32 as Stack::load
+// keeps them for f32 and quantized weights, crates/qwen3tts/src/qwen3.rs:242-246).
+template <typename T, typename P, typename CT = half_t>
 __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float *norms, const float *cos_t,
                                                       const float *sin_t, P pos, T *q_out, float *k_out,
-                                                      half_t *kc, half_t *vc, int b, int heads, int n_kv, int hd,
+                                                      CT *kc, CT *vc, int b, int heads, int n_kv, int hd,
                                                       int cap, float eps, float q_scale, int ys, int64_t ystride,
                                                       bool round16) {
 #pragma clang fp contract(off)
@@ -202,11 +203,11 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const T *qkv, const float 
     }
     const int kh = h - heads;
     const int64_t dst = ((static_cast<int64_t>(bi) * n_kv + kh) * cap + p) * hd;
-    kc[dst + lane] = static_cast<half_t>(o1);
-    kc[dst + lane + half] = static_cast<half_t>(o2);
+    kc[dst + lane] = static_cast<CT>(o1);
+    kc[dst + lane + half] = static_cast<CT>(o2);
     const T *vs = row + (heads + n_kv + kh) * hd;
-    vc[dst + lane] = static_cast<half_t>(ld(vs + lane));
-    vc[dst + lane + half] = static_cast<half_t>(ld(vs + lane + half));
+    vc[dst + lane] = static_cast<CT>(ld(vs + lane));
+    vc[dst + lane + half] = static_cast<CT>(ld(vs + lane + half));
     if (k_out) {
         float *fk = k_out + (static_cast<int64_t>(bi) * n_kv + kh) * hd;
         fk[lane] = o1;

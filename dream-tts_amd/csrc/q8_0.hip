@@ -549,7 +549,7 @@ bool q8_lds_fits(int64_t m, int nb, int32_t mode) {
 
 template <typename XT>
 int q8_lds_launch(const char *name, const XT *x, const void *w, float *y, int64_t m, int64_t k, int64_t n,
-                  int32_t mode, int nb, void *workspace, bool packed, hipStream_t stream) {
+                  int32_t mode, int nb, void *workspace, bool packed, hipStream_t stream, bool merge = true) {
     const int64_t ranges = k / 32 / nb;
     const size_t need = ranges > 1 ? static_cast<size_t>(ranges * m * n) * sizeof(float) : 0;
     DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
@@ -571,7 +571,7 @@ int q8_lds_launch(const char *name, const XT *x, const void *w, float *y, int64_
         default: q8_lds_nb<4, XT>(nb, mode, packed, grid, stream, p, part); break;
     }
     DTTS_LAUNCH_CHECK(name);
-    if (part) {
+    if (part && merge) {
         q8_merge<<<grid_for(m * n, 256), 256, 0, stream>>>(part, y, m * n, static_cast<int>(ranges));
         DTTS_LAUNCH_CHECK(name);
     }
@@ -620,6 +620,22 @@ int q8_packed(const char *name, const XT *x, const void *packed, float *y, int64
 }
 
 }  // namespace
+
+int q8_stack_ranges(int64_t m, int64_t k, int64_t n) {
+    const int nb = pick_q8_nb(m, k, n);
+    return nb ? static_cast<int>(k / 32 / nb) : 0;
+}
+
+int q8_stack_gemm(const float *x, const void *packed, float *y, float *part, int64_t m, int64_t k, int64_t n,
+                  int32_t mode, hipStream_t stream) {
+    const char *name = "dtts_stack (Q8_0 projection)";
+    const int nb = pick_q8_nb(m, k, n);
+    DTTS_REQUIRE(nb > 0 && k % 256 == 0 && m <= 64, "%s: shape (%lld, %lld, %lld) not supported", name, (long long)m,
+                 (long long)k, (long long)n);
+    DTTS_REQUIRE(k / 32 / nb == 1 || part, "%s: no room for the k ranges", name);
+    return q8_lds_launch(name, x, packed, y, m, k, n, mode, nb, part, true, stream, false);
+}
+
 }  // namespace dtts
 
 extern "C" int dtts_gemm_q8_0(const dtts_f16 *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,

@@ -28,9 +28,11 @@
 #include "attn.hpp"
 #include "gemm_nt.hpp"
 #include "norm_rope.hpp"
+#include "proj.hpp"
 
 struct dtts_stack {
     dtts_stack_geometry geo;
+    int32_t how = DTTS_WEIGHT_F16;  // the layers' weight kind (Stack::load's `how`)
     std::vector<dtts_stack_layer> layers;
     const float *final_norm = nullptr;
     float *cos_t = nullptr, *sin_t = nullptr;  // [capacity, head_dim / 2]
@@ -163,9 +165,12 @@ hipError_t launch_norm(const float *x, Partials add, const float *scale, float *
 }
 
 // t = f16(silu(g) * u) from the gate|up projection's partials (gate columns, then up columns, ys
-// arrays of [rows, 2 * ffn]); four columns per thread.
-__global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t, int rows, int ffn,
+// arrays of [rows, 2 * ffn]); four columns per thread. TO = float: the f32 swiglu_mul the
+// reference feeds an f32 or quantized down projection.
+template <typename TO = half_t>
+__global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, TO *t, int rows, int ffn,
                                                           bool round16 = false) {
+    typedef TO TO4 __attribute__((ext_vector_type(4)));
     const int c4n = ffn / 4;
     const int64_t total = static_cast<int64_t>(rows) * c4n;
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
@@ -177,10 +182,10 @@ __global__ __launch_bounds__(256) void stack_gateup_merge(Partials gu, half_t *t
             g = round_f16x4(g);
             u = round_f16x4(u);
         }
-        half4_t o;
+        TO4 o;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = static_cast<half_t>(silu_mul(g[j], u[j]));
-        *reinterpret_cast<half4_t *>(t + row * ffn + col) = o;
+        for (int j = 0; j < 4; ++j) o[j] = static_cast<TO>(silu_mul(g[j], u[j]));
+        *reinterpret_cast<TO4 *>(t + row * ffn + col) = o;
     }
 }
 
@@ -337,6 +342,145 @@ hipError_t enqueue_step(const dtts_stack &s, const float *x, float *out, const d
     // h + the last MLP output, then the final norm
     return launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, lanes, dim, g.eps,
                        stream, nullptr, pending_round);
+}
+
+// ---------------------------------------------------------------- f32 and Q8_0 layers
+//
+// Stack::load with Weight::F32 or Weight::Quant keeps f32 caches (crates/qwen3tts/src/qwen3.rs:
+// 242-246), and Proj::forward hands those projections the f32 hidden state and takes f32 back
+// (crates/tts-nn/src/lib.rs:509-531): no f16 rounding anywhere in the step. Per layer:
+//   a = rms_norm(h)                          rms kernel (f32 out; adds the previous projection)
+//   qkv = proj(a)                            f32 (Proj::Dense) or Q8_0 (QMatMul) A-sharing kernel
+//   q, cache[pos] <- QK-norm, RoPE, append   qk-rope kernel on f32 caches (the composed route:
+//                                            rms_norm over each head, rope, slice_set in f32)
+//   o = attention(q, cache)                  decode attention over the f32 caches, f32 out
+//   h += proj(o) * attn_scale                (summed by the next norm)
+//   t = swiglu_mul(proj_gate(a), proj_up(a)) gate|up rows in one projection, f32 merge
+//   h += proj(t) * mlp_scale
+// The projections' k ranges are left as partials and summed in order by the consumer.
+
+bool weight_kind_dense_f32(int32_t how) { return how == DTTS_WEIGHT_F32; }
+int32_t q8_mode_of(int32_t how) { return how == DTTS_WEIGHT_Q8_0_A32 ? DTTS_Q8_W8A32 : DTTS_Q8_W8A8; }
+
+int proj_ranges(int32_t how, int64_t m, int64_t k, int64_t n) {
+    return weight_kind_dense_f32(how) ? f32_proj_ranges(m, k, n) : q8_stack_ranges(m, k, n);
+}
+
+// Whether the kind's projection kernel takes [m, k] x [n, k]: m <= 64, n % 64 == 0, and k a
+// multiple of 32 (f32) or 256 (Q8_0, the packed layout).
+bool proj_shape_ok(int32_t how, int64_t k, int64_t n) {
+    return n % 64 == 0 && (weight_kind_dense_f32(how) ? k % 32 == 0 : k % 256 == 0) && proj_ranges(how, 64, k, n) > 0;
+}
+
+struct PlanW {  // workspace carve-up of the f32 / Q8_0 step
+    size_t h, a, qkv, q, o, fbuf, t, part, attn_part, total;
+    size_t part_bytes, attn_bytes;
+    int max_window;
+};
+
+PlanW plan_w(const dtts_stack_geometry &g, int32_t how, int64_t lanes, int64_t cap) {
+    PlanW p{};
+    const int64_t qw = g.heads * g.head_dim, kvw = g.n_kv * g.head_dim, qkvw = qw + 2 * kvw;
+    const int64_t aw = g.dim > g.ffn ? g.dim : g.ffn;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += align256(bytes);
+        return at;
+    };
+    const size_t f = sizeof(float) * lanes;
+    p.h = take(f * g.dim);
+    p.a = take(f * aw);
+    p.qkv = take(f * qkvw);
+    p.q = take(f * qw);
+    p.o = take(f * qw);
+    p.fbuf = take(f * (g.dim > 2 * g.ffn ? g.dim : 2 * g.ffn));
+    p.t = take(f * g.ffn);
+    const int64_t shapes[4][2] = {{g.dim, qkvw}, {qw, g.dim}, {g.dim, 2 * g.ffn}, {g.ffn, g.dim}};
+    size_t pb = 0;
+    for (const auto &sh : shapes) {
+        const int r = proj_ranges(how, lanes, sh[0], sh[1]);
+        const size_t v = r > 1 ? f * sh[1] * r : 0;
+        pb = v > pb ? v : pb;
+    }
+    p.part_bytes = pb;
+    p.part = take(pb);
+    const int64_t win = g.window > 0 && g.window < cap ? g.window : cap;
+    p.max_window = static_cast<int>(win);
+    p.attn_bytes = attn_workspace_bytes(lanes, g.n_kv, g.heads / g.n_kv, g.head_dim, win);
+    p.attn_part = take(p.attn_bytes);
+    p.total = off;
+    return p;
+}
+
+// One f32 or Q8_0 projection: the partials (several k ranges) or the plain output, as its
+// consumer reads them.
+hipError_t proj_w(int32_t how, const float *x, const void *w, float *plain, float *part, int m, int k, int n,
+                  Partials &out, hipStream_t stream) {
+    const int r = proj_ranges(how, m, k, n);
+    out = r > 1 ? Partials{part, r, static_cast<int64_t>(m) * n} : Partials{plain, 1, 0};
+    if (weight_kind_dense_f32(how)) return f32_proj_launch(x, static_cast<const float *>(w), plain, part, m, k, n, false, stream);
+    return q8_stack_gemm(x, w, plain, part, m, k, n, q8_mode_of(how), stream) == DTTS_OK ? hipSuccess
+                                                                                          : hipErrorInvalidValue;
+}
+
+hipError_t enqueue_step_w(const dtts_stack &s, const float *x, float *out, const dtts_stack_cache *caches, int lanes,
+                          int cap, char *ws, const PlanW &pl, hipStream_t stream) {
+    const dtts_stack_geometry &g = s.geo;
+    const int dim = static_cast<int>(g.dim), hd = static_cast<int>(g.head_dim);
+    const int heads = static_cast<int>(g.heads), n_kv = static_cast<int>(g.n_kv), ffn = static_cast<int>(g.ffn);
+    const int qw = heads * hd, qkvw = (heads + 2 * n_kv) * hd;
+    const int gqa = heads / n_kv;
+    float *h = reinterpret_cast<float *>(ws + pl.h);
+    float *a = reinterpret_cast<float *>(ws + pl.a);
+    float *qkv = reinterpret_cast<float *>(ws + pl.qkv);
+    float *q = reinterpret_cast<float *>(ws + pl.q);
+    float *o = reinterpret_cast<float *>(ws + pl.o);
+    float *fbuf = reinterpret_cast<float *>(ws + pl.fbuf);
+    float *t = reinterpret_cast<float *>(ws + pl.t);
+    float *part = pl.part_bytes ? reinterpret_cast<float *>(ws + pl.part) : nullptr;
+    float *apart = pl.attn_bytes ? reinterpret_cast<float *>(ws + pl.attn_part) : nullptr;
+    const int max_chunks = apart ? (pl.max_window + kChunk - 1) / kChunk : 0;
+    const float qscale = g.qk_norm ? 1.0f : static_cast<float>(1.0 / std::sqrt(static_cast<double>(g.head_dim)));
+    const DevSpans spans{s.pos, static_cast<int>(g.window)};
+    const int32_t how = s.how;
+    Partials pending{};  // the previous layer's down projection, not yet in h
+    const float *pending_scale = nullptr;
+    for (int64_t li = 0; li < g.layers; ++li) {
+        const dtts_stack_layer &L = s.layers[li];
+        float *kc = static_cast<float *>(caches[li].k);
+        float *vc = static_cast<float *>(caches[li].v);
+        STACK_STEP(launch_norm(li == 0 ? x : h, pending, pending_scale, h, L.attn_norm, a, lanes, dim, g.eps, stream));
+        Partials r{};
+        STACK_STEP(proj_w(how, a, L.wqkv, qkv, part, lanes, dim, qkvw, r, stream));
+        const int waves = lanes * (heads + n_kv);
+        qk_rope_kernel<float, DevPositions, float><<<static_cast<unsigned>((waves + 3) / 4), 256, 0, stream>>>(
+            r.p, g.qk_norm ? L.qk_norms : nullptr, s.cos_t, s.sin_t, DevPositions{s.pos}, q, nullptr, kc, vc, lanes,
+            heads, n_kv, hd, cap, g.eps, qscale, r.ys, r.stride, false);
+        STACK_STEP(hipGetLastError());
+        STACK_STEP(launch_attention(q, static_cast<const float *>(kc), static_cast<const float *>(vc), o, apart,
+                                    max_chunks, lanes, n_kv, gqa, hd, cap, spans, stream));
+        const float *attn_scale = g.layer_scale ? L.attn_scale : nullptr;
+        STACK_STEP(proj_w(how, o, L.wo, fbuf, part, lanes, qw, dim, r, stream));
+        STACK_STEP(launch_norm(h, r, attn_scale, h, L.ffn_norm, a, lanes, dim, g.eps, stream));
+        STACK_STEP(proj_w(how, a, L.w_gateup, fbuf, part, lanes, dim, 2 * ffn, r, stream));
+        stack_gateup_merge<float><<<grid_for(int64_t(lanes) * ffn / 4, 256, 4), 256, 0, stream>>>(r, t, lanes, ffn);
+        STACK_STEP(hipGetLastError());
+        STACK_STEP(proj_w(how, t, L.wdown, fbuf, part, lanes, ffn, dim, pending, stream));
+        pending_scale = g.layer_scale ? L.mlp_scale : nullptr;
+    }
+    return launch_norm(h, pending, pending_scale, static_cast<float *>(nullptr), s.final_norm, out, lanes, dim, g.eps,
+                       stream);
+}
+
+size_t step_bytes(const dtts_stack &s, int64_t lanes, int64_t cap) {
+    return s.how == DTTS_WEIGHT_F16 ? plan_of(s.geo, lanes, cap).total : plan_w(s.geo, s.how, lanes, cap).total;
+}
+
+hipError_t enqueue_any(const dtts_stack &s, const float *x, float *out, const dtts_stack_cache *caches, int lanes,
+                       int cap, char *ws, hipStream_t stream) {
+    if (s.how == DTTS_WEIGHT_F16) return enqueue_step(s, x, out, caches, lanes, cap, ws, plan_of(s.geo, lanes, cap), stream);
+    return enqueue_step_w(s, x, out, caches, lanes, cap, ws, plan_w(s.geo, s.how, lanes, cap), stream);
 }
 
 // ---------------------------------------------------------------- prefill (t >= 2)
@@ -1005,8 +1149,16 @@ using dtts::half_t;
 
 extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stack_layer *layers,
                                  const float *final_norm, dtts_stack **out) {
+    return dtts_stack_create_as(geo, layers, final_norm, DTTS_WEIGHT_F16, out);
+}
+
+extern "C" int dtts_stack_create_as(const dtts_stack_geometry *geo, const dtts_stack_layer *layers,
+                                    const float *final_norm, int32_t how, dtts_stack **out) {
     DTTS_REQUIRE(geo && layers && final_norm && out, "dtts_stack_create: null argument");
     *out = nullptr;
+    DTTS_REQUIRE(how == DTTS_WEIGHT_F16 || how == DTTS_WEIGHT_F32 || how == DTTS_WEIGHT_Q8_0 ||
+                     how == DTTS_WEIGHT_Q8_0_A32,
+                 "dtts_stack_create: weight kind %d unknown", how);
     const dtts_stack_geometry &g = *geo;
     DTTS_REQUIRE(g.layers > 0 && g.dim > 0 && g.heads > 0 && g.n_kv > 0 && g.ffn > 0 && g.capacity > 0,
                  "dtts_stack_create: bad geometry (layers %lld, dim %lld, heads %lld, n_kv %lld, ffn %lld, "
@@ -1022,9 +1174,15 @@ extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stac
                  (long long)gqa);
     DTTS_REQUIRE(g.window >= 0 && g.eps >= 0.0f && g.rope_base > 0.0, "dtts_stack_create: bad window, eps or base");
     const int64_t qw = g.heads * g.head_dim, qkvw = (g.heads + 2 * g.n_kv) * g.head_dim;
-    DTTS_REQUIRE(dtts::tiles_ok(g.dim, qkvw, 0) && dtts::tiles_ok(qw, g.dim, 2) && dtts::tiles_ok(g.dim, 2 * g.ffn, 1) &&
-                     dtts::tiles_ok(g.ffn, g.dim, 2),
-                 "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of 128");
+    if (how == DTTS_WEIGHT_F16)
+        DTTS_REQUIRE(dtts::tiles_ok(g.dim, qkvw, 0) && dtts::tiles_ok(qw, g.dim, 2) &&
+                         dtts::tiles_ok(g.dim, 2 * g.ffn, 1) && dtts::tiles_ok(g.ffn, g.dim, 2),
+                     "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of 128");
+    else
+        DTTS_REQUIRE(dtts::proj_shape_ok(how, g.dim, qkvw) && dtts::proj_shape_ok(how, qw, g.dim) &&
+                         dtts::proj_shape_ok(how, g.dim, 2 * g.ffn) && dtts::proj_shape_ok(how, g.ffn, g.dim),
+                     "dtts_stack_create: projection shapes need dim, heads*head_dim and ffn multiples of %d",
+                     how == DTTS_WEIGHT_F32 ? 64 : 256);
     DTTS_REQUIRE(g.dim % 4 == 0 && g.dim <= 8192, "dtts_stack_create: dim %lld (a multiple of 4, at most 8192)",
                  (long long)g.dim);
     DTTS_REQUIRE(g.capacity < (int64_t(1) << 24) && g.dim * g.ffn < (int64_t(1) << 31) && qkvw * g.dim < (int64_t(1) << 31),
@@ -1046,6 +1204,7 @@ extern "C" int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stac
     dtts_stack *s = new (std::nothrow) dtts_stack();
     DTTS_REQUIRE(s, "dtts_stack_create: out of host memory");
     s->geo = g;
+    s->how = how;
     s->layers.assign(layers, layers + g.layers);
     s->final_norm = final_norm;
     const int64_t half = g.head_dim / 2;
@@ -1080,7 +1239,7 @@ extern "C" void dtts_stack_destroy(dtts_stack *s) {
 
 extern "C" size_t dtts_stack_workspace_bytes(const dtts_stack *s, int64_t lanes, int64_t cap) {
     if (!s || lanes <= 0 || lanes > dtts::kStackMaxLanes || cap <= 0) return 0;
-    return dtts::plan_of(s->geo, lanes, cap).total;
+    return dtts::step_bytes(*s, lanes, cap);
 }
 
 extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, const dtts_stack_cache *caches,
@@ -1102,8 +1261,8 @@ extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, cons
     for (int64_t i = 0; i < g.layers; ++i)
         DTTS_REQUIRE(caches[i].k && caches[i].v && dtts::aligned(caches[i].k, 16) && dtts::aligned(caches[i].v, 16),
                      "%s: layer %lld cache missing or misaligned", name, (long long)i);
-    const dtts::Plan pl = dtts::plan_of(g, lanes, cap);
-    DTTS_REQUIRE(ws_bytes >= pl.total, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, pl.total);
+    const size_t need = dtts::step_bytes(*s, lanes, cap);
+    DTTS_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < %zu needed", name, ws_bytes, need);
     dtts::Positions p{};
     for (int64_t i = 0; i < lanes; ++i) {
         // Stack::forward refuses start + t > capacity (crates/qwen3tts/src/qwen3.rs:303-309)
@@ -1115,8 +1274,7 @@ extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, cons
     DTTS_LAUNCH_CHECK(name);
     char *ws = static_cast<char *>(workspace);
     if (!(flags & DTTS_STACK_GRAPH)) {
-        DTTS_HIP_CHECK(dtts::enqueue_step(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, pl,
-                                          stream),
+        DTTS_HIP_CHECK(dtts::enqueue_any(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, stream),
                        name);
         return DTTS_OK;
     }
@@ -1134,8 +1292,7 @@ extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, cons
         if (!s->capture_stream) DTTS_HIP_CHECK(hipStreamCreateWithFlags(&s->capture_stream, hipStreamNonBlocking), name);
         DTTS_HIP_CHECK(hipStreamBeginCapture(s->capture_stream, hipStreamCaptureModeThreadLocal), name);
         const hipError_t le =
-            dtts::enqueue_step(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, pl,
-                               s->capture_stream);
+            dtts::enqueue_any(*s, x, out, caches, static_cast<int>(lanes), static_cast<int>(cap), ws, s->capture_stream);
         hipGraph_t graph = nullptr;
         const hipError_t ee = hipStreamEndCapture(s->capture_stream, &graph);
         hipError_t ie = hipSuccess;
@@ -1151,7 +1308,7 @@ extern "C" int dtts_stack_decode(dtts_stack *s, const float *x, float *out, cons
 }
 
 extern "C" size_t dtts_stack_prefill_workspace_bytes(const dtts_stack *s, int64_t lanes, int64_t t) {
-    if (!s || lanes <= 0 || t < 2 || lanes * t > (int64_t(1) << 20)) return 0;
+    if (!s || s->how != DTTS_WEIGHT_F16 || lanes <= 0 || t < 2 || lanes * t > (int64_t(1) << 20)) return 0;
     return dtts::prefill_plan_of(s->geo, lanes, t).total;
 }
 
@@ -1160,6 +1317,10 @@ extern "C" int dtts_stack_prefill(dtts_stack *s, const float *x, float *out, con
                                   size_t ws_bytes, hipStream_t stream) {
     const char *name = "dtts_stack_prefill";
     DTTS_REQUIRE(s, "%s: null stack", name);
+    if (s->how != DTTS_WEIGHT_F16) {
+        dtts::set_error("%s: the prefill branch runs f16 layers (this stack was made with weight kind %d)", name, s->how);
+        return DTTS_ERR_UNSUPPORTED;
+    }
     DTTS_REQUIRE(lanes >= 0 && t >= 2, "%s: %lld lanes, t = %lld (t >= 2; one position is dtts_stack_decode)", name,
                  (long long)lanes, (long long)t);
     if (lanes == 0) return DTTS_OK;

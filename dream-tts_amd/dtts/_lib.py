@@ -108,6 +108,9 @@ SIGNATURES = {
     "dtts_gemm_q8_0_ws_f32": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
     "dtts_gemm_q8_0_packed_f32": [_P, _P, _P, _I64, _I64, _I64, _I32, _P, _SZ, _P],
     "dtts_stack_create": [_P, _P, _P, _P],
+    "dtts_stack_create_as": [_P, _P, _P, _I32, _P],
+    "dtts_gemm_f32_nt_workspace_bytes": [_I64, _I64, _I64],
+    "dtts_gemm_f32_nt": [_P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "dtts_stack_destroy": [_P],
     "dtts_stack_workspace_bytes": [_P, _I64, _I64],
     "dtts_stack_decode": [_P, _P, _P, _P, _I64, _I64, _P, _P, _SZ, _I32, _P],
@@ -135,7 +138,7 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_codec_hop": ctypes.c_int64, "dtts_codec_workspace_bytes": ctypes.c_size_t,
              "dtts_decode_attention_workspace_bytes": ctypes.c_size_t,
              "dtts_gemm_f16_workspace_bytes": ctypes.c_size_t, "dtts_stack_destroy": None,
-             "dtts_stack_workspace_bytes": ctypes.c_size_t, "dtts_stack_prefill_workspace_bytes": ctypes.c_size_t, "dtts_codec_front_destroy": None,
+             "dtts_stack_workspace_bytes": ctypes.c_size_t, "dtts_gemm_f32_nt_workspace_bytes": ctypes.c_size_t, "dtts_stack_prefill_workspace_bytes": ctypes.c_size_t, "dtts_codec_front_destroy": None,
              "dtts_codec_front_workspace_bytes": ctypes.c_size_t,
              "dtts_codec_document_workspace_bytes": ctypes.c_size_t, "dtts_checkpoint_close": None,
              "dtts_checkpoint_count": ctypes.c_int64, "dtts_codec_model_destroy": None,

@@ -308,6 +308,23 @@ def gateup_silu(a, w_gu, workspace=None, out=None):
     return y
 
 
+def gemm_f32_nt(x, w_nk, workspace=None):
+    """Proj::Dense's forward (crates/tts-nn/src/lib.rs:438-459, 527) on the [out, in] layout:
+    x [m, k] f32 . w [n, k]^T f32 -> [m, n] f32 (dtts_gemm_f32_nt)."""
+    _mat(x, "gemm_f32_nt", "x", _F32)
+    _mat(w_nk, "gemm_f32_nt", "w", _F32)
+    m, k = x.shape
+    n = w_nk.shape[0]
+    if w_nk.shape[1] != k:
+        raise DttsError(f"gemm_f32_nt: w [{n}, {w_nk.shape[1]}] for k = {k}")
+    y = torch.empty((m, n), dtype=_F32, device=x.device)
+    need = int(lib().dtts_gemm_f32_nt_workspace_bytes(m, k, n))
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    call("dtts_gemm_f32_nt", ptr(x), ptr(w_nk), ptr(y), m, k, n, ptr(workspace), workspace.numel(), stream_handle())
+    return y
+
+
 def swiglu_mul(gate, up):
     """fused::swiglu_mul (crates/tts-nn/src/fused.rs:376-385), f32."""
     _check(gate, "swiglu_mul", (_F32,), "gate")

@@ -18,6 +18,12 @@ from . import synth
 from ._lib import call, lib, stream_handle
 
 GRAPH = 1  # DTTS_STACK_GRAPH
+# Stack::load's weight kinds (DTTS_WEIGHT_*): every kind but f16 keeps f32 caches
+WEIGHTS = {"f16": 0, "f32": 1, "q8_0": 2, "q8_0_a32": 3}
+
+
+def cache_dtype(weight: str):
+    return torch.float16 if weight == "f16" else torch.float32
 
 
 @dataclass(frozen=True)
@@ -132,24 +138,39 @@ def _f32_dev(a, dev):
 
 
 class State:
-    """Per-layer f16 caches [lanes, n_kv, cap, head_dim] (State::new_state_with, qwen3.rs:
-    245-268), zero-filled."""
+    """Per-layer caches [lanes, n_kv, cap, head_dim] (State::new_state_with, qwen3.rs:245-268),
+    zero-filled: f16, or f32 for a stack of another weight kind."""
 
-    def __init__(self, geo: Geometry, lanes: int, cap: int, dev):
+    def __init__(self, geo: Geometry, lanes: int, cap: int, dev, dtype=torch.float16):
         shape = (lanes, geo.n_kv, cap, geo.head_dim)
-        self.k = [torch.zeros(shape, dtype=torch.float16, device=dev) for _ in range(geo.layers)]
-        self.v = [torch.zeros(shape, dtype=torch.float16, device=dev) for _ in range(geo.layers)]
+        self.k = [torch.zeros(shape, dtype=dtype, device=dev) for _ in range(geo.layers)]
+        self.v = [torch.zeros(shape, dtype=dtype, device=dev) for _ in range(geo.layers)]
         self.lanes, self.cap = lanes, cap
         self._c = (_Cache * geo.layers)()
         for i in range(geo.layers):
             self._c[i].k, self._c[i].v = self.k[i].data_ptr(), self.v[i].data_ptr()
 
 
-def upload(geo: Geometry, layers, final_norm, dev):
+def _q8_packed_dev(a, dev):
+    """QTensor::quantize_onto of an [out, in] f32 weight (the library's host quantizer, GGML
+    blocks), uploaded and repacked for the matrix cores (dtts_q8_0_repack)."""
+    from . import ops
+
+    a = np.ascontiguousarray(a, np.float32)
+    blocks = torch.from_numpy(ops.q8_0_quantize(a)).to(dev)
+    return ops.q8_0_repack(blocks, a.shape[1])
+
+
+def upload(geo: Geometry, layers, final_norm, dev, weight: str = "f16"):
     """Host checkpoint-layout weights -> the device tensors dtts_stack_create takes, arranged as
     Layer::load arranges them: q|k|v rows concatenated, gate|up rows concatenated, q_norm folded
-    with 1/sqrt(head_dim), projections in f16, norms and scales in f32."""
+    with 1/sqrt(head_dim), projections of the weight kind (f16; f32; Q8_0 blocks, repacked),
+    norms and scales in f32."""
     def f16(a):
+        if weight == "f32":
+            return _f32_dev(a, dev)
+        if weight in ("q8_0", "q8_0_a32"):
+            return _q8_packed_dev(a, dev)
         return _f16_dev(a, dev)
 
     def f32(a):
@@ -198,13 +219,14 @@ def c_geometry(geo: Geometry) -> _Geometry:
 class Stack:
     """Device weights + a dtts_stack handle (keeps every device tensor alive)."""
 
-    def __init__(self, geo: Geometry, layers, final_norm, dev):
+    def __init__(self, geo: Geometry, layers, final_norm, dev, weight: str = "f16"):
         """layers / final_norm: host checkpoint-layout weights (random_weights' form), uploaded
         here; or device tensors already in the library's layouts (upload's or
-        random_device_weights' form, recognised by final_norm being a torch tensor)."""
-        self.geo, self.dev = geo, dev
+        random_device_weights' form, recognised by final_norm being a torch tensor). weight:
+        Stack::load's `how` (a WEIGHTS key)."""
+        self.geo, self.dev, self.weight = geo, dev, weight
         if not isinstance(final_norm, torch.Tensor):
-            layers, final_norm = upload(geo, layers, final_norm, dev)
+            layers, final_norm = upload(geo, layers, final_norm, dev, weight)
         self._keep = [final_norm]
 
         def ptr(t):
@@ -221,8 +243,8 @@ class Stack:
                 setattr(ls[i], name, ptr(L[name]))
         self._g, self._l = g, ls
         handle = ctypes.c_void_p()
-        call("dtts_stack_create", ctypes.byref(g), ctypes.cast(ls, ctypes.c_void_p),
-             ctypes.c_void_p(final_norm.data_ptr()), ctypes.byref(handle))
+        call("dtts_stack_create_as", ctypes.byref(g), ctypes.cast(ls, ctypes.c_void_p),
+             ctypes.c_void_p(final_norm.data_ptr()), WEIGHTS[weight], ctypes.byref(handle))
         self.handle = handle
         self._ws = None
 
@@ -231,6 +253,7 @@ class Stack:
         """A stack created elsewhere (dtts_stack_model_load); `owner` keeps it alive and destroys it."""
         s = cls.__new__(cls)
         s.geo, s.dev, s.handle, s._keep, s._ws, s._owner = geo, dev, handle, [], None, owner
+        s.weight = "f16"
         return s
 
     def close(self):
@@ -248,7 +271,7 @@ class Stack:
         return sum(t.numel() * t.element_size() for t in self._keep)
 
     def new_state(self, lanes: int, cap: int | None = None) -> State:
-        return State(self.geo, lanes, cap or self.geo.capacity, self.dev)
+        return State(self.geo, lanes, cap or self.geo.capacity, self.dev, cache_dtype(self.weight))
 
     def workspace_bytes(self, lanes: int, cap: int) -> int:
         return int(lib().dtts_stack_workspace_bytes(self.handle, lanes, cap))

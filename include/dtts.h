@@ -333,21 +333,32 @@ typedef struct dtts_stack_geometry {
     int64_t capacity;             /* RoPE table length (Stack::load's capacity); caches may be shorter */
 } dtts_stack_geometry;
 
-/* Device pointers, kept (not copied) by dtts_stack_create; norms and scales f32, projections f16
- * in the checkpoint's [out, in] layout, 16-byte aligned. */
+/* The layers' weight kinds (Stack::load's `how`, crates/qwen3tts/src/qwen3.rs:228-250; Weight,
+ * crates/tts-nn/src/lib.rs:403-430). Every kind but F16 keeps f32 caches, as Stack::load does. */
+#define DTTS_WEIGHT_F16 0     /* Proj::Half: f16 [out, in] projections, f16 caches */
+#define DTTS_WEIGHT_F32 1     /* Proj::Dense: f32 [out, in] projections, f32 caches */
+#define DTTS_WEIGHT_Q8_0 2    /* Proj::Quant(Q8_0): dtts_q8_0_repack'd blocks of the [out, in] weight; the
+                                 f32 activations quantized per 32-block (candle CPU's vec_dot); f32 caches */
+#define DTTS_WEIGHT_Q8_0_A32 3 /* the same blocks with the f32 activations unquantized (the dequantized
+                                  product a GPU QMatMul takes); f32 caches */
+
+/* Device pointers, kept (not copied) by dtts_stack_create; norms and scales f32, projections in
+ * the checkpoint's [out, in] layout (rows of the stack's weight kind: f16, f32, or Q8_0 blocks
+ * repacked by dtts_q8_0_repack), 16-byte aligned. */
 typedef struct dtts_stack_layer {
     const float *attn_norm, *ffn_norm; /* [dim] */
-    const dtts_f16 *wqkv;              /* [(heads + 2 n_kv) head_dim, dim]: q, k, v rows (Layer::load's cat) */
-    const dtts_f16 *wo;                /* [dim, heads head_dim] */
-    const dtts_f16 *w_gateup;          /* [2 ffn, dim]: gate rows, then up rows */
-    const dtts_f16 *wdown;             /* [dim, ffn] */
+    const void *wqkv;                  /* [(heads + 2 n_kv) head_dim, dim]: q, k, v rows (Layer::load's cat) */
+    const void *wo;                    /* [dim, heads head_dim] */
+    const void *w_gateup;              /* [2 ffn, dim]: gate rows, then up rows */
+    const void *wdown;                 /* [dim, ffn] */
     const float *qk_norms;             /* [2, head_dim]: q's weight times 1/sqrt(head_dim), then k's (qk_norm) */
     const float *attn_scale, *mlp_scale; /* [dim] (layer_scale) */
 } dtts_stack_layer;
 
-/* One layer's cache (State's Cache, qwen3.rs:122-126): k and v [lanes, n_kv, cap, head_dim] f16. */
+/* One layer's cache (State's Cache, qwen3.rs:122-126): k and v [lanes, n_kv, cap, head_dim], f16
+ * for a DTTS_WEIGHT_F16 stack and f32 for the other kinds (Stack::load's kv dtype). */
 typedef struct dtts_stack_cache {
-    dtts_f16 *k, *v;
+    void *k, *v;
 } dtts_stack_cache;
 
 typedef struct dtts_stack dtts_stack;
@@ -356,6 +367,13 @@ typedef struct dtts_stack dtts_stack;
  * lib.rs:1178-1205) on the current device. */
 int dtts_stack_create(const dtts_stack_geometry *geo, const dtts_stack_layer *layers, const float *final_norm,
                       dtts_stack **out);
+/* The same with the layers' weight kind (DTTS_WEIGHT_*): Stack::load(.., how, ..). dtts_stack_create
+ * is DTTS_WEIGHT_F16. F32 layers take dim, heads*head_dim and ffn multiples of 64; Q8_0 layers
+ * multiples of 256 (the packed layout), with the gate and up rows quantized and repacked as one
+ * [2 ffn, dim] weight (each row's blocks are its own, so this is the two QMatMuls). The prefill
+ * branch (dtts_stack_prefill) takes F16 stacks only. */
+int dtts_stack_create_as(const dtts_stack_geometry *geo, const dtts_stack_layer *layers, const float *final_norm,
+                         int32_t how, dtts_stack **out);
 void dtts_stack_destroy(dtts_stack *stack);
 
 /* Device scratch bytes for a step of `lanes` lanes over caches of capacity `cap`. */
@@ -536,6 +554,16 @@ int dtts_gemm_f16_nt_noalloc(const dtts_f16 *a, const dtts_f16 *w_nk, float *c, 
 int dtts_gemm_f16_gateup_silu(const dtts_f16 *a, const dtts_f16 *w_gu, float *y, int64_t m,
                               int64_t k, int64_t ffn, void *workspace, size_t ws_bytes,
                               hipStream_t stream);
+
+/* Proj::Dense's forward (matmul_2d of f32 activations by an f32 weight, crates/tts-nn/src/
+ * lib.rs:438-459, 527) on the checkpoint's [out, in] layout: y[m, n] = x[m, k] . w[n, k]^T, f32
+ * throughout, on the f32 matrix cores. m <= 64, k % 32 == 0, n % 64 == 0, x and w 16-byte
+ * aligned. k is split into ranges over workgroups when that fills the GPU; the ranges' partials
+ * then go to the workspace (dtts_gemm_f32_nt_workspace_bytes, 16-byte aligned; required when
+ * nonzero) and a second launch sums them in range order. */
+size_t dtts_gemm_f32_nt_workspace_bytes(int64_t m, int64_t k, int64_t n);
+int dtts_gemm_f32_nt(const float *x, const float *w, float *y, int64_t m, int64_t k, int64_t n, void *workspace,
+                     size_t workspace_bytes, hipStream_t stream);
 
 /* fused::swiglu_mul / SwigluMul (crates/tts-nn/src/fused.rs:289-385): y = (g / (1 + exp(-g))) * u,
  * f32, n elements. */

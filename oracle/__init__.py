@@ -393,6 +393,51 @@ def kv_append_f16(k_bits, v_bits, pos, kcache, vcache):
 
 # ---------------------------------------------------------------- GEMMs
 
+def _stack_decode_dense(geo, layers, final_norm, x, kcaches, vcaches, pos, weight):
+    """stack_decode_f32 for the f32 and Q8_0 weight kinds (f32 caches, f32 projections in and out,
+    no f16 rounding anywhere), citing qwen3.rs line by line."""
+    b = x.shape[0]
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw = heads * hd, n_kv * hd
+    pos = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, np.int32), (b,)))
+    cos_t, sin_t = rope_table_f32(geo.capacity, hd, geo.rope_base)  # Stack::load (qwen3.rs:240)
+    span = pos + 1
+    wstart = np.where(span > geo.window, span - geo.window, 0).astype(np.int32) if geo.window else np.zeros(b, np.int32)
+    for c in list(kcaches) + list(vcaches):
+        assert c.dtype == np.float32 and c.flags["C_CONTIGUOUS"], "f32 caches for this weight kind"
+    h = _f32(x).copy()
+    for li, L in enumerate(layers):
+        normed = rms_norm_f32(h, L["attn_norm"], geo.eps)                             # :339
+        qkv = _proj_as(normed, np.concatenate([L["wq"], L["wk"], L["wv"]], axis=0), weight)  # :340, :69-77
+        q = qkv[:, :qw].reshape(b, heads, hd)                                         # :358-364
+        k = qkv[:, qw:qw + kvw].reshape(b, n_kv, hd)
+        v = qkv[:, qw + kvw:].reshape(b, n_kv, hd)
+        if geo.qk_norm:                                                               # :369-376
+            s = np.float32(1.0 / np.sqrt(np.float64(hd)))
+            q = rms_norm_f32(q, _f32(L["q_norm"]) * s, geo.eps)                       # :78-91 (folded)
+            k = rms_norm_f32(k, _f32(L["k_norm"]), geo.eps)
+        q = rope_halfsplit_f32(q, cos_t, sin_t, pos)                                  # :381-387
+        k = rope_halfsplit_f32(k, cos_t, sin_t, pos)
+        for i in range(b):                                                            # :391-392 (slice_set, f32)
+            kcaches[li][i, :, pos[i]] = k[i]
+            vcaches[li][i, :, pos[i]] = v[i]
+        if not geo.qk_norm:
+            q = q * np.float32(1.0 / np.sqrt(np.float64(hd)))                         # :404-408
+        attn = decode_attention_f32(q.reshape(b, n_kv, heads // n_kv, hd), kcaches[li], vcaches[li],
+                                    span, wstart).reshape(b, qw)                      # :413-414
+        o = _proj_as(attn, L["wo"], weight)                                           # :446
+        if geo.layer_scale:
+            o = o * _f32(L["attn_scale"])                                             # :447-450
+        h = h + o                                                                     # :451
+        normed = rms_norm_f32(h, L["ffn_norm"], geo.eps)                              # :453
+        tail = swiglu_mul_f32(_proj_as(normed, L["gate"], weight), _proj_as(normed, L["up"], weight))  # :454-457
+        mlp = _proj_as(tail, L["down"], weight)                                       # :458
+        if geo.layer_scale:
+            mlp = mlp * _f32(L["mlp_scale"])                                          # :459-462
+        h = h + mlp                                                                   # :463
+    return rms_norm_f32(h, final_norm, geo.eps)                                       # :466
+
+
 def decode_attention_f32(q, k, v, span, window_start=0):
     """attn::decode_attention's CPU path (crates/tts-nn/src/attn.rs:18-73, 85-126, 189-226).
     q [b, n_kv, gqa, D] f32; caches [b, n_kv, cap, D] as f16 bit patterns (uint16) or f32; span
@@ -512,7 +557,30 @@ def _proj_half(x, w_out_in):
     return y if _skinny_eligible(m, k, w_out_in.shape[0]) else f16_to_f32(f32_to_f16(y))
 
 
-def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
+STACK_WEIGHTS = ("f16", "f32", "q8_0", "q8_0_a32")
+
+
+def _proj_as(x, w_out_in, weight):
+    """Proj::forward for each weight kind (crates/tts-nn/src/lib.rs:509-531), f32 in and out:
+    f16 -> Proj::Half's routing; f32 -> Proj::Dense's f32 GEMM (matmul_2d, lib.rs:438-459),
+    evaluated in float64 and rounded once; q8_0 -> QMatMul on the Q8_0 blocks of the weight
+    (QTensor::quantize_onto, lib.rs:480-486) with the f32 activations quantized per block
+    (candle CPU's vec_dot, q8_0_matmul_w8a8); q8_0_a32 -> the same blocks times the unquantized
+    f32 activations (float64, rounded once)."""
+    if weight == "f16":
+        return _proj_half(x, w_out_in)
+    x = _f32(x)
+    if weight == "f32":
+        return (x.astype(np.float64) @ _f32(w_out_in).astype(np.float64).T).astype(np.float32)
+    blocks = q8_0_quantize(_f32(w_out_in))
+    if weight == "q8_0":
+        return q8_0_matmul_w8a8(x, blocks)
+    if weight == "q8_0_a32":
+        return q8_0_matmul_f64(x, blocks).astype(np.float32)
+    raise ValueError(f"weight kind {weight!r}")
+
+
+def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos, weight="f16"):
     """Stack::forward at t = 1 (crates/qwen3tts/src/qwen3.rs:294-467) with f16 weights and f16
     caches, each lane at its own position; the projections follow Proj::Half's routing by lane
     count (f32 outputs for 8, 16, .. 48 lanes, f16 outputs otherwise, one lane included). geo: an object with the Geometry fields (dim, layers,
@@ -520,7 +588,14 @@ def stack_decode_f32(geo, layers, final_norm, x, kcaches, vcaches, pos):
     dicts of checkpoint-layout f32 weights (wq, wk, wv, wo, gate, up, down [out, in]; attn_norm,
     ffn_norm; q_norm, k_norm; attn_scale, mlp_scale); x [b, dim] f32; kcaches / vcaches: per
     layer uint16 [b, n_kv, cap, head_dim], updated in place; pos int32[b]. Returns the final
-    rms_norm of the residual stream, [b, dim] f32."""
+    rms_norm of the residual stream, [b, dim] f32.
+
+    weight: Stack::load's `how` (qwen3.rs:228-250), one of STACK_WEIGHTS. Every kind but f16 keeps
+    f32 caches (kcaches / vcaches float32 arrays, qwen3.rs:242-246), which qkrope::eligible refuses
+    (qkrope.rs:11-18), so its step takes the composed route (qwen3.rs:358-400): rms_norm over each
+    head with the folded norms, rope, and the f32 k and v set into the caches as they are."""
+    if weight != "f16":
+        return _stack_decode_dense(geo, layers, final_norm, x, kcaches, vcaches, pos, weight)
     b = x.shape[0]
     hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
     qw, kvw = heads * hd, n_kv * hd

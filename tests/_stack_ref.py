@@ -19,20 +19,53 @@ def with_layers(geo, n):
     return replace(geo, layers=n)
 
 
-def inputs(geo, seed, lanes, cap, fill=True):
-    """x [lanes, dim] f32 and per-layer caches (uint16 f16 bits), pre-filled with N(0,1) history
-    when fill is set."""
+def inputs(geo, seed, lanes, cap, fill=True, weight="f16"):
+    """x [lanes, dim] f32 and per-layer caches, pre-filled with N(0,1) history when fill is set:
+    uint16 f16 bits for an f16 stack, float32 for the other weight kinds (Stack::load's kv dtype)."""
     x = synth.normal(seed, "stack.x", (lanes, geo.dim))
     shape = (lanes, geo.n_kv, cap, geo.head_dim)
+    f16 = weight == "f16"
     kc, vc = [], []
     for i in range(geo.layers):
         if fill:
-            kc.append(synth.f16_bits(synth.normal(seed, f"stack.k{i}", shape)))
-            vc.append(synth.f16_bits(synth.normal(seed, f"stack.v{i}", shape)))
+            k, v = synth.normal(seed, f"stack.k{i}", shape), synth.normal(seed, f"stack.v{i}", shape)
+            kc.append(synth.f16_bits(k) if f16 else k.astype(np.float32))
+            vc.append(synth.f16_bits(v) if f16 else v.astype(np.float32))
         else:
-            kc.append(np.zeros(shape, np.uint16))
-            vc.append(np.zeros(shape, np.uint16))
+            kc.append(np.zeros(shape, np.uint16 if f16 else np.float32))
+            vc.append(np.zeros(shape, np.uint16 if f16 else np.float32))
     return x, kc, vc
+
+
+def _q8(w):
+    """Q8_0 blocks of an [n, k] weight as ggml's quantize_row_q8_0 forms them, in numpy: per 32-block
+    amax, d = amax / 127 and id = 1 / d in f32, codes rounded half away from zero, d stored in f16.
+    Returns (codes [n, k/32, 32] float64, d [n, k/32] float64)."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    wb = w.reshape(n, k // 32, 32)
+    d = (np.abs(wb).max(-1) / np.float32(127)).astype(np.float32)
+    inv = np.zeros_like(d)
+    np.divide(np.float32(1), d, out=inv, where=d != 0)
+    t = (wb * inv[..., None]).astype(np.float32).astype(np.float64)
+    q = np.sign(t) * np.floor(np.abs(t) + 0.5)
+    return q, d.astype(np.float16).astype(np.float64)
+
+
+def proj_kind_f64(a, w, weight):
+    """Proj::forward for the f32 and Q8_0 weight kinds in float64 (crates/tts-nn/src/lib.rs:509-531):
+    the dense product, the dequantized weight times the activations (q8_0_a32), or both sides
+    quantized per block and the integer block dots scaled by the two f16 scales (q8_0)."""
+    a = np.asarray(a, np.float64)
+    if weight == "f32":
+        return a @ np.asarray(w, np.float64).T
+    qw, dw = _q8(w)
+    if weight == "q8_0_a32":
+        deq = (qw * dw[..., None]).reshape(w.shape)
+        return a @ deq.T
+    qa, da = _q8(a.astype(np.float32))
+    dots = np.einsum("mbj,nbj->mnb", qa, qw)
+    return (dots * da[:, None, :] * dw[None, :, :]).sum(-1)
 
 
 def _eligible(m, k, n):
@@ -59,8 +92,11 @@ def _rope(x, pos, geo):
     return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], -1)
 
 
-def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
-    """Returns (out [b, dim] float64, kc, vc) with the caches as new uint16 arrays."""
+def stack_f64(geo, layers, final_norm, x, kc, vc, pos, weight="f16"):
+    """Returns (out [b, dim] float64, kc, vc) with the caches as new arrays (uint16 f16 bits for an
+    f16 stack; float32 for the other weight kinds, whose step rounds nothing to f16)."""
+    if weight != "f16":
+        return _stack_dense_f64(geo, layers, final_norm, x, kc, vc, pos, weight)
     b = x.shape[0]
     hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
     qw, kvw, gqa = heads * hd, n_kv * hd, heads // n_kv
@@ -106,6 +142,52 @@ def stack_f64(geo, layers, final_norm, x, kc, vc, pos):
         g, u = out(a @ _h(L["gate"]).T, geo.dim, geo.ffn), out(a @ _h(L["up"]).T, geo.dim, geo.ffn)
         t = _h(g / (1.0 + np.exp(-g)) * u)
         m = out(t @ _h(L["down"]).T, geo.ffn, geo.dim)
+        if geo.layer_scale:
+            m = m * L["mlp_scale"]
+        h = h + m
+    return _rms(h, final_norm, geo.eps), kc, vc
+
+
+def _stack_dense_f64(geo, layers, final_norm, x, kc, vc, pos, weight):
+    b = x.shape[0]
+    hd, heads, n_kv = geo.head_dim, geo.heads, geo.n_kv
+    qw, kvw, gqa = heads * hd, n_kv * hd, heads // n_kv
+    pos = np.broadcast_to(np.asarray(pos, np.int64), (b,))
+    kc = [k.copy() for k in kc]
+    vc = [v.copy() for v in vc]
+    h = np.asarray(x, np.float64)
+    for li, L in enumerate(layers):
+        a = _rms(h, L["attn_norm"], geo.eps)
+        qkv = proj_kind_f64(a, np.concatenate([L["wq"], L["wk"], L["wv"]], 0), weight)
+        q = qkv[:, :qw].reshape(b, heads, hd)
+        k = qkv[:, qw:qw + kvw].reshape(b, n_kv, hd)
+        v = qkv[:, qw + kvw:].reshape(b, n_kv, hd)
+        if geo.qk_norm:
+            q = _rms(q, np.float64(L["q_norm"]) / np.sqrt(hd), geo.eps)
+            k = _rms(k, L["k_norm"], geo.eps)
+        q, k = _rope(q, pos, geo), _rope(k, pos, geo)
+        if not geo.qk_norm:
+            q = q / np.sqrt(hd)
+        for i in range(b):
+            kc[li][i, :, pos[i]] = k[i]
+            vc[li][i, :, pos[i]] = v[i]
+        att = np.empty((b, heads, hd))
+        for i in range(b):
+            hi = pos[i] + 1
+            lo = hi - geo.window if geo.window and hi > geo.window else 0
+            kk = kc[li][i, :, lo:hi].astype(np.float64)
+            vv = vc[li][i, :, lo:hi].astype(np.float64)
+            qg = q[i].reshape(n_kv, gqa, hd)
+            sc = np.einsum("hgd,hnd->hgn", qg, kk)
+            e = np.exp(sc - sc.max(-1, keepdims=True))
+            att[i] = np.einsum("hgn,hnd->hgd", e / e.sum(-1, keepdims=True), vv).reshape(heads, hd)
+        o = proj_kind_f64(att.reshape(b, qw), L["wo"], weight)
+        if geo.layer_scale:
+            o = o * L["attn_scale"]
+        h = h + o
+        a = _rms(h, L["ffn_norm"], geo.eps)
+        g, u = proj_kind_f64(a, L["gate"], weight), proj_kind_f64(a, L["up"], weight)
+        m = proj_kind_f64(g / (1.0 + np.exp(-g)) * u, L["down"], weight)
         if geo.layer_scale:
             m = m * L["mlp_scale"]
         h = h + m

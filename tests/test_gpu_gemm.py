@@ -247,3 +247,27 @@ def test_q8_0_mode_and_dtype_refusals(dev):
                 ops.q8_0_matmul(xx, bd, mode, workspace=ws)
         with pytest.raises(ops.DttsError, match="not taken with"):
             ops.q8_0_matmul_packed(xx, ops.q8_0_repack(bd, k), n, mode)
+
+
+# ---------------------------------------------------------------- f32 projections (Proj::Dense)
+
+@pytest.mark.parametrize("m,k,n", [(48, 1024, 4096), (48, 1024, 3072), (48, 3072, 1024), (1, 2048, 6144),
+                                   (8, 256, 64), (64, 512, 128), (33, 96, 192)])
+def test_gemm_f32_nt(dev, m, k, n):
+    """dtts_gemm_f32_nt against float64 on the same f32 operands: max-rel <= 1e-5 (f32 products
+    and sums on the matrix cores, in another order), and split and single-range runs agree."""
+    x = synth.normal(100, "x32", (m, k)).astype(np.float32)
+    w = synth.normal(100, "w32", (n, k), 0, 0.02).astype(np.float32)
+    got = to_host(ops.gemm_f32_nt(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev)))
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    ab, rl = rel(got, want)
+    assert rl <= 1e-5, (ab, rl)
+
+
+def test_gemm_f32_nt_refusals(dev):
+    x = torch.zeros((8, 100), device=dev)
+    with pytest.raises(ops.DttsError, match="multiple of 32"):
+        ops.gemm_f32_nt(x, torch.zeros((64, 100), device=dev))
+    x = torch.zeros((65, 128), device=dev)
+    with pytest.raises(ops.DttsError, match="m <= 64"):
+        ops.gemm_f32_nt(x, torch.zeros((64, 128), device=dev))

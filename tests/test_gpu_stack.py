@@ -7,6 +7,7 @@ Eager launches and the captured graph run the same kernels and must agree bit fo
 after step as positions advance. Geometries: QK-norm (talker / code predictor form) and
 no-QK-norm with LayerScale and a sliding window (the codec transformer's form), caches long
 enough for the attention split, the talker's own widths, and the argument checks."""
+import ctypes
 from dataclasses import replace
 
 import numpy as np
@@ -15,6 +16,7 @@ import torch
 
 import oracle
 from dtts import DttsError, stack, synth
+from dtts._lib import call
 
 from _stack_ref import SMALL, WINDOWED, inputs, with_layers
 from _util import rel, to_dev, to_host
@@ -153,3 +155,108 @@ def test_stack_rejects_bad_arguments(dev):
         stack.Stack(replace(geo, heads=3), layers, fn, dev)
     with pytest.raises(DttsError, match="multiples of 128"):
         stack.Stack(replace(geo, ffn=500), stack.random_weights(replace(geo, ffn=500), 95)[0], fn, dev)
+
+
+# ---------------------------------------------------------------- f32 and Q8_0 layers
+# Stack::load with Weight::F32 or Weight::Quant (crates/qwen3tts/src/qwen3.rs:228-250): f32
+# caches, Proj::forward's f32 activations into every projection (lib.rs:509-531), the composed QK
+# route. Bars against oracle.stack_decode_f32(weight=...): f32 and the unquantized-activation Q8_0
+# kind max-rel 1e-5 on the output and on every cache entry written (f32 sums in another order);
+# W8A8 2e-2, the north star's tolerance for int8 GEMM outputs at unit scale: an activation whose
+# f32 value differs from the oracle's in the last bit can land on the other side of a code's
+# rounding boundary (one code step of one block moves a dot by ~4/(127 sqrt(k)) of it), and the
+# next projections then quantize shifted inputs, so GPU and oracle become two W8A8 evaluations
+# apart by the quantization noise itself (measured: 1e-7 until a first flip, 6e-4 after one at the
+# small widths, 7.7e-3 at the talker's; the per-projection W8A8 kernel is held to 1e-5 on
+# identical inputs in test_gpu_gemm.py); every other cache entry bit-identical.
+
+class PairW(Pair):
+    def __init__(self, dev, geo, seed, lanes, cap, weight, tol):
+        self.geo, self.lanes, self.cap, self.tol, self.weight = geo, lanes, cap, tol, weight
+        self.layers, self.fn = stack.random_weights(geo, seed)
+        self.x, self.kc, self.vc = inputs(geo, seed, lanes, cap, weight=weight)
+        self.st = stack.Stack(geo, self.layers, self.fn, dev, weight=weight)
+        self.state = self.st.new_state(lanes, cap)
+        assert self.state.k[0].dtype == torch.float32
+        for i in range(geo.layers):
+            self.state.k[i].copy_(torch.from_numpy(self.kc[i]).to(dev))
+            self.state.v[i].copy_(torch.from_numpy(self.vc[i]).to(dev))
+        self.dev = dev
+
+    def step(self, pos, scale=1.0, graph=False):
+        xs = (self.x * np.float32(scale)).astype(np.float32)
+        before = [(k.copy(), v.copy()) for k, v in zip(self.kc, self.vc)]
+        want = oracle.stack_decode_f32(self.geo, self.layers, self.fn, xs, self.kc, self.vc, pos, weight=self.weight)
+        got = to_host(self.st.decode(to_dev(xs, self.dev), self.state, pos, graph=graph))
+        torch.cuda.synchronize()
+        worst = rel(got, want)[1]
+        assert worst < self.tol, (self.weight, worst)
+        pos = np.broadcast_to(np.asarray(pos), (self.lanes,))
+        for li in range(self.geo.layers):
+            for dev_t, ora, old in ((self.state.k[li], self.kc[li], before[li][0]),
+                                    (self.state.v[li], self.vc[li], before[li][1])):
+                g = to_host(dev_t)
+                mask = np.ones(g.shape, bool)
+                for i, p in enumerate(pos):
+                    mask[i, :, p] = False
+                assert np.array_equal(g[mask], old[mask]), "a cache slot off the lanes' positions changed"
+                worst_c = rel(g[~mask], ora[~mask])[1]
+                assert worst_c < self.tol, (self.weight, "cache", worst_c)
+                ora[...] = g
+        print(f"{self.weight}: out max-rel {worst:.2e}", flush=True)
+        return got
+
+
+KIND_TOL = {"f32": 1e-5, "q8_0_a32": 1e-5, "q8_0": 2e-2}
+
+
+@pytest.mark.parametrize("weight", ["f32", "q8_0", "q8_0_a32"])
+def test_stack_weight_kinds_small(dev, weight):
+    """QK-norm geometry and the windowed, LayerScale, no-QK-norm one, steps eager and graph."""
+    p = PairW(dev, replace(SMALL, dim=256, ffn=512), 96, 5, 64, weight, KIND_TOL[weight])
+    start = np.array([0, 63, 17, 40, 1], np.int32) - np.array([0, 2, 0, 0, 0], np.int32)
+    p.step(start)
+    p.step(start + 1, graph=True)
+    w = PairW(dev, replace(WINDOWED, dim=256, ffn=512, heads=4, n_kv=4), 97, 4, 32, weight, KIND_TOL[weight])
+    pos = np.array([0, 3, 20, 27], np.int32)
+    for s in range(3):
+        w.step(pos + s, scale=1 + 0.1 * s, graph=(s % 2 == 1))
+
+
+@pytest.mark.parametrize("weight", ["f32", "q8_0", "q8_0_a32"])
+def test_stack_weight_kinds_talker_widths(dev, weight):
+    """The talker's widths (dim 2048, 16/8 heads, D 128, ffn 6144), 2 of its 28 layers, 48 lanes
+    at per-lane positions, through the captured graph."""
+    geo = with_layers(replace(stack.TALKER, capacity=256), 2)
+    lanes = 48
+    p = PairW(dev, geo, 98, lanes, 256, weight, KIND_TOL[weight])
+    p.step(synth.randint(98, "stack.talker.pos", (lanes,), 0, 254).astype(np.int32), graph=True)
+
+
+def test_stack_weight_kind_checks(dev):
+    """Q8_0 layers need widths that are multiples of 256 (the packed layout); the prefill branch
+    runs f16 stacks only; an unknown kind is refused."""
+    geo = replace(SMALL, dim=256, ffn=640)
+    layers, fn = stack.random_weights(geo, 99)
+    with pytest.raises(DttsError, match="multiples? of 256"):  # the repack at upload, or create itself
+        stack.Stack(geo, layers, fn, dev, weight="q8_0")
+    # create's own check, on weights whose rows the repack accepted
+    geo_ok = replace(SMALL, dim=256, ffn=512)
+    ok = stack.Stack(geo_ok, *stack.random_weights(geo_ok, 99), dev, weight="q8_0")
+    g = stack.c_geometry(replace(geo_ok, ffn=640))
+    handle = ctypes.c_void_p()
+    with pytest.raises(DttsError, match="multiples of 256"):
+        call("dtts_stack_create_as", ctypes.byref(g), ctypes.cast(ok._l, ctypes.c_void_p),
+             ctypes.c_void_p(ok._keep[0].data_ptr()), stack.WEIGHTS["q8_0"], ctypes.byref(handle))
+    geo = SMALL
+    layers, fn = stack.random_weights(geo, 99)
+    st = stack.Stack(geo, layers, fn, dev, weight="f32")
+    with pytest.raises(DttsError, match="f16 layers"):
+        st.prefill(torch.zeros((1, 2, geo.dim), device=dev), st.new_state(1, 16), 0,
+                   workspace=torch.empty(256, dtype=torch.uint8, device=dev))
+    stack.WEIGHTS["bogus"] = 7
+    try:
+        with pytest.raises(DttsError, match="weight kind 7"):
+            stack.Stack(geo, layers, fn, dev, weight="bogus")
+    finally:
+        del stack.WEIGHTS["bogus"]

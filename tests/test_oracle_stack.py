@@ -95,3 +95,70 @@ def test_stack_oracle_routes_by_lane_count():
     one = oracle.stack_decode_f32(geo, layers, fn, np.ascontiguousarray(x[:1]), k1, v1, pos[:1])
     assert not np.array_equal(one[0], eight[0])
     assert rel(one[0], eight[0])[1] < 2e-3
+
+
+# The f32 and Q8_0 weight kinds (Stack::load's `how`, qwen3.rs:228-250): f32 caches, f32
+# projections in and out, the composed QK route. Against the float64 restatement: the f32 and
+# unquantized-activation kinds differ by f32 rounding only (measured 1.2e-7 to 2.7e-7); W8A8 may
+# also differ by an activation code that f32 and float64 evaluations put on different sides of a
+# rounding boundary, each worth one code step of one block (none at these seeds: 1.8e-7 to 2.7e-7).
+@pytest.mark.parametrize("weight,bar", [("f32", 2e-6), ("q8_0_a32", 2e-6), ("q8_0", 1e-4)])
+@pytest.mark.parametrize("geo,lanes,cap,steps", [(SMALL, 3, 64, 3), (WINDOWED, 4, 32, 5), (SMALL, 8, 64, 2)])
+def test_stack_oracle_weight_kinds_match_f64(weight, bar, geo, lanes, cap, steps):
+    seed = 82
+    layers, fn = stack.random_weights(geo, seed)
+    x, kc, vc = inputs(geo, seed, lanes, cap, weight=weight)
+    start = synth.randint(seed, "stack.pos", (lanes,), 0, cap - steps).astype(np.int32)
+    worst_out, worst_cache = 0.0, 0.0
+    for s in range(steps):
+        pos = start + s
+        xs = x * np.float32(1.0 + 0.1 * s)
+        kr, vr = [k.copy() for k in kc], [v.copy() for v in vc]
+        got = oracle.stack_decode_f32(geo, layers, fn, xs, kc, vc, pos, weight=weight)
+        want, kr, vr = stack_f64(geo, layers, fn, xs, kr, vr, pos, weight=weight)
+        worst_out = max(worst_out, rel(got, want)[1])
+        for li in range(geo.layers):
+            for a, b in ((kc[li], kr[li]), (vc[li], vr[li])):
+                worst_cache = max(worst_cache, rel(a, b)[1])
+    assert worst_out < bar, worst_out
+    assert worst_cache < bar, worst_cache
+
+
+def test_stack_oracle_weight_kinds_differ():
+    """The kinds are distinguishable: on one step, f32 weights, the Q8_0 blocks with f32 activations
+    and W8A8 give results further apart than the bars above (so a kind run as another fails)."""
+    geo, lanes, cap = SMALL, 4, 16
+    layers, fn = stack.random_weights(geo, 83)
+    outs = {}
+    for weight in ("f32", "q8_0_a32", "q8_0"):
+        x, kc, vc = inputs(geo, 83, lanes, cap, weight=weight)
+        outs[weight] = oracle.stack_decode_f32(geo, layers, fn, x, kc, vc, np.array([0, 5, 9, 15], np.int32),
+                                               weight=weight)
+    assert rel(outs["q8_0_a32"], outs["f32"])[1] > 1e-3
+    assert rel(outs["q8_0"], outs["q8_0_a32"])[1] > 1e-3
+
+
+def test_stack_oracle_f32_kinds_residual_identity_and_exact_cache():
+    """With zero output and down projections the f32-cache step returns rms_norm(x) exactly, and the
+    f32 caches hold each lane's roped k and its v at its position only."""
+    geo = SMALL
+    layers, fn = stack.random_weights(geo, 84)
+    for L in layers:
+        L["wo"] = np.zeros_like(L["wo"])
+        L["down"] = np.zeros_like(L["down"])
+    lanes, cap = 4, 16
+    x, kc, vc = inputs(geo, 84, lanes, cap, weight="f32")
+    before = [(k.copy(), v.copy()) for k, v in zip(kc, vc)]
+    pos = np.array([0, 15, 7, 3], np.int32)
+    out = oracle.stack_decode_f32(geo, layers, fn, x, kc, vc, pos, weight="f32")
+    assert np.array_equal(out, oracle.rms_norm_f32(x, fn, geo.eps))
+    for (k0, v0), k1, v1 in zip(before, kc, vc):
+        for i, p in enumerate(pos):
+            k0[i, :, p], v0[i, :, p] = k1[i, :, p], v1[i, :, p]
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    # layer 0's v is the v rows of the f32 projection of rms_norm(x), stored unrounded
+    a = oracle.rms_norm_f32(x, layers[0]["attn_norm"], geo.eps)
+    v_rows = layers[0]["wv"]
+    want_v = (a.astype(np.float64) @ v_rows.astype(np.float64).T).astype(np.float32).reshape(lanes, geo.n_kv, geo.head_dim)
+    for i, p in enumerate(pos):
+        assert np.array_equal(vc[0][i, :, p], want_v[i])
