@@ -13,6 +13,7 @@
 //   output conv         tanh in the epilogue
 // Every tensor stored is one the unfused chain would store (f16), so the arithmetic matches the
 // composed form up to summation order.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -23,7 +24,18 @@
 struct dtts_codec {
     dtts_codec_geometry geo;
     dtts_codec_weights w;
-    bool f32;  // made by dtts_codec_create_f32: every tensor f32, every conv the f32 kernel
+    bool f32;  // made by dtts_codec_create_f32: every tensor and sum at f32 accuracy
+    // An f32 codec whose convs all fit the split tiles runs them on the f16 matrix cores with
+    // split operands (conv_split.hip): activations stored as f16 hi/lo pairs, each conv weight
+    // converted once here. Otherwise (or with DTTS_F32_CODEC_KERNEL=f32 set at create) every
+    // tensor is plain f32 and every conv the f32 matrix-core kernel.
+    bool split = false;
+    struct SplitW {
+        const void *src;      // the caller's f32 weight
+        dtts::half_t *w3;     // [cout, k * 3 cin]
+        float inv;            // 2^-s
+    };
+    std::vector<SplitW> splitw;
     // A decode runs its lanes as two halves, one on the caller's stream and one on `side`, forked
     // and joined with the two events: each launch of one half fills the ramp and tail of the
     // other's (measured: 19.58 -> 19.06 ms for config 5).
@@ -51,8 +63,9 @@ inline bool stores_snaked(bool f32, int64_t cout) { return f32 || cout > kStoreS
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-int64_t stage_elems(const dtts_codec_geometry &g, int64_t frames) {
+int64_t stage_elems(const dtts_codec_geometry &g, int64_t frames, bool split = false) {
     int64_t m = frames * g.channels[0];
+    if (split && frames * g.latent_dim > m) m = frames * g.latent_dim;  // the latent, split
     int64_t len = frames;
     for (int64_t i = 0; i < g.n_blocks; ++i) {
         len *= g.rates[i];
@@ -92,6 +105,62 @@ using dtts::set_error;
 
 namespace dtts {
 namespace {
+// Every conv of an f32 codec as (weight, cin, cout, k, dilation), the output conv excluded.
+template <typename F>
+void for_each_conv(const dtts_codec_geometry &g, const dtts_codec_weights &w, F &&f) {
+    f(w.head_w, g.latent_dim, g.channels[0], g.head_kernel, int64_t(1));
+    for (int64_t i = 0; i < g.n_blocks; ++i) {
+        const int64_t cin = g.channels[i], cout = g.channels[i + 1];
+        f(w.blocks[i].up_w, cin, g.rates[i] * cout, int64_t(2), int64_t(1));
+        for (int j = 0; j < 3; ++j) {
+            f(w.blocks[i].units[j].conv1_w, cout, cout, g.ru_kernel, g.ru_dilations[j]);
+            f(w.blocks[i].units[j].conv2_w, cout, cout, int64_t(1), int64_t(1));
+        }
+    }
+}
+
+// Converts an f32 codec's conv weights to the split form when every conv (and the output conv's
+// split-input window kernel) takes its shape; leaves c->split false otherwise.
+int split_codec_weights(dtts_codec *c) {
+    const char *env = std::getenv("DTTS_F32_CODEC_KERNEL");
+    if (env && std::strcmp(env, "f32") == 0) return DTTS_OK;
+    const dtts_codec_geometry &g = c->geo;
+    bool ok = g.latent_dim % 8 == 0;
+    for_each_conv(g, c->w, [&](const void *, int64_t cin, int64_t cout, int64_t k, int64_t dil) {
+        ok = ok && conv_split_supported(1, 1, cin, cout, k, dil);
+    });
+    dtts_conv_desc od{};
+    od.lanes = od.len = 1;
+    od.cin = g.channels[g.n_blocks];
+    od.cout = 1;
+    od.k = g.out_kernel;
+    od.dilation = 1;
+    od.x = reinterpret_cast<const void *>(uintptr_t(256));  // at decode: a workspace buffer (256-byte aligned)
+    ok = ok && conv_f32_narrow_split_eligible(&od);
+    if (!ok) return DTTS_OK;
+    int rc = DTTS_OK;
+    for_each_conv(g, c->w, [&](const void *w, int64_t cin, int64_t cout, int64_t k, int64_t) {
+        if (rc != DTTS_OK) return;
+        dtts_codec::SplitW sw{w, nullptr, 1.0f};
+        const hipError_t e = hipMalloc(&sw.w3, sizeof(half_t) * static_cast<size_t>(3 * k * cin * cout));
+        if (e != hipSuccess) {
+            set_error("dtts_codec_create_f32: %s", hipGetErrorString(e));
+            rc = DTTS_ERR_HIP;
+            return;
+        }
+        c->splitw.push_back(sw);
+        rc = split_weight(static_cast<const float *>(w), cout, k, cin, sw.w3, c->splitw.back().inv, nullptr);
+    });
+    if (rc == DTTS_OK) c->split = true;
+    return rc;
+}
+
+const dtts_codec::SplitW *split_of(const dtts_codec *c, const void *w) {
+    for (const auto &sw : c->splitw)
+        if (sw.src == w) return &sw;
+    return nullptr;
+}
+
 int codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, bool f32, dtts_codec **out) {
     DTTS_REQUIRE(geo && w && out, "dtts_codec_create: null argument");
     *out = nullptr;
@@ -130,6 +199,13 @@ int codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *w, bo
             dtts_codec_destroy(c);
             set_error("dtts_codec_create: %s", hipGetErrorString(e));
             return DTTS_ERR_HIP;
+        }
+    }
+    if (f32) {
+        int rc = split_codec_weights(c);
+        if (rc != DTTS_OK) {
+            dtts_codec_destroy(c);
+            return rc;
         }
     }
     for (int64_t i = 0; i < g.n_blocks; ++i) {
@@ -179,6 +255,8 @@ extern "C" void dtts_codec_destroy(dtts_codec *c) {
         if (p) (void)hipFree(p);
     for (float *p : c->phase_brecip)
         if (p) (void)hipFree(p);
+    for (const auto &sw : c->splitw)
+        if (sw.w3) (void)hipFree(sw.w3);
     delete c;
 }
 
@@ -192,7 +270,7 @@ namespace {
 size_t plan_bytes(const dtts_codec *c, int64_t lanes, int64_t frames) {
     if (lanes <= 0) return 0;
     const size_t esize = c->f32 ? 4 : 2;
-    return 4 * round_up(static_cast<size_t>(lanes * stage_elems(c->geo, frames)) * esize, 256);
+    return 4 * round_up(static_cast<size_t>(lanes * stage_elems(c->geo, frames, c->split)) * esize, 256);
 }
 // The decode's two halves: lanes [0, first) and [first, lanes).
 int64_t first_half(int64_t lanes) { return (lanes + 1) / 2; }
@@ -211,14 +289,50 @@ namespace {
 
 struct Stage {
     bool ru;           // a fused residual unit (r) rather than one conv (d)
+    bool split_in;     // split codec: the latent (d.x, f32) stored split at d.y (rows lanes * len, d.cin wide)
     dtts_conv_desc d;
     dtts_ru_desc r;
+    int64_t cv;        // channels of the output's rows: d.cout, or cout / rate for a TransConv
     char name[32];
 };
 
-int run_stage(const Stage &st, bool f32, hipStream_t stream) {
+int run_stage(const Stage &st, const dtts_codec *c, hipStream_t stream) {
     if (st.ru) return residual_unit_nlc_f16(&st.r, stream);
-    return f32 ? conv1d_nlc_f32(&st.d, stream) : conv1d_nlc_f16(&st.d, stream);
+    if (!c->split) return c->f32 ? conv1d_nlc_f32(&st.d, stream) : conv1d_nlc_f16(&st.d, stream);
+    const dtts_conv_desc &d = st.d;
+    if (st.split_in)
+        return split_activations(static_cast<const float *>(d.x), static_cast<half_t *>(d.y), d.lanes * d.len, d.cin,
+                                 stream);
+    if (d.cout == 1) return conv1d_nlc_f32_narrow_split(&d, stream);
+    const dtts_codec::SplitW *sw = split_of(c, d.w);
+    DTTS_REQUIRE(sw, "dtts_codec (split): a conv weight was not converted at create");
+    SplitConv s{};
+    s.lanes = d.lanes;
+    s.len = d.len;
+    s.cs = d.cin;
+    s.cout = d.cout;
+    s.k = d.k;
+    s.dil = d.dilation;
+    s.pad_left = d.pad_left;
+    s.cv = st.cv;
+    s.x = static_cast<const half_t *>(d.x);
+    s.w = sw->w3;
+    s.w_inv = sw->inv;
+    s.bias = static_cast<const float *>(d.bias);
+    s.res = static_cast<const half_t *>(d.residual);
+    s.y_pre = static_cast<half_t *>(d.y_pre);
+    s.y = static_cast<half_t *>(d.y);
+    s.a_out = d.out_alpha;
+    s.r_out = d.out_brecip;
+    return conv1d_nlc_split(s, stream);
+}
+
+const char *stage_kernel_name(const Stage &st, const dtts_codec *c) {
+    if (st.ru) return residual_unit_kernel_name(&st.r);
+    if (!c->split) return c->f32 ? conv_f32_kernel_name(&st.d) : conv_kernel_name(&st.d);
+    if (st.split_in) return "split_act_kernel";
+    if (st.d.cout == 1) return "conv_nlc_f32_narrow<true>";
+    return conv_split_kernel_name(st.d.lanes, st.d.len, st.d.cin, st.d.cout, st.d.k, st.d.dilation);
 }
 
 // The decode of `lanes` lanes as a list of conv launches over four buffers of one plan's
@@ -235,9 +349,10 @@ int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lan
             if (p != a && p != b && p != d) return p;
         return nullptr;
     };
-    auto push = [&](const dtts_conv_desc &d, const char *fmt, long long a, long long b) {
+    auto push = [&](const dtts_conv_desc &d, const char *fmt, long long a, long long b, int64_t cv = 0) {
         Stage st{};
         st.d = d;
+        st.cv = cv > 0 ? cv : d.cout;
         snprintf(st.name, sizeof(st.name), fmt, a, b);
         plan.push_back(st);
     };
@@ -251,6 +366,16 @@ int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lan
 
     // head conv, then block 0's SnakeBeta in the epilogue
     char *x = buf[0];
+    if (c->split) {  // the latent, stored split for the head conv
+        char *lat = pick(x, nullptr, nullptr);
+        Stage st{};
+        st.split_in = true;
+        st.d = desc(lanes, frames, g.latent_dim, g.latent_dim, 1, 1, latent, nullptr, nullptr, lat);
+        st.cv = g.latent_dim;
+        snprintf(st.name, sizeof(st.name), "latent");
+        plan.push_back(st);
+        latent = lat;
+    }
     {
         dtts_conv_desc d = desc(lanes, frames, g.latent_dim, g.channels[0], g.head_kernel, 1, latent, w.head_w, w.head_b, x);
         d.out_alpha = w.blocks[0].act_alpha;
@@ -290,7 +415,7 @@ int build_plan(const dtts_codec *c, const void *latent, void *audio, int64_t lan
                 d.out_alpha = c->phase_alpha[i];
                 d.out_brecip = c->phase_brecip[i];
             }
-            push(d, "block%lld.up%.0lld", (long long)i, 0);
+            push(d, "block%lld.up%.0lld", (long long)i, 0, cout);
         }
         len *= rate;
         for (int j = 0; j < 3 && fused; ++j) {
@@ -403,7 +528,7 @@ int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *la
     if (rc != DTTS_OK) return rc;
     if (b.empty()) {
         for (const Stage &st : a)
-            if ((rc = run_stage(st, c->f32, stream)) != DTTS_OK) return rc;
+            if ((rc = run_stage(st, c, stream)) != DTTS_OK) return rc;
         return DTTS_OK;
     }
     std::lock_guard<std::mutex> hold(c->split_lock);
@@ -411,8 +536,8 @@ int codec_decode(const char *name, const dtts_codec *c, bool f32, const void *la
     DTTS_HIP_CHECK(hipEventRecord(c->fork, stream), name);
     DTTS_HIP_CHECK(hipStreamWaitEvent(c->side, c->fork, 0), name);
     for (size_t i = 0; i < a.size() && rc == DTTS_OK; ++i) {
-        rc = run_stage(a[i], c->f32, stream);
-        if (rc == DTTS_OK) rc = run_stage(b[i], c->f32, c->side);
+        rc = run_stage(a[i], c, stream);
+        if (rc == DTTS_OK) rc = run_stage(b[i], c, c->side);
     }
     // join, whatever was enqueued: the caller's stream then orders after all of the side's work
     const hipError_t e1 = hipEventRecord(c->join, c->side);
@@ -452,7 +577,7 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const void *latent, void 
     int status = DTTS_OK;
     hipError_t he = hipEventRecord(ev[0], stream);
     for (size_t i = 0; i < plan.size() && he == hipSuccess && status == DTTS_OK; ++i) {
-        status = dtts::run_stage(plan[i], c->f32, stream);
+        status = dtts::run_stage(plan[i], c, stream);
         if (status == DTTS_OK) he = hipEventRecord(ev[i + 1], stream);
     }
     if (he == hipSuccess && status == DTTS_OK) he = hipEventSynchronize(ev.back());
@@ -473,7 +598,7 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const void *latent, void 
             s.bytes = 2.0 * r.lanes * r.len * c * (r.y_pre ? 3.0 : 2.0) + 2.0 * c * c * (r.k + 1);
         } else {
             const dtts_conv_desc &d = plan[i].d;
-            snprintf(s.kernel, sizeof(s.kernel), "%s", c->f32 ? dtts::conv_f32_kernel_name(&d) : dtts::conv_kernel_name(&d));
+            snprintf(s.kernel, sizeof(s.kernel), "%s", dtts::stage_kernel_name(plan[i], c));
             s.lanes = d.lanes;
             s.len = d.len;
             s.cin = d.cin;
@@ -484,6 +609,10 @@ extern "C" int dtts_codec_profile(const dtts_codec *c, const void *latent, void 
             const double outs = (d.y_pre ? 2.0 : 1.0) + (d.residual ? 1.0 : 0.0);
             const double es = c->f32 ? 4.0 : 2.0;
             s.bytes = es * d.lanes * d.len * (d.cin + d.cout * outs) + es * d.cout * d.k * d.cin;
+            if (plan[i].split_in) {  // a conversion: f32 in, the split pair out
+                s.flops = 0.0;
+                s.bytes = 8.0 * d.lanes * d.len * d.cin;
+            }
         }
         he = hipEventElapsedTime(&s.ms, ev[i], ev[i + 1]);
     }

@@ -272,6 +272,9 @@ constexpr int kNarrowBM = 256, kNarrowKC = 32, kNarrowPitch = kNarrowKC + 4, kNa
 constexpr int kNarrowRows = kNarrowBM + kNarrowMaxHalo;
 constexpr int kNarrowVec = (kNarrowRows * (kNarrowKC / 4) + 255) / 256;  // window float4s per thread, at most
 
+// SPLIT: x holds rows [hi(cin) | lo(cin)] of f16 (an f32 codec's split storage), each value read
+// as hi + lo in f32.
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
     __shared__ __attribute__((aligned(16))) float win[kNarrowRows * kNarrowPitch];
     __shared__ __attribute__((aligned(16))) float wsh[7 * kNarrowKC];
@@ -280,7 +283,7 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
     const int l0 = (tile - lane_idx * p.tiles_m) * kNarrowBM;
     const int rows = kNarrowBM + (p.k - 1) * p.dil;
     const int nvec = rows * (kNarrowKC / 4);
-    const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;
+    const float *xl = p.x + static_cast<int64_t>(lane_idx) * p.L * p.cin;  // f32 rows (SPLIT: the same byte count)
     const int tid = threadIdx.x;
     float acc = 0.0f;
     for (int c0 = 0; c0 < p.cin; c0 += kNarrowKC) {
@@ -291,8 +294,17 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
             buf[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
             const int r = v >> 3, q = v & 7;
             const int s = l0 - p.pad_left + r;
-            if (v < nvec && s >= 0 && s < p.L)
-                buf[i] = *reinterpret_cast<const float4_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + q * 4);
+            if (v < nvec && s >= 0 && s < p.L) {
+                if constexpr (SPLIT) {
+                    const half_t *hr = reinterpret_cast<const half_t *>(xl) + static_cast<int64_t>(s) * 2 * p.cin + c0 + q * 4;
+                    const half4_t h = *reinterpret_cast<const half4_t *>(hr);
+                    const half4_t lo = *reinterpret_cast<const half4_t *>(hr + p.cin);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) buf[i][j] = static_cast<float>(h[j]) + static_cast<float>(lo[j]);
+                } else {
+                    buf[i] = *reinterpret_cast<const float4_t *>(xl + static_cast<int64_t>(s) * p.cin + c0 + q * 4);
+                }
+            }
         }
         if (c0 > 0) __syncthreads();  // every thread is done with the previous chunk's window
         if (tid < p.k * kNarrowKC) {
@@ -443,7 +455,7 @@ int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
     if (nlc_f32_narrow(d)) {
         p.tiles_m = static_cast<int>((d->len + kNarrowBM - 1) / kNarrowBM);
         DTTS_REQUIRE(d->lanes * p.tiles_m < (int64_t(1) << 31), "%s: too many tiles", name);
-        conv_nlc_f32_narrow<<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
+        conv_nlc_f32_narrow<false><<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
         e = hipGetLastError();
     } else if (nlc_f32_tiled(d)) {
         DTTS_REQUIRE(d->lanes * (d->cout / f32_tile_bn(d->cout)) * ((d->len + 127) / 128) < (int64_t(1) << 31),
@@ -465,6 +477,39 @@ int conv1d_nlc_f32(const dtts_conv_desc *d, hipStream_t stream) {
         e = hipGetLastError();
     }
     DTTS_HIP_CHECK(e, name);
+    return DTTS_OK;
+}
+
+bool conv_f32_narrow_split_eligible(const dtts_conv_desc *d) { return d && nlc_f32_narrow(d); }
+
+int conv1d_nlc_f32_narrow_split(const dtts_conv_desc *d, hipStream_t stream) {
+    const char *name = "dtts_codec (split output conv)";
+    DTTS_REQUIRE(conv_f32_narrow_split_eligible(d) && d->lanes > 0 && d->len > 0 && d->w && d->y,
+                 "%s: shape not supported", name);
+    DTTS_REQUIRE(d->act == 0 || d->act == 1 || d->act == 3, "%s: act %d unknown", name, d->act);
+    NlcF32Params p{};
+    p.x = static_cast<const float *>(d->x);
+    p.w = static_cast<const float *>(d->w);
+    p.bias = static_cast<const float *>(d->bias);
+    p.a_in = d->in_alpha;
+    p.r_in = d->in_brecip;
+    p.res = static_cast<const float *>(d->residual);
+    p.scale = d->out_scale;
+    p.y_pre = static_cast<float *>(d->y_pre);
+    p.y = static_cast<float *>(d->y);
+    p.a_out = d->out_alpha;
+    p.r_out = d->out_brecip;
+    p.L = static_cast<int>(d->len);
+    p.cin = static_cast<int>(d->cin);
+    p.cout = 1;
+    p.k = static_cast<int>(d->k);
+    p.dil = static_cast<int>(d->dilation);
+    p.pad_left = static_cast<int>(d->pad_left);
+    p.act = d->act;
+    p.tiles_m = static_cast<int>((d->len + kNarrowBM - 1) / kNarrowBM);
+    DTTS_REQUIRE(d->lanes * p.tiles_m < (int64_t(1) << 31), "%s: too many tiles", name);
+    conv_nlc_f32_narrow<true><<<static_cast<unsigned>(d->lanes * p.tiles_m), 256, 0, stream>>>(p);
+    DTTS_LAUNCH_CHECK(name);
     return DTTS_OK;
 }
 

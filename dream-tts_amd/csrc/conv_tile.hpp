@@ -399,9 +399,14 @@ __device__ __forceinline__ void conv_mainloop_regs(const ConvArgs &p, const half
 }
 
 // acc += window(x) . w over all taps for the workgroup's BM x BN tile, direct staging.
-template <typename Cfg, bool SNAKE_IN, int KT>
+// SPLIT: x holds f32 values as f16 pairs, each row [hi(cs) | lo(cs)] with cs = cin / 3, and the
+// reduction runs over K' = 3 cs channels per tap: chunks of the first third read hi, of the
+// second lo, of the third hi again, against weights [w_hi | w_hi | w_lo] (so the sum is
+// xh.wh + xl.wh + xh.wl); only the window's source offset changes.
+template <typename Cfg, bool SNAKE_IN, int KT, bool SPLIT = false>
 __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const half_t *xl, int l0, int n0, char *smem,
                                                      float16_t (&acc)[Cfg::TM][Cfg::TN]) {
+    static_assert(!(SPLIT && SNAKE_IN), "split operands take no prologue SnakeBeta");
     constexpr int RB = Cfg::ROW_BYTES;
     constexpr int SEGS = Cfg::SEGS;
     const int tid = threadIdx.x;
@@ -411,10 +416,14 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
     const int rows = Cfg::BM + (p.k - 1) * p.dil;
     const int win0 = l0 - p.pad_left;
     const int K = p.k * p.cin;
+    const int cs = SPLIT ? p.cin / 3 : p.cin;    // channels of a stored row (per half when SPLIT)
+    const int x_ld = SPLIT ? 2 * cs : p.cin;     // halves per stored row
+    // the stored offset of K' chunk c0: hi for the first and third thirds, lo for the second
+    auto x_off = [&](int c0) { return SPLIT && c0 >= 2 * cs ? c0 - 2 * cs : c0; };
     const int a_inst = (rows + Cfg::RPI - 1) / Cfg::RPI;
     const int b_inst = (KT > 0 ? KT : p.k) * Cfg::BN / Cfg::RPI;
     const __amdgpu_buffer_rsrc_t rsa =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(xl), 0, p.L * p.cin * 2, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(xl), 0, p.L * x_ld * 2, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rsb =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(p.w), 0, p.cout * K * 2, kBufferWord3);
 
@@ -428,7 +437,7 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
         const int r = slot / SEGS;
         const int q = (slot % SEGS) ^ seg_swizzle<Cfg::KC>(r);
         const int s = win0 + r;
-        va[i] = (r < rows && s >= 0 && s < p.L) ? static_cast<uint32_t>((s * p.cin + q * 8) * 2) : kOutOfRange;
+        va[i] = (r < rows && s >= 0 && s < p.L) ? static_cast<uint32_t>((s * x_ld + q * 8) * 2) : kOutOfRange;
     }
 #pragma unroll
     for (int i = 0; i < Cfg::B_PER_W; ++i) {
@@ -442,10 +451,11 @@ __device__ __forceinline__ void conv_mainloop_direct(const ConvArgs &p, const ha
     auto issue = [&](int c0, int st) {
         char *base = smem + st * Cfg::STAGE_BYTES;
         const uint32_t so = static_cast<uint32_t>(c0 * 2);
+        const uint32_t sx = static_cast<uint32_t>(x_off(c0) * 2);
 #pragma unroll
         for (int i = 0; i < Cfg::A_PER_W; ++i) {
             const int j = wave + i * Cfg::NW;
-            if (j < a_inst) load_lds_16(rsa, base + j * 1024, va[i], so);
+            if (j < a_inst) load_lds_16(rsa, base + j * 1024, va[i], sx);
         }
 #pragma unroll
         for (int i = 0; i < Cfg::B_PER_W; ++i) {

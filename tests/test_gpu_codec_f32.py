@@ -68,7 +68,10 @@ def test_f32_and_f16_codecs_refuse_each_others_decode(dev):
              1, 4, ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(need), None)
 
 
-def test_f32_codec_profile_names_the_f32_kernels(dev):
+def test_f32_codec_profile_names_the_split_kernels(dev):
+    """The f32 codec runs its convs on the f16 matrix cores with split operands: a stage storing
+    the latent split, every conv on conv_split_mfma, the output conv on the f32 window kernel
+    reading split input; profiled launches give the decode's audio bit for bit."""
     geo = SMALL
     model = codec.Codec(geo, _weights(geo, 13), dev, dtype="f32")
     latent = to_dev(synth.normal(13, "latent", (2, 8, geo.latent_dim)), dev)
@@ -76,6 +79,26 @@ def test_f32_codec_profile_names_the_f32_kernels(dev):
     audio = torch.empty((2, 8 * geo.hop), dtype=torch.float32, device=dev)
     stages = model.profile(latent, out=audio)
     assert np.array_equal(to_host(audio), ref)
-    assert len(stages) == 2 + sum(1 + 6 for _ in geo.channels[1:])  # every residual unit as two convs
-    assert all("f32" in s["kernel"] for s in stages)
+    assert len(stages) == 3 + sum(1 + 6 for _ in geo.channels[1:])  # every residual unit as two convs
+    assert stages[0]["kernel"] == "split_act_kernel" and stages[-1]["kernel"] == "conv_nlc_f32_narrow<true>"
+    assert all(s["kernel"].startswith("conv_split_mfma<") for s in stages[1:-1])
     assert sum(s["flops"] for s in stages) == pytest.approx(2 * 8 * geo.flops_per_frame(), rel=1e-9)
+
+
+def test_split_and_f32_kernels_agree(dev, monkeypatch):
+    """The split-operand codec against the plain-f32 one (DTTS_F32_CODEC_KERNEL=f32 at create: f32
+    tensors, f32 matrix cores): both f32-accurate, so they differ by f32 summation order and the
+    dropped lo.lo products (~2^-22 of each term), amplified by the SnakeBeta chain; bar 1e-4 of the
+    audio's scale (the codec.wav gate is 5e-3)."""
+    geo = SMALL
+    w = _weights(geo, 14)
+    latent = to_dev(synth.normal(14, "latent", (3, 24, geo.latent_dim)), dev)
+    split = codec.Codec(geo, w, dev, dtype="f32")
+    monkeypatch.setenv("DTTS_F32_CODEC_KERNEL", "f32")
+    plain = codec.Codec(geo, w, dev, dtype="f32")
+    a, b = to_host(split.decode(latent)), to_host(plain.decode(latent))
+    assert "conv_split_mfma" in split.profile(latent)[1]["kernel"]
+    assert "conv_nlc_f32_mfma" in plain.profile(latent)[1]["kernel"]
+    d = float(np.max(np.abs(a - b)))
+    print(f"max|split - f32| {d:.2e}, audio max {np.max(np.abs(b)):.3f}")
+    assert d <= 1e-4 * max(1.0, float(np.max(np.abs(b))))
