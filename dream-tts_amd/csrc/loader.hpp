@@ -23,6 +23,8 @@ struct Build {
     char *raw = nullptr;         // second pass: device copy of the file's byte buffer
     const char *host0 = nullptr; // first byte of the file's byte buffer (host mapping)
     size_t used = 0;
+    char *q8tmp = nullptr;            // second pass: GGML blocks of one projection before its repack
+    size_t q8max = 0;                 // first pass: the largest such staging
     std::unordered_set<size_t> sent;  // byte offsets of the raw tensors uploaded
     int rc = DTTS_OK;
 

@@ -17,8 +17,42 @@ struct dtts_stack_model {
 namespace dtts {
 namespace {
 
-void stack_plan(Build &b, const std::string &prefix, const dtts_stack_geometry &g, dtts_stack_layer *layers,
-                const float *&final_norm) {
+// A projection of the stack's weight kind, built from one or more [rows, cols] source tensors
+// stacked along rows (Layer::load's q|k|v cat, gate|up): f16 or f32 rows converted in place; Q8_0
+// rows quantized into a staging buffer of GGML blocks (QTensor::quantize_onto, bit for bit the
+// host quantizer) and repacked into the arena once the projection is whole.
+struct Proj {
+    Build &b;
+    int32_t how;
+    int64_t rows, cols;
+    void *dst = nullptr;
+    Proj(Build &b_, int32_t how_, int64_t rows_, int64_t cols_) : b(b_), how(how_), rows(rows_), cols(cols_) {
+        if (how == DTTS_WEIGHT_F16) dst = b.alloc<dtts_f16>(rows * cols);
+        else if (how == DTTS_WEIGHT_F32) dst = b.alloc<float>(rows * cols);
+        else {
+            dst = b.alloc<uint8_t>(static_cast<int64_t>(dtts_q8_0_packed_bytes(rows, cols)));
+            const size_t staging = static_cast<size_t>(rows * (cols / 32) * 34);
+            if (staging > b.q8max) b.q8max = staging;
+        }
+    }
+    void put(const dtts_tensor_info &t, int64_t row0, int64_t n) {
+        if (b.dry || b.rc != DTTS_OK) return;
+        if (how == DTTS_WEIGHT_F16)
+            b.rows_into(t, static_cast<dtts_f16 *>(dst), row0, n, cols);
+        else if (how == DTTS_WEIGHT_F32)
+            b.ok(dtts_convert_f32(b.src(t), t.dtype, static_cast<float *>(dst) + row0 * cols, n * cols, b.stream));
+        else
+            b.ok(dtts_convert_q8_0(b.src(t), t.dtype, b.q8tmp + row0 * (cols / 32) * 34, n, cols, b.stream));
+    }
+    const void *done() {
+        if (!b.dry && b.rc == DTTS_OK && how != DTTS_WEIGHT_F16 && how != DTTS_WEIGHT_F32)
+            b.ok(dtts_q8_0_repack(b.q8tmp, dst, rows, cols, b.stream));
+        return dst;
+    }
+};
+
+void stack_plan(Build &b, const std::string &prefix, const dtts_stack_geometry &g, int32_t how,
+                dtts_stack_layer *layers, const float *&final_norm) {
     dtts_tensor_info t;
     const int64_t D = g.head_dim, qw = g.heads * D, kvw = g.n_kv * D, dim = g.dim;
     // q's norm weight times 1/sqrt(head_dim) in f32, as the host path folds it
@@ -30,24 +64,28 @@ void stack_plan(Build &b, const std::string &prefix, const dtts_stack_geometry &
         L.attn_norm = b.f32(t, dim);
         if (!b.need(p + "post_attention_layernorm.weight", {dim}, t)) return;
         L.ffn_norm = b.f32(t, dim);
-        dtts_f16 *qkv = b.alloc<dtts_f16>((qw + 2 * kvw) * dim);
+        Proj qkv(b, how, qw + 2 * kvw, dim);
         if (!b.need(p + "self_attn.q_proj.weight", {qw, dim}, t)) return;
-        b.rows_into(t, qkv, 0, qw, dim);
+        qkv.put(t, 0, qw);
         if (!b.need(p + "self_attn.k_proj.weight", {kvw, dim}, t)) return;
-        b.rows_into(t, qkv, qw, kvw, dim);
+        qkv.put(t, qw, kvw);
         if (!b.need(p + "self_attn.v_proj.weight", {kvw, dim}, t)) return;
-        b.rows_into(t, qkv, qw + kvw, kvw, dim);
-        L.wqkv = qkv;
+        qkv.put(t, qw + kvw, kvw);
+        L.wqkv = qkv.done();
+        Proj wo(b, how, dim, qw);
         if (!b.need(p + "self_attn.o_proj.weight", {dim, qw}, t)) return;
-        L.wo = b.f16(t, dim * qw);
-        dtts_f16 *gu = b.alloc<dtts_f16>(2 * g.ffn * dim);
+        wo.put(t, 0, dim);
+        L.wo = wo.done();
+        Proj gu(b, how, 2 * g.ffn, dim);
         if (!b.need(p + "mlp.gate_proj.weight", {g.ffn, dim}, t)) return;
-        b.rows_into(t, gu, 0, g.ffn, dim);
+        gu.put(t, 0, g.ffn);
         if (!b.need(p + "mlp.up_proj.weight", {g.ffn, dim}, t)) return;
-        b.rows_into(t, gu, g.ffn, g.ffn, dim);
-        L.w_gateup = gu;
+        gu.put(t, g.ffn, g.ffn);
+        L.w_gateup = gu.done();
+        Proj down(b, how, dim, g.ffn);
         if (!b.need(p + "mlp.down_proj.weight", {dim, g.ffn}, t)) return;
-        L.wdown = b.f16(t, dim * g.ffn);
+        down.put(t, 0, dim);
+        L.wdown = down.done();
         L.qk_norms = nullptr;
         if (g.qk_norm) {
             float *qk = b.alloc<float>(2 * D);
@@ -74,19 +112,30 @@ void stack_plan(Build &b, const std::string &prefix, const dtts_stack_geometry &
 
 extern "C" int dtts_stack_model_load(const dtts_checkpoint *ck, const char *prefix, const dtts_stack_geometry *geo,
                                      hipStream_t stream, dtts_stack_model **out) {
+    return dtts_stack_model_load_as(ck, prefix, geo, DTTS_WEIGHT_F16, stream, out);
+}
+
+extern "C" int dtts_stack_model_load_as(const dtts_checkpoint *ck, const char *prefix, const dtts_stack_geometry *geo,
+                                        int32_t how, hipStream_t stream, dtts_stack_model **out) {
     const char *name = "dtts_stack_model_load";
     DTTS_REQUIRE(ck && prefix && geo && out, "%s: null argument", name);
     *out = nullptr;
     DTTS_REQUIRE(geo->layers > 0 && geo->layers <= 1024 && geo->dim > 0 && geo->heads > 0 && geo->n_kv > 0 &&
                      geo->head_dim > 0 && geo->ffn > 0,
                  "%s: bad geometry", name);
+    DTTS_REQUIRE(how == DTTS_WEIGHT_F16 || how == DTTS_WEIGHT_F32 || how == DTTS_WEIGHT_Q8_0 ||
+                     how == DTTS_WEIGHT_Q8_0_A32,
+                 "%s: weight kind %d unknown", name, how);
+    if (how == DTTS_WEIGHT_Q8_0 || how == DTTS_WEIGHT_Q8_0_A32)
+        DTTS_REQUIRE(geo->dim % 256 == 0 && (geo->heads * geo->head_dim) % 256 == 0 && geo->ffn % 256 == 0,
+                     "%s: Q8_0 layers need dim, heads*head_dim and ffn multiples of 256", name);
     std::vector<dtts_stack_layer> layers(static_cast<size_t>(geo->layers));
     const float *final_norm = nullptr;
     dtts::Build b;
     b.who = name;
     b.ck = ck;
     b.stream = stream;
-    dtts::stack_plan(b, prefix, *geo, layers.data(), final_norm);
+    dtts::stack_plan(b, prefix, *geo, how, layers.data(), final_norm);
     if (b.rc != DTTS_OK) return b.rc;
     dtts_stack_model *m = new (std::nothrow) dtts_stack_model();
     DTTS_REQUIRE(m, "%s: out of host memory", name);
@@ -95,25 +144,29 @@ extern "C" int dtts_stack_model_load(const dtts_checkpoint *ck, const char *pref
     const size_t raw_bytes = dtts::Build::raw_span(ck, host0);
     hipError_t e = hipMalloc(&m->arena, m->bytes);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&b.raw), raw_bytes ? raw_bytes : 1);
+    if (e == hipSuccess && b.q8max) e = hipMalloc(reinterpret_cast<void **>(&b.q8tmp), b.q8max);
     if (e != hipSuccess) {
         if (b.raw) (void)hipFree(b.raw);
+        if (b.q8tmp) (void)hipFree(b.q8tmp);
         dtts_stack_model_destroy(m);
-        dtts::set_error("%s: allocating %zu + %zu bytes: %s", name, b.used, raw_bytes, hipGetErrorString(e));
+        dtts::set_error("%s: allocating %zu + %zu + %zu bytes: %s", name, b.used, raw_bytes, b.q8max,
+                        hipGetErrorString(e));
         return DTTS_ERR_HIP;
     }
     b.dry = false;
     b.arena = static_cast<char *>(m->arena);
     b.host0 = host0;
     b.used = 0;
-    dtts::stack_plan(b, prefix, *geo, layers.data(), final_norm);
+    dtts::stack_plan(b, prefix, *geo, how, layers.data(), final_norm);
     e = hipStreamSynchronize(stream);
     (void)hipFree(b.raw);
+    if (b.q8tmp) (void)hipFree(b.q8tmp);
     int rc = b.rc;
     if (rc == DTTS_OK && e != hipSuccess) {
         dtts::set_error("%s: %s", name, hipGetErrorString(e));
         rc = DTTS_ERR_HIP;
     }
-    if (rc == DTTS_OK) rc = dtts_stack_create(geo, layers.data(), final_norm, &m->stack);
+    if (rc == DTTS_OK) rc = dtts_stack_create_as(geo, layers.data(), final_norm, how, &m->stack);
     if (rc != DTTS_OK) {
         dtts_stack_model_destroy(m);
         return rc;

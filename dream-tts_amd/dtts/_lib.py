@@ -96,6 +96,7 @@ SIGNATURES = {
     "dtts_codec_model_bytes": [_P],
     "dtts_convert_f32_scaled": [_P, _I32, _P, _I64, _F32, _P],
     "dtts_stack_model_load": [_P, ctypes.c_char_p, _P, _P, _P],
+    "dtts_stack_model_load_as": [_P, ctypes.c_char_p, _P, _I32, _P, _P],
     "dtts_stack_model_destroy": [_P],
     "dtts_stack_model_stack": [_P],
     "dtts_stack_model_bytes": [_P],

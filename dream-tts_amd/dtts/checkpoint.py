@@ -147,17 +147,18 @@ class StackModel:
     """Stack::load: a decoder stack's weights converted from a checkpoint into one device arena;
     `.stack` decodes like a dtts.stack.Stack."""
 
-    def __init__(self, ck: Checkpoint, prefix: str, geo: stack.Geometry, dev):
+    def __init__(self, ck: Checkpoint, prefix: str, geo: stack.Geometry, dev, weight: str = "f16"):
         self._g = stack.c_geometry(geo)
         h = ctypes.c_void_p()
-        args = (ck.handle, prefix.encode(), ctypes.byref(self._g))
+        args = (ck.handle, prefix.encode(), ctypes.byref(self._g), stack.WEIGHTS[weight])
         if dev is None:
-            call("dtts_stack_model_load", *args, ctypes.c_void_p(), ctypes.byref(h))
+            call("dtts_stack_model_load_as", *args, ctypes.c_void_p(), ctypes.byref(h))
         else:
             with torch.cuda.device(dev):
-                call("dtts_stack_model_load", *args, stream_handle(dev), ctypes.byref(h))
+                call("dtts_stack_model_load_as", *args, stream_handle(dev), ctypes.byref(h))
         self.handle, self.dev = h, dev
         self.stack = stack.Stack.from_handle(geo, ctypes.c_void_p(lib().dtts_stack_model_stack(h)), dev, self)
+        self.stack.weight = weight
 
     @property
     def nbytes(self):

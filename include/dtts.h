@@ -856,6 +856,12 @@ size_t dtts_codec_model_bytes(const dtts_codec_model *model); /* the arena's siz
 typedef struct dtts_stack_model dtts_stack_model;
 int dtts_stack_model_load(const dtts_checkpoint *ck, const char *prefix, const dtts_stack_geometry *geo,
                           hipStream_t stream, dtts_stack_model **out);
+/* Stack::load with its `how` (DTTS_WEIGHT_*; dtts_stack_model_load is DTTS_WEIGHT_F16): projections
+ * converted to f32, or quantized on the device to Q8_0 as QTensor::quantize_onto does
+ * (crates/tts-nn/src/lib.rs:480-486; bit for bit the host quantizer) and repacked; the stack is
+ * created with that kind (f32 caches for all but F16). */
+int dtts_stack_model_load_as(const dtts_checkpoint *ck, const char *prefix, const dtts_stack_geometry *geo,
+                             int32_t how, hipStream_t stream, dtts_stack_model **out);
 void dtts_stack_model_destroy(dtts_stack_model *model);
 dtts_stack *dtts_stack_model_stack(const dtts_stack_model *model);
 size_t dtts_stack_model_bytes(const dtts_stack_model *model);

@@ -172,10 +172,13 @@ def test_f64_source_rounds_through_f32(dev):
     assert np.array_equal(out.cpu().numpy(), want) and want[0] != np.float16(0.745849579666197)
 
 
-@pytest.mark.parametrize("which", ["SMALL", "WINDOWED"])
-def test_stack_model_load_decodes_like_host_upload(dev, tmp_path, which):
-    """Stack::load from a checkpoint (QK-norm with D = 128; LayerScale with a window at D = 64)
-    steps bit for bit like the same weights uploaded by the host path, over two steps."""
+@pytest.mark.parametrize("which,weight", [("SMALL", "f16"), ("WINDOWED", "f16"), ("SMALL", "f32"),
+                                          ("WINDOWED", "f32"), ("SMALL", "q8_0"), ("SMALL", "q8_0_a32")])
+def test_stack_model_load_decodes_like_host_upload(dev, tmp_path, which, weight):
+    """Stack::load(.., how, ..) from a checkpoint (QK-norm with D = 128; LayerScale with a window
+    at D = 64), for each weight kind: f16, f32, and Q8_0 quantized on the device (the device
+    quantizer is the host's bit for bit), steps bit for bit like the same weights uploaded by the
+    host path, over two steps."""
     import _stack_ref
     from dtts import stack
 
@@ -185,8 +188,8 @@ def test_stack_model_load_decodes_like_host_upload(dev, tmp_path, which):
     path = tmp_path / "stack.safetensors"
     _ckpt.write(path, _ckpt.stack_tensors(geo, layers, fn, prefix))
     with checkpoint.Checkpoint(path) as ck:
-        model = checkpoint.StackModel(ck, prefix, geo, dev)
-    host = stack.Stack(geo, layers, fn, dev)
+        model = checkpoint.StackModel(ck, prefix, geo, dev, weight=weight)
+    host = stack.Stack(geo, layers, fn, dev, weight=weight)
     lanes, cap = 3, geo.capacity
     sa, sb = model.stack.new_state(lanes, cap), host.new_state(lanes, cap)
     pos = np.array([0, 7, cap - 3], np.int32)
