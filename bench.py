@@ -322,6 +322,20 @@ def workload_cfg4(dev, args):
                     res[f"k{k}_n{n}_m{m}_{mode}{tag}"] = {"us": t * 1e3,
                                                           "gbs": (wb + 2.0 * m * k + 4.0 * m * n) / t / 1e6,
                                                           "tops": 2.0 * m * n * k / t / 1e9}
+            # Proj::forward's own interface: f32 activations (the _f32 entry points), W8A8
+            # quantizing them directly and W8A32 at f32 precision
+            x32 = torch.from_numpy(synth.normal(0, f"cfg4.x32.{m}", (m, k)).astype(np.float32)).to(dev)
+            for mode in ("w8a8", "w8a32"):
+                variants = (("_f32", lambda: [ops.q8_0_matmul(x32, b, mode) for b in sets]),
+                            ("_ws_f32", lambda: [ops.q8_0_matmul(x32, b, mode, workspace=ws) for b in sets]),
+                            ("_packed_f32", lambda: [ops.q8_0_matmul_packed(x32, pb, n, mode, workspace=ws)
+                                                     for pb in packed]))
+                for tag, fn in variants:
+                    t = _graph_time(fn, reps=5) / copies
+                    wb = 34.0 * n * k / 32
+                    res[f"k{k}_n{n}_m{m}_{mode}{tag}"] = {"us": t * 1e3,
+                                                          "gbs": (wb + 4.0 * m * k + 4.0 * m * n) / t / 1e6,
+                                                          "tops": 2.0 * m * n * k / t / 1e9}
         del sets, packed
     best = max(r["gbs"] for r in res.values())
     return _line("config4: Q8_0 projections (GGML blocks), weights rotated past the MALL, graph-replayed",
@@ -380,8 +394,30 @@ def workload_stack(dev, args):
             best = res[name]
         del st, state, layers, pstate
         torch.cuda.empty_cache()
+        if name != "talker":
+            continue
+        # the talker at Stack::load's other weight kinds (f32 caches): decode steps, graph-replayed
+        for kind in ("f32", "q8_0", "q8_0_a32"):
+            layers, fn = stack.random_device_weights(geo, dev, seed=0, weight=kind)
+            st = stack.Stack(geo, layers, fn, dev, weight=kind)
+            state = st.new_state(lanes, cap)
+            for t in state.k + state.v:
+                t.copy_(torch.randn(t.shape, generator=gen, device=dev))
+            ws = st.workspace(lanes, cap)
+            t_graph = _time(lambda: st.decode(x, state, pos, out=out, graph=True, workspace=ws), reps=20)
+            if not torch.isfinite(out).all():
+                raise SystemExit(f"bench: non-finite talker output ({kind})")
+            wk = sum(v.numel() * v.element_size() for L in layers for key, v in L.items()
+                     if key in ("wqkv", "wo", "w_gateup", "wdown"))
+            kvk = kv * 2  # f32 caches
+            res[f"talker_{kind}"] = {"ms_graph": round(t_graph, 4), "tokens_per_s": round(lanes / (t_graph / 1e3), 1),
+                                     "weight_bytes": wk, "kv_bytes": kvk, "gbs": round((wk + kvk) / t_graph / 1e6, 1),
+                                     "us_per_layer": round(t_graph * 1e3 / geo.layers, 2)}
+            del st, state, layers
+            torch.cuda.empty_cache()
     return _line("row f-2: decoder-stack decode step, 48 lanes at per-lane positions (talker 28 layers, cap 2048; "
-                 "code predictor 5 layers), f16 weights and KV cache, one HIP graph per step",
+                 "code predictor 5 layers), f16 weights and KV cache, one HIP graph per step; the talker also "
+                 "with f32 and Q8_0 layers (f32 caches)",
                  "talker decode tokens/s at 48 lanes", best["tokens_per_s"], "tokens/s", res,
                  {"dtype": "f16 weights / f32 activations",
                   "frac_hbm_peak": round(best["gbs"] / PEAK_HBM_GBS, 4)})

@@ -185,15 +185,26 @@ def upload(geo: Geometry, layers, final_norm, dev, weight: str = "f16"):
     return out, f32(final_norm)
 
 
-def random_device_weights(geo: Geometry, dev, seed: int = 0):
+def random_device_weights(geo: Geometry, dev, seed: int = 0, weight: str = "f16"):
     """Device weights drawn with torch's generator on the device (for full-size benchmarks, where
-    the host generator would take minutes): projections N(0, 0.02) f16, norms U(0.9, 1.1),
+    the host generator would take minutes): projections N(0, 0.02) of the weight kind (f16; f32;
+    Q8_0 quantized on the device by dtts_convert_q8_0 and repacked), norms U(0.9, 1.1),
     LayerScale U(0.05, 0.15), in dtts_stack_create's layouts."""
+    from . import ops
+    from ._lib import ptr
+
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
 
     def w(rows, cols):
-        return (torch.randn((rows, cols), generator=g, device=dev) * 0.02).half()
+        v = torch.randn((rows, cols), generator=g, device=dev) * 0.02
+        if weight == "f32":
+            return v
+        if weight in ("q8_0", "q8_0_a32"):
+            blocks = torch.empty(rows * cols // 32 * 34, dtype=torch.uint8, device=dev)
+            call("dtts_convert_q8_0", ptr(v), 0, ptr(blocks), rows, cols, stream_handle(dev))  # 0: DTTS_DT_F32
+            return ops.q8_0_repack(blocks.view(rows, cols // 32, 34), cols)
+        return v.half()
 
     def u(n, lo=0.9, hi=1.1):
         return torch.rand((n,), generator=g, device=dev) * (hi - lo) + lo
