@@ -195,6 +195,121 @@ NtSplit pick_nt_split(int64_t groups, int nb, int64_t k, bool can_split) {
     return most;
 }
 
+// ---------------------------------------------------------------- one launch, k over the waves
+//
+// For the per-op entry points at short k (k * ceil(m/16) <= 3072): workgroup x owns 16 output
+// columns (16 gate and the matching 16 up rows for gate|up) and all of k; wave w takes the slab
+// [w * NCW * 64, (w + 1) * NCW * 64). Every lane requests its weight and A fragments for the
+// whole slab before the first MFMA (the per-wave kernel above requests A inside its MFMA loop,
+// where the compiler puts a wait before each use: one memory round trip per chunk). The slab
+// partials meet in LDS and are summed in wave order, so the output is complete in one launch,
+// with no workspace and no merge. Past that k the A fragments each workgroup reads (48 rows x k)
+// outweigh the 16 weight rows it streams, and the A-sharing kernel with its range merge is the
+// faster of the two (measured at the talker's and config 3's shapes, 8 and 48 rows).
+template <int MB, int NCW, int MODE>
+__global__ __launch_bounds__(1024) void gemm_row_nt(GemmParams p) {
+    constexpr int NB = MODE == 1 ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) float4v rsum[];  // [NB][waves][MB][64]
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, r = lane & 15;
+    const int k0 = wave * NCW * 64 + g * 16;
+    const int col = blockIdx.x * 16 + r;
+    half8_t b[NB][NCW][2];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const half_t *wr = p.w + static_cast<int64_t>(nb == 0 ? col : p.n / 2 + col) * p.k + k0;
+#pragma unroll
+        for (int c = 0; c < NCW; ++c) {
+            b[nb][c][0] = *reinterpret_cast<const half8_t *>(wr + c * 64);
+            b[nb][c][1] = *reinterpret_cast<const half8_t *>(wr + c * 64 + 8);
+        }
+    }
+    half8_t av[MB][NCW][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int row = mb * 16 + r;
+        const half_t *ar = p.a + static_cast<int64_t>(row < p.m ? row : 0) * p.k + k0;
+#pragma unroll
+        for (int c = 0; c < NCW; ++c) {
+            av[mb][c][0] = *reinterpret_cast<const half8_t *>(ar + c * 64);
+            av[mb][c][1] = *reinterpret_cast<const half8_t *>(ar + c * 64 + 8);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first wait
+    float4v acc[NB][MB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCW; ++c)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const bool live = mb * 16 + r < p.m;  // rows past m multiply zeros
+            const half8_t a0 = live ? av[mb][c][0] : half8_t{};
+            const half8_t a1 = live ? av[mb][c][1] : half8_t{};
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[nb][c][0], acc[nb][mb], 0, 0, 0);
+                acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[nb][c][1], acc[nb][mb], 0, 0, 0);
+            }
+        }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) rsum[((nb * nw + wave) * MB + mb) * 64 + lane] = acc[nb][mb];
+    __syncthreads();
+    // C layout of 16x16: lane l holds column l & 15, rows 4 * (l >> 4) + i
+    for (int t = threadIdx.x; t < MB * 64; t += blockDim.x) {
+        const int mb = t >> 6, l = t & 63;
+        float4v s0 = rsum[mb * 64 + l];
+        for (int q = 1; q < nw; ++q) s0 += rsum[(q * MB + mb) * 64 + l];
+        float4v s1 = float4v{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == 1) {
+            s1 = rsum[(nw * MB + mb) * 64 + l];
+            for (int q = 1; q < nw; ++q) s1 += rsum[((nw + q) * MB + mb) * 64 + l];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = mb * 16 + (l >> 4) * 4 + i;
+            if (row < p.m) gemm_store<MODE>(p, row, blockIdx.x * 16 + (l & 15), s0[i], s1[i]);
+        }
+    }
+}
+
+// Chunks of 64 k per wave for gemm_row_nt (0: not applicable): 2, or 3 when two would need more
+// than 16 waves; m <= 64 and k * ceil(m/16) <= 3072.
+inline int pick_row(int64_t m, int64_t k, int64_t cols) {
+    if (m <= 0 || m > 64 || cols % 16 != 0 || cols / 16 >= 65536) return 0;
+    const int64_t mb = (m + 15) / 16;
+    if (k * mb > 3072) return 0;
+    if (k % 128 == 0 && k / 128 <= 16) return 2;
+    if (k % 192 == 0 && k / 192 <= 16) return 3;
+    return 0;
+}
+
+template <int MODE, int NCW>
+hipError_t launch_row_mb(const GemmParams &p, hipStream_t stream) {
+    const int nw = p.k / (NCW * 64);
+    const int mb = (p.m + 15) / 16;
+    const size_t lds = static_cast<size_t>(MODE == 1 ? 2 : 1) * nw * mb * 64 * sizeof(float4v);
+    const dim3 grid(static_cast<unsigned>((MODE == 1 ? p.n / 2 : p.n) / 16));
+    const dim3 block(static_cast<unsigned>(nw * 64));
+    switch (mb) {
+        case 1: gemm_row_nt<1, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+        case 2: gemm_row_nt<2, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+        case 3: gemm_row_nt<3, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+        default: gemm_row_nt<4, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+    }
+    return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_row(const GemmParams &p, int ncw, hipStream_t stream) {
+    return ncw == 3 ? launch_row_mb<MODE, 3>(p, stream) : launch_row_mb<MODE, 2>(p, stream);
+}
+
 // ---------------------------------------------------------------- the A-sharing kernel
 //
 // Workgroup (x, y) = 4 waves: 64 weight rows (output columns; for gate|up, 32 gate rows and the
@@ -375,6 +490,7 @@ inline size_t wave_kernel_workspace_bytes(int64_t m, int64_t k, int64_t n, int m
 }
 
 size_t nt_workspace_bytes(int64_t m, int64_t k, int64_t n, int mode) {
+    if (pick_row(m, k, mode == 1 ? n / 2 : n) > 0) return 0;
     const LdsPlan pl = pick_lds(m, k, n, mode);
     if (pl.nc > 0) return lds_partial_bytes(pl, m, n);
     return wave_kernel_workspace_bytes(m, k, n, mode);
@@ -397,6 +513,8 @@ hipError_t launch_nt_mb(const GemmParams &p, dim3 grid, unsigned threads, size_t
 
 template <int MODE>
 hipError_t launch_nt(const GemmParams &p0, int mb_blocks, void *workspace, size_t ws_bytes, hipStream_t stream) {
+    const int ncw = pick_row(p0.m, p0.k, MODE == 1 ? p0.n / 2 : p0.n);
+    if (ncw > 0 && aligned(p0.a, 16) && aligned(p0.w, 16)) return launch_row<MODE>(p0, ncw, stream);
     const LdsPlan pl = pick_lds(p0.m, p0.k, p0.n, MODE);
     if (pl.nc > 0) {
         const size_t need = lds_partial_bytes(pl, p0.m, p0.n);

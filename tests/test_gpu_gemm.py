@@ -61,6 +61,17 @@ def test_gemm_k_split_over_workgroups_matches_single_pass(dev, m, k, n, gateup):
         assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
 
 
+def test_short_k_projections_take_one_launch_without_workspace():
+    """k * ceil(m/16) <= 3072 (config 3's QKV and gate|up, the predictor's projections): one
+    launch with k over the waves of a workgroup, so the entry points ask for no workspace; the
+    talker's k = 2048 at 48 rows and config 3's down projection keep the split and its merge."""
+    for m, k, n, gu in ((48, 1024, 4096, False), (48, 1024, 3072, True), (8, 3072, 1024, False),
+                        (16, 2048, 2048, False), (64, 128, 48, False)):
+        assert ops.gemm_workspace_bytes(m, k, n, gu) == 0, (m, k, n, gu)
+    for m, k, n, gu in ((48, 3072, 1024, False), (48, 2048, 4096, False), (48, 2048, 6144, True)):
+        assert ops.gemm_workspace_bytes(m, k, n, gu) > 0, (m, k, n, gu)
+
+
 @pytest.mark.parametrize("m,k,ffn", [(48, 1024, 3072), (8, 1024, 3072), (48, 2048, 6144), (3, 64, 16)])
 def test_gateup_silu_matches_oracle(dev, m, k, ffn):
     a, w = _ab(81, m, k, 2 * ffn)
