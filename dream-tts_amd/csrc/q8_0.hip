@@ -13,6 +13,7 @@
 // through LDS in slab order.
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -206,6 +207,134 @@ __global__ __launch_bounds__(1024) void gemm_q8_0(Q8Params<XT> p) {
             if (row < p.m) p.y[static_cast<int64_t>(row) * p.n + col] = s[i];
         }
     }
+}
+
+// One launch at short k (k * ceil(m/16) <= 3072, as the f16 projections): workgroup x owns 16
+// columns and all of k, wave w (at most 8) the NBW blocks from w * NBW. Every lane requests its weights (the
+// packed layout's contiguous 8-byte groups and scales, or the GGML blocks' 2-byte units) and its
+// activations for all NBW blocks before the first MFMA -- gemm_q8_0 above walks its slab a block
+// at a time, one memory round trip each. The block arithmetic is gemm_q8_0's; the waves' partials
+// meet in LDS and are summed in wave order, with no workspace and no merge launch. W8A16 and
+// W8A32 only (q8_row_wins).
+template <int MB, int NBW, int MODE, bool PACKED, typename XT>
+__global__ __launch_bounds__(512) void gemm_q8_row(Q8Params<XT> p) {
+    static_assert((MODE == kA16 && sizeof(XT) == 2) || (MODE == kA32 && sizeof(XT) == 4),
+                  "W8A16 on f16 activations or W8A32 on f32 ones (q8_row_wins)");
+    static_assert(NBW % 2 == 0, "whole 16-byte weight loads and 4-byte scale loads");
+    extern __shared__ __attribute__((aligned(16))) float4v qsum[];  // [waves][MB][64]
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, r = lane & 15;
+    const int nblocks = p.k / 32;
+    const int col = blockIdx.x * 16 + r;
+    const int b0 = wave * NBW;
+    uint64_t q8[NBW];
+    float dw[NBW];
+    if constexpr (PACKED) {
+        const uint8_t *row = p.w + static_cast<int64_t>(col) * (p.k + 2 * nblocks);
+        const uint8_t *qs = row + (static_cast<int64_t>(g) * nblocks + b0) * 8;
+#pragma unroll
+        for (int b = 0; b < NBW; b += 2) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(qs + b * 8);
+            q8[b] = static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32);
+            q8[b + 1] = static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32);
+        }
+        const uint32_t *ds = reinterpret_cast<const uint32_t *>(row + p.k + 2 * b0);
+#pragma unroll
+        for (int b = 0; b < NBW; b += 2) {
+            const uint32_t v = ds[b / 2];
+            half_t h0, h1;
+            const uint16_t u0 = static_cast<uint16_t>(v & 0xffff), u1 = static_cast<uint16_t>(v >> 16);
+            __builtin_memcpy(&h0, &u0, 2);
+            __builtin_memcpy(&h1, &u1, 2);
+            dw[b] = static_cast<float>(h0);
+            dw[b + 1] = static_cast<float>(h1);
+        }
+    } else {
+        const uint8_t *wrow = p.w + (static_cast<int64_t>(col) * nblocks + b0) * 34;
+#pragma unroll
+        for (int b = 0; b < NBW; ++b) load_wblock(wrow + b * 34, g, q8[b], dw[b]);
+    }
+    // the lane's activations: row mb * 16 + r, elements 8g .. 8g + 7 of each block
+    typedef typename std::conditional<sizeof(XT) == 2, half8_t, float4v>::type XV;
+    constexpr int XW = sizeof(XT) == 2 ? 1 : 2;  // vectors per 8 elements
+    XV xv[MB][NBW][XW];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+        const int row = mb * 16 + r;
+        const XT *xr = p.x + static_cast<int64_t>(row < p.m ? row : 0) * p.k + b0 * 32 + g * 8;
+#pragma unroll
+        for (int b = 0; b < NBW; ++b)
+#pragma unroll
+            for (int j = 0; j < XW; ++j) xv[mb][b][j] = *reinterpret_cast<const XV *>(xr + b * 32 + j * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first wait
+    float4v acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NBW; ++b)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const bool live = mb * 16 + r < p.m;  // rows past m carry zeros
+            if constexpr (MODE == kA16) {
+                const half8_t x8 = live ? xv[mb][b][0] : half8_t{};
+                const float4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(x8, widen_w8(q8[b]), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb][i] += pr[i] * dw[b];
+            } else {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = live ? xv[mb][b][j / 4][j % 4] : 0.0f;
+                half8_t hi, lo;
+                float inv;
+                split_block8<16, 32>(v, hi, lo, inv);
+                const half8_t wv = widen_w8(q8[b]);
+                float4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, wv, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, wv, pr, 0, 0, 0);
+                // the C fragment holds rows 4g + i; their scales live in lanes 4g + i
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb][i] += (pr[i] * dw[b]) * __shfl(inv, g * 4 + i, 64);
+            }
+        }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) qsum[(wave * MB + mb) * 64 + lane] = acc[mb];
+    __syncthreads();
+    // C layout of 16x16: lane l holds column l & 15, rows 4 * (l >> 4) + i
+    for (int t = threadIdx.x; t < MB * 64; t += blockDim.x) {
+        const int mb = t >> 6, l = t & 63;
+        float4v s = qsum[mb * 64 + l];
+        for (int q = 1; q < nw; ++q) s += qsum[(q * MB + mb) * 64 + l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = mb * 16 + (l >> 4) * 4 + i;
+            if (row < p.m) p.y[static_cast<int64_t>(row) * p.n + blockIdx.x * 16 + (l & 15)] = s[i];
+        }
+    }
+}
+
+// Blocks per wave for gemm_q8_row (0: not applicable): the fewest of 4, 6, 8 and 12 that need at
+// most 8 waves (two waves per SIMD, so a lane's activations for its blocks fit its registers);
+// m <= 64, k * ceil(m/16) <= 3072, n a multiple of 16.
+int pick_q8_row(int64_t m, int64_t k, int64_t n) {
+    if (m <= 0 || m > 64 || k % 32 != 0 || n % 16 != 0 || n / 16 >= 65536) return 0;
+    if (k * ((m + 15) / 16) > 3072) return 0;
+    const int64_t nblocks = k / 32;
+    for (int nbw : {4, 6, 8, 12})
+        if (nblocks % nbw == 0 && nblocks / nbw <= 8) return nbw;
+    return 0;
+}
+
+// Where the one-launch kernel beats the A-sharing kernel and its merge (measured at config 4's
+// shapes, m = 1, 8 and 48, graph-replayed): W8A16 on the packed layout everywhere it applies, and
+// on GGML blocks (five 2-byte loads per block) up to 4 blocks per wave; W8A32 on the packed
+// layout up to 4 blocks per wave at m <= 16. Not W8A8: every workgroup would quantize all of x
+// again, where the A-sharing kernel quantizes its slab once per 64 columns.
+bool q8_row_wins(int32_t mode, bool packed, int nbw, int64_t m) {
+    if (nbw == 0) return false;
+    if (mode == DTTS_Q8_W8A16) return packed || nbw == 4;
+    if (mode == DTTS_Q8_W8A32) return packed && nbw == 4 && m <= 16;
+    return false;
 }
 
 // LDS of the A-sharing kernel: the activation slab of MB*16 rows by NB blocks as f16 (W8A16),
@@ -458,6 +587,58 @@ bool mode_ok(int32_t mode) {
     return mode == DTTS_Q8_W8A8 || mode == DTTS_Q8_W8A32;
 }
 
+template <int MB, int NBW, int MODE, typename XT>
+void q8_row_kernel(bool packed, unsigned grid, unsigned threads, size_t lds, hipStream_t stream, const Q8Params<XT> &p) {
+    if (packed)
+        gemm_q8_row<MB, NBW, MODE, true, XT><<<grid, threads, lds, stream>>>(p);
+    else
+        gemm_q8_row<MB, NBW, MODE, false, XT><<<grid, threads, lds, stream>>>(p);
+}
+
+// W8A16 for f16 activations, W8A32 for f32 ones: the modes q8_row_wins takes.
+template <int MB, int NBW, typename XT>
+void q8_row_modes(bool packed, unsigned grid, unsigned threads, size_t lds, hipStream_t stream, const Q8Params<XT> &p) {
+    q8_row_kernel<MB, NBW, sizeof(XT) == 2 ? kA16 : kA32, XT>(packed, grid, threads, lds, stream, p);
+}
+
+// gemm_q8_row over (m, k, n) with pick_q8_row's nbw, in the mode q8_row_wins takes for XT (the
+// caller checked shape, mode and pointers).
+template <typename XT>
+int q8_row_launch(const char *name, const XT *x, const void *w, float *y, int64_t m, int64_t k, int64_t n,
+                  int nbw, bool packed, hipStream_t stream) {
+    DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
+    Q8Params<XT> p{};
+    p.x = x;
+    p.w = static_cast<const uint8_t *>(w);
+    p.y = y;
+    p.m = static_cast<int>(m);
+    p.k = static_cast<int>(k);
+    p.n = static_cast<int>(n);
+    const int mb = static_cast<int>((m + 15) / 16);
+    const int nw = static_cast<int>(k / 32 / nbw);
+    const unsigned grid = static_cast<unsigned>(n / 16), threads = static_cast<unsigned>(64 * nw);
+    const size_t lds = static_cast<size_t>(nw) * mb * 64 * sizeof(float4v);
+    auto launch = [&](auto mbc) {
+        constexpr int MB = decltype(mbc)::value;
+        // pick_q8_row's bound k * MB <= 3072 leaves 6 blocks per wave at MB <= 2 and 8 or 12 at MB = 1
+        if constexpr (MB == 1) {
+            if (nbw == 12) return q8_row_modes<MB, 12, XT>(packed, grid, threads, lds, stream, p);
+            if (nbw == 8) return q8_row_modes<MB, 8, XT>(packed, grid, threads, lds, stream, p);
+        }
+        if constexpr (MB <= 2)
+            if (nbw == 6) return q8_row_modes<MB, 6, XT>(packed, grid, threads, lds, stream, p);
+        q8_row_modes<MB, 4, XT>(packed, grid, threads, lds, stream, p);
+    };
+    switch (mb) {
+        case 1: launch(std::integral_constant<int, 1>{}); break;
+        case 2: launch(std::integral_constant<int, 2>{}); break;
+        case 3: launch(std::integral_constant<int, 3>{}); break;
+        default: launch(std::integral_constant<int, 4>{}); break;
+    }
+    DTTS_LAUNCH_CHECK(name);
+    return DTTS_OK;
+}
+
 template <typename XT>
 int q8_plain(const char *name, const XT *x, const void *blocks, float *y, int64_t m, int64_t k, int64_t n,
              int32_t mode, hipStream_t stream) {
@@ -471,6 +652,8 @@ int q8_plain(const char *name, const XT *x, const void *blocks, float *y, int64_
     DTTS_REQUIRE(n % 16 == 0, "%s: n = %lld not a multiple of 16", name, (long long)n);
     DTTS_REQUIRE(aligned(x, 16) && aligned(blocks, 2), "%s: x must be 16-byte aligned", name);
     DTTS_REQUIRE(k < (int64_t(1) << 30) && n < (int64_t(1) << 30), "%s: shape too large", name);
+    if (const int nbw = pick_q8_row(m, k, n); q8_row_wins(mode, false, nbw, m))
+        return q8_row_launch(name, x, blocks, y, m, k, n, nbw, false, stream);
     Q8Params<XT> p{};
     p.x = x;
     p.w = static_cast<const uint8_t *>(blocks);
@@ -586,10 +769,11 @@ int q8_ws(const char *name, const XT *x, const void *blocks, float *y, int64_t m
     DTTS_REQUIRE(mode_ok<XT>(mode), "%s: mode %d (%s) not taken with %s activations", name, mode, mode_name(mode),
                  sizeof(XT) == 2 ? "f16" : "f32");
     if (m == 0) return DTTS_OK;
-    // On the GGML layout the A-sharing kernel pays for its 2-byte weight loads only once a slab
-    // serves more than 16 rows (measured at m = 1, 8 and 48); below that, and without room for
-    // the ranges, the workspace-free kernel runs.
-    const int nb = m > 16 ? pick_q8_nb(m, k, n) : 0;
+    // Where the one-launch kernel wins, it runs (q8_plain takes it). Otherwise, on the GGML layout
+    // the A-sharing kernel pays for its 2-byte weight loads only once a slab serves more than 16 rows
+    // (measured at m = 1, 8 and 48); below that, and without room for the ranges, the
+    // workspace-free kernel runs.
+    const int nb = m > 16 && !q8_row_wins(mode, false, pick_q8_row(m, k, n), m) ? pick_q8_nb(m, k, n) : 0;
     const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
     if (!nb || (need && (!workspace || ws_bytes < need)))
         return q8_plain(plain_name, x, blocks, y, m, k, n, mode, stream);
@@ -610,6 +794,10 @@ int q8_packed(const char *name, const XT *x, const void *packed, float *y, int64
     if (m == 0) return DTTS_OK;
     DTTS_REQUIRE(m <= 64, "%s: m = %lld > 64 (decode shapes only)", name, (long long)m);
     DTTS_REQUIRE(x && packed && y, "%s: null pointer", name);
+    if (const int nbw = pick_q8_row(m, k, n); q8_row_wins(mode, true, nbw, m)) {
+        DTTS_REQUIRE(aligned(x, 16) && aligned(packed, 16), "%s: x and packed must be 16-byte aligned", name);
+        return q8_row_launch(name, x, packed, y, m, k, n, nbw, true, stream);
+    }
     const int nb = pick_q8_nb(m, k, n);
     const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
     DTTS_REQUIRE(nb > 0, "%s: shape not supported", name);
