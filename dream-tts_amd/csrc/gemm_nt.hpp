@@ -296,11 +296,15 @@ hipError_t launch_row_mb(const GemmParams &p, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(MODE == 1 ? 2 : 1) * nw * mb * 64 * sizeof(float4v);
     const dim3 grid(static_cast<unsigned>((MODE == 1 ? p.n / 2 : p.n) / 16));
     const dim3 block(static_cast<unsigned>(nw * 64));
-    switch (mb) {
-        case 1: gemm_row_nt<1, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
-        case 2: gemm_row_nt<2, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
-        case 3: gemm_row_nt<3, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
-        default: gemm_row_nt<4, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+    if constexpr (NCW == 3) {  // k > 2048 with k * ceil(m/16) <= 3072: one row block
+        gemm_row_nt<1, NCW, MODE><<<grid, block, lds, stream>>>(p);
+    } else {
+        switch (mb) {
+            case 1: gemm_row_nt<1, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+            case 2: gemm_row_nt<2, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+            case 3: gemm_row_nt<3, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+            default: gemm_row_nt<4, NCW, MODE><<<grid, block, lds, stream>>>(p); break;
+        }
     }
     return hipGetLastError();
 }
