@@ -45,7 +45,8 @@ const char *conv_split_kernel_name(int64_t lanes, int64_t len, int64_t cs, int64
 int conv1d_nlc_split(const SplitConv &s, hipStream_t stream);
 // Tap-major f32 [cout, k cs] -> the split weight w3 [cout, k * 3 cs] (synchronises `stream` once to
 // read the weight's largest magnitude).
-int split_weight(const float *w, int64_t cout, int64_t k, int64_t cs, half_t *w3, float &w_inv, hipStream_t stream);
+int split_weight(const float *w, int64_t cout, int64_t k, int64_t cs, half_t *w3, float &w_inv, hipStream_t stream,
+                 const char *name = "dtts_codec_create_f32 (split weights)");
 // f32 [rows, C] -> split rows.
 int split_activations(const float *x, half_t *y, int64_t rows, int64_t C, hipStream_t stream);
 // The f32 single-output-channel conv (conv_nlc_f32.hip) reading a split input (d->x: rows

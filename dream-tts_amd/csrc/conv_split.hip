@@ -222,6 +222,26 @@ __global__ __launch_bounds__(256) void split_weight_kernel(const float *w, half_
     }
 }
 
+// Split rows [hi(C) | lo(C)] -> f32 [rows, C] (hi + lo), 8 values per thread.
+__global__ __launch_bounds__(256) void join_act_kernel(const half_t *x, float *y, int64_t rows, int C) {
+    const int c8 = C / 8;
+    const int64_t total = rows * c8;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t r = e / c8;
+        const int c = static_cast<int>(e - r * c8) * 8;
+        const half8_t hi = *reinterpret_cast<const half8_t *>(x + r * 2 * C + c);
+        const half8_t lo = *reinterpret_cast<const half8_t *>(x + r * 2 * C + C + c);
+        float4_t a, b;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            a[q] = static_cast<float>(hi[q]) + static_cast<float>(lo[q]);
+            b[q] = static_cast<float>(hi[4 + q]) + static_cast<float>(lo[4 + q]);
+        }
+        *reinterpret_cast<float4_t *>(y + r * C + c) = a;
+        *reinterpret_cast<float4_t *>(y + r * C + c + 4) = b;
+    }
+}
+
 // f32 [rows, C] -> split rows [hi(C) | lo(C)], 8 values per thread.
 __global__ __launch_bounds__(256) void split_act_kernel(const float *x, half_t *y, int64_t rows, int C) {
 #pragma clang fp contract(off)
@@ -292,8 +312,8 @@ int conv1d_nlc_split(const SplitConv &s, hipStream_t stream) {
     return DTTS_OK;
 }
 
-int split_weight(const float *w, int64_t cout, int64_t k, int64_t cs, half_t *w3, float &w_inv, hipStream_t stream) {
-    const char *name = "dtts_codec_create_f32 (split weights)";
+int split_weight(const float *w, int64_t cout, int64_t k, int64_t cs, half_t *w3, float &w_inv, hipStream_t stream,
+                 const char *name) {
     const int64_t n = cout * k * cs;
     unsigned *bits = nullptr;
     DTTS_HIP_CHECK(hipMalloc(&bits, sizeof(unsigned)), name);
@@ -331,3 +351,120 @@ int split_activations(const float *x, half_t *y, int64_t rows, int64_t C, hipStr
 }
 
 }  // namespace dtts
+
+// ---------------------------------------------------------------- the op-level entry points
+//
+// NlcConv on f32 operands through the split route: the weight is split once at load
+// (dtts_conv_split_weight), and each call splits x (and the residual) into the workspace, runs the
+// split conv and joins the outputs back to f32.
+
+using dtts::half_t;
+
+namespace {
+
+size_t split_ws_align(size_t b) { return (b + 255) & ~size_t(255); }
+
+struct SplitWs {
+    size_t x, res, y, y_pre, total;
+};
+
+SplitWs split_ws_plan(const dtts_conv_desc *d) {
+    SplitWs w{};
+    const size_t rows = static_cast<size_t>(d->lanes) * static_cast<size_t>(d->len);
+    w.x = split_ws_align(rows * d->cin * 4);
+    w.res = d->residual ? split_ws_align(rows * d->cout * 4) : 0;
+    w.y = split_ws_align(rows * d->cout * 4);
+    w.y_pre = d->y_pre ? split_ws_align(rows * d->cout * 4) : 0;
+    w.total = w.x + w.res + w.y + w.y_pre;
+    return w;
+}
+
+}  // namespace
+
+extern "C" size_t dtts_conv_split_weight_bytes(int64_t cout, int64_t k, int64_t cin) {
+    return cout > 0 && k > 0 && cin > 0 ? static_cast<size_t>(cout) * k * 3 * cin * sizeof(half_t) : 0;
+}
+
+extern "C" int dtts_conv_split_weight(const float *w_tm, int64_t cout, int64_t k, int64_t cin, void *w_split,
+                                      float *w_inv, hipStream_t stream) {
+    const char *name = "dtts_conv_split_weight";
+    DTTS_REQUIRE(cout > 0 && k > 0 && k <= 7 && cin > 0 && cin % 8 == 0, "%s: bad shape (cout %lld, k %lld, cin %lld)",
+                 name, (long long)cout, (long long)k, (long long)cin);
+    DTTS_REQUIRE(w_tm && w_split && w_inv, "%s: null pointer", name);
+    DTTS_REQUIRE(cout * k * cin < (int64_t(1) << 31), "%s: weight too large", name);
+    float inv = 1.0f;
+    const int rc = dtts::split_weight(w_tm, cout, k, cin, static_cast<half_t *>(w_split), inv, stream, name);
+    if (rc != DTTS_OK) return rc;
+    *w_inv = inv;
+    return DTTS_OK;
+}
+
+extern "C" size_t dtts_conv1d_nlc_f32_split_workspace_bytes(const dtts_conv_desc *desc) {
+    if (!desc || desc->lanes <= 0 || desc->len <= 0 || desc->cin <= 0 || desc->cout <= 0) return 0;
+    return split_ws_plan(desc).total;
+}
+
+extern "C" int dtts_conv1d_nlc_f32_split(const dtts_conv_desc *desc, float w_inv, void *workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+    const char *name = "dtts_conv1d_nlc_f32_split";
+    DTTS_REQUIRE(desc, "%s: null descriptor", name);
+    const dtts_conv_desc &d = *desc;
+    DTTS_REQUIRE(d.lanes >= 0 && d.len >= 0 && d.cin > 0 && d.cout > 0 && d.k >= 1 && d.dilation >= 1 &&
+                     d.pad_left >= 0 && d.pad_left <= (d.k - 1) * d.dilation,
+                 "%s: bad shape", name);
+    if (d.lanes == 0 || d.len == 0) return DTTS_OK;
+    DTTS_REQUIRE(d.x && d.w && d.y, "%s: null pointer", name);
+    if (d.in_alpha || d.act != 0 || d.out_scale || (d.out_alpha == nullptr) != (d.out_brecip == nullptr) ||
+        !dtts::conv_split_supported(d.lanes, d.len, d.cin, d.cout, d.k, d.dilation)) {
+        dtts::set_error("%s: no split kernel for this conv (prologue SnakeBeta, activation, out_scale, or shape "
+                        "cin %lld cout %lld k %lld dilation %lld); use dtts_conv1d_nlc_f32_ex",
+                        name, (long long)d.cin, (long long)d.cout, (long long)d.k, (long long)d.dilation);
+        return DTTS_ERR_UNSUPPORTED;
+    }
+    DTTS_REQUIRE(std::isfinite(w_inv) && w_inv > 0.0f, "%s: w_inv %g is not a positive power of two", name, w_inv);
+    const SplitWs plan = split_ws_plan(desc);
+    DTTS_REQUIRE(workspace && workspace_bytes >= plan.total && dtts::aligned(workspace, 256),
+                 "%s: workspace %zu bytes (256-byte aligned) < %zu needed", name, workspace_bytes, plan.total);
+    DTTS_REQUIRE(dtts::aligned(d.x, 16) && dtts::aligned(d.w, 16) && dtts::aligned(d.y, 16) &&
+                     (!d.residual || dtts::aligned(d.residual, 16)) && (!d.y_pre || dtts::aligned(d.y_pre, 16)),
+                 "%s: x, w, residual, y_pre and y must be 16-byte aligned", name);
+    char *ws = static_cast<char *>(workspace);
+    half_t *xs = reinterpret_cast<half_t *>(ws);
+    half_t *rs = d.residual ? reinterpret_cast<half_t *>(ws + plan.x) : nullptr;
+    half_t *ys = reinterpret_cast<half_t *>(ws + plan.x + plan.res);
+    half_t *yps = d.y_pre ? reinterpret_cast<half_t *>(ws + plan.x + plan.res + plan.y) : nullptr;
+    const int64_t rows = d.lanes * d.len;
+    int rc = dtts::split_activations(static_cast<const float *>(d.x), xs, rows, d.cin, stream);
+    if (rc == DTTS_OK && rs) rc = dtts::split_activations(static_cast<const float *>(d.residual), rs, rows, d.cout, stream);
+    if (rc != DTTS_OK) return rc;
+    dtts::SplitConv sc{};
+    sc.lanes = d.lanes;
+    sc.len = d.len;
+    sc.cs = d.cin;
+    sc.cout = d.cout;
+    sc.k = d.k;
+    sc.dil = d.dilation;
+    sc.pad_left = d.pad_left;
+    sc.cv = d.cout;
+    sc.x = xs;
+    sc.w = static_cast<const half_t *>(d.w);
+    sc.w_inv = w_inv;
+    sc.bias = static_cast<const float *>(d.bias);
+    sc.res = rs;
+    sc.y_pre = yps;
+    sc.y = ys;
+    sc.a_out = d.out_alpha;
+    sc.r_out = d.out_brecip;
+    rc = dtts::conv1d_nlc_split(sc, stream);
+    if (rc != DTTS_OK) return rc;
+    const unsigned grid = dtts::grid_for(rows * (d.cout / 8), 256);
+    dtts::join_act_kernel<<<grid, 256, 0, stream>>>(ys, static_cast<float *>(d.y), rows, static_cast<int>(d.cout));
+    DTTS_LAUNCH_CHECK(name);
+    if (yps) {
+        dtts::join_act_kernel<<<grid, 256, 0, stream>>>(yps, static_cast<float *>(d.y_pre), rows,
+                                                        static_cast<int>(d.cout));
+        DTTS_LAUNCH_CHECK(name);
+    }
+    return DTTS_OK;
+}
+

@@ -36,6 +36,10 @@ SIGNATURES = {
     "dtts_snake_alpha_f32": [_P, _P, _P, _I64, _I64, _I64, _P],
     "dtts_conv1d_nlc_f16_ex": [_P, _P],
     "dtts_conv1d_nlc_f32_ex": [_P, _P],
+    "dtts_conv_split_weight_bytes": [_I64, _I64, _I64],
+    "dtts_conv_split_weight": [_P, _I64, _I64, _I64, _P, _P, _P],
+    "dtts_conv1d_nlc_f32_split_workspace_bytes": [_P],
+    "dtts_conv1d_nlc_f32_split": [_P, _F32, _P, _SZ, _P],
     "dtts_causal_conv1d_nlc_f16": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "dtts_snake_conv_residual_nlc_f16": [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                          _I64, _P],
@@ -146,7 +150,9 @@ _RESTYPES = {"dtts_last_error": ctypes.c_char_p, "dtts_codec_destroy": None,
              "dtts_codec_model_front": ctypes.c_void_p, "dtts_codec_model_wave": ctypes.c_void_p,
              "dtts_codec_model_bytes": ctypes.c_size_t, "dtts_stack_model_destroy": None,
              "dtts_stack_model_stack": ctypes.c_void_p, "dtts_stack_model_bytes": ctypes.c_size_t,
-             "dtts_gemm_q8_0_workspace_bytes": ctypes.c_size_t, "dtts_q8_0_packed_bytes": ctypes.c_size_t}
+             "dtts_gemm_q8_0_workspace_bytes": ctypes.c_size_t, "dtts_q8_0_packed_bytes": ctypes.c_size_t,
+             "dtts_conv_split_weight_bytes": ctypes.c_size_t,
+             "dtts_conv1d_nlc_f32_split_workspace_bytes": ctypes.c_size_t}
 
 
 class DttsError(RuntimeError):

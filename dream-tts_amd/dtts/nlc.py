@@ -79,6 +79,45 @@ def conv1d(x, w_tm, bias=None, *, k, dilation=1, pad_left=None, snake_in=None, r
     return (y_pre, y) if want_pre else y
 
 
+def split_weight(w_tm, k):
+    """dtts_conv_split_weight: a tap-major f32 weight [cout, k*cin] -> (the split weight
+    [cout, k*3*cin] f16, w_inv = 2^-s) for conv1d_f32_split. Synchronises the stream once."""
+    name = "nlc.split_weight"
+    cout, kc = w_tm.shape
+    _need(w_tm, name, "w_tm", torch.float32, (cout, kc))
+    cin = kc // k
+    w3 = torch.empty(int(lib().dtts_conv_split_weight_bytes(cout, k, cin)) // 2, dtype=torch.float16,
+                     device=w_tm.device).view(cout, 3 * kc)
+    inv = ctypes.c_float(0.0)
+    call("dtts_conv_split_weight", _p(w_tm), cout, k, cin, _p(w3), ctypes.byref(inv), stream_handle())
+    return w3, inv.value
+
+
+def conv1d_f32_split(x, w3, w_inv, bias=None, *, k, dilation=1, pad_left=None, residual=None, snake_out=None,
+                     want_pre=False, workspace=None):
+    """NlcConv on f32 operands through the split route (dtts_conv1d_nlc_f32_split): x, bias,
+    residual f32 as conv1d takes them, the weight as split_weight returns it. Returns y, or
+    (y_pre, y) when want_pre."""
+    name = "nlc.conv1d_f32_split"
+    lanes, length, cin = x.shape
+    cout = w3.shape[0]
+    _need(x, name, "x", torch.float32)
+    _need(w3, name, "w3", torch.float16, (cout, 3 * k * cin))
+    _need(bias, name, "bias", torch.float32, (cout,))
+    _need(residual, name, "residual", torch.float32, (lanes, length, cout))
+    y = torch.empty((lanes, length, cout), dtype=torch.float32, device=x.device)
+    y_pre = torch.empty_like(y) if want_pre else None
+    d = ConvDesc(lanes, length, cin, cout, k, dilation,
+                 (k - 1) * dilation if pad_left is None else pad_left,
+                 _p(x), _p(w3), _p(bias), None, None, _p(residual), _p(y_pre),
+                 _p(snake_out[0]) if snake_out else None, _p(snake_out[1]) if snake_out else None,
+                 _p(y), 0, None)
+    need = int(lib().dtts_conv1d_nlc_f32_split_workspace_bytes(ctypes.byref(d)))
+    ws = workspace if workspace is not None else torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    call("dtts_conv1d_nlc_f32_split", ctypes.byref(d), ctypes.c_float(w_inv), _p(ws), ws.numel(), stream_handle())
+    return (y_pre, y) if want_pre else y
+
+
 class RuDesc(ctypes.Structure):
     _fields_ = [("lanes", ctypes.c_int64), ("len", ctypes.c_int64), ("channels", ctypes.c_int64),
                 ("k", ctypes.c_int64), ("dilation", ctypes.c_int64)] + [

@@ -127,6 +127,25 @@ int dtts_conv1d_nlc_f16_ex(const dtts_conv_desc *desc, hipStream_t stream);
  * (k-1)*dilation <= 64 and x, w are 16-byte aligned; a direct kernel otherwise. */
 int dtts_conv1d_nlc_f32_ex(const dtts_conv_desc *desc, hipStream_t stream);
 
+/* The same f32 conv at f32 accuracy on the f16 matrix cores (NlcConv, crates/tts-nn/src/
+ * nlcconv.rs:15-198; the route the f32 codec takes). The weight is split once at load:
+ * dtts_conv_split_weight scales the tap-major f32 weight [cout, k*cin] by a power of two 2^s (its
+ * largest magnitude then in [2^14, 2^15)) and writes [cout, k*3*cin] f16, per tap [hi | hi | lo]
+ * of the scaled values, and w_inv = 2^-s; it synchronises `stream` once (to read the weight's
+ * largest magnitude). Each dtts_conv1d_nlc_f32_split call then splits x (and the residual) into
+ * f16 hi/lo pairs in the workspace, computes sum(xh wh + xl wh + xh wl) in f32 (the dropped xl wl
+ * is ~2^-22 of a term), adds bias and residual in f32, applies the epilogue SnakeBeta at full
+ * precision, and writes f32 y (and y_pre). desc->w is the split weight; every other operand is
+ * f32 as dtts_conv1d_nlc_f32_ex takes it. Taken for cin and cout multiples of 32, k <= 7 with
+ * (k-1)*dilation <= 64 (cout a multiple of 96 for k > 2), no prologue SnakeBeta, act 0 and no
+ * out_scale; anything else returns DTTS_ERR_UNSUPPORTED. */
+size_t dtts_conv_split_weight_bytes(int64_t cout, int64_t k, int64_t cin);
+int dtts_conv_split_weight(const float *w_tm, int64_t cout, int64_t k, int64_t cin, void *w_split,
+                           float *w_inv, hipStream_t stream);
+size_t dtts_conv1d_nlc_f32_split_workspace_bytes(const dtts_conv_desc *desc);
+int dtts_conv1d_nlc_f32_split(const dtts_conv_desc *desc, float w_inv, void *workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
 /* nlc::causal_conv1d (crates/tts-nn/src/nlc.rs:70-132): causal, pad (k-1)*dilation. Any lane
  * count (the reference requires one, crates/tts-nn/src/nlcconv.rs:192). */
 int dtts_causal_conv1d_nlc_f16(const dtts_f16 *x, const dtts_f16 *w_tm, const dtts_f16 *bias,
@@ -688,8 +707,11 @@ int dtts_codec_create(const dtts_codec_geometry *geo, const dtts_codec_weights *
 /* The same stack at the reference's own precision: every conv weight and bias is f32 in the same
  * layouts, and the codec decodes f32 activations with dtts_codec_decode_f32 only. The reference
  * keeps its waveform stack f32 because f16 storage "missed the fixtures by 6x"
- * (crates/qwen3tts/src/codec.rs:33-43, WAV_DTYPE = F32); every conv runs the f32 channels-last
- * kernel (dtts_conv1d_nlc_f32_ex) and every residual unit is its two convs. */
+ * (crates/qwen3tts/src/codec.rs:33-43, WAV_DTYPE = F32). Every conv runs at f32 accuracy on the
+ * f16 matrix cores (the split route of dtts_conv1d_nlc_f32_split: activations stored as f16 hi/lo
+ * pairs, weights split once here), every residual unit is its two convs, and the output conv
+ * reads the split activations directly. Create synchronises the null stream once per conv weight
+ * (its largest magnitude picks the split's scale). */
 int dtts_codec_create_f32(const dtts_codec_geometry *geo, const dtts_codec_weights *weights,
                           dtts_codec **out);
 void dtts_codec_destroy(dtts_codec *codec);

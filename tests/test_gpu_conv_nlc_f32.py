@@ -154,3 +154,76 @@ def test_single_output_channel_f32(dev, lanes, cin, length, k, dil, pad, ops):
     else:
         got = to_host(nlc.conv1d(to_dev(x, dev), w_tm, to_dev(b, dev), **kw))
         assert rel(got, want)[1] < 1e-5 and rel(got, exact)[1] < 1e-5
+
+
+# ---------------------------------------------------------------- the split route
+# dtts_conv1d_nlc_f32_split: the same f32 NlcConv at f32 accuracy on the f16 matrix cores (x and the
+# residual split into f16 hi/lo pairs, the weight scaled by 2^s and split once at load, three f16
+# products per term, xl*wl dropped). Held to NlcConv's own bar, max-rel < 1e-5 (nlc.rs:294-405),
+# against the oracle's NlcConv restatement and torch float64, at nlc.rs:362-398's fused-conv shapes
+# and the codec's stages.
+
+SPLIT_SHAPES = [
+    (1, 96, 96, 4200, 7, 9), (1, 32, 96, 4096, 7, 1), (1, 128, 192, 5000, 7, 3), (1, 64, 96, 4097, 1, 1),  # nlc.rs
+    (3, 96, 96, 700, 7, 9), (2, 192, 192, 513, 7, 3), (2, 384, 384, 300, 7, 1), (2, 768, 768, 250, 1, 1),   # codec
+    (2, 1024, 1536, 60, 7, 1), (2, 192, 192, 600, 1, 1), (2, 384, 384, 300, 1, 1),
+]
+
+
+@pytest.mark.parametrize("lanes,cin,cout,length,k,dil", SPLIT_SHAPES)
+def test_split_conv_matches_oracle_and_torch(dev, lanes, cin, cout, length, k, dil):
+    x, w, b = _case(110, lanes, length, cin, cout, k)
+    w3, inv = nlc.split_weight(to_dev(nlc.tap_major_weight(w), dev), k)
+    got = to_host(nlc.conv1d_f32_split(to_dev(x, dev), w3, inv, to_dev(b, dev), k=k, dilation=dil))
+    want = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil)
+    assert rel(got, want)[1] < 1e-5, rel(got, want)
+    assert rel(got, _torch_f64(x, w, b, dil, (k - 1) * dil))[1] < 1e-5
+
+
+@pytest.mark.parametrize("lanes,c,length,k,dil", [(2, 96, 3000, 7, 9), (1, 192, 1100, 1, 1), (2, 384, 300, 7, 3)])
+def test_split_conv_residual_snake_out(dev, lanes, c, length, k, dil):
+    """The codec's epilogue on the split route: bias, residual, y_pre and the output SnakeBeta at
+    full precision, and a centred pad."""
+    x, w, b = _case(111, lanes, length, c, c, k)
+    res = synth.normal(111, "res", (lanes, length, c))
+    a2 = synth.uniform(111, "a2", (c,), 0.5, 1.5)
+    r2 = (1.0 / a2).astype(np.float32)
+    w3, inv = nlc.split_weight(to_dev(nlc.tap_major_weight(w), dev), k)
+    pad = (k - 1) * dil // 2
+    y_pre, y = nlc.conv1d_f32_split(to_dev(x, dev), w3, inv, to_dev(b, dev), k=k, dilation=dil, pad_left=pad,
+                                    residual=to_dev(res, dev), snake_out=(to_dev(a2, dev), to_dev(r2, dev)),
+                                    want_pre=True)
+    want_pre = oracle.conv1d_nlc_f32(x, oracle.tap_weight_f32(w), b, dil, pad_left=pad, res=res)
+    assert rel(to_host(y_pre), want_pre)[1] < 1e-5
+    assert rel(to_host(y_pre), _torch_f64(x, w, b, dil, pad) + res)[1] < 1e-5
+    assert rel(to_host(y), oracle.snake_nlc_f32(want_pre, a2, r2))[1] < 1e-5
+
+
+def test_split_conv_refuses_what_it_has_no_kernel_for(dev):
+    """A prologue SnakeBeta, an activation or a shape off the split tiles: DTTS_ERR_UNSUPPORTED,
+    nothing written (the shim then calls dtts_conv1d_nlc_f32_ex)."""
+    import ctypes
+
+    from dtts import DttsError
+    from dtts._lib import call, stream_handle
+
+    x, w, b = _case(112, 1, 300, 96, 96, 7)
+    w3, inv = nlc.split_weight(to_dev(nlc.tap_major_weight(w), dev), 7)
+    xd = to_dev(x, dev)
+    y = torch.full((1, 300, 96), 7.0, dtype=torch.float32, device=dev)
+    alpha = torch.ones(96, dtype=torch.float32, device=dev)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    for in_alpha, act in ((alpha, 0), (None, 1)):
+        d = nlc.ConvDesc(1, 300, 96, 96, 7, 1, 6, xd.data_ptr(), w3.data_ptr(), None,
+                         None if in_alpha is None else in_alpha.data_ptr(),
+                         None if in_alpha is None else in_alpha.data_ptr(), None, None, None, None, y.data_ptr(),
+                         act, None)
+        with pytest.raises(DttsError, match="no split kernel"):
+            call("dtts_conv1d_nlc_f32_split", ctypes.byref(d), ctypes.c_float(inv), ws.data_ptr(), ws.numel(),
+                 stream_handle())
+    x40, w40, _ = _case(112, 1, 300, 40, 96, 7)
+    w3b, invb = nlc.split_weight(to_dev(nlc.tap_major_weight(w40), dev), 7)
+    with pytest.raises(DttsError, match="no split kernel"):
+        nlc.conv1d_f32_split(to_dev(x40, dev), w3b, invb, k=7)
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
