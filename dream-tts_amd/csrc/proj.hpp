@@ -8,8 +8,8 @@
 
 namespace dtts {
 
-// k ranges of a Q8_0 projection on packed weights (0: shape not supported).
-int q8_stack_ranges(int64_t m, int64_t k, int64_t n);
+// k ranges of a Q8_0 projection on packed weights in `mode` (0: shape not supported).
+int q8_stack_ranges(int64_t m, int64_t k, int64_t n, int32_t mode);
 // x [m, k] f32, packed weights [n, k] (dtts_q8_0_repack's layout); mode DTTS_Q8_W8A8 or _W8A32.
 // Partials to `part` when there are several ranges (no merge), else y.
 int q8_stack_gemm(const float *x, const void *packed, float *y, float *part, int64_t m, int64_t k, int64_t n,

@@ -466,6 +466,16 @@ __global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params<XT> p, float *part) 
                 for (int i = 0; i < 4; ++i) acc[mb][i] += (pr[i] * dw[b]) * inv[i];
             }
         }
+        if constexpr (MB >= 2) {
+            // fold each block's products into the accumulators before the next block's MFMAs
+            // issue: left to itself the compiler issues all NB * MB block products first and holds
+            // their results (~480 registers at MB = 3, NB = 16: one wave per SIMD; 84 this way, and
+            // the gate|up projection at the talker's shape 30.3 -> 21.4 us). At MB = 1 the
+            // overlap is worth more than the occupancy.
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) asm volatile("" : "+v"(acc[mb]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     float *dst = part ? part + static_cast<int64_t>(blockIdx.y) * p.m * p.n : p.y;
 #pragma unroll
@@ -488,10 +498,14 @@ __global__ __launch_bounds__(256) void q8_merge(const float *part, float *y, int
 
 // Blocks per k range for the A-sharing kernel: the widest range that still gives >= 192
 // workgroups and keeps the f16 slab within 64 KB of LDS (else the narrowest); 0 when the shape
-// does not fit it.
-int pick_q8_nb(int64_t m, int64_t k, int64_t n) {
+// does not fit it. W8A32 above 16 rows takes eight-block ranges: its two f16 slabs then leave room
+// for three workgroups per CU (52 KB at 48 rows, against 103 KB and one at sixteen blocks; the
+// gate|up projection at the talker's shape 41.6 -> 29.7 us), where the other modes measured
+// faster with the wider ranges.
+int pick_q8_nb(int64_t m, int64_t k, int64_t n, int32_t mode) {
     const int64_t nblocks = k / 32, tiles = n / 64, rows = (m + 15) / 16 * 16;
     if (m <= 0 || m > 64 || n % 64 != 0 || nblocks % 8 != 0 || tiles >= 65536) return 0;
+    if (mode == DTTS_Q8_W8A32 && m > 16) return 8;
     for (int nb : {32, 16})
         if (nblocks % nb == 0 && tiles * (nblocks / nb) >= 192 && rows * (nb * 32 + 8) * 2 <= 65536) return nb;
     return 8;
@@ -773,7 +787,7 @@ int q8_ws(const char *name, const XT *x, const void *blocks, float *y, int64_t m
     // the A-sharing kernel pays for its 2-byte weight loads only once a slab serves more than 16 rows
     // (measured at m = 1, 8 and 48); below that, and without room for the ranges, the
     // workspace-free kernel runs.
-    const int nb = m > 16 && !q8_row_wins(mode, false, pick_q8_row(m, k, n), m) ? pick_q8_nb(m, k, n) : 0;
+    const int nb = m > 16 && !q8_row_wins(mode, false, pick_q8_row(m, k, n), m) ? pick_q8_nb(m, k, n, mode) : 0;
     const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
     if (!nb || (need && (!workspace || ws_bytes < need)))
         return q8_plain(plain_name, x, blocks, y, m, k, n, mode, stream);
@@ -798,7 +812,7 @@ int q8_packed(const char *name, const XT *x, const void *packed, float *y, int64
         DTTS_REQUIRE(aligned(x, 16) && aligned(packed, 16), "%s: x and packed must be 16-byte aligned", name);
         return q8_row_launch(name, x, packed, y, m, k, n, nbw, true, stream);
     }
-    const int nb = pick_q8_nb(m, k, n);
+    const int nb = pick_q8_nb(m, k, n, mode);
     const size_t need = dtts_gemm_q8_0_workspace_bytes(m, k, n);
     DTTS_REQUIRE(nb > 0, "%s: shape not supported", name);
     DTTS_REQUIRE(!need || (workspace && ws_bytes >= need), "%s: workspace %zu bytes < %zu needed", name, ws_bytes, need);
@@ -809,15 +823,15 @@ int q8_packed(const char *name, const XT *x, const void *packed, float *y, int64
 
 }  // namespace
 
-int q8_stack_ranges(int64_t m, int64_t k, int64_t n) {
-    const int nb = pick_q8_nb(m, k, n);
+int q8_stack_ranges(int64_t m, int64_t k, int64_t n, int32_t mode) {
+    const int nb = pick_q8_nb(m, k, n, mode);
     return nb ? static_cast<int>(k / 32 / nb) : 0;
 }
 
 int q8_stack_gemm(const float *x, const void *packed, float *y, float *part, int64_t m, int64_t k, int64_t n,
                   int32_t mode, hipStream_t stream) {
     const char *name = "dtts_stack (Q8_0 projection)";
-    const int nb = pick_q8_nb(m, k, n);
+    const int nb = pick_q8_nb(m, k, n, mode);
     DTTS_REQUIRE(nb > 0 && k % 256 == 0 && m <= 64, "%s: shape (%lld, %lld, %lld) not supported", name, (long long)m,
                  (long long)k, (long long)n);
     DTTS_REQUIRE(k / 32 / nb == 1 || part, "%s: no room for the k ranges", name);
@@ -838,7 +852,7 @@ extern "C" int dtts_gemm_q8_0_f32(const float *x, const void *blocks, float *y, 
 
 extern "C" size_t dtts_gemm_q8_0_workspace_bytes(int64_t m, int64_t k, int64_t n) {
     if (m <= 0 || k <= 0 || n <= 0 || k % 32 != 0) return 0;
-    const int nb = dtts::pick_q8_nb(m, k, n);
+    const int nb = dtts::pick_q8_nb(m, k, n, DTTS_Q8_W8A32);  // the mode with the most ranges
     const int64_t ranges = nb ? k / 32 / nb : 1;
     return ranges > 1 ? static_cast<size_t>(ranges * m * n) * sizeof(float) : 0;
 }

@@ -363,7 +363,7 @@ bool weight_kind_dense_f32(int32_t how) { return how == DTTS_WEIGHT_F32; }
 int32_t q8_mode_of(int32_t how) { return how == DTTS_WEIGHT_Q8_0_A32 ? DTTS_Q8_W8A32 : DTTS_Q8_W8A8; }
 
 int proj_ranges(int32_t how, int64_t m, int64_t k, int64_t n) {
-    return weight_kind_dense_f32(how) ? f32_proj_ranges(m, k, n) : q8_stack_ranges(m, k, n);
+    return weight_kind_dense_f32(how) ? f32_proj_ranges(m, k, n) : q8_stack_ranges(m, k, n, q8_mode_of(how));
 }
 
 // Whether the kind's projection kernel takes [m, k] x [n, k]: m <= 64, n % 64 == 0, and k a
