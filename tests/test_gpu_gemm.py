@@ -282,3 +282,52 @@ def test_gemm_f32_nt_refusals(dev):
     x = torch.zeros((65, 128), device=dev)
     with pytest.raises(ops.DttsError, match="m <= 64"):
         ops.gemm_f32_nt(x, torch.zeros((64, 128), device=dev))
+
+
+# ---------------------------------------------------------------- one-launch kernels at their edges
+# gemm_row_nt (k * ceil(m/16) <= 3072: two or three 64-k chunks per wave, up to 16 waves) and
+# gemm_q8_row (4, 6, 8 or 12 blocks per wave, up to 8 waves): every row-block count, the chunk
+# choices and the last k each takes, against the same oracle bars as the split kernels.
+
+@pytest.mark.parametrize("m,k,n,gateup", [
+    (1, 128, 64, False), (16, 2048, 256, False), (16, 3072, 128, False), (17, 1536, 512, False),
+    (33, 1024, 192, False), (48, 1024, 96, True), (64, 768, 128, False), (64, 256, 64, True), (5, 2880, 80, False),
+])
+def test_one_launch_projection_edges(dev, m, k, n, gateup):
+    assert ops.gemm_workspace_bytes(m, k, n, gateup) == 0  # the one-launch kernel takes these
+    a, w = _ab(90, m, k, 2 * n if gateup else n)
+    ad, wd = to_dev(a, dev), to_dev(w, dev)
+    gu = oracle.gemm_f16_f32acc(a, np.ascontiguousarray(w.T))
+    if gateup:
+        got, want = to_host(ops.gateup_silu(ad, wd)), oracle.swiglu_mul_f32(gu[:, :n].copy(), gu[:, n:].copy())
+    else:
+        got, want = to_host(ops.matmul_nt(ad, wd)), gu
+    ab, rl = rel(got, want)
+    assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 256, 64), (16, 768, 128), (1, 1536, 64), (1, 2048, 128), (16, 3072, 64),
+                                   (9, 2304, 64)])
+def test_q8_0_one_launch_edges(dev, m, k, n):
+    """W8A16 on GGML blocks and the packed layout, W8A32 on the packed layout, at the one-launch
+    kernel's block-per-wave choices (4, 6, 8, 12); where both layouts take it (4 blocks per wave:
+    k <= 1024 at these m) the packed and GGML W8A16 results agree bit for bit."""
+    w = synth.normal(91, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    bd = torch.from_numpy(blocks).to(dev)
+    packed = ops.q8_0_repack(bd, k) if k % 256 == 0 else None
+    xb = synth.f16_bits(synth.normal(91, "x", (m, k)))
+    x16 = synth.from_f16_bits(xb)
+    want16 = oracle.q8_0_matmul_f64(x16, blocks)
+    g16 = to_host(ops.q8_0_matmul(to_dev(xb, dev), bd, "w8a16"))
+    ab, rl = rel(g16, want16)
+    assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
+    if packed is not None:
+        p16 = to_host(ops.q8_0_matmul_packed(to_dev(xb, dev), packed, n, "w8a16"))
+        ab, rl = rel(p16, want16)
+        assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
+        if k <= 1024:
+            assert np.array_equal(p16, g16)
+        x32 = synth.normal(91, "x32", (m, k)).astype(np.float32)
+        g32 = to_host(ops.q8_0_matmul_packed(torch.from_numpy(x32).to(dev), packed, n, "w8a32"))
+        assert rel(g32, oracle.q8_0_matmul_f64(x32, blocks))[1] <= 1e-5
