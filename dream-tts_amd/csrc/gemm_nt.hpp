@@ -278,14 +278,15 @@ __global__ __launch_bounds__(1024) void gemm_row_nt(GemmParams p) {
     }
 }
 
-// Chunks of 64 k per wave for gemm_row_nt (0: not applicable): 2, or 3 when two would need more
-// than 16 waves; m <= 64 and k * ceil(m/16) <= 3072.
+// Chunks of 64 k per wave for gemm_row_nt (0: not applicable): 2, or 3 for one row block when
+// two would need more than 16 waves or do not divide k; m <= 64 and k * ceil(m/16) <= 3072.
+// launch_row_mb instantiates three chunks per wave for one row block only.
 inline int pick_row(int64_t m, int64_t k, int64_t cols) {
     if (m <= 0 || m > 64 || cols % 16 != 0 || cols / 16 >= 65536) return 0;
     const int64_t mb = (m + 15) / 16;
     if (k * mb > 3072) return 0;
     if (k % 128 == 0 && k / 128 <= 16) return 2;
-    if (k % 192 == 0 && k / 192 <= 16) return 3;
+    if (mb == 1 && k % 192 == 0 && k / 192 <= 16) return 3;
     return 0;
 }
 
@@ -296,7 +297,8 @@ hipError_t launch_row_mb(const GemmParams &p, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(MODE == 1 ? 2 : 1) * nw * mb * 64 * sizeof(float4v);
     const dim3 grid(static_cast<unsigned>((MODE == 1 ? p.n / 2 : p.n) / 16));
     const dim3 block(static_cast<unsigned>(nw * 64));
-    if constexpr (NCW == 3) {  // k > 2048 with k * ceil(m/16) <= 3072: one row block
+    if constexpr (NCW == 3) {  // pick_row takes three chunks per wave for one row block only
+        if (mb != 1) return hipErrorInvalidValue;
         gemm_row_nt<1, NCW, MODE><<<grid, block, lds, stream>>>(p);
     } else {
         switch (mb) {

@@ -313,15 +313,23 @@ __global__ __launch_bounds__(512) void gemm_q8_row(Q8Params<XT> p) {
     }
 }
 
+// The (row blocks, blocks per wave) pairs q8_row_launch instantiates: 4 blocks per wave at any
+// row-block count, 6 up to two row blocks, 8 and 12 for one (a lane holds MB x NBW activation
+// blocks in registers).
+constexpr bool q8_row_instantiated(int64_t mb, int nbw) {
+    return nbw == 4 || (nbw == 6 && mb <= 2) || ((nbw == 8 || nbw == 12) && mb == 1);
+}
+
 // Blocks per wave for gemm_q8_row (0: not applicable): the fewest of 4, 6, 8 and 12 that need at
-// most 8 waves (two waves per SIMD, so a lane's activations for its blocks fit its registers);
-// m <= 64, k * ceil(m/16) <= 3072, n a multiple of 16.
+// most 8 waves (two waves per SIMD, so a lane's activations for its blocks fit its registers) and
+// are instantiated for the row-block count; m <= 64, k * ceil(m/16) <= 3072, n a multiple of 16.
 int pick_q8_row(int64_t m, int64_t k, int64_t n) {
     if (m <= 0 || m > 64 || k % 32 != 0 || n % 16 != 0 || n / 16 >= 65536) return 0;
-    if (k * ((m + 15) / 16) > 3072) return 0;
+    const int64_t mb = (m + 15) / 16;
+    if (k * mb > 3072) return 0;
     const int64_t nblocks = k / 32;
     for (int nbw : {4, 6, 8, 12})
-        if (nblocks % nbw == 0 && nblocks / nbw <= 8) return nbw;
+        if (nblocks % nbw == 0 && nblocks / nbw <= 8 && q8_row_instantiated(mb, nbw)) return nbw;
     return 0;
 }
 
@@ -634,7 +642,7 @@ int q8_row_launch(const char *name, const XT *x, const void *w, float *y, int64_
     const size_t lds = static_cast<size_t>(nw) * mb * 64 * sizeof(float4v);
     auto launch = [&](auto mbc) {
         constexpr int MB = decltype(mbc)::value;
-        // pick_q8_row's bound k * MB <= 3072 leaves 6 blocks per wave at MB <= 2 and 8 or 12 at MB = 1
+        // the blocks per wave q8_row_instantiated lists for MB
         if constexpr (MB == 1) {
             if (nbw == 12) return q8_row_modes<MB, 12, XT>(packed, grid, threads, lds, stream, p);
             if (nbw == 8) return q8_row_modes<MB, 8, XT>(packed, grid, threads, lds, stream, p);
@@ -643,6 +651,8 @@ int q8_row_launch(const char *name, const XT *x, const void *w, float *y, int64_
             if (nbw == 6) return q8_row_modes<MB, 6, XT>(packed, grid, threads, lds, stream, p);
         q8_row_modes<MB, 4, XT>(packed, grid, threads, lds, stream, p);
     };
+    DTTS_REQUIRE(q8_row_instantiated(mb, nbw), "%s: no one-launch kernel for %d blocks per wave at %d row blocks", name,
+                 nbw, mb);
     switch (mb) {
         case 1: launch(std::integral_constant<int, 1>{}); break;
         case 2: launch(std::integral_constant<int, 2>{}); break;

@@ -331,3 +331,40 @@ def test_q8_0_one_launch_edges(dev, m, k, n):
         x32 = synth.normal(91, "x32", (m, k)).astype(np.float32)
         g32 = to_host(ops.q8_0_matmul_packed(torch.from_numpy(x32).to(dev), packed, n, "w8a32"))
         assert rel(g32, oracle.q8_0_matmul_f64(x32, blocks))[1] <= 1e-5
+
+
+# The one-launch kernels are instantiated for some (row blocks, chunks per wave) pairs only: three
+# 64-k chunks per wave (k a multiple of 192, not of 128) for one 16-row block; 6 Q8_0 blocks per
+# wave up to two row blocks, 8 and 12 for one. Shapes outside those pairs take the k-split kernels,
+# and every row of the result is computed (a shape routed to a kernel of fewer row blocks or
+# blocks per wave would leave rows or k unreduced).
+
+@pytest.mark.parametrize("m,k,n,gateup", [(48, 576, 128, False), (33, 192, 64, True), (20, 1344, 64, False),
+                                          (17, 960, 32, False), (64, 576, 64, True)])
+def test_projection_shapes_off_the_one_launch_instances(dev, m, k, n, gateup):
+    a, w = _ab(92, m, k, 2 * n if gateup else n)
+    ad, wd = to_dev(a, dev), to_dev(w, dev)
+    gu = oracle.gemm_f16_f32acc(a, np.ascontiguousarray(w.T))
+    if gateup:
+        got, want = to_host(ops.gateup_silu(ad, wd)), oracle.swiglu_mul_f32(gu[:, :n].copy(), gu[:, n:].copy())
+    else:
+        got, want = to_host(ops.matmul_nt(ad, wd)), gu
+    ab, rl = rel(got, want)
+    assert ab <= 2e-2 and rl <= 1e-4, (ab, rl)
+
+
+@pytest.mark.parametrize("m,k,n", [(24, 1280, 64), (32, 1280, 128), (40, 768, 64)])
+def test_q8_0_shapes_off_the_one_launch_instances(dev, m, k, n):
+    """k = 1280 takes 8 blocks per wave, instantiated for one row block only: at 17-32 rows the
+    packed W8A16 product goes to the A-sharing kernel; the GGML and packed results agree with
+    float64 on the dequantized weights."""
+    w = synth.normal(93, "w", (n, k), 0, 0.02)
+    blocks = ops.q8_0_quantize(w)
+    bd = torch.from_numpy(blocks).to(dev)
+    packed = ops.q8_0_repack(bd, k)
+    xb = synth.f16_bits(synth.normal(93, "x", (m, k)))
+    want = oracle.q8_0_matmul_f64(synth.from_f16_bits(xb), blocks)
+    for got in (to_host(ops.q8_0_matmul(to_dev(xb, dev), bd, "w8a16")),
+                to_host(ops.q8_0_matmul_packed(to_dev(xb, dev), packed, n, "w8a16"))):
+        ab, rl = rel(got, want)
+        assert ab <= 2e-2 and rl <= 1e-3, (ab, rl)
