@@ -421,13 +421,17 @@ extern "C" int dtts_conv1d_nlc_f32_split(const dtts_conv_desc *desc, float w_inv
                         name, (long long)d.cin, (long long)d.cout, (long long)d.k, (long long)d.dilation);
         return DTTS_ERR_UNSUPPORTED;
     }
-    DTTS_REQUIRE(std::isfinite(w_inv) && w_inv > 0.0f, "%s: w_inv %g is not a positive power of two", name, w_inv);
+    int w_exp = 0;
+    DTTS_REQUIRE(std::isfinite(w_inv) && w_inv > 0.0f && std::frexp(w_inv, &w_exp) == 0.5f,
+                 "%s: w_inv %g is not a positive power of two", name, w_inv);
     const SplitWs plan = split_ws_plan(desc);
     DTTS_REQUIRE(workspace && workspace_bytes >= plan.total && dtts::aligned(workspace, 256),
                  "%s: workspace %zu bytes (256-byte aligned) < %zu needed", name, workspace_bytes, plan.total);
     DTTS_REQUIRE(dtts::aligned(d.x, 16) && dtts::aligned(d.w, 16) && dtts::aligned(d.y, 16) &&
-                     (!d.residual || dtts::aligned(d.residual, 16)) && (!d.y_pre || dtts::aligned(d.y_pre, 16)),
-                 "%s: x, w, residual, y_pre and y must be 16-byte aligned", name);
+                     (!d.residual || dtts::aligned(d.residual, 16)) && (!d.y_pre || dtts::aligned(d.y_pre, 16)) &&
+                     (!d.bias || dtts::aligned(d.bias, 16)) && (!d.out_alpha || dtts::aligned(d.out_alpha, 16)) &&
+                     (!d.out_brecip || dtts::aligned(d.out_brecip, 16)),
+                 "%s: x, w, bias, residual, y_pre, y and the SnakeBeta vectors must be 16-byte aligned", name);
     char *ws = static_cast<char *>(workspace);
     half_t *xs = reinterpret_cast<half_t *>(ws);
     half_t *rs = d.residual ? reinterpret_cast<half_t *>(ws + plan.x) : nullptr;

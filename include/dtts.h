@@ -138,7 +138,8 @@ int dtts_conv1d_nlc_f32_ex(const dtts_conv_desc *desc, hipStream_t stream);
  * precision, and writes f32 y (and y_pre). desc->w is the split weight; every other operand is
  * f32 as dtts_conv1d_nlc_f32_ex takes it. Taken for cin and cout multiples of 32, k <= 7 with
  * (k-1)*dilation <= 64 (cout a multiple of 96 for k > 2), no prologue SnakeBeta, act 0 and no
- * out_scale; anything else returns DTTS_ERR_UNSUPPORTED. */
+ * out_scale; anything else returns DTTS_ERR_UNSUPPORTED. Every operand is 16-byte aligned, and
+ * w_inv is the power of two dtts_conv_split_weight returned (DTTS_ERR_INVALID otherwise). */
 size_t dtts_conv_split_weight_bytes(int64_t cout, int64_t k, int64_t cin);
 int dtts_conv_split_weight(const float *w_tm, int64_t cout, int64_t k, int64_t cin, void *w_split,
                            float *w_inv, hipStream_t stream);

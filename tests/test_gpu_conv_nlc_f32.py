@@ -201,7 +201,8 @@ def test_split_conv_residual_snake_out(dev, lanes, c, length, k, dil):
 
 def test_split_conv_refuses_what_it_has_no_kernel_for(dev):
     """A prologue SnakeBeta, an activation or a shape off the split tiles: DTTS_ERR_UNSUPPORTED,
-    nothing written (the shim then calls dtts_conv1d_nlc_f32_ex)."""
+    nothing written (the shim then calls dtts_conv1d_nlc_f32_ex). A bias off 16-byte alignment or
+    a w_inv that is not a power of two: DTTS_ERR_INVALID, nothing written."""
     import ctypes
 
     from dtts import DttsError
@@ -225,5 +226,12 @@ def test_split_conv_refuses_what_it_has_no_kernel_for(dev):
     w3b, invb = nlc.split_weight(to_dev(nlc.tap_major_weight(w40), dev), 7)
     with pytest.raises(DttsError, match="no split kernel"):
         nlc.conv1d_f32_split(to_dev(x40, dev), w3b, invb, k=7)
+    bias = torch.zeros(100, dtype=torch.float32, device=dev)
+    for bias_ptr, w_inv, msg in ((bias.data_ptr() + 4, inv, "16-byte aligned"), (None, inv * 1.5, "power of two")):
+        d = nlc.ConvDesc(1, 300, 96, 96, 7, 1, 6, xd.data_ptr(), w3.data_ptr(), bias_ptr, None, None, None, None,
+                         None, None, y.data_ptr(), 0, None)
+        with pytest.raises(DttsError, match=msg):
+            call("dtts_conv1d_nlc_f32_split", ctypes.byref(d), ctypes.c_float(w_inv), ws.data_ptr(), ws.numel(),
+                 stream_handle())
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())
