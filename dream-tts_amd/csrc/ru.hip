@@ -20,8 +20,8 @@
 // accumulators.
 //
 // Main loop, per KC-channel chunk: the dilated window of u (BM + (k-1)*dil rows) is loaded into
-// registers one chunk ahead, SnakeBeta'd in f32 (fma_mix reads the f16 directly) and written to
-// LDS while the previous chunk is on the matrix cores; W1's slice for the chunk goes straight
+// registers two or three chunks ahead, SnakeBeta'd in f32 (fma_mix reads the f16 directly) and
+// written to LDS while the previous chunk is on the matrix cores; W1's slice for the chunk goes straight
 // from memory to LDS (buffer_load ... lds), XOR-swizzled rows. Two LDS stages, one barrier per
 // chunk.
 #include "conv_tile.hpp"
@@ -291,11 +291,15 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
     };
 
     // Pipeline. Chunk c computes from stage c & 1. During chunk c: W1 of chunk c+1 streams into
-    // stage (c+1) & 1, the window of chunk c+2 into registers, and the registers holding chunk
+    // stage (c+1) & 1, the window of chunk c+PD into registers, and the registers holding chunk
     // c+1's window are snaked into stage (c+1) & 1. Stage (c+1) & 1 was last read by chunk c-1,
     // which every wave finished before the barrier that closed it.
     char *stage[2] = {smem, smem + Cfg::STAGE};
-    WinRegs R[2];
+    // chunk c's window in R[c % PD], loaded PD chunks ahead: three for the 192-channel unit (one
+    // workgroup per CU, so no second workgroup's work covers the loads' latency), two for the
+    // 96-channel one (two workgroups per CU; the registers of a third set slowed it)
+    constexpr int PD = C == 192 ? 3 : 2;
+    WinRegs R[PD];
     // W2 [C][C] in 16-byte segments (8 input channels of one output channel), loaded during the
     // last chunk and stored in the A-fragment order conv2 reads (see below)
     half8_t w2r[Cfg::W2_PER_T];
@@ -310,36 +314,38 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
     w_issue(0, stage[0]);
     win_load(R[0], 0);
     if (Cfg::CHUNKS > 1) win_load(R[1], KC);
-    wait_vmem();
+    if (PD == 3 && Cfg::CHUNKS > 2) win_load(R[PD - 1], 2 * KC);
+    wait_vmem_le<(Cfg::CHUNKS > PD - 1 ? PD - 1 : Cfg::CHUNKS - 1) * Cfg::A_PER_T>();  // W1 and chunk 0's window
     win_store(R[0], 0, stage[0]);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < Cfg::CHUNKS; ++c) {
         const int cur = c & 1, nxt = cur ^ 1;
         if (c + 1 < Cfg::CHUNKS) w_issue((c + 1) * KC, stage[nxt]);
-        if (c + 2 < Cfg::CHUNKS) win_load(R[cur], (c + 2) * KC);
+        if (c + PD < Cfg::CHUNKS) win_load(R[c % PD], (c + PD) * KC);
         if (c + 1 == Cfg::CHUNKS) w2_load();
         if (c + 1 < Cfg::CHUNKS) {
-            // the window of chunk c+1 (loaded a chunk ago; the compiler waits for those registers)
-            // is snaked in the shadow of chunk c's MFMAs
+            // the window of chunk c+1 (loaded PD-1 chunks ago; the compiler waits for those
+            // registers) is snaked in the shadow of chunk c's MFMAs
             const SnakeK kk = snake_consts((c + 1) * KC);
             constexpr int NE = 8 * Cfg::A_PER_T;
+            WinRegs &Rn = R[(c + 1) % PD];
             compute(stage[cur], [&](int t) {
                 if constexpr (KT > 0) {
-                    snake_elems(R[nxt], kk, t * NE / KT, (t + 1) * NE / KT);
+                    snake_elems(Rn, kk, t * NE / KT, (t + 1) * NE / KT);
                 } else {
-                    if (t < 0) snake_elems(R[nxt], kk, 0, NE);
+                    if (t < 0) snake_elems(Rn, kk, 0, NE);
                 }
             });
         } else {
             compute(stage[cur], [](int) {});
         }
-        // W1 of chunk c+1 has landed (only the newest window loads may be in flight)
-        if (c + 2 < Cfg::CHUNKS)
+        // W1 of chunk c+1 has landed (only the newest window loads, chunk c+PD's, may be in flight)
+        if (c + PD < Cfg::CHUNKS)
             wait_vmem_le<Cfg::A_PER_T>();
         else if (c + 1 < Cfg::CHUNKS)
             wait_vmem();
-        if (c + 1 < Cfg::CHUNKS) win_write(R[nxt], stage[nxt]);
+        if (c + 1 < Cfg::CHUNKS) win_write(R[(c + 1) % PD], stage[nxt]);
         stage_barrier();
     }
 
@@ -370,10 +376,10 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
     }
 
     // h2 = f16(SnakeBeta2(f16(acc))), packed as conv2's B fragments: fragment kk of position block
-    // i holds channels 16kk + {0..3, 8..11} + 4hf, in that order
+    // i holds channels 16kk + {0..3, 8..11} + 4hf, in that order (accumulator block j gives
+    // fragments 2j and 2j+1)
     half8_t h2[TM][C / 16];
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
+    auto make_h2 = [&](int j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int ch = 32 * j + 8 * g + 4 * hf;
@@ -385,10 +391,8 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
                 for (int e = 0; e < 4; ++e)
                     h2[i][2 * j + (g >> 1)][(g & 1) * 4 + e] = snake_h(static_cast<half_t>(acc[i][j][4 * g + e]), ka[e], rr[e]);
         }
-
-    // conv2: acc = b2 + W2 . h2, reduction over the channels in the fragments' order
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
+    };
+    auto b2_init = [&](int j) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const float4_t b = *reinterpret_cast<const float4_t *>(tab + 5 * C + 32 * j + 8 * g + 4 * hf);
@@ -397,17 +401,43 @@ __global__ __launch_bounds__(Cfg::THREADS, Cfg::WPE) void ru_nlc_f16(RuArgs q) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = b[e];
         }
-    __syncthreads();  // W2 in LDS
+    };
     const half_t *w2l = W2s + l32 * Cfg::W2_PITCH + 8 * hf;
+    auto conv2_step = [&](int j, int kk) {
+        const half8_t a = *reinterpret_cast<const half8_t *>(w2l + 32 * j * Cfg::W2_PITCH + 16 * kk);
 #pragma unroll
-    for (int kk = 0; kk < C / 16; ++kk)
+        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, h2[i][kk], acc[i][j], 0, 0, 0);
+    };
+    // conv2: acc = b2 + W2 . h2, each output block's k-steps summed in order
+    if constexpr (TN >= 6) {
+        // block s's accumulators restart at b2 once its fragments exist and take k-steps
+        // 0 .. 2s+1, the blocks before it k-steps 2s and 2s+1: block s+1's SnakeBeta runs in the
+        // shadow of step s's MFMAs
+        make_h2(0);
+        __syncthreads();  // W2 in LDS
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const half8_t a = *reinterpret_cast<const half8_t *>(w2l + 32 * j * Cfg::W2_PITCH + 16 * kk);
+        for (int s2 = 0; s2 < TN; ++s2) {
+            b2_init(s2);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, h2[i][kk], acc[i][j], 0, 0, 0);
+            for (int kk = 0; kk < 2 * s2 + 2; ++kk) {
+                conv2_step(s2, kk);
+                if (kk >= 2 * s2)
+#pragma unroll
+                    for (int j = 0; j < s2; ++j) conv2_step(j, kk);
+            }
+            if (s2 + 1 < TN) make_h2(s2 + 1);
         }
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) make_h2(j);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b2_init(j);
+        __syncthreads();  // W2 in LDS
+#pragma unroll
+        for (int kk = 0; kk < C / 16; ++kk)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) conv2_step(j, kk);
+    }
 
     // y = f16(acc + u), y_pre, SnakeBeta_out. The values are made in the transposed layout (a
     // lane: one position, runs of four channels) and go out through the wave's own LDS block, so
