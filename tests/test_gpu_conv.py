@@ -189,15 +189,15 @@ def test_conv_rejects_bad_shapes(dev):
         nlc.conv1d(x, w[:, :100].contiguous(), None, k=7)
 
 
-@pytest.mark.parametrize("lanes,c,length,dil,out_snake", [(2, 96, 3000, 9, True), (3, 96, 700, 1, False),
-                                                           (2, 192, 1100, 3, True), (1, 192, 257, 9, False),
-                                                           (2, 96, 900, 3, True), (2, 192, 600, 1, False),
-                                                           (2, 96, 500, 2, True), (1, 192, 300, 5, False)])
-def test_fused_residual_unit_matches_composed_chain(dev, lanes, c, length, dil, out_snake):
+@pytest.mark.parametrize("lanes,c,length,dil,out_snake,k", [
+    (2, 96, 3000, 9, True, 7), (3, 96, 700, 1, False, 7), (2, 192, 1100, 3, True, 7), (1, 192, 257, 9, False, 7),
+    (2, 96, 900, 3, True, 7), (2, 192, 600, 1, False, 7), (2, 96, 500, 2, True, 7), (1, 192, 300, 5, False, 7),
+    (2, 192, 800, 4, True, 3), (2, 96, 600, 2, False, 5), (1, 192, 300, 1, False, 1), (2, 96, 520, 1, True, 1)])
+def test_fused_residual_unit_matches_composed_chain(dev, lanes, c, length, dil, out_snake, k):
     """dtts_residual_unit_nlc_f16 against the oracle's unfused chain with the same f16 storage
-    points: h = conv7(snake1(x)); h2 = snake2(h); y = conv1(h2) + x; [snake_out(y)]. The codec's
-    dilations (1, 3, 9) at both widths, and others (2, 5) a caller may pass."""
-    k = 7
+    points: h = conv_k(snake1(x)); h2 = snake2(h); y = conv1(h2) + x; [snake_out(y)]. The codec's
+    k = 7 and dilations (1, 3, 9) at both widths, other dilations (2, 5) a caller may pass, and
+    k = 1, 3, 5 (the kernel form with the tap count at run time)."""
     x = synth.f16_bits(synth.normal(44, "x", (lanes, length, c)))
     w1 = synth.f16_bits(synth.normal(44, "w1", (c, c, k), 0, np.sqrt(1.0 / (c * k))))
     w2 = synth.f16_bits(synth.normal(44, "w2", (c, c, 1), 0, np.sqrt(1.0 / c)))
