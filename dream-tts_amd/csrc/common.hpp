@@ -48,6 +48,27 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
+// ---------------------------------------------------------------- ordered sums of k-range partials
+
+// The sum of n float4 partials `stride` floats apart, in range order, with up to U of the loads
+// requested together: a plain loop issues each load only after the previous add, one memory round
+// trip per range. ZERO_START: the sum is 0 + p[0] + p[stride] + ... (as a loop from zero adds);
+// otherwise it starts at p[0].
+template <int U, bool ZERO_START>
+__device__ __forceinline__ float4_t ordered_sum4(const float *p, int n, int64_t stride) {
+    float4_t u = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < n; k0 += U) {
+        float4_t v[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k)
+            if (k0 + k < n) v[k] = *reinterpret_cast<const float4_t *>(p + (k0 + k) * stride);
+#pragma unroll
+        for (int k = 0; k < U; ++k)
+            if (k0 + k < n) u = (!ZERO_START && k0 + k == 0) ? v[k] : u + v[k];
+    }
+    return u;
+}
+
 // ---------------------------------------------------------------- division by a constant
 
 // n / d for 32-bit n and a divisor fixed at launch: q = (umulhi(n, m) + n) >> l with

@@ -158,12 +158,11 @@ __global__ __launch_bounds__(256) void gemm_merge_splits(GemmParams p, int yspli
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t row = e / c4n;
         const int col = static_cast<int>(e - row * c4n) * 4;
-        float4v s0 = float4v{0.f, 0.f, 0.f, 0.f}, s1 = float4v{0.f, 0.f, 0.f, 0.f};
-        for (int y = 0; y < ysplit; ++y) {
-            const float *pr = p.part + (static_cast<int64_t>(y) * p.m + row) * p.n + col;
-            s0 += *reinterpret_cast<const float4v *>(pr);
-            if constexpr (MODE == 1) s1 += *reinterpret_cast<const float4v *>(pr + p.n / 2);
-        }
+        const float *pr = p.part + row * p.n + col;
+        const int64_t stride = static_cast<int64_t>(p.m) * p.n;
+        const float4v s0 = ordered_sum4<8, true>(pr, ysplit, stride);
+        float4v s1 = float4v{0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == 1) s1 = ordered_sum4<8, true>(pr + p.n / 2, ysplit, stride);
 #pragma unroll
         for (int i = 0; i < 4; ++i) gemm_store<MODE>(p, row, col + i, s0[i], s1[i]);
     }

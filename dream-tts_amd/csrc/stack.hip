@@ -62,20 +62,10 @@ struct Partials {
     int64_t stride;
 };
 
-// The ordered sum of ys partial float4s `stride` floats apart: the first U requested together,
-// then summed in order (a plain loop would wait for each load before issuing the next).
+// The ordered sum of ys partial float4s `stride` floats apart, U of the loads requested together.
 template <int U>
 __device__ __forceinline__ float4_t sum_parts(const float *p, int ys, int64_t stride) {
-    float4_t v[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-        if (k < ys) v[k] = *reinterpret_cast<const float4_t *>(p + k * stride);
-    float4_t u = v[0];
-#pragma unroll
-    for (int k = 1; k < U; ++k)
-        if (k < ys) u += v[k];
-    for (int k = U; k < ys; ++k) u += *reinterpret_cast<const float4_t *>(p + k * stride);
-    return u;
+    return ordered_sum4<U, false>(p, ys, stride);
 }
 
 // Each component rounded to f16 and widened back.
