@@ -236,17 +236,40 @@ __global__ __launch_bounds__(256) void decode_attn_merge(const float *part, OutT
     int lo, hi;
     sp.get(lane_idx, lo, hi);
     const int nch = chunks_of(lo, hi);
+    constexpr int U = 8;  // chunk states requested together (a loop would wait for each in turn)
     for (int t = threadIdx.x; t < GQA * D; t += 256) {
         const int g = t / D, d = t - (t / D) * D;
         const float *pr = part + (static_cast<int64_t>(bh) * max_chunks * GQA + g) * (D + 2);
         const int64_t stride = static_cast<int64_t>(GQA) * (D + 2);
-        float mx = -INFINITY;
-        for (int c = 0; c < nch; ++c) mx = fmaxf(mx, pr[c * stride + D + 1]);
         float num = 0.0f, den = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-            const float f = __builtin_expf(pr[c * stride + D + 1] - mx);
-            num += pr[c * stride + d] * f;
-            den += pr[c * stride + D] * f;
+        if (nch <= U) {
+            float mc[U], nc[U], dc[U];
+#pragma unroll
+            for (int c = 0; c < U; ++c)
+                if (c < nch) {
+                    mc[c] = pr[c * stride + D + 1];
+                    nc[c] = pr[c * stride + d];
+                    dc[c] = pr[c * stride + D];
+                }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < U; ++c)
+                if (c < nch) mx = fmaxf(mx, mc[c]);
+#pragma unroll
+            for (int c = 0; c < U; ++c)
+                if (c < nch) {
+                    const float f = __builtin_expf(mc[c] - mx);
+                    num += nc[c] * f;
+                    den += dc[c] * f;
+                }
+        } else {
+            float mx = -INFINITY;
+            for (int c = 0; c < nch; ++c) mx = fmaxf(mx, pr[c * stride + D + 1]);
+            for (int c = 0; c < nch; ++c) {
+                const float f = __builtin_expf(pr[c * stride + D + 1] - mx);
+                num += pr[c * stride + d] * f;
+                den += pr[c * stride + D] * f;
+            }
         }
         store_out(out + (static_cast<int64_t>(bh) * GQA + g) * D + d, num / den);
     }
