@@ -105,3 +105,15 @@ def test_decode_attention_rejects_bad_arguments(dev):
     big_k = torch.zeros((257, 1, 4, 64), dtype=torch.float16, device=dev)
     with pytest.raises(DttsError, match="lanes"):
         ops.decode_attention(big_q, big_k, big_k, 4)
+
+
+def test_decode_attention_split_past_eight_chunks(dev):
+    """The merge requests up to eight chunks' states at once and loops past that: windows of
+    4700 (ten chunks of 512), 4096 (eight) and 4097 (nine, the last of one position)."""
+    b, n_kv, gqa, cap = 3, 2, 2, 4700
+    q, k, v = _inputs(75, b, n_kv, gqa, cap)
+    span = np.array([4700, 4096, 4200], np.int32)
+    ws = np.array([0, 0, 103], np.int32)
+    want = oracle.decode_attention_f32(q, k, v, span, ws)
+    split = _run(dev, q, k, v, span, ws)
+    assert rel(split, want)[1] < 1e-5
