@@ -240,8 +240,16 @@ __global__ __launch_bounds__(256) void qk_rope_span_kernel(const T *qkv, const f
     const bool is_q = h < heads;
     const bool act = lane < half;
     auto ld = [&](const T *q) {
-        float v = static_cast<float>(q[0]);
-        for (int y = 1; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
+        // the first eight ranges' partials requested together, summed in range order
+        float w[8];
+#pragma unroll
+        for (int y = 0; y < 8; ++y)
+            if (y < ys) w[y] = static_cast<float>(q[y * ystride]);
+        float v = w[0];
+#pragma unroll
+        for (int y = 1; y < 8; ++y)
+            if (y < ys) v += w[y];
+        for (int y = 8; y < ys; ++y) v += static_cast<float>(q[y * ystride]);
         return round16 ? static_cast<float>(static_cast<half_t>(v)) : v;
     };
     float x1 = 0.0f, x2 = 0.0f;
