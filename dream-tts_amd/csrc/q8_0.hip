@@ -498,8 +498,16 @@ __global__ __launch_bounds__(256) void gemm_q8_lds(Q8Params<XT> p, float *part) 
 // y = the k ranges' partials summed in range order.
 __global__ __launch_bounds__(256) void q8_merge(const float *part, float *y, int64_t mn, int ranges) {
     for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < mn; e += int64_t(gridDim.x) * 256) {
-        float s = part[e];
-        for (int q = 1; q < ranges; ++q) s += part[q * mn + e];
+        // the first eight ranges' partials requested together, summed in range order
+        float w[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (q < ranges) w[q] = part[q * mn + e];
+        float s = w[0];
+#pragma unroll
+        for (int q = 1; q < 8; ++q)
+            if (q < ranges) s += w[q];
+        for (int q = 8; q < ranges; ++q) s += part[q * mn + e];
         y[e] = s;
     }
 }
