@@ -41,8 +41,47 @@ __device__ __forceinline__ void split_store8(half_t *dst, int cv, const float (&
     *reinterpret_cast<half8_t *>(dst + cv) = lo;
 }
 
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+
+// The tile's per-column constants in LDS, past the stages and the epilogue's staging: the f32 bias,
+// and SnakeBeta's alpha and 1/beta, of its BN GEMM columns. They are written before the main loop,
+// whose barriers publish them, so the epilogue reads them from LDS instead of waiting on global
+// loads inside its loop.
+template <typename Cfg>
+struct SplitTab {
+    static constexpr int OFFSET = Cfg::TAB_OFFSET;
+    static constexpr int BYTES = OFFSET + 3 * Cfg::BN * 4;
+};
+
+template <typename Cfg>
+__device__ __forceinline__ void split_table(char *smem, int n0, const SplitArgs &a) {
+    float *tab = reinterpret_cast<float *>(smem + SplitTab<Cfg>::OFFSET);
+    for (int c = threadIdx.x; c < Cfg::BN; c += Cfg::THREADS) {
+        tab[c] = a.bias ? a.bias[n0 + c] : 0.0f;
+        tab[Cfg::BN + c] = a.a_out ? a.a_out[n0 + c] : 0.0f;
+        tab[2 * Cfg::BN + c] = a.r_out ? a.r_out[n0 + c] : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void split_store8_buf(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t lo_off,
+                                                 const float (&v)[8]) {
+    half8_t hi, lo;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        hi[q] = static_cast<half_t>(v[q]);
+        lo[q] = static_cast<half_t>(v[q] - static_cast<float>(hi[q]));
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_t, hi), rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_t, lo), rs, off + lo_off, 0, 0);
+}
+
 // The tile's outputs, one 32-row block per wave at a time through the wave's LDS region (as the
-// f16 epilogue does): a lane then owns 8 consecutive GEMM columns of one position.
+// f16 epilogue does): a lane then owns 8 consecutive GEMM columns of one position. The residual,
+// y_pre and y rows of the tile's lane are reached through buffer resources sized to that lane's
+// rows, and a position past the sequence gets an offset beyond them: its loads read zeros and its
+// stores are dropped by the hardware's range check, so no branch splits a block and the loads of
+// a block's groups are all in flight together (conv_split_supported keeps a lane's output rows
+// under 2^31 bytes).
 template <typename Cfg>
 __device__ __forceinline__ void split_epilogue(const float16_t (&acc)[Cfg::TM][Cfg::TN], char *smem, int64_t row0,
                                                int l0, int n0, const SplitArgs &a) {
@@ -55,9 +94,18 @@ __device__ __forceinline__ void split_epilogue(const float16_t (&acc)[Cfg::TM][C
     const int l32 = lane & 31, hf = lane >> 5;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     float *E = reinterpret_cast<float *>(smem) + wave * 32 * Cfg::EPI_PITCH;
+    const float *tab = reinterpret_cast<const float *>(smem + SplitTab<Cfg>::OFFSET);
     const int nw = n0 + wn * Cfg::WTN;
     const int cv = a.cv, R = a.c.cout / a.cv;
     const int lmax = a.c.L;
+    const uint32_t lane_bytes = static_cast<uint32_t>(static_cast<int64_t>(lmax) * R * 2 * cv * 2);
+    const int64_t base = row0 * R * 2 * cv;
+    const __amdgpu_buffer_rsrc_t rs_res =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(a.res ? a.res + base : a.y + base), 0, lane_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs_y = __builtin_amdgcn_make_buffer_rsrc(a.y + base, 0, lane_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs_yp =
+        __builtin_amdgcn_make_buffer_rsrc(a.y_pre ? a.y_pre + base : a.y + base, 0, lane_bytes, kBufferWord3);
+    const uint32_t lo_off = static_cast<uint32_t>(cv * 2);
 #pragma unroll
     for (int i = 0; i < Cfg::TM; ++i) {
         const int lb = l0 + wm * Cfg::WTM + i * 32;
@@ -74,37 +122,38 @@ __device__ __forceinline__ void split_epilogue(const float16_t (&acc)[Cfg::TM][C
             const int g = lane + 64 * u;
             const int mr = g / CG, cg = g - (g / CG) * CG;
             const int l = lb + mr;
-            if (l >= lmax) continue;
             const int n = nw + cg * 8;
             const int ph = n / cv, c = n - ph * cv;
-            const int64_t off = ((row0 + l) * R + ph) * 2 * cv + c;
+            const uint32_t off = l < lmax ? static_cast<uint32_t>(((static_cast<int64_t>(l) * R + ph) * 2 * cv + c) * 2)
+                                          : kOutOfRange;
             const float4_t *src = reinterpret_cast<const float4_t *>(E + mr * Cfg::EPI_PITCH + cg * 8);
             const float4_t v0 = src[0], v1 = src[1];
-            const float4_t b0 = a.bias ? *reinterpret_cast<const float4_t *>(a.bias + n) : float4_t{0.f, 0.f, 0.f, 0.f};
-            const float4_t b1 = a.bias ? *reinterpret_cast<const float4_t *>(a.bias + n + 4) : float4_t{0.f, 0.f, 0.f, 0.f};
+            const int tc = n - n0;
+            const float4_t b0 = *reinterpret_cast<const float4_t *>(tab + tc);
+            const float4_t b1 = *reinterpret_cast<const float4_t *>(tab + tc + 4);
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
             const float b[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
 #pragma unroll
             for (int q = 0; q < 8; ++q) v[q] = v[q] * a.w_inv + b[q];
             if (a.res) {
-                const half8_t rh = *reinterpret_cast<const half8_t *>(a.res + off);
-                const half8_t rl = *reinterpret_cast<const half8_t *>(a.res + off + cv);
+                const half8_t rh = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs_res, off, 0, 0));
+                const half8_t rl = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs_res, off + lo_off, 0, 0));
 #pragma unroll
                 for (int q = 0; q < 8; ++q) v[q] = v[q] + (static_cast<float>(rh[q]) + static_cast<float>(rl[q]));
             }
-            if (a.y_pre) split_store8(a.y_pre + off, cv, v);
+            if (a.y_pre) split_store8_buf(rs_yp, off, lo_off, v);
             if (a.a_out) {
-                const float4_t a0 = *reinterpret_cast<const float4_t *>(a.a_out + n);
-                const float4_t a1 = *reinterpret_cast<const float4_t *>(a.a_out + n + 4);
-                const float4_t r0 = *reinterpret_cast<const float4_t *>(a.r_out + n);
-                const float4_t r1 = *reinterpret_cast<const float4_t *>(a.r_out + n + 4);
+                const float4_t a0 = *reinterpret_cast<const float4_t *>(tab + Cfg::BN + tc);
+                const float4_t a1 = *reinterpret_cast<const float4_t *>(tab + Cfg::BN + tc + 4);
+                const float4_t r0 = *reinterpret_cast<const float4_t *>(tab + 2 * Cfg::BN + tc);
+                const float4_t r1 = *reinterpret_cast<const float4_t *>(tab + 2 * Cfg::BN + tc + 4);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     v[q] = snake_f32(v[q], a0[q], r0[q]);
                     v[q + 4] = snake_f32(v[q + 4], a1[q], r1[q]);
                 }
             }
-            split_store8(a.y + off, cv, v);
+            split_store8_buf(rs_y, off, lo_off, v);
         }
     }
 }
@@ -112,11 +161,12 @@ __device__ __forceinline__ void split_epilogue(const float16_t (&acc)[Cfg::TM][C
 template <typename Cfg, int KT>
 __global__ __launch_bounds__(Cfg::THREADS, Cfg::MIN_WG) void conv_split_mfma(SplitArgs a) {
     static_assert(Cfg::STAGING == kStageDirect, "split operands use direct staging");
-    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS_BYTES];
+    __shared__ __attribute__((aligned(16))) char smem[SplitTab<Cfg>::BYTES];
     int lane_idx, m_tile, n_tile;
     if (!conv_tile_coords(a.c, lane_idx, m_tile, n_tile)) return;
     const int l0 = m_tile * Cfg::BM;
     const int n0 = n_tile * Cfg::BN;
+    split_table<Cfg>(smem, n0, a);
     const half_t *xl = a.c.x + static_cast<int64_t>(lane_idx) * a.c.L * (2 * (a.c.cin / 3));
     float16_t acc[Cfg::TM][Cfg::TN];
 #pragma unroll
@@ -262,7 +312,11 @@ __global__ __launch_bounds__(256) void split_act_kernel(const float *x, half_t *
 bool conv_split_supported(int64_t lanes, int64_t len, int64_t cs, int64_t cout, int64_t k, int64_t dil) {
     int hmax;
     const int kmax = split_class(k, dil, hmax);
-    if (!kmax || cs % 32 != 0 || cout % 32 != 0 || !direct_offsets_fit(len, 3 * cs, cout, k)) return false;
+    // a lane's split output rows (len positions x cout GEMM columns, 4 bytes each) are one epilogue
+    // buffer range, below the 2^31 offset that marks rows past the sequence
+    if (!kmax || cs % 32 != 0 || cout % 32 != 0 || !direct_offsets_fit(len, 3 * cs, cout, k) ||
+        len * cout * 4 >= (int64_t(1) << 31))
+        return false;
     return with_split_tile_k(kmax, lanes, static_cast<int>(len), static_cast<int>(3 * cs), static_cast<int>(cout),
                              [](auto) {});
 }
