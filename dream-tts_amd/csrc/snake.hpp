@@ -13,12 +13,40 @@ constexpr float kInv2Pi = 0.159154943091895335768883763372514362f;
 // it is used wherever the snake's result is stored as f16.
 __device__ __forceinline__ float sin_rev_f16out(float t) { return __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(t)); }
 
-// y = x + r * sin^2(a x). The f32 form uses the full-precision library sinf: f32 outputs are
-// held to the reference's 1e-6-of-scale accuracy bound (crates/tts-nn/src/fused.rs:2356-2391).
-__device__ __forceinline__ float snake_f32(float x, float a, float r) {
-    const float s = sinf(a * x);
-    return x + r * (s * s);
+// sin^2(a x) for f32 a and x, within 1.5e-7 of the exact value for |a x| <= 2^20 (measured
+// against f64 over 1.2e8 random points). The product a x is carried exactly as the
+// pair th + tl (the fma gives the rounding error of th). Cody and Waite's additive reduction
+// takes off the nearest multiple k of pi/2, held as three f32 parts P1 + P2 + P3 (P1 = f32(pi/2),
+// each next part the f32 rounding of what is left; their sum is pi/2 to 1.1e-23): th - k P1 is
+// exact in the fma, the later parts and tl are small. sin r on |r| <= pi/4 is its Taylor series
+// through r^9 (truncation under 2e-9), and sin^2(r + k pi/2) is sin^2 r for even k and
+// 1 - sin^2 r for odd k, so no cosine is needed. Larger and non-finite arguments take the library
+// sinf of the rounded product. The library sinf of the rounded product everywhere loses up to
+// 1e-6 to that rounding alone at |a x| ~ 30 (where the codec's convs drive SnakeBeta), and costs
+// about twice the instructions.
+__device__ __forceinline__ float sin2_f32(float a, float x) {
+    const float th = a * x;
+    if (!(__builtin_fabsf(th) <= 0x1p20f)) {
+        const float s = sinf(th);
+        return s * s;
+    }
+    const float tl = __builtin_fmaf(a, x, -th);
+    const float k = __builtin_rintf(th * 0x1.45f306p-1f);   // 2/pi
+    float r = __builtin_fmaf(-k, 0x1.921fb6p+0f, th);       // P1
+    r = __builtin_fmaf(-k, -0x1.777a5cp-25f, r);            // P2
+    r = __builtin_fmaf(-k, -0x1.ee59dap-50f, r + tl);       // P3
+    const float r2 = r * r;
+    float p = __builtin_fmaf(r2, 0x1.71de3ap-19f, -0x1.a01a02p-13f);  // 1/9!, -1/7!
+    p = __builtin_fmaf(r2, p, 0x1.111112p-7f);                       // 1/5!
+    p = __builtin_fmaf(r2, p, -0x1.555556p-3f);                      // -1/3!
+    const float s = __builtin_fmaf(r * r2, p, r);
+    const float s2 = s * s;
+    return (static_cast<int>(k) & 1) ? 1.0f - s2 : s2;
 }
+
+// y = x + r * sin^2(a x). f32 outputs are held to the reference's 1e-6-of-scale accuracy bound
+// (crates/tts-nn/src/fused.rs:2356-2391).
+__device__ __forceinline__ float snake_f32(float x, float a, float r) { return x + r * sin2_f32(a, x); }
 
 // The f16-storage snake with ka = a / (2 pi) precomputed per channel: x * ka, fract, sin, s*s
 // and one fma (which reads x as f16 directly: v_fma_mix_f32) per element.

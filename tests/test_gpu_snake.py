@@ -68,6 +68,30 @@ def test_snake_f32_wide_sweep_accuracy(dev):
     assert np.max(np.abs(got - want) / scale) < 2e-6
 
 
+def test_snake_f32_exact_product_reduction(dev):
+    # The f32 SnakeBeta reduces the exact product a x, not its f32 rounding: with x in [-1, 1],
+    # r = 1 and a up to 2^20, y is within 4e-7 of x + sin^2(a x) in f64 (the product's rounding
+    # alone would move sin^2 by up to |a x| 2^-24, 0.03 at 2^19). Past |a x| = 2^20 y stays in
+    # [x, x + r]; inf and nan give nan.
+    c, length = 16, 2048
+    x = synth.uniform(23, "x", (length, c), -1.0, 1.0)
+    a = (2.0 ** np.linspace(-2.0, 20.0, c)).astype(np.float32)
+    r = np.ones(c, np.float32)
+    got = to_host(ops.snake_beta_nlc(to_dev(x, dev), to_dev(a, dev), to_dev(r, dev))).astype(np.float64)
+    want = oracle.snake_nlc_f64(x, a, r)
+    assert np.max(np.abs(got - want)) < 4e-7
+
+    big = np.array([[3.0e6, -7.5e8, 1.0e30, np.inf, -np.inf, np.nan, 2.0e6, -1.0]], np.float32)
+    ab = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 0.7, 3.0e6], np.float32)
+    rb = np.full(8, 2.5, np.float32)
+    yb = to_host(ops.snake_beta_nlc(to_dev(big, dev), to_dev(ab, dev), to_dev(rb, dev)))[0]
+    assert np.all(np.isnan(yb[3:6]))
+    for j in (0, 1, 2, 6, 7):
+        lo, hi = sorted((float(big[0, j]), float(big[0, j]) + 2.5))
+        tol = np.spacing(np.float32(abs(big[0, j]) + 2.5))
+        assert lo - tol <= yb[j] <= hi + tol, (j, yb[j])
+
+
 @pytest.mark.parametrize("rows,c", [(33, 7), (601, 1536), (4801, 24), (2000, 96), (9, 8)])
 def test_snake_nlc_f16(dev, rows, c):
     x = synth.f16_bits(synth.normal(22, "x", (rows, c), 0, 3))
