@@ -117,10 +117,13 @@ __global__ __launch_bounds__(64 * WM * WN, WM * WN / 2) void conv_nlc_f32_mfma(N
                 float4_t v = xr[i];
                 if constexpr (SNAKE) {
                     const int s = l0 - p.pad_left + j;
-                    if (s >= 0 && s < p.L)
+                    if (s >= 0 && s < p.L) {
+                        float x[4] = {v[0], v[1], v[2], v[3]}, a[4], r[4];
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            v[q] = snake_f32(v[q], p.a_in[c0 + c4 * 4 + q], p.r_in[c0 + c4 * 4 + q]);
+                        for (int q = 0; q < 4; ++q) a[q] = p.a_in[c0 + c4 * 4 + q], r[q] = p.r_in[c0 + c4 * 4 + q];
+                        snake_f32_group<4>(x, a, r);
+                        v = float4_t{x[0], x[1], x[2], x[3]};
+                    }
                 }
                 *reinterpret_cast<float4_t *>(&xs[b][j * XP + c4 * 4]) = v;
             }
@@ -350,8 +353,12 @@ __global__ __launch_bounds__(256) void conv_nlc_f32_narrow(NlcF32Params p) {
                 float4_t x = buf[i];
                 const int s = l0 - p.pad_left + r;
                 if (p.a_in && s >= 0 && s < p.L) {
+                    float xv[4] = {x[0], x[1], x[2], x[3]};
+                    float a[4], rr[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) x[j] = snake_f32(x[j], p.a_in[c0 + q * 4 + j], p.r_in[c0 + q * 4 + j]);
+                    for (int j = 0; j < 4; ++j) a[j] = p.a_in[c0 + q * 4 + j], rr[j] = p.r_in[c0 + q * 4 + j];
+                    snake_f32_group<4>(xv, a, rr);
+                    x = float4_t{xv[0], xv[1], xv[2], xv[3]};
                 }
                 *reinterpret_cast<float4_t *>(win + r * kNarrowPitch + q * 4) = x;
             }

@@ -147,11 +147,9 @@ __device__ __forceinline__ void split_epilogue(const float16_t (&acc)[Cfg::TM][C
                 const float4_t a1 = *reinterpret_cast<const float4_t *>(tab + Cfg::BN + tc + 4);
                 const float4_t r0 = *reinterpret_cast<const float4_t *>(tab + 2 * Cfg::BN + tc);
                 const float4_t r1 = *reinterpret_cast<const float4_t *>(tab + 2 * Cfg::BN + tc + 4);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    v[q] = snake_f32(v[q], a0[q], r0[q]);
-                    v[q + 4] = snake_f32(v[q + 4], a1[q], r1[q]);
-                }
+                const float aa[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                const float rr[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+                snake_f32_group<8>(v, aa, rr);
             }
             split_store8_buf(rs_y, off, lo_off, v);
         }

@@ -24,12 +24,11 @@ __device__ __forceinline__ float sin_rev_f16out(float t) { return __builtin_amdg
 // sinf of the rounded product. The library sinf of the rounded product everywhere loses up to
 // 1e-6 to that rounding alone at |a x| ~ 30 (where the codec's convs drive SnakeBeta), and costs
 // about twice the instructions.
-__device__ __forceinline__ float sin2_f32(float a, float x) {
+__device__ __forceinline__ bool sin2_f32_reducible(float a, float x) { return __builtin_fabsf(a * x) <= 0x1p20f; }
+
+// The reduction and series alone, for arguments sin2_f32_reducible accepts.
+__device__ __forceinline__ float sin2_f32_reduced(float a, float x) {
     const float th = a * x;
-    if (!(__builtin_fabsf(th) <= 0x1p20f)) {
-        const float s = sinf(th);
-        return s * s;
-    }
     const float tl = __builtin_fmaf(a, x, -th);
     const float k = __builtin_rintf(th * 0x1.45f306p-1f);   // 2/pi
     float r = __builtin_fmaf(-k, 0x1.921fb6p+0f, th);       // P1
@@ -42,6 +41,34 @@ __device__ __forceinline__ float sin2_f32(float a, float x) {
     const float s = __builtin_fmaf(r * r2, p, r);
     const float s2 = s * s;
     return (static_cast<int>(k) & 1) ? 1.0f - s2 : s2;
+}
+
+__device__ __forceinline__ float sin2_f32(float a, float x) {
+    if (!sin2_f32_reducible(a, x)) {
+        const float s = sinf(a * x);
+        return s * s;
+    }
+    return sin2_f32_reduced(a, x);
+}
+
+// SnakeBeta over N values (parameters per value): the reduced form for all of them as straight-line
+// code, then one branch for the group, taken only when an argument is past the reduction's range.
+// A branch per value (as sin2_f32 has) serialises the values and costs more than their arithmetic.
+template <int N>
+__device__ __forceinline__ void snake_f32_group(float (&v)[N], const float (&a)[N], const float (&r)[N]) {
+    float s2[N];
+    bool far = false;
+#pragma unroll
+    for (int q = 0; q < N; ++q) {
+        s2[q] = sin2_f32_reduced(a[q], v[q]);
+        far |= !sin2_f32_reducible(a[q], v[q]);
+    }
+    if (far) {
+#pragma unroll
+        for (int q = 0; q < N; ++q) s2[q] = sin2_f32(a[q], v[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < N; ++q) v[q] = v[q] + r[q] * s2[q];
 }
 
 // y = x + r * sin^2(a x). f32 outputs are held to the reference's 1e-6-of-scale accuracy bound

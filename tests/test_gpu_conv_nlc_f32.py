@@ -199,6 +199,32 @@ def test_split_conv_residual_snake_out(dev, lanes, c, length, k, dil):
     assert rel(to_host(y), oracle.snake_nlc_f32(want_pre, a2, r2))[1] < 1e-5
 
 
+def test_split_conv_snake_out_past_the_reduction_range(dev):
+    """Every eighth channel's alpha puts |alpha * y_pre| past 2^20, where the epilogue's group of
+    eight takes the library sine for all eight values: the far channels keep y - y_pre in [0, r]
+    (at alpha 3e9 their sine turns on y_pre's last bits, which the split store rounds), the other
+    channels (the far ones' neighbours in the same groups) are SnakeBeta of y_pre within 1e-5 of
+    max(|y_pre|, r, 1) (fused.rs:2356-2391's scale; y_pre is stored split, to 2^-22 of itself)."""
+    lanes, c, length, k = 1, 96, 700, 7
+    x, w, b = _case(113, lanes, length, c, c, k)
+    a2 = synth.uniform(113, "a2", (c,), 0.5, 1.5)
+    a2[3::8] = 3.0e9
+    r2 = (1.0 / synth.uniform(113, "b2", (c,), 0.5, 1.5)).astype(np.float32)
+    w3, inv = nlc.split_weight(to_dev(nlc.tap_major_weight(w), dev), k)
+    y_pre, y = nlc.conv1d_f32_split(to_dev(x, dev), w3, inv, to_dev(b, dev), k=k, dilation=1,
+                                    snake_out=(to_dev(a2, dev), to_dev(r2, dev)), want_pre=True)
+    y_pre, y = to_host(y_pre).astype(np.float64), to_host(y).astype(np.float64)
+    big = np.zeros(c, bool)
+    big[3::8] = True
+    assert (np.abs(a2 * y_pre) > 2.0 ** 20)[..., big].mean() > 0.99
+    scale = np.maximum(np.maximum(np.abs(y_pre), r2), 1.0)
+    want = y_pre + r2 * np.sin(a2 * y_pre) ** 2
+    assert np.max((np.abs(y - want) / scale)[..., ~big]) < 1e-5
+    d = (y - y_pre)[..., big]
+    tol = 1e-6 * scale[..., big]
+    assert np.all(d >= -tol) and np.all(d <= r2[big] + tol)
+
+
 def test_split_conv_refuses_what_it_has_no_kernel_for(dev):
     """A prologue SnakeBeta, an activation or a shape off the split tiles: DTTS_ERR_UNSUPPORTED,
     nothing written (the shim then calls dtts_conv1d_nlc_f32_ex). A bias off 16-byte alignment or
