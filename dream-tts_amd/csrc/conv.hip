@@ -174,7 +174,9 @@ Choice choose(const dtts_conv_desc *d) {
     const bool aligned16 = aligned(d->x, 16) && aligned(d->w, 16) && aligned(d->y, 16) &&
                            (!d->bias || aligned(d->bias, 16)) && (!d->residual || aligned(d->residual, 16)) &&
                            (!d->y_pre || aligned(d->y_pre, 16)) && (!d->out_scale || aligned(d->out_scale, 16));
-    if (!aligned16 || d->cin % 32 != 0 || d->cout % 32 != 0 || d->k > 7) return c;
+    // the tile epilogue addresses a lane's output rows (len x cout halves) as one buffer range
+    if (!aligned16 || d->cin % 32 != 0 || d->cout % 32 != 0 || d->k > 7 || d->len * d->cout * 2 >= (int64_t(1) << 31))
+        return c;
     if (d->k == 1) {
         c.kmax = 1;
         c.hmax = 0;

@@ -41,8 +41,6 @@ __device__ __forceinline__ void split_store8(half_t *dst, int cv, const float (&
     *reinterpret_cast<half8_t *>(dst + cv) = lo;
 }
 
-typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
-
 // The tile's per-column constants in LDS, past the stages and the epilogue's staging: the f32 bias,
 // and SnakeBeta's alpha and 1/beta, of its BN GEMM columns. They are written before the main loop,
 // whose barriers publish them, so the epilogue reads them from LDS instead of waiting on global

@@ -175,6 +175,7 @@ __device__ __forceinline__ int seg_swizzle(int r) {
 typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 constexpr uint32_t kOutOfRange = 0x80000000u;
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));  // a 16-byte buffer load or store
 
 __device__ __forceinline__ void load_lds_16(__amdgpu_buffer_rsrc_t rs, char *lds, uint32_t voffset,
                                             uint32_t soffset) {
@@ -657,7 +658,11 @@ __device__ __forceinline__ void wave_lds_order() {
 // (D[channel][position]): a lane holds one position and runs of four consecutive channels, which
 // go to LDS as 16-byte writes; rows then come back 8 channels per lane, so bias, residual and the
 // stores move 16 coalesced bytes per lane. The bias and the first block's residual rows are
-// requested up front, each next block's residual rows while the current block is written. `ld` is the output row length (cout), `n0` the tile's first output
+// requested up front, each next block's residual rows while the current block is written. The
+// residual, y_pre and y rows are reached through buffer resources bounded to the lane's rows
+// (lmax * ld halves, under 2^31 bytes: the route's eligibility checks it); a position past the
+// sequence gets an offset beyond them, so its loads read zeros and its stores are dropped, and no
+// branch splits a block. `ld` is the output row length (cout), `n0` the tile's first output
 // channel, `lmax` the lane's length. Called after the main loop's closing barrier (smem free).
 // PLAIN: no activation and no scale, known at compile time. The general form reads act and scale
 // at run time, but they are uniform over the tile: branching on them per element costs more scalar
@@ -685,6 +690,16 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
         const int cg = (lane + 64 * u) % CG;
         bb[u] = bias ? *reinterpret_cast<const half8_t *>(bias + nw + cg * 8) : half8_t{};
     }
+    const uint32_t lane_bytes = static_cast<uint32_t>(static_cast<int64_t>(lmax) * ld * 2);
+    const int64_t base = row0 * ld;
+    const __amdgpu_buffer_rsrc_t rs_res =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(res ? res + base : y + base), 0, lane_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs_y = __builtin_amdgcn_make_buffer_rsrc(y + base, 0, lane_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs_yp =
+        __builtin_amdgcn_make_buffer_rsrc(y_pre ? y_pre + base : y + base, 0, lane_bytes, kBufferWord3);
+    auto out_off = [&](int l, int n) -> uint32_t {
+        return l < lmax ? static_cast<uint32_t>((static_cast<int64_t>(l) * ld + n) * 2) : kOutOfRange;
+    };
     auto load_res = [&](int i, half8_t (&dst)[NG]) {
         const int lb = l0 + wm * Cfg::WTM + i * 32;
 #pragma unroll
@@ -692,8 +707,8 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
             const int g = lane + 64 * u;
             const int mr = g / CG, cg = g - (g / CG) * CG;
             dst[u] = half8_t{};
-            if (res && lb + mr < lmax)
-                dst[u] = *reinterpret_cast<const half8_t *>(res + (row0 + lb + mr) * ld + nw + cg * 8);
+            if (res)
+                dst[u] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs_res, out_off(lb + mr, nw + cg * 8), 0, 0));
         }
     };
     load_res(0, rr[0]);
@@ -719,12 +734,11 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
             const int g = lane + 64 * u;
             const int mr = g / CG, cg = g - (g / CG) * CG;
             const int l = lb + mr;
-            if (l >= lmax) continue;
             const int n = nw + cg * 8;
             const float4_t *src = reinterpret_cast<const float4_t *>(E + mr * Cfg::EPI_PITCH + cg * 8);
             const float4_t v0 = src[0], v1 = src[1];
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            const int64_t off = (row0 + l) * ld + n;
+            const uint32_t off = out_off(l, n);
             half8_t h;
             if constexpr (PLAIN) {
 #pragma unroll
@@ -761,7 +775,7 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
                     for (int q = 0; q < 8; ++q) h[q] = static_cast<half_t>(v[q]);
                 }
             }
-            if (y_pre) *reinterpret_cast<half8_t *>(y_pre + off) = h;
+            if (y_pre) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_t, h), rs_yp, off, 0, 0);
             if (a_out) {
                 const int c = n - n0;
                 const float4_t ka0 = *reinterpret_cast<const float4_t *>(tab + c);
@@ -774,7 +788,7 @@ __device__ __forceinline__ void conv_epilogue_form(const float16_t (&acc)[Cfg::T
                     h[q + 4] = snake_f16k(h[q + 4], ka1[q], kr1[q]);
                 }
             }
-            *reinterpret_cast<half8_t *>(y + off) = h;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u_t, h), rs_y, off, 0, 0);
         }
     }
 }
