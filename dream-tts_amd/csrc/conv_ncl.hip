@@ -91,17 +91,26 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
         }
     };
     auto store = [&](int c0, int b) {
+        if constexpr (SNAKE) {
+            // the window's SnakeBeta as one group (alpha 0 leaves a padding or idle value as it is)
+            float a[XE], r[XE];
+#pragma unroll
+            for (int i = 0; i < XE; ++i) {
+                const int e = tid + i * 256;
+                const int ci = e / rows, j = e - (e / rows) * rows;
+                const int s = l0 - p.pad_left + j;
+                const bool live = e < nx && s >= 0 && s < p.L;
+                a[i] = live ? p.a_in[c0 + ci] : 0.0f;
+                r[i] = live ? p.r_in[c0 + ci] : 0.0f;
+            }
+            snake_f32_group<XE>(xr, a, r);
+        }
 #pragma unroll
         for (int i = 0; i < XE; ++i) {
             const int e = tid + i * 256;
             if (e < nx) {
                 const int ci = e / rows, j = e - (e / rows) * rows;
-                float v = xr[i];
-                if constexpr (SNAKE) {
-                    const int s = l0 - p.pad_left + j;
-                    if (s >= 0 && s < p.L) v = snake_f32(v, p.a_in[c0 + ci], p.r_in[c0 + ci]);
-                }
-                xs[b][j * XP + ci] = v;  // transposed: row = position
+                xs[b][j * XP + ci] = xr[i];  // transposed: row = position
             }
         }
 #pragma unroll
@@ -169,17 +178,30 @@ __global__ __launch_bounds__(256, 2) void conv_ncl_f32_mfma(NclParams p) {
         const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
         rv[r] = p.res ? p.res[ybase + static_cast<int64_t>(co) * p.L + pos] : 0.0f;
     }
+    float v[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
-        const int64_t off = ybase + static_cast<int64_t>(co) * p.L + pos;
-        float v = acc[r];
-        if (p.bias) v += p.bias[co];
-        if (p.res) v += rv[r];
-        if (p.act == 1) v = tanhf(v);
-        if (p.y_pre) p.y_pre[off] = v;
-        if (p.a_out) v = snake_f32(v, p.a_out[co], p.r_out[co]);
-        p.y[off] = v;
+        v[r] = acc[r];
+        if (p.bias) v[r] += p.bias[co];
+        if (p.res) v[r] += rv[r];
+        if (p.act == 1) v[r] = tanhf(v[r]);
+        if (p.y_pre) p.y_pre[ybase + static_cast<int64_t>(co) * p.L + pos] = v[r];
+    }
+    if (p.a_out) {
+        float a[16], rr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+            a[r] = p.a_out[co];
+            rr[r] = p.r_out[co];
+        }
+        snake_f32_group<16>(v, a, rr);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int co = co0 + wm * 32 + (r >> 2) * 8 + kh * 4 + (r & 3);
+        p.y[ybase + static_cast<int64_t>(co) * p.L + pos] = v[r];
     }
 }
 
