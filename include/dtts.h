@@ -134,11 +134,11 @@ int dtts_conv1d_nlc_f32_ex(const dtts_conv_desc *desc, hipStream_t stream);
  * of the scaled values, and w_inv = 2^-s; it synchronises `stream` once (to read the weight's
  * largest magnitude). Each dtts_conv1d_nlc_f32_split call then splits x (and the residual) into
  * f16 hi/lo pairs in the workspace, computes sum(xh wh + xl wh + xh wl) in f32 (the dropped xl wl
- * is ~2^-22 of a term), adds bias and residual in f32, applies the epilogue SnakeBeta at full
- * precision, and writes f32 y (and y_pre). desc->w is the split weight; every other operand is
+ * is ~2^-22 of a term), adds bias and residual in f32, applies the epilogue SnakeBeta at f32
+ * accuracy, and writes f32 y (and y_pre). desc->w is the split weight; every other operand is
  * f32 as dtts_conv1d_nlc_f32_ex takes it. Taken for cin and cout multiples of 32, k <= 7 with
- * (k-1)*dilation <= 64 (cout a multiple of 96 for k > 2), no prologue SnakeBeta, act 0 and no
- * out_scale; anything else returns DTTS_ERR_UNSUPPORTED. Every operand is 16-byte aligned, and
+ * (k-1)*dilation <= 64 (cout a multiple of 96 for k > 2), len * cout * 4 < 2^31, no prologue
+ * SnakeBeta, act 0 and no out_scale; anything else returns DTTS_ERR_UNSUPPORTED. Every operand is 16-byte aligned, and
  * w_inv is the power of two dtts_conv_split_weight returned (DTTS_ERR_INVALID otherwise). */
 size_t dtts_conv_split_weight_bytes(int64_t cout, int64_t k, int64_t cin);
 int dtts_conv_split_weight(const float *w_tm, int64_t cout, int64_t k, int64_t cin, void *w_split,
