@@ -22,8 +22,7 @@ __device__ __forceinline__ float sin_rev_f16out(float t) { return __builtin_amdg
 // through r^9 (truncation under 2e-9), and sin^2(r + k pi/2) is sin^2 r for even k and
 // 1 - sin^2 r for odd k, so no cosine is needed. Larger and non-finite arguments take the library
 // sinf of the rounded product. The library sinf of the rounded product everywhere loses up to
-// 1e-6 to that rounding alone at |a x| ~ 30 (where the codec's convs drive SnakeBeta), and costs
-// about twice the instructions.
+// 1e-6 to that rounding alone at |a x| ~ 30 (where the codec's convs drive SnakeBeta).
 __device__ __forceinline__ bool sin2_f32_reducible(float a, float x) { return __builtin_fabsf(a * x) <= 0x1p20f; }
 
 // The reduction and series alone, for arguments sin2_f32_reducible accepts.
