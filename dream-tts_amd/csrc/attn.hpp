@@ -12,9 +12,10 @@
 // heads that share them. The span is split over groups of 16 lanes (4 per wave), each group
 // taking every G-th position; a lane of a group owns D/16 dimensions: the score is a 16-lane
 // shuffle reduction, and each group keeps a running softmax state (max m, sum l, weighted sum of
-// v) updated position by position (online softmax). The groups' states are combined through LDS
-// at the end: out = sum_k acc_k e^(m_k - M) / sum_k l_k e^(m_k - M), M the largest m_k. This is
-// the reference's exp(s - max) / sum weighting, regrouped; its K and V traffic is one pass.
+// v) updated position by position, or for f16 caches four positions at a time (online softmax).
+// The groups' states are combined through LDS at the end: out = sum_k acc_k e^(m_k - M) /
+// sum_k l_k e^(m_k - M), M the largest m_k (exponentials taken in base 2, below). This is the
+// reference's exp(s - max) / sum weighting, regrouped; its K and V traffic is one pass.
 // HBM-bound: 2 * D * (span - window_start) cache bytes per (lane, kv head).
 //
 // Long spans are split (flash-decoding): with a workspace, each workgroup takes kChunk positions
@@ -102,6 +103,13 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
+// The softmax runs in base 2: q is scaled by log2(e) as it is loaded, so scores, running maxima
+// and the chunk states' m are log2 of the natural-base ones and every weight is one v_exp_f32
+// (2^x; the library expf adds a range reduction and overflow checks, ~12 instructions). 2^x of a
+// difference below -126 flushes to 0: such a weight is under 1e-38 of the running maximum's.
+constexpr float kLog2e = 1.44269504088896340736f;
+__device__ __forceinline__ float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 constexpr int kChunk = 512;  // positions per workgroup when a span is split
 
 // Chunks of a lane's window [lo, hi) when split.
@@ -140,7 +148,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
     for (int g = 0; g < GQA; ++g) {
         const float *qp = q + (static_cast<int64_t>(bh) * GQA + g) * D + j * E;
 #pragma unroll
-        for (int e = 0; e < E; ++e) qv[g][e] = qp[e];
+        for (int e = 0; e < E; ++e) qv[g][e] = qp[e] * kLog2e;
     }
     float m[GQA], l[GQA], acc[GQA][E];
 #pragma unroll
@@ -160,8 +168,8 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
             for (int e = 0; e < E; ++e) s += qv[g][e] * kr[e];
             s = group16_sum(s);
             const float mn = fmaxf(m[g], s);
-            const float c = __builtin_expf(m[g] - mn);  // 0 on the group's first position
-            const float w = __builtin_expf(s - mn);
+            const float c = softmax_exp2(m[g] - mn);  // 0 on the group's first position
+            const float w = softmax_exp2(s - mn);
             l[g] = l[g] * c + w;
 #pragma unroll
             for (int e = 0; e < E; ++e) acc[g][e] = acc[g][e] * c + w * vr[e];
@@ -189,10 +197,10 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
             float mn = m[g];
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) mn = fmaxf(mn, s[u]);
-            const float c = __builtin_expf(m[g] - mn);  // 0 on the group's first block
+            const float c = softmax_exp2(m[g] - mn);  // 0 on the group's first block
             float w[UNROLL];
 #pragma unroll
-            for (int u = 0; u < UNROLL; ++u) w[u] = __builtin_expf(s[u] - mn);
+            for (int u = 0; u < UNROLL; ++u) w[u] = softmax_exp2(s[u] - mn);
             float lv = l[g] * c;
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) lv += w[u];
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
         float den = 0.0f, num = 0.0f;
 #pragma unroll 4
         for (int k = 0; k < G; ++k) {
-            const float f = __builtin_expf(sm_m[k][g] - mx);  // 0 for groups that saw no position
+            const float f = softmax_exp2(sm_m[k][g] - mx);  // 0 for groups that saw no position
             den += sm_l[k][g] * f;
             num += sm_acc[k][g][d] * f;
         }
@@ -268,7 +276,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
 }
 
 // Merges the chunk states of each (lane, kv head): out = sum_c num_c e^(m_c - M) / sum_c den_c
-// e^(m_c - M), M the largest m_c, chunks in order.
+// e^(m_c - M), M the largest m_c, chunks in order (m in log2 units, so 2^(m_c - M)).
 template <int D, int GQA, typename Src, typename OutT>
 __global__ __launch_bounds__(256) void decode_attn_merge(const float *part, OutT *out, int max_chunks, int n_kv,
                                                          Src sp) {
@@ -299,7 +307,7 @@ __global__ __launch_bounds__(256) void decode_attn_merge(const float *part, OutT
 #pragma unroll
             for (int c = 0; c < U; ++c)
                 if (c < nch) {
-                    const float f = __builtin_expf(mc[c] - mx);
+                    const float f = softmax_exp2(mc[c] - mx);
                     num += nc[c] * f;
                     den += dc[c] * f;
                 }
@@ -307,7 +315,7 @@ __global__ __launch_bounds__(256) void decode_attn_merge(const float *part, OutT
             float mx = -INFINITY;
             for (int c = 0; c < nch; ++c) mx = fmaxf(mx, pr[c * stride + D + 1]);
             for (int c = 0; c < nch; ++c) {
-                const float f = __builtin_expf(pr[c * stride + D + 1] - mx);
+                const float f = softmax_exp2(pr[c * stride + D + 1] - mx);
                 num += pr[c * stride + d] * f;
                 den += pr[c * stride + D] * f;
             }
@@ -316,16 +324,28 @@ __global__ __launch_bounds__(256) void decode_attn_merge(const float *part, OutT
     }
 }
 
+// Unused dynamic LDS that holds decode attention to at most 5 workgroups per CU (f16 caches) or
+// 4 (f32 caches), one wave per SIMD each: the kernel's registers would let 6 and 5 run, and more
+// rows in flight than that measured slower (f32 caches: the F32 and Q8_0 talker steps 5.44 ->
+// 5.85 ms at 5; f16 caches: attention 35.5 against 36.0 us at 6). 160 KB of LDS per CU.
+template <typename T, int D, int GQA>
+constexpr size_t attn_lds_pad() {
+    constexpr size_t wg = sizeof(T) == 4 ? 4 : 5;
+    constexpr size_t stat = sizeof(float) * (2 * 16 * GQA + 16 * GQA * D);  // the kernel's own LDS
+    return stat < 160 * 1024 / wg ? (160 * 1024 / wg - stat) / 512 * 512 : 0;
+}
+
 template <typename T, int D, int GQA, typename Src, typename OutT>
 hipError_t launch_gqa(const float *q, const T *kc, const T *vc, OutT *out, float *part, int max_chunks, int64_t b,
                       int64_t n_kv, int64_t cap, const Src &sp, hipStream_t stream) {
     const unsigned grid = static_cast<unsigned>(b * n_kv);
+    constexpr size_t pad = attn_lds_pad<T, D, GQA>();
     if (!part) {
-        decode_attn_kernel<T, D, GQA, 4, Src, OutT><<<grid, 256, 0, stream>>>(
+        decode_attn_kernel<T, D, GQA, 4, Src, OutT><<<grid, 256, pad, stream>>>(
             q, kc, vc, out, nullptr, 0, static_cast<int>(n_kv), static_cast<int>(cap), sp);
         return hipGetLastError();
     }
-    decode_attn_kernel<T, D, GQA, 4, Src, OutT><<<dim3(grid, max_chunks), 256, 0, stream>>>(
+    decode_attn_kernel<T, D, GQA, 4, Src, OutT><<<dim3(grid, max_chunks), 256, pad, stream>>>(
         q, kc, vc, out, part, max_chunks, static_cast<int>(n_kv), static_cast<int>(cap), sp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
