@@ -105,8 +105,8 @@ __device__ __forceinline__ float group16_sum(float v) {
 
 // The softmax runs in base 2: q is scaled by log2(e) as it is loaded, so scores, running maxima
 // and the chunk states' m are log2 of the natural-base ones and every weight is one v_exp_f32
-// (2^x; the library expf adds a range reduction and overflow checks, ~12 instructions). 2^x of a
-// difference below -126 flushes to 0: such a weight is under 1e-38 of the running maximum's.
+// (2^x; the library expf adds a range reduction and overflow checks, ~12 instructions). A weight
+// 2^x with x below -126 is under 1e-38 of the running maximum's, whatever the unit rounds it to.
 constexpr float kLog2e = 1.44269504088896340736f;
 __device__ __forceinline__ float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -181,8 +181,8 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(const float *q, co
     // caches the online-softmax state moves once per UNROLL positions: one running maximum over
     // the block, one rescale of l and acc (one exponential for it), then the block's weighted rows
     // in order (decode attention 41.6 -> 39-40 us, the f16 talker step -2%). With f32 caches the
-    // per-position update stays: the block form measured 5-6% slower there (the F32 and Q8_0
-    // talker steps), its freed registers raising occupancy past what the wider rows want.
+    // per-position update stays: held to four workgroups per CU (below), the block form measured
+    // within +-2% there.
     auto step_block = [&](const float (&kr)[UNROLL][E], const float (&vr)[UNROLL][E]) {
 #pragma unroll
         for (int g = 0; g < GQA; ++g) {
